@@ -1,0 +1,138 @@
+"""Build libictc_hip.so for gfx950 with hipcc (no cmake/ninja).
+
+Steps:
+  1. generate ``generated/ictc_cg_table.hpp`` (CG constants from the frozen basis);
+  2. write one translation unit per (input_lmax, edge_lmax, output_lmax, kernel
+     kind) with the explicit template instantiation, plus ``tp_instances.def``
+     listing the compiled combinations for the dispatch tables;
+  3. compile every TU to an object in parallel, largest first;
+  4. link the objects and the API TUs into ``ictc_o3/lib/libictc_hip.so``.
+
+Every HIP TU is compiled with ``-Xclang -target-feature -Xclang -packed-fp32-ops``
+(no packed FP32 VALU instructions are generated).
+
+``ICTC_HIP_COMBOS`` (e.g. ``"333,222,033"``) restricts the degree combinations for
+quick development builds; entries left out report ICTC_ERR_UNSUPPORTED at run time.
+
+Usage: python build.py [-j JOBS]
+"""
+from __future__ import annotations
+
+import argparse
+import concurrent.futures as cf
+import os
+import subprocess
+import sys
+import time
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.dirname(HERE)                         # ictc-o3-hp-ascend_amd/
+REPO = os.path.dirname(PKG)
+INCLUDE = os.path.join(REPO, "include")
+GEN = os.path.join(HERE, "generated")
+OBJ = os.path.join(HERE, "_build")
+LIB_DIR = os.path.join(PKG, "ictc_o3", "lib")
+LIB = os.path.join(LIB_DIR, "libictc_hip.so")
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+FLAGS = ["--offload-arch=" + ARCH, "-O3", "-std=c++20", "-fPIC", "-Wno-c99-designator",
+         "-mcode-object-version=5",
+         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+         "-I", INCLUDE, "-I", HERE]
+
+API_SOURCES = ["tp_api.hip", "harmonics_api.hip"]
+HARM_LMAX = 6
+INSTANCE_KINDS = {
+    "fwd": ("tp_kernels.hpp", "template int launch_forward<{a}, {b}, {c}>(const ictc_tp_desc&, "
+            "const float*, const float*, const float*, float*, int64_t, hipStream_t);"),
+    "bwd": ("tp_kernels.hpp", "template int launch_backward<{a}, {b}, {c}>(const ictc_tp_desc&, "
+            "const float*, const float*, const float*, const float*, float*, float*, float*, "
+            "int64_t, hipStream_t);"),
+}
+
+
+def _combos():
+    spec = os.environ.get("ICTC_HIP_COMBOS", "").strip()
+    if spec:
+        out = []
+        for tok in spec.split(","):
+            tok = tok.strip()
+            if len(tok) != 3 or not tok.isdigit() or any(int(ch) > 3 for ch in tok):
+                raise SystemExit(f"bad ICTC_HIP_COMBOS entry {tok!r}")
+            out.append(tuple(int(ch) for ch in tok))
+        return sorted(set(out))
+    return [(a, b, c) for a in range(4) for b in range(4) for c in range(4)]
+
+
+def _cost(a: int, b: int, c: int, kind: str) -> int:
+    """Rough compile cost (path-set size) to start the biggest TUs first."""
+    n = sum((2 * i + 1) * (2 * j + 1) * (2 * k + 1) for i in range(a + 1) for j in range(b + 1)
+            for k in range(c + 1) if abs(i - j) <= k <= i + j and (i + j + k) % 2 == 0)
+    return n * (4 if kind == "bwd" else 1)
+
+
+def _write_if_changed(path: str, text: str) -> None:
+    if not os.path.exists(path) or open(path).read() != text:
+        with open(path, "w") as fh:
+            fh.write(text)
+
+
+def _generate(combos) -> list:
+    os.makedirs(GEN, exist_ok=True)
+    subprocess.run([sys.executable, os.path.join(HERE, "gen_cg_table.py"),
+                    os.path.join(GEN, "ictc_cg_table.hpp")], check=True)
+    _write_if_changed(os.path.join(GEN, "tp_instances.def"),
+                      "".join(f"ICTC_DECLARE({a}, {b}, {c})\n" for a, b, c in combos))
+    units = []
+    for a, b, c in combos:
+        for kind, (header, line) in INSTANCE_KINDS.items():
+            path = os.path.join(GEN, f"tp_inst_{a}{b}{c}_{kind}.hip")
+            _write_if_changed(path, f'#include "{header}"\nnamespace ictc {{\n'
+                                    f'{line.format(a=a, b=b, c=c)}\n}}  // namespace ictc\n')
+            units.append((_cost(a, b, c, kind), path))
+    for l in range(HARM_LMAX + 1):
+        path = os.path.join(GEN, f"harm_inst_{l}.hip")
+        _write_if_changed(path, '#include "harmonics.hpp"\nnamespace ictc {\n'
+                                f'template int launch_harmonics<{l}>(int, const float*, const float*, '
+                                'const float*, const float*, float*, int64_t, hipStream_t);\n'
+                                '}  // namespace ictc\n')
+        units.append((60 * (l + 1) ** 3, path))
+    units.sort(reverse=True)
+    return [p for _, p in units]
+
+
+def _compile(src: str) -> str:
+    os.makedirs(OBJ, exist_ok=True)
+    obj = os.path.join(OBJ, os.path.splitext(os.path.basename(src))[0] + ".o")
+    cmd = [HIPCC, *FLAGS, "-c", src, "-o", obj]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {src}:\n{res.stderr}")
+    return obj
+
+
+def build(jobs: int | None = None, verbose: bool = True) -> str:
+    t0 = time.time()
+    combos = _combos()
+    units = [os.path.join(HERE, s) for s in API_SOURCES] + _generate(combos)
+    jobs = jobs or max(1, min(len(units), os.cpu_count() or 1))
+    with cf.ThreadPoolExecutor(max_workers=jobs) as pool:
+        objs = list(pool.map(_compile, units))
+    os.makedirs(LIB_DIR, exist_ok=True)
+    tmp = LIB + ".tmp"
+    res = subprocess.run([HIPCC, "--offload-arch=" + ARCH, "-shared", "-fPIC", *objs, "-o", tmp],
+                         capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed:\n{res.stderr}")
+    os.replace(tmp, LIB)
+    if verbose:
+        print(f"built {LIB} ({len(combos)} degree combinations, {len(units)} units, "
+              f"{time.time() - t0:.0f}s)", flush=True)
+    return LIB
+
+
+if __name__ == "__main__":
+    ap = argparse.ArgumentParser()
+    ap.add_argument("-j", "--jobs", type=int, default=None)
+    build(ap.parse_args().jobs)

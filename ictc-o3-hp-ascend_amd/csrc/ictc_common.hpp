@@ -1,0 +1,126 @@
+// Shared device helpers for the ictc_o3 HIP kernels (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "ictc_hip.h"
+
+namespace ictc {
+
+constexpr int kWave = 64;
+
+template <int N>
+struct Int {
+  static constexpr int value = N;
+  constexpr operator int() const { return N; }
+};
+
+// Compile-time loop: f(Int<B>{}), f(Int<B+1>{}), ..., f(Int<E-1>{}).
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(Int<B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
+// Full triangle/parity path set of (LIN, LE, LOUT) in ascending (l1,l2,l3) order,
+// the enumeration order of the reference owner (ictd_irreps.py:2161-2175).
+struct PathTable {
+  int n = 0;
+  int l1[ICTC_MAX_PATHS] = {};
+  int l2[ICTC_MAX_PATHS] = {};
+  int l3[ICTC_MAX_PATHS] = {};
+  int bond[ICTC_MAX_PATHS] = {};  // first bond entry of the path, M_p stored [k][i]
+  int nbond = 0;
+};
+
+constexpr PathTable make_paths(int lin, int le, int lout) {
+  PathTable t{};
+  for (int a = 0; a <= lin; ++a)
+    for (int b = 0; b <= le; ++b)
+      for (int c = 0; c <= lout; ++c) {
+        const int lo = a > b ? a - b : b - a;
+        if (c < lo || c > a + b || ((a + b + c) & 1)) continue;
+        t.l1[t.n] = a;
+        t.l2[t.n] = b;
+        t.l3[t.n] = c;
+        t.bond[t.n] = t.nbond;
+        t.nbond += (2 * a + 1) * (2 * c + 1);
+        ++t.n;
+      }
+  return t;
+}
+
+template <int LIN, int LE, int LOUT>
+struct Paths {
+  static constexpr PathTable tab = make_paths(LIN, LE, LOUT);
+  static constexpr int N = tab.n;
+  static constexpr int NB = tab.nbond;
+  static constexpr int NX = (LIN + 1) * (LIN + 1);
+  static constexpr int NY = (LE + 1) * (LE + 1);
+};
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Vector of NV consecutive floats: one global load/store instruction per lane.
+template <int NV>
+struct Vec {
+  float v[NV];
+};
+
+template <int NV>
+__device__ __forceinline__ Vec<NV> load_vec(const float* __restrict__ p) {
+  Vec<NV> r;
+  if constexpr (NV == 1) {
+    r.v[0] = p[0];
+  } else if constexpr (NV == 2) {
+    const f32x2 t = *reinterpret_cast<const f32x2*>(p);
+    r.v[0] = t.x;
+    r.v[1] = t.y;
+  } else {
+    static_assert(NV == 4, "NV must be 1, 2 or 4");
+    const f32x4 t = *reinterpret_cast<const f32x4*>(p);
+    r.v[0] = t.x;
+    r.v[1] = t.y;
+    r.v[2] = t.z;
+    r.v[3] = t.w;
+  }
+  return r;
+}
+
+// Streaming store: the outputs are written once and not re-read by this kernel.
+template <int NV>
+__device__ __forceinline__ void store_vec_nt(float* __restrict__ p, const Vec<NV>& r) {
+  if constexpr (NV == 1) {
+    __builtin_nontemporal_store(r.v[0], p);
+  } else if constexpr (NV == 2) {
+    f32x2 t = {r.v[0], r.v[1]};
+    __builtin_nontemporal_store(t, reinterpret_cast<f32x2*>(p));
+  } else {
+    f32x4 t = {r.v[0], r.v[1], r.v[2], r.v[3]};
+    __builtin_nontemporal_store(t, reinterpret_cast<f32x4*>(p));
+  }
+}
+
+template <int NV>
+__device__ __forceinline__ void store_vec(float* __restrict__ p, const Vec<NV>& r) {
+  if constexpr (NV == 1) {
+    p[0] = r.v[0];
+  } else if constexpr (NV == 2) {
+    *reinterpret_cast<f32x2*>(p) = f32x2{r.v[0], r.v[1]};
+  } else {
+    *reinterpret_cast<f32x4*>(p) = f32x4{r.v[0], r.v[1], r.v[2], r.v[3]};
+  }
+}
+
+// Sum over the 64 lanes of a wave; every lane receives the total.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+}  // namespace ictc

@@ -1,0 +1,109 @@
+// extern "C" entry points of the tensor-product family: descriptor validation and
+// dispatch to the per-degree instantiations compiled in generated/tp_inst_*.hip.
+#include "tp_kernels.hpp"
+
+namespace ictc {
+
+// Explicit instantiations live in separate translation units (parallel build).
+#define ICTC_DECLARE(A, B, C)                                                                  \
+  extern template int launch_forward<A, B, C>(const ictc_tp_desc&, const float*, const float*,   \
+                                              const float*, float*, int64_t, hipStream_t);      \
+  extern template int launch_backward<A, B, C>(const ictc_tp_desc&, const float*, const float*,  \
+                                               const float*, const float*, float*, float*, float*, \
+                                               int64_t, hipStream_t);
+#include "generated/tp_instances.def"
+#undef ICTC_DECLARE
+
+// Dispatch tables indexed by input_lmax*16 + edge_lmax*4 + output_lmax; entries of
+// combinations left out of a (development) build are null and report UNSUPPORTED.
+#define ICTC_DECLARE(A, B, C) [A * 16 + B * 4 + C] = &launch_forward<A, B, C>,
+const FwdLaunch kFwdTable[64] = {
+#include "generated/tp_instances.def"
+};
+#undef ICTC_DECLARE
+#define ICTC_DECLARE(A, B, C) [A * 16 + B * 4 + C] = &launch_backward<A, B, C>,
+const BwdLaunch kBwdTable[64] = {
+#include "generated/tp_instances.def"
+};
+#undef ICTC_DECLARE
+
+// Host-side validation of a descriptor against the compiled path enumeration.
+int check_desc(const ictc_tp_desc* d) {
+  if (d == nullptr) return ICTC_ERR_INVALID_ARGUMENT;
+  if (d->channels < 1 || d->num_paths < 0 || d->num_paths > ICTC_MAX_PATHS || d->out_components < 0)
+    return ICTC_ERR_INVALID_ARGUMENT;
+  if (d->input_lmax < 0 || d->edge_lmax < 0 || d->output_lmax < 0) return ICTC_ERR_INVALID_ARGUMENT;
+  if (d->input_lmax > 3 || d->edge_lmax > 3 || d->output_lmax > 3) return ICTC_ERR_UNSUPPORTED;
+  const PathTable t = make_paths(d->input_lmax, d->edge_lmax, d->output_lmax);
+  bool seen[ICTC_MAX_PATHS] = {};
+  int present = 0;
+  for (int s = 0; s < t.n; ++s) {
+    const int gi = d->gate_index[s];
+    if (gi < 0) continue;
+    if (gi >= d->num_paths || seen[gi]) return ICTC_ERR_INVALID_ARGUMENT;
+    seen[gi] = true;
+    ++present;
+    if (d->out_offset[s] < 0 || d->out_offset[s] + 2 * t.l3[s] + 1 > d->out_components)
+      return ICTC_ERR_INVALID_ARGUMENT;
+  }
+  if (present != d->num_paths) return ICTC_ERR_INVALID_ARGUMENT;
+  return ICTC_OK;
+}
+
+inline int table_index(const ictc_tp_desc* d) {
+  return d->input_lmax * 16 + d->edge_lmax * 4 + d->output_lmax;
+}
+
+}  // namespace ictc
+
+extern "C" {
+
+const char* ictc_hip_status_string(int status) {
+  switch (status) {
+    case ICTC_OK: return "ok";
+    case ICTC_ERR_INVALID_ARGUMENT: return "invalid argument";
+    case ICTC_ERR_UNSUPPORTED: return "unsupported degree combination";
+    case ICTC_ERR_LAUNCH: return "kernel launch failed";
+    case ICTC_ERR_INDEX: return "index out of range";
+    default: return "unknown status";
+  }
+}
+
+int ictc_hip_abi_version(void) { return 1; }
+
+int ictc_hip_tp_slot_count(int input_lmax, int edge_lmax, int output_lmax) {
+  if (input_lmax < 0 || edge_lmax < 0 || output_lmax < 0 || input_lmax > 3 || edge_lmax > 3 ||
+      output_lmax > 3)
+    return -1;
+  return ictc::make_paths(input_lmax, edge_lmax, output_lmax).n;
+}
+
+int ictc_hip_tp_forward(const ictc_tp_desc* desc, const float* features, const float* harmonics,
+                        const float* gates, float* out, int64_t rows, hipStream_t stream) {
+  const int st = ictc::check_desc(desc);
+  if (st != ICTC_OK) return st;
+  if (rows < 0) return ICTC_ERR_INVALID_ARGUMENT;
+  if (rows == 0) return ICTC_OK;
+  if (!features || !harmonics || !gates || !out) return ICTC_ERR_INVALID_ARGUMENT;
+  const ictc::FwdLaunch fn = ictc::kFwdTable[ictc::table_index(desc)];
+  if (fn == nullptr) return ICTC_ERR_UNSUPPORTED;
+  return fn(*desc, features, harmonics, gates, out, rows, stream);
+}
+
+int ictc_hip_tp_backward(const ictc_tp_desc* desc, const float* features, const float* harmonics,
+                         const float* gates, const float* grad_out, float* grad_features,
+                         float* grad_harmonics, float* grad_gates, int64_t rows, hipStream_t stream) {
+  const int st = ictc::check_desc(desc);
+  if (st != ICTC_OK) return st;
+  if (rows < 0) return ICTC_ERR_INVALID_ARGUMENT;
+  if (rows == 0) return ICTC_OK;
+  if (!harmonics || !gates || !grad_out) return ICTC_ERR_INVALID_ARGUMENT;
+  if ((grad_harmonics || grad_gates) && !features) return ICTC_ERR_INVALID_ARGUMENT;
+  if (!grad_features && !grad_harmonics && !grad_gates) return ICTC_OK;
+  const ictc::BwdLaunch fn = ictc::kBwdTable[ictc::table_index(desc)];
+  if (fn == nullptr) return ICTC_ERR_UNSUPPORTED;
+  return fn(*desc, features, harmonics, gates, grad_out, grad_features, grad_harmonics, grad_gates,
+            rows, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,302 @@
+// Channelwise path-preserving CG tensor product: forward and fused VJP (gfx950).
+//
+// Math (per instance e, path p = (l1,l2,l3), channel c, output component k):
+//   M_p[e,i,k] = s_p * sum_j Y[e, l2^2+j] * Chat_p[i,j,k]            ("bond")
+//   out[e, (o_p+k)*C + c] = g[e,p,c] * sum_i x[e, (l1^2+i)*C + c] * M_p[e,i,k]
+// which is EdgeWeightedPathPreservingTensorProduct._forward_index_add
+// (reference ictc_o3/basis/ictd_irreps.py:2669-2748) with the Y-side contracted
+// first, as the reference's bond projection does (backends/ascend/tensor_product.py:30-55,
+// structured_product.py:7-22).
+//
+// Launch shape: one 256-thread workgroup per tile of kTileEdges instances.
+//   1. the tile's harmonics are staged in LDS and the bond matrices M_p of all
+//      tile instances are built cooperatively into LDS (CG read from __constant__);
+//   2. each wave then owns whole instances: lane l covers channels
+//      [l*NV, l*NV+NV) (+64*NV per chunk), so every global access of a wave is one
+//      contiguous run of 64*NV floats along the channel axis.  M_p is read from LDS
+//      as a wave-uniform broadcast.
+// The instance loop never round-trips intermediates through HBM: the forward reads
+// x, Y, g once and writes out once; the VJP reads x, Y, g, dout once and writes
+// dx, dY, dg once.
+#pragma once
+#include "ictc_common.hpp"
+#include "generated/ictc_cg_table.hpp"
+
+namespace ictc {
+
+constexpr int kTileEdges = 8;
+constexpr int kBlock = 256;
+constexpr int kWavesPerBlock = kBlock / kWave;
+
+template <int LIN, int LE, int LOUT>
+__device__ __forceinline__ void build_bond(const float (*sY)[Paths<LIN, LE, LOUT>::NY],
+                                           float (*sM)[Paths<LIN, LE, LOUT>::NB > 0 ? Paths<LIN, LE, LOUT>::NB : 1],
+                                           const ictc_tp_desc& d, int tid) {
+  using PS = Paths<LIN, LE, LOUT>;
+  static_for<0, PS::N>([&](auto P) {
+    constexpr int p = P;
+    constexpr int l1 = PS::tab.l1[p], l2 = PS::tab.l2[p], l3 = PS::tab.l3[p];
+    constexpr int ni = 2 * l1 + 1, nj = 2 * l2 + 1, no = 2 * l3 + 1;
+    constexpr int boff = PS::tab.bond[p];
+    constexpr int cgo = CGTab<l1, l2, l3>::offset;
+    const float s = d.scale[p];
+    for (int t = tid; t < kTileEdges * ni * no; t += kBlock) {
+      const int e = t / (ni * no);
+      const int r = t - e * (ni * no);  // M_p stored [k][i]: r = k*ni + i
+      const int k = r / ni;
+      const int i = r - k * ni;
+      float acc = 0.f;
+      static_for<0, nj>([&](auto J) {
+        acc = fmaf(sY[e][l2 * l2 + J], kCGFlat[cgo + (i * nj + J) * no + k], acc);
+      });
+      sM[e][boff + r] = acc * s;
+    }
+  });
+}
+
+template <int LIN, int LE, int LOUT, int NV>
+__global__ void __launch_bounds__(kBlock)
+tp_forward_kernel(const float* __restrict__ x, const float* __restrict__ y,
+                  const float* __restrict__ g, float* __restrict__ out,
+                  const ictc_tp_desc d, int64_t rows) {
+  using PS = Paths<LIN, LE, LOUT>;
+  constexpr int NX = PS::NX, NY = PS::NY;
+  constexpr int NBS = PS::NB > 0 ? PS::NB : 1;
+  __shared__ float sY[kTileEdges][NY];
+  __shared__ float sM[kTileEdges][NBS];
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid / kWave;
+  const int64_t e0 = static_cast<int64_t>(blockIdx.x) * kTileEdges;
+  for (int t = tid; t < kTileEdges * NY; t += kBlock) {
+    const int e = t / NY;
+    sY[e][t - e * NY] = (e0 + e < rows) ? y[(e0 + e) * NY + (t - e * NY)] : 0.f;
+  }
+  __syncthreads();
+  build_bond<LIN, LE, LOUT>(sY, sM, d, tid);
+  __syncthreads();
+
+  const int C = d.channels;
+  const int64_t xw = static_cast<int64_t>(NX) * C;
+  const int64_t gw = static_cast<int64_t>(d.num_paths) * C;
+  const int64_t ow = static_cast<int64_t>(d.out_components) * C;
+  for (int le = wave; le < kTileEdges; le += kWavesPerBlock) {
+    const int64_t e = e0 + le;
+    if (e >= rows) break;
+    const float* __restrict__ xe = x + e * xw;
+    const float* __restrict__ ge = g + e * gw;
+    float* __restrict__ oe = out + e * ow;
+    for (int c = lane * NV; c < C; c += kWave * NV) {
+      Vec<NV> xr[NX];
+#pragma unroll
+      for (int m = 0; m < NX; ++m) xr[m] = load_vec<NV>(xe + static_cast<int64_t>(m) * C + c);
+      static_for<0, PS::N>([&](auto P) {
+        constexpr int p = P;
+        constexpr int l1 = PS::tab.l1[p], l3 = PS::tab.l3[p];
+        constexpr int ni = 2 * l1 + 1, no = 2 * l3 + 1;
+        constexpr int boff = PS::tab.bond[p];
+        const int gi = d.gate_index[p];
+        if (gi < 0) return;
+        const Vec<NV> gv = load_vec<NV>(ge + static_cast<int64_t>(gi) * C + c);
+        const int oo = d.out_offset[p];
+        static_for<0, no>([&](auto K) {
+          Vec<NV> acc;
+#pragma unroll
+          for (int v = 0; v < NV; ++v) acc.v[v] = 0.f;
+          static_for<0, ni>([&](auto I) {
+            const float m = sM[le][boff + K * ni + I];
+#pragma unroll
+            for (int v = 0; v < NV; ++v) acc.v[v] = fmaf(xr[l1 * l1 + I].v[v], m, acc.v[v]);
+          });
+#pragma unroll
+          for (int v = 0; v < NV; ++v) acc.v[v] *= gv.v[v];
+          store_vec_nt<NV>(oe + static_cast<int64_t>(oo + K) * C + c, acc);
+        });
+      });
+    }
+  }
+}
+
+// Fused VJP.  For each path:  go_k = g * dout_k
+//   dx[l1,i]  += sum_k M_p[i,k] * go_k                        (structured_product.py:49-58)
+//   dg[p]      = sum_k dout_k * sum_i x_i M_p[i,k]             (structured_product.py:75-87)
+//   dY[l2,j]  += s_p * sum_{i,k} Chat_p[i,j,k] * sum_c x_i go_k  (structured_product.py:61-72
+//                                                              composed with the bond adjoint)
+// The dY channel sum is a per-lane partial followed by one wave reduction per instance.
+template <int LIN, int LE, int LOUT, int NV>
+__global__ void __launch_bounds__(kBlock)
+tp_backward_kernel(const float* __restrict__ x, const float* __restrict__ y,
+                   const float* __restrict__ g, const float* __restrict__ go,
+                   float* __restrict__ dx, float* __restrict__ dy, float* __restrict__ dg,
+                   const ictc_tp_desc d, int64_t rows) {
+  using PS = Paths<LIN, LE, LOUT>;
+  constexpr int NX = PS::NX, NY = PS::NY;
+  constexpr int NBS = PS::NB > 0 ? PS::NB : 1;
+  __shared__ float sY[kTileEdges][NY];
+  __shared__ float sM[kTileEdges][NBS];
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid / kWave;
+  const int64_t e0 = static_cast<int64_t>(blockIdx.x) * kTileEdges;
+  for (int t = tid; t < kTileEdges * NY; t += kBlock) {
+    const int e = t / NY;
+    sY[e][t - e * NY] = (e0 + e < rows) ? y[(e0 + e) * NY + (t - e * NY)] : 0.f;
+  }
+  __syncthreads();
+  build_bond<LIN, LE, LOUT>(sY, sM, d, tid);
+  __syncthreads();
+
+  const bool need_dx = dx != nullptr;
+  const bool need_dy = dy != nullptr;
+  const bool need_dg = dg != nullptr;
+  const bool need_x = need_dy || need_dg;
+  const int C = d.channels;
+  const int64_t xw = static_cast<int64_t>(NX) * C;
+  const int64_t gw = static_cast<int64_t>(d.num_paths) * C;
+  const int64_t ow = static_cast<int64_t>(d.out_components) * C;
+  for (int le = wave; le < kTileEdges; le += kWavesPerBlock) {
+    const int64_t e = e0 + le;
+    if (e >= rows) break;
+    const float* __restrict__ xe = x + e * xw;
+    const float* __restrict__ ge = g + e * gw;
+    const float* __restrict__ oe = go + e * ow;
+    float dyl[NY];
+#pragma unroll
+    for (int j = 0; j < NY; ++j) dyl[j] = 0.f;
+    for (int c = lane * NV; c < C; c += kWave * NV) {
+      Vec<NV> xr[NX];
+      Vec<NV> dxr[NX];
+#pragma unroll
+      for (int m = 0; m < NX; ++m) {
+        if (need_x) {
+          xr[m] = load_vec<NV>(xe + static_cast<int64_t>(m) * C + c);
+        } else {
+#pragma unroll
+          for (int v = 0; v < NV; ++v) xr[m].v[v] = 0.f;
+        }
+#pragma unroll
+        for (int v = 0; v < NV; ++v) dxr[m].v[v] = 0.f;
+      }
+      static_for<0, PS::N>([&](auto P) {
+        constexpr int p = P;
+        constexpr int l1 = PS::tab.l1[p], l2 = PS::tab.l2[p], l3 = PS::tab.l3[p];
+        constexpr int ni = 2 * l1 + 1, nj = 2 * l2 + 1, no = 2 * l3 + 1;
+        constexpr int boff = PS::tab.bond[p];
+        using CG = CGTab<l1, l2, l3>;
+        const int gi = d.gate_index[p];
+        if (gi < 0) {
+          if (need_dg) return;  // absent path: no gate block to write
+          return;
+        }
+        const Vec<NV> gv = load_vec<NV>(ge + static_cast<int64_t>(gi) * C + c);
+        const int oo = d.out_offset[p];
+        Vec<NV> o[no];
+        static_for<0, no>([&](auto K) {
+          o[K] = load_vec<NV>(oe + static_cast<int64_t>(oo + K) * C + c);
+        });
+        if (need_dg) {
+          Vec<NV> dgv;
+#pragma unroll
+          for (int v = 0; v < NV; ++v) dgv.v[v] = 0.f;
+          static_for<0, no>([&](auto K) {
+            Vec<NV> base;
+#pragma unroll
+            for (int v = 0; v < NV; ++v) base.v[v] = 0.f;
+            static_for<0, ni>([&](auto I) {
+              const float m = sM[le][boff + K * ni + I];
+#pragma unroll
+              for (int v = 0; v < NV; ++v) base.v[v] = fmaf(xr[l1 * l1 + I].v[v], m, base.v[v]);
+            });
+#pragma unroll
+            for (int v = 0; v < NV; ++v) dgv.v[v] = fmaf(base.v[v], o[K].v[v], dgv.v[v]);
+          });
+          store_vec_nt<NV>(dg + e * gw + static_cast<int64_t>(gi) * C + c, dgv);
+        }
+        Vec<NV> gov[no];
+        static_for<0, no>([&](auto K) {
+#pragma unroll
+          for (int v = 0; v < NV; ++v) gov[K].v[v] = gv.v[v] * o[K].v[v];
+        });
+        if (need_dx) {
+          static_for<0, ni>([&](auto I) {
+            static_for<0, no>([&](auto K) {
+              const float m = sM[le][boff + K * ni + I];
+#pragma unroll
+              for (int v = 0; v < NV; ++v)
+                dxr[l1 * l1 + I].v[v] = fmaf(m, gov[K].v[v], dxr[l1 * l1 + I].v[v]);
+            });
+          });
+        }
+        if (need_dy) {
+          float part[nj];
+#pragma unroll
+          for (int j = 0; j < nj; ++j) part[j] = 0.f;
+          static_for<0, ni>([&](auto I) {
+            static_for<0, no>([&](auto K) {
+              float t = 0.f;
+#pragma unroll
+              for (int v = 0; v < NV; ++v) t = fmaf(xr[l1 * l1 + I].v[v], gov[K].v[v], t);
+              static_for<0, nj>([&](auto J) {
+                constexpr float cg = CG::v[(I * nj + J) * no + K];
+                if constexpr (cg != 0.0f) part[J] = fmaf(cg, t, part[J]);
+              });
+            });
+          });
+          const float s = d.scale[p];
+#pragma unroll
+          for (int j = 0; j < nj; ++j) dyl[l2 * l2 + j] = fmaf(s, part[j], dyl[l2 * l2 + j]);
+        }
+      });
+      if (need_dx) {
+        float* __restrict__ dxe = dx + e * xw;
+#pragma unroll
+        for (int m = 0; m < NX; ++m) store_vec_nt<NV>(dxe + static_cast<int64_t>(m) * C + c, dxr[m]);
+      }
+    }
+    if (need_dy) {
+      float mine = 0.f;
+#pragma unroll
+      for (int j = 0; j < NY; ++j) {
+        const float tot = wave_sum(dyl[j]);
+        if (lane == j) mine = tot;
+      }
+      if (lane < NY) dy[e * NY + lane] = mine;
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------- launchers
+using FwdLaunch = int (*)(const ictc_tp_desc&, const float*, const float*, const float*, float*,
+                          int64_t, hipStream_t);
+using BwdLaunch = int (*)(const ictc_tp_desc&, const float*, const float*, const float*,
+                          const float*, float*, float*, float*, int64_t, hipStream_t);
+
+inline int launch_status() { return hipGetLastError() == hipSuccess ? ICTC_OK : ICTC_ERR_LAUNCH; }
+
+template <int LIN, int LE, int LOUT>
+int launch_forward(const ictc_tp_desc& d, const float* x, const float* y, const float* g, float* out,
+                   int64_t rows, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>((rows + kTileEdges - 1) / kTileEdges));
+  if (d.channels % (2 * kWave) == 0)
+    hipLaunchKernelGGL((tp_forward_kernel<LIN, LE, LOUT, 2>), grid, dim3(kBlock), 0, stream, x, y, g,
+                       out, d, rows);
+  else
+    hipLaunchKernelGGL((tp_forward_kernel<LIN, LE, LOUT, 1>), grid, dim3(kBlock), 0, stream, x, y, g,
+                       out, d, rows);
+  return launch_status();
+}
+
+template <int LIN, int LE, int LOUT>
+int launch_backward(const ictc_tp_desc& d, const float* x, const float* y, const float* g,
+                    const float* go, float* dx, float* dy, float* dg, int64_t rows, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>((rows + kTileEdges - 1) / kTileEdges));
+  if (d.channels % (2 * kWave) == 0)
+    hipLaunchKernelGGL((tp_backward_kernel<LIN, LE, LOUT, 2>), grid, dim3(kBlock), 0, stream, x, y, g,
+                       go, dx, dy, dg, d, rows);
+  else
+    hipLaunchKernelGGL((tp_backward_kernel<LIN, LE, LOUT, 1>), grid, dim3(kBlock), 0, stream, x, y, g,
+                       go, dx, dy, dg, d, rows);
+  return launch_status();
+}
+
+}  // namespace ictc

@@ -1,0 +1,28 @@
+"""Prune adjoints the autograd engine will not execute.
+
+Same contract as the reference's ``required_gradients``
+(``ictc_o3/autograd/adjoint_requirements.py:12-26``): ``ctx.needs_input_grad``
+reflects requires_grad at graph construction, but a ``torch.autograd.grad`` call
+that targets only some leaves (e.g. positions for forces) will not run the
+gradient nodes of the others.  When the engine can be queried, only adjoints
+whose gradient edge will execute are requested; otherwise every declared
+gradient is kept.
+"""
+import torch
+
+
+def required_gradients(inputs, declared):
+    query = getattr(torch._C, "_will_engine_execute_node", None)
+    if query is None or torch.compiler.is_compiling():
+        return tuple(bool(d) for d in declared)
+    result = []
+    for tensor, needed in zip(inputs, declared):
+        if not needed or tensor is None:
+            result.append(False)
+            continue
+        try:
+            node = torch.autograd.graph.get_gradient_edge(tensor).node
+            result.append(bool(query(node)))
+        except (RuntimeError, AttributeError, AssertionError):
+            result.append(True)
+    return tuple(result)

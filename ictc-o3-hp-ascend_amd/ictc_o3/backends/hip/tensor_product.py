@@ -1,0 +1,195 @@
+"""Channelwise path-preserving tensor product on the HIP kernels, with autograd to
+any order.
+
+The map out = F(x, Y, g) is trilinear in (features x, harmonics Y, gates g), so
+its VJP (Gx, GY, Gg) is trilinear as well and every mixed derivative is one of
+the same two kernels with an operand substituted -- the bilinear-substitution
+scheme of the reference's structured adjoint (``backends/ascend/structured_product.py:97-183``):
+
+    <hx, Gx(Y,g,o)> : d/dY = GY(hx,g,o),  d/dg = Gg(hx,Y,o),  d/do = F(hx,Y,g)
+    <hY, GY(x,g,o)> : d/dx = Gx(hY,g,o),  d/dg = Gg(x,hY,o),  d/do = F(x,hY,g)
+    <hg, Gg(x,Y,o)> : d/dx = Gx(Y,hg,o),  d/dY = GY(x,hg,o),  d/do = F(x,Y,hg)
+
+Both Functions call each other through ``.apply``, so ``create_graph=True`` chains
+to third and higher order with no separate code path.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Dict, Optional, Sequence, Tuple
+
+import torch
+
+from ... import _lib
+from ...autograd.adjoint_requirements import required_gradients
+from ...basis.ictd_irreps import PathPlan, triangle_paths
+
+
+class TensorProductPlan:
+    """Immutable launch description of one owner (paths, channels, degrees)."""
+
+    def __init__(self, paths: Sequence[Tuple[int, int, int]], channels: int, input_lmax: int,
+                 edge_lmax: int, lmax: Optional[int] = None):
+        paths = [tuple(int(v) for v in p) for p in paths]
+        if not paths:
+            raise ValueError("a tensor product needs at least one path")
+        self.channels, self.input_lmax, self.edge_lmax = int(channels), int(input_lmax), int(edge_lmax)
+        self.output_lmax = max(p[2] for p in paths)
+        self.lmax = max(lmax if lmax is not None else 0, self.input_lmax, self.edge_lmax, self.output_lmax)
+        if any(i > self.input_lmax or j > self.edge_lmax for i, j, _ in paths):
+            raise ValueError("Declared input degrees must cover every tensor-product path")
+        if max(self.input_lmax, self.edge_lmax, self.output_lmax) > 3:
+            raise ValueError("the HIP tensor-product kernels support degrees up to 3")
+        self.plan = PathPlan(paths, channels)
+        self.plan.path_counts_by_l = {l: self.plan.path_counts_by_l.get(l, 0) for l in range(self.lmax + 1)}
+        self.paths = self.plan.paths
+        full = triangle_paths(self.input_lmax, self.edge_lmax, self.output_lmax)
+        index = {p: i for i, p in enumerate(paths)}
+        missing = set(paths) - set(full)
+        if missing:
+            raise ValueError(f"paths {sorted(missing)} violate the triangle/parity rule")
+        desc = _lib.TpDesc()
+        desc.channels = self.channels
+        desc.input_lmax, desc.edge_lmax, desc.output_lmax = self.input_lmax, self.edge_lmax, self.output_lmax
+        desc.num_paths = len(paths)
+        desc.out_components = self.plan.output_components
+        for s, p in enumerate(full):
+            gi = index.get(p, -1)
+            desc.gate_index[s] = gi
+            desc.out_offset[s] = self.plan.output_component_offset[gi] if gi >= 0 else 0
+            desc.scale[s] = self.plan.scales[gi] if gi >= 0 else 0.0
+        self.desc = desc
+        self.num_paths = len(paths)
+        self.x_width = self.channels * (self.input_lmax + 1) ** 2
+        self.y_width = (self.edge_lmax + 1) ** 2
+        self.gate_width = self.num_paths * self.channels
+        self.out_width = self.plan.output_components * self.channels
+
+
+def _forward_raw(plan: TensorProductPlan, x, y, g) -> torch.Tensor:
+    rows = x.shape[0]
+    out = torch.empty(rows, plan.out_width, device=x.device, dtype=torch.float32)
+    _lib.check(_lib.lib().ictc_hip_tp_forward(ctypes.byref(plan.desc), x.data_ptr(), y.data_ptr(),
+                                               g.data_ptr(), out.data_ptr(), rows,
+                                               _lib.stream_of(x.device)), "ictc_hip_tp_forward")
+    return out
+
+
+def _backward_raw(plan: TensorProductPlan, need, x, y, g, go):
+    rows = go.shape[0]
+    dev = go.device
+    dx = torch.empty(rows, plan.x_width, device=dev, dtype=torch.float32) if need[0] else None
+    dy = torch.empty(rows, plan.y_width, device=dev, dtype=torch.float32) if need[1] else None
+    dg = torch.empty(rows, plan.gate_width, device=dev, dtype=torch.float32) if need[2] else None
+    if any(need):
+        _lib.check(_lib.lib().ictc_hip_tp_backward(
+            ctypes.byref(plan.desc), _lib.ptr(x) if (need[1] or need[2]) else None, y.data_ptr(),
+            g.data_ptr(), go.data_ptr(), _lib.ptr(dx), _lib.ptr(dy), _lib.ptr(dg), rows,
+            _lib.stream_of(dev)), "ictc_hip_tp_backward")
+    return dx, dy, dg
+
+
+def _add(acc, value):
+    if value is None:
+        return acc
+    return value if acc is None else acc + value
+
+
+class _Forward(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, plan, x, y, g):
+        ctx.plan = plan
+        ctx.save_for_backward(x, y, g)
+        return _forward_raw(plan, x, y, g)
+
+    @staticmethod
+    def backward(ctx, go):
+        x, y, g = ctx.saved_tensors
+        need = required_gradients((x, y, g), ctx.needs_input_grad[1:])
+        if go is None or not any(need):
+            return None, None, None, None
+        dx, dy, dg = vjp(ctx.plan, need, x, y, g, go.contiguous())
+        return None, dx, dy, dg
+
+
+class _Backward(torch.autograd.Function):
+    """(dx, dY, dg) = VJP(x, Y, g; go); outputs not requested are empty placeholders."""
+
+    @staticmethod
+    def forward(ctx, plan, need, x, y, g, go):
+        ctx.plan, ctx.need = plan, need
+        ctx.set_materialize_grads(False)
+        ctx.save_for_backward(x, y, g, go)
+        dx, dy, dg = _backward_raw(plan, need, x, y, g, go)
+        empty = go.new_empty(0)
+        outs = tuple(t if t is not None else empty for t in (dx, dy, dg))
+        for t, n in zip(outs, need):
+            if not n:
+                ctx.mark_non_differentiable(t)
+        return outs
+
+    @staticmethod
+    def backward(ctx, hx, hy, hg):
+        plan, need_out = ctx.plan, ctx.need
+        x, y, g, go = ctx.saved_tensors
+        hx = hx if need_out[0] else None
+        hy = hy if need_out[1] else None
+        hg = hg if need_out[2] else None
+        nx, ny, ng, no = required_gradients((x, y, g, go), ctx.needs_input_grad[2:])
+        gx = gy = gg = ggo = None
+        if hx is not None:
+            hx = hx.contiguous()
+            if ny or ng:
+                _, a, b = vjp(plan, (False, ny, ng), hx, y, g, go)
+                gy, gg = _add(gy, a), _add(gg, b)
+            if no:
+                ggo = _add(ggo, _Forward.apply(plan, hx, y, g))
+        if hy is not None:
+            hy = hy.contiguous()
+            if nx or ng:
+                a, _, b = vjp(plan, (nx, False, ng), x, hy, g, go)
+                gx, gg = _add(gx, a), _add(gg, b)
+            if no:
+                ggo = _add(ggo, _Forward.apply(plan, x, hy, g))
+        if hg is not None:
+            hg = hg.contiguous()
+            if nx or ny:
+                a, b, _ = vjp(plan, (nx, ny, False), x, y, hg, go)
+                gx, gy = _add(gx, a), _add(gy, b)
+            if no:
+                ggo = _add(ggo, _Forward.apply(plan, x, y, hg))
+        return None, None, gx, gy, gg, ggo
+
+
+def vjp(plan, need, x, y, g, go):
+    """(dx, dY, dg) with None for entries not in ``need``; differentiable."""
+    need = tuple(bool(n) for n in need)
+    if not any(need):
+        return None, None, None
+    outs = _Backward.apply(plan, need, x, y, g, go)
+    return tuple(o if n else None for o, n in zip(outs, need))
+
+
+def tensor_product(plan: TensorProductPlan, features: torch.Tensor, harmonics: torch.Tensor,
+                   gates: torch.Tensor) -> torch.Tensor:
+    """Packed ir_mul TP: features [E, C(L_in+1)^2], harmonics [E,(L_e+1)^2],
+    gates [E, P*C] (path weights already folded in) -> [E, NOC*C]."""
+    return _Forward.apply(plan, features.contiguous(), harmonics.contiguous(), gates.contiguous())
+
+
+def blocks_to_packed(blocks: Dict[int, torch.Tensor], lmax: int) -> torch.Tensor:
+    """{l: [E,C,2l+1]} -> ir_mul packed [E, C(lmax+1)^2]."""
+    rows = next(iter(blocks.values())).shape[0]
+    return torch.cat([blocks[l].transpose(1, 2).reshape(rows, -1) for l in range(lmax + 1)], -1)
+
+
+def packed_to_blocks(plan: TensorProductPlan, out: torch.Tensor) -> Dict[int, torch.Tensor]:
+    """ir_mul packed output -> {l: [E, count_l*C, 2l+1]} (owner dict layout)."""
+    result, off, rows, c = {}, 0, out.shape[0], plan.channels
+    for l in range(plan.lmax + 1):
+        count, width = plan.plan.path_counts_by_l.get(l, 0), 2 * l + 1
+        span = count * c * width
+        result[l] = out[:, off:off + span].reshape(rows, count, width, c).transpose(2, 3).reshape(
+            rows, count * c, width)
+        off += span
+    return result

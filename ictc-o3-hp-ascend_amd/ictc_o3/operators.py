@@ -1,0 +1,181 @@
+"""Public ictc_o3 operators on MI355X (gfx950) HIP kernels.
+
+Same names, signatures, layouts and autograd semantics as the reference's
+``ictc_o3/operators.py`` (``__all__`` at ``:232-234``); the device is a ROCm GPU
+(torch device type ``"cuda"``) instead of an Ascend NPU.  Every operator runs its
+arithmetic in ``libictc_hip.so``; there is no CPU or eager fallback.
+"""
+from __future__ import annotations
+
+import torch
+
+from ictc_o3.backends.hip.runtime import require_gpu_fp32, strict_fp32
+
+
+def _degree(value, name):
+    if not isinstance(value, int) or isinstance(value, bool) or value < 0:
+        raise ValueError(f"{name} must be a nonnegative integer")
+
+
+def _positive_integer(value, name):
+    if not isinstance(value, int) or isinstance(value, bool) or value < 1:
+        raise ValueError(f"{name} must be a positive integer")
+
+
+def _require_gpu_device(device) -> torch.device:
+    device = torch.device(device)
+    if device.type != "cuda":
+        raise ValueError("This operator factory requires a ROCm GPU device")
+    return device
+
+
+class EdgeTensorProduct(torch.nn.Module):
+    """Path-preserving TP with live external gates (reference ``operators.py:19-139``).
+
+    ``layout="ir_mul"`` stores each degree as [angular, channel] (channel-contiguous,
+    the kernels' native layout); ``"mul_ir"`` stores [channel, angular] and is
+    transposed around the kernels.  Output multiplicities keep the owner's path order.
+    """
+
+    def __init__(self, tp, *, input_lmax, edge_lmax, layout="ir_mul"):
+        super().__init__()
+        from ictc_o3.basis.ictd_irreps import EdgeWeightedPathPreservingTensorProduct
+        if not isinstance(tp, EdgeWeightedPathPreservingTensorProduct):
+            raise TypeError("Expected an ICTC path-preserving tensor product")
+        _degree(input_lmax, "input_lmax")
+        _degree(edge_lmax, "edge_lmax")
+        require_gpu_fp32(tp.weight)
+        if layout not in ("ir_mul", "mul_ir"):
+            raise ValueError("layout must be ir_mul or mul_ir")
+        if tp.internal_compute_dtype != torch.float32:
+            raise ValueError("Tensor-product internal compute dtype must be FP32")
+        if not tp.paths or any(i > input_lmax or j > edge_lmax for i, j, _ in tp.paths):
+            raise ValueError("Declared input degrees must cover every tensor-product path")
+        strict_fp32()
+        self.tp, self.input_lmax, self.edge_lmax, self.layout = tp, input_lmax, edge_lmax, layout
+        self.plan = tp.hip_plan(input_lmax, edge_lmax)
+
+    @classmethod
+    def create(cls, *, channels=64, input_lmax=2, edge_lmax=2, output_lmax=None, layout="ir_mul",
+               device="cuda"):
+        _positive_integer(channels, "channels")
+        _degree(input_lmax, "input_lmax")
+        _degree(edge_lmax, "edge_lmax")
+        output_lmax = input_lmax if output_lmax is None else output_lmax
+        _degree(output_lmax, "output_lmax")
+        device = _require_gpu_device(device)
+        from ictc_o3.basis.ictd_irreps import EdgeWeightedPathPreservingTensorProduct
+        paths = [(i, j, k) for i in range(input_lmax + 1) for j in range(edge_lmax + 1)
+                 for k in range(output_lmax + 1) if abs(i - j) <= k <= i + j and (i + j + k) % 2 == 0]
+        tp = EdgeWeightedPathPreservingTensorProduct(
+            channels=channels, lmax=max(input_lmax, edge_lmax, output_lmax), allowed_paths=paths,
+            internal_compute_dtype=torch.float32).to(device=device, dtype=torch.float32)
+        with torch.no_grad():
+            tp.weight.fill_(1.)
+        tp.weight.requires_grad_(False)
+        return cls(tp, input_lmax=input_lmax, edge_lmax=edge_lmax, layout=layout)
+
+    @property
+    def paths(self):
+        return tuple(tuple(p) for p in self.tp.paths)
+
+    @property
+    def gate_width(self):
+        return self.tp.num_paths * self.tp.channels
+
+    @property
+    def output_width(self):
+        return sum(count * self.tp.channels * (2 * l + 1) for l, count in self.tp.path_counts_by_l.items())
+
+    def pack_input(self, blocks):
+        parts = []
+        for l in range(self.input_lmax + 1):
+            value = blocks[l]
+            if value.shape[1:] != (self.tp.channels, 2 * l + 1):
+                raise ValueError("Input block must have shape [E,C,2*l+1]")
+            if self.layout == "ir_mul":
+                value = value.transpose(1, 2)
+            parts.append(value.reshape(value.shape[0], self.tp.channels * (2 * l + 1)))
+        return torch.cat(parts, -1)
+
+    def unpack_output(self, output):
+        result, offset = {}, 0
+        for l in range(self.tp.lmax + 1):
+            count, width = self.tp.path_counts_by_l.get(l, 0), 2 * l + 1
+            span = count * self.tp.channels * width
+            value = output[:, offset:offset + span]
+            if self.layout == "ir_mul":
+                value = value.reshape(output.shape[0], count, width, self.tp.channels).transpose(2, 3)
+            result[l] = value.reshape(output.shape[0], count * self.tp.channels, width)
+            offset += span
+        return result
+
+    # -------------------------------------------------------------- layout helpers
+    def _to_ir_mul_features(self, features):
+        if self.layout == "ir_mul":
+            return features.contiguous()
+        rows, c, parts, off = features.shape[0], self.tp.channels, [], 0
+        for l in range(self.input_lmax + 1):
+            width = c * (2 * l + 1)
+            parts.append(features[:, off:off + width].reshape(rows, c, 2 * l + 1).transpose(1, 2)
+                         .reshape(rows, width))
+            off += width
+        return torch.cat(parts, -1)
+
+    def _from_ir_mul_output(self, out):
+        if self.layout == "ir_mul":
+            return out
+        rows, c, parts, off = out.shape[0], self.tp.channels, [], 0
+        for l in range(self.tp.lmax + 1):
+            count, width = self.tp.path_counts_by_l.get(l, 0), 2 * l + 1
+            span = count * c * width
+            parts.append(out[:, off:off + span].reshape(rows, count, width, c).transpose(2, 3)
+                         .reshape(rows, span))
+            off += span
+        return torch.cat(parts, -1)
+
+    def _check(self, features, harmonics, gates):
+        require_gpu_fp32(features, harmonics, self.tp.weight, *(() if gates is None else (gates,)))
+        if features.ndim != 2 or features.shape[1] != self.tp.channels * (self.input_lmax + 1) ** 2:
+            raise ValueError("Packed features must have shape [E,C*(L_in+1)^2]")
+        rows = features.shape[0]
+        if harmonics.shape != (rows, (self.edge_lmax + 1) ** 2):
+            raise ValueError("Harmonics must have shape [E,(L_edge+1)^2]")
+        if gates is not None and gates.shape not in ((rows, self.gate_width),
+                                                     (rows, self.tp.num_paths, self.tp.channels)):
+            raise ValueError("External gates must have shape [E,P*C] or [E,P,C]")
+        return rows
+
+    def forward(self, features, harmonics, gates):
+        from ictc_o3.backends.hip.tensor_product import tensor_product
+        rows = self._check(features, harmonics, gates)
+        if not rows:
+            zero = sum(v.sum() * 0 for v in (features, harmonics, self.tp.weight,
+                                             *(() if gates is None else (gates,))))
+            return features.new_empty(0, self.output_width) + zero
+        out = tensor_product(self.plan, self._to_ir_mul_features(features), harmonics,
+                             self.tp.effective_gates(gates, rows))
+        return self._from_ir_mul_output(out)
+
+
+def direction_harmonics(directions, lmax, *, policy="auto"):
+    """Direction harmonics Y_0..Y_lmax in the ICTC basis, returned as a list of
+    [..., 2l+1] tensors (reference ``operators.py:173-186``).  Computed by the HIP
+    harmonics kernel, with analytic first and second derivatives."""
+    _degree(lmax, "lmax")
+    if policy not in ("auto", "generated", "reference"):
+        raise ValueError("policy must be auto, generated or reference")
+    require_gpu_fp32(directions)
+    from ictc_o3.backends.hip.harmonics import direction_harmonics_packed
+    packed = direction_harmonics_packed(directions, lmax)
+    return [packed[..., l * l:(l + 1) ** 2] for l in range(lmax + 1)]
+
+
+def normalized_silu(features, scale=1.):
+    require_gpu_fp32(features)
+    if not isinstance(scale, (int, float)) or isinstance(scale, bool):
+        raise TypeError("scale must be a fixed numeric scalar")
+    return torch.nn.functional.silu(features) * float(scale)
+
+
+__all__ = ["EdgeTensorProduct", "direction_harmonics", "normalized_silu", "strict_fp32"]

@@ -1,0 +1,142 @@
+/*
+ * ictc_hip.h -- C ABI of the MI355X (gfx950) ictc_o3 equivariant operator library.
+ *
+ * libictc_hip.so exports plain extern "C" entry points taking device pointers,
+ * sizes and a hipStream_t.  Nothing here allocates device memory: the caller owns
+ * every input, output and workspace buffer.  Launches are asynchronous on the
+ * given stream; every entry point is reentrant and keeps no mutable global state.
+ *
+ * Data layout (all float32, row-major, channel-contiguous "ir_mul" packing):
+ *   features   [rows, C*(L_in+1)^2]     per degree l: (2l+1) rows of C channels
+ *   harmonics  [rows, (L_edge+1)^2]     Y_0 | Y_1 | ... (ICTC basis)
+ *   gates      [rows, P*C]              per path p (owner order): C channels
+ *   output     [rows, C*NOC]            per output degree l, per path with l3=l
+ *                                       (owner order), (2l+1) rows of C channels
+ * where P = number of paths and NOC = sum_p (2 l3_p + 1).
+ *
+ * Return value: ICTC_OK (0) or an ictc_status code; ictc_hip_status_string()
+ * names it.  Invalid arguments are rejected before any launch.
+ */
+#ifndef ICTC_HIP_H
+#define ICTC_HIP_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ICTC_MAX_PATHS 64
+
+typedef enum ictc_status {
+    ICTC_OK = 0,
+    ICTC_ERR_INVALID_ARGUMENT = 1,   /* null pointer, negative size, bad descriptor */
+    ICTC_ERR_UNSUPPORTED = 2,        /* degree combination not compiled in */
+    ICTC_ERR_LAUNCH = 3,             /* hipLaunchKernel / hipGetLastError failed */
+    ICTC_ERR_INDEX = 4               /* graph or species index out of range (checked kernels) */
+} ictc_status;
+
+/*
+ * Path-preserving channelwise tensor-product descriptor.
+ *
+ * The kernels enumerate the full triangle/parity path set of
+ * (input_lmax, edge_lmax, output_lmax) in ascending (l1,l2,l3) order -- the
+ * order of reference ictc_o3/operators.py:54-55 and ictd_irreps.py:2161-2175.
+ * slot s of that enumeration is described by:
+ *   gate_index[s]  index p of the path in the owner's path list (gates row block
+ *                  p), or -1 when the owner does not contain that path;
+ *   out_offset[s]  first output component of the path
+ *                  (o_offset[l3] + path_offset[p]*(2 l3+1), reference
+ *                  ictd_irreps.py:2514-2526 and operators.py:107-115);
+ *   scale[s]       'element' path normalisation 1/sqrt(#paths with this l3)
+ *                  (reference ictd_irreps.py:101-133).  The CG tensors compiled
+ *                  into the library carry the 'component' normalisation
+ *                  (ictd_irreps.py:136-142).
+ */
+typedef struct ictc_tp_desc {
+    int32_t channels;          /* C >= 1 */
+    int32_t input_lmax;        /* 0..3 */
+    int32_t edge_lmax;         /* 0..3 */
+    int32_t output_lmax;       /* 0..3 */
+    int32_t num_paths;         /* P: number of owner paths (gate blocks) */
+    int32_t out_components;    /* NOC */
+    int32_t gate_index[ICTC_MAX_PATHS];
+    int32_t out_offset[ICTC_MAX_PATHS];
+    float scale[ICTC_MAX_PATHS];
+} ictc_tp_desc;
+
+/* Human-readable name of a status code (static string). */
+const char* ictc_hip_status_string(int status);
+
+/* Library ABI version, bumped on any signature or layout change. */
+int ictc_hip_abi_version(void);
+
+/* Number of slots (full path-set size) the kernels enumerate for these degrees. */
+int ictc_hip_tp_slot_count(int input_lmax, int edge_lmax, int output_lmax);
+
+/*
+ * TP forward:  out[e, path p, k, c] = gates[e,p,c] * sum_i x[e,l1,i,c] * M_p[e,i,k],
+ *              M_p[e,i,k] = scale_p * sum_j Y[e,l2,j] * Chat_p[i,j,k].
+ * Replaces the packed standalone TP of reference
+ * ictc_o3/backends/ascend/packed_tensor_product.py:60-80 (_Product.forward), whose
+ * CPU definition is EdgeWeightedPathPreservingTensorProduct._forward_index_add
+ * (ictc_o3/basis/ictd_irreps.py:2669-2748).  rows may be 0 (no launch).
+ */
+int ictc_hip_tp_forward(const ictc_tp_desc* desc,
+                        const float* features, const float* harmonics, const float* gates,
+                        float* out, int64_t rows, hipStream_t stream);
+
+/*
+ * TP vector-Jacobian product.  Given grad_out (same layout as out) writes
+ *   grad_features  [rows, C*(L_in+1)^2]   (if non-null)
+ *   grad_harmonics [rows, (L_edge+1)^2]   (if non-null)
+ *   grad_gates     [rows, P*C]            (if non-null)
+ * each fully overwritten (not accumulated).  Replaces
+ * packed_tensor_product.py:82-110 (_Product.backward) and the structured adjoints
+ * _left_grad/_right_grad/_weight_grad (structured_product.py:49-87), with the
+ * bond projection Y -> M folded in (structured_product.py:7-22).  Because the map
+ * is trilinear in (features, harmonics, gates), every mixed second derivative is
+ * this entry point or ictc_hip_tp_forward with one operand substituted
+ * (structured_product.py:146-158).
+ */
+int ictc_hip_tp_backward(const ictc_tp_desc* desc,
+                         const float* features, const float* harmonics, const float* gates,
+                         const float* grad_out,
+                         float* grad_features, float* grad_harmonics, float* grad_gates,
+                         int64_t rows, hipStream_t stream);
+
+/*
+ * Direction harmonics (ICTC basis, component-normalised) and their analytic
+ * derivative contractions, one thread per direction.
+ *   directions [rows, 3]; Y has (lmax+1)^2 components Y_0 | Y_1 | ...
+ *   ICTC_HARM_VALUE : out[rows,(lmax+1)^2] = Y(n)
+ *   ICTC_HARM_VJP   : out[rows,3] = d/dn <u, Y(n)>                   (u: [rows,(lmax+1)^2])
+ *   ICTC_HARM_JVP   : out[rows,(lmax+1)^2] = dY(n)[t]                (t: [rows,3])
+ *   ICTC_HARM_HVP   : out[rows,3] = d2/dn2 <u, Y(n)> [t]
+ *   ICTC_HARM_JVP2  : out[rows,(lmax+1)^2] = d2Y(n)[t, s]            (s: [rows,3])
+ *   ICTC_HARM_T3    : out[rows,3] = d3/dn3 <u, Y(n)> [t, s]
+ * Replaces direction_harmonics_all (reference ictc_o3/basis/ictd_irreps.py:1113-1168)
+ * and the generated kernel with analytic first/second adjoints
+ * (ictc_o3/ops/generated_direction_harmonics.py:43-194; ascendc/direction.py:11-62).
+ * Unused operand pointers may be null.  lmax <= ICTC_HARM_MAX_LMAX.
+ */
+#define ICTC_HARM_MAX_LMAX 6
+typedef enum ictc_harm_mode {
+    ICTC_HARM_VALUE = 0,
+    ICTC_HARM_VJP = 1,
+    ICTC_HARM_JVP = 2,
+    ICTC_HARM_HVP = 3,
+    ICTC_HARM_JVP2 = 4,
+    ICTC_HARM_T3 = 5
+} ictc_harm_mode;
+
+int ictc_hip_direction_harmonics(int lmax, int mode, const float* directions, const float* u,
+                                 const float* t, const float* s, float* out, int64_t rows,
+                                 hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ICTC_HIP_H */

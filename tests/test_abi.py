@@ -1,0 +1,85 @@
+"""C-ABI checks that need no GPU: the library loads, exports every entry point the
+public headers declare, and rejects invalid descriptors before any launch."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from conftest import ROOT
+
+
+def _declared_symbols():
+    names = set()
+    inc = os.path.join(ROOT, "include")
+    for fn in os.listdir(inc):
+        if fn.endswith(".h"):
+            text = open(os.path.join(inc, fn)).read()
+            names.update(re.findall(r"^\s*(?:const\s+)?[A-Za-z_][A-Za-z0-9_]*\s*\**\s*(ictc_hip_[A-Za-z0-9_]+)\s*\(",
+                                    text, flags=re.M))
+    return names
+
+
+def test_library_exports_every_declared_symbol():
+    from ictc_o3 import _lib
+    lib = _lib.lib()
+    declared = _declared_symbols()
+    assert declared, "no declarations parsed"
+    for name in declared:
+        assert hasattr(lib, name), f"{name} declared in include/ but not exported"
+    assert set(_lib.exported_symbols()) == declared
+
+
+def test_status_strings_and_slot_counts():
+    from ictc_o3 import _lib
+    lib = _lib.lib()
+    assert lib.ictc_hip_status_string(0) == b"ok"
+    assert lib.ictc_hip_status_string(2) == b"unsupported degree combination"
+    assert lib.ictc_hip_tp_slot_count(2, 2, 2) == 11
+    assert lib.ictc_hip_tp_slot_count(3, 3, 3) == 23
+    assert lib.ictc_hip_tp_slot_count(0, 3, 3) == 4
+    assert lib.ictc_hip_tp_slot_count(4, 3, 3) == -1
+
+
+def _desc(c=64, lmax=2):
+    from ictc_o3.backends.hip.tensor_product import TensorProductPlan
+    from ictc_o3.basis.ictd_irreps import triangle_paths
+    return TensorProductPlan(triangle_paths(lmax, lmax, lmax), c, lmax, lmax).desc
+
+
+def test_descriptor_validation_rejects_before_launch():
+    from ictc_o3 import _lib
+    lib = _lib.lib()
+    fwd = lib.ictc_hip_tp_forward
+    fake = ctypes.c_void_p(16)  # never dereferenced: every call below fails validation
+    d = _desc()
+    assert fwd(None, fake, fake, fake, fake, 4, None) == 1
+    bad = _desc()
+    bad.channels = 0
+    assert fwd(ctypes.byref(bad), fake, fake, fake, fake, 4, None) == 1
+    bad = _desc()
+    bad.gate_index[3] = bad.gate_index[4]          # duplicate gate block
+    assert fwd(ctypes.byref(bad), fake, fake, fake, fake, 4, None) == 1
+    bad = _desc()
+    bad.out_offset[0] = bad.out_components          # output block past the end
+    assert fwd(ctypes.byref(bad), fake, fake, fake, fake, 4, None) == 1
+    bad = _desc()
+    bad.input_lmax = 4
+    assert fwd(ctypes.byref(bad), fake, fake, fake, fake, 4, None) == 2
+    assert fwd(ctypes.byref(d), fake, fake, fake, fake, -1, None) == 1
+    assert fwd(ctypes.byref(d), None, fake, fake, fake, 4, None) == 1
+    # zero rows: valid, nothing launched
+    assert fwd(ctypes.byref(d), None, None, None, None, 0, None) == 0
+    bwd = lib.ictc_hip_tp_backward
+    # gradients to harmonics need the features operand
+    assert bwd(ctypes.byref(d), None, fake, fake, fake, None, fake, None, 4, None) == 1
+
+
+def test_python_guards_reject_cpu_tensors():
+    import torch
+    from ictc_o3.backends.hip.runtime import require_gpu_fp32
+    with pytest.raises(ValueError):
+        require_gpu_fp32(torch.zeros(3))
+    from ictc_o3 import EdgeTensorProduct
+    with pytest.raises(ValueError):
+        EdgeTensorProduct.create(channels=8, device="cpu")
