@@ -33,9 +33,13 @@ struct PathTable {
   int l2[ICTC_MAX_PATHS] = {};
   int l3[ICTC_MAX_PATHS] = {};
   int bond[ICTC_MAX_PATHS] = {};  // first bond entry of the path, M_p stored [k][i]
+  int out[ICTC_MAX_PATHS] = {};   // first output component of the path
   int nbond = 0;
+  int noc = 0;                    // output components
 };
 
+// Output layout: ascending l3, and within one l3 the paths in enumeration order
+// (the owner's path_offset: groups sorted by (l1,l2), reference ictd_irreps.py:2514-2526).
 constexpr PathTable make_paths(int lin, int le, int lout) {
   PathTable t{};
   for (int a = 0; a <= lin; ++a)
@@ -50,6 +54,12 @@ constexpr PathTable make_paths(int lin, int le, int lout) {
         t.nbond += (2 * a + 1) * (2 * c + 1);
         ++t.n;
       }
+  for (int l = 0; l <= lout; ++l)
+    for (int p = 0; p < t.n; ++p)
+      if (t.l3[p] == l) {
+        t.out[p] = t.noc;
+        t.noc += 2 * l + 1;
+      }
   return t;
 }
 
@@ -58,6 +68,7 @@ struct Paths {
   static constexpr PathTable tab = make_paths(LIN, LE, LOUT);
   static constexpr int N = tab.n;
   static constexpr int NB = tab.nbond;
+  static constexpr int NOC = tab.noc;
   static constexpr int NX = (LIN + 1) * (LIN + 1);
   static constexpr int NY = (LE + 1) * (LE + 1);
 };
@@ -113,6 +124,67 @@ __device__ __forceinline__ void store_vec(float* __restrict__ p, const Vec<NV>& 
     *reinterpret_cast<f32x2*>(p) = f32x2{r.v[0], r.v[1]};
   } else {
     *reinterpret_cast<f32x4*>(p) = f32x4{r.v[0], r.v[1], r.v[2], r.v[3]};
+  }
+}
+
+// Returns p unchanged, but opaque to the optimiser: reads through the result cannot
+// be hoisted out of the enclosing loop iteration (keeps per-instance LDS tables from
+// being promoted wholesale into registers).
+__device__ __forceinline__ const float* opaque_lds_row(const float* p) {
+  uint32_t off = 0;
+  asm volatile("" : "+s"(off));
+  return p + off;
+}
+
+// ---------------------------------------------------------------- buffer resources
+// Raw buffer descriptors (base in SGPRs, 32-bit offsets, hardware range check on
+// num_records).  A descriptor over a null pointer gets num_records = 0: its loads
+// return 0 and its stores are discarded, which is how optional outputs are skipped
+// without branches.
+using rsrc_t = __amdgpu_buffer_rsrc_t;
+constexpr int kRsrcWord3 = 0x00020000;  // gfx9-family raw buffer, 32-bit dwords
+constexpr int kNonTemporal = 2;         // nt cache-policy bit
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, base ? bytes : 0u, kRsrcWord3);
+}
+
+// The whole byte offset goes into the per-lane voffset (soffset = 0): the range check
+// then compares exactly that offset with num_records.
+template <int NV>
+__device__ __forceinline__ Vec<NV> buf_load(rsrc_t r, uint32_t off) {
+  const uint32_t voff = off, soff = 0;
+  Vec<NV> out;
+  if constexpr (NV == 1) {
+    out.v[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+  } else if constexpr (NV == 2) {
+    const f32x2 t = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
+    out.v[0] = t.x;
+    out.v[1] = t.y;
+  } else {
+    const f32x4 t = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+    out.v[0] = t.x;
+    out.v[1] = t.y;
+    out.v[2] = t.z;
+    out.v[3] = t.w;
+  }
+  return out;
+}
+
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+template <int NV, int policy = kNonTemporal>
+__device__ __forceinline__ void buf_store(rsrc_t r, uint32_t off, const Vec<NV>& v) {
+  const uint32_t voff = off, soff = 0;
+  if constexpr (NV == 1) {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned int, v.v[0]), r, voff, soff, policy);
+  } else if constexpr (NV == 2) {
+    const f32x2 t = {v.v[0], v.v[1]};
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, t), r, voff, soff, policy);
+  } else {
+    const f32x4 t = {v.v[0], v.v[1], v.v[2], v.v[3]};
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, t), r, voff, soff, policy);
   }
 }
 

@@ -34,19 +34,12 @@ int check_desc(const ictc_tp_desc* d) {
     return ICTC_ERR_INVALID_ARGUMENT;
   if (d->input_lmax < 0 || d->edge_lmax < 0 || d->output_lmax < 0) return ICTC_ERR_INVALID_ARGUMENT;
   if (d->input_lmax > 3 || d->edge_lmax > 3 || d->output_lmax > 3) return ICTC_ERR_UNSUPPORTED;
+  // The kernels compile the full path set of the degrees with its canonical layout;
+  // the descriptor must state exactly that (path subsets are mapped by the caller).
   const PathTable t = make_paths(d->input_lmax, d->edge_lmax, d->output_lmax);
-  bool seen[ICTC_MAX_PATHS] = {};
-  int present = 0;
-  for (int s = 0; s < t.n; ++s) {
-    const int gi = d->gate_index[s];
-    if (gi < 0) continue;
-    if (gi >= d->num_paths || seen[gi]) return ICTC_ERR_INVALID_ARGUMENT;
-    seen[gi] = true;
-    ++present;
-    if (d->out_offset[s] < 0 || d->out_offset[s] + 2 * t.l3[s] + 1 > d->out_components)
-      return ICTC_ERR_INVALID_ARGUMENT;
-  }
-  if (present != d->num_paths) return ICTC_ERR_INVALID_ARGUMENT;
+  if (d->num_paths != t.n || d->out_components != t.noc) return ICTC_ERR_INVALID_ARGUMENT;
+  for (int s = 0; s < t.n; ++s)
+    if (d->gate_index[s] != s || d->out_offset[s] != t.out[s]) return ICTC_ERR_INVALID_ARGUMENT;
   return ICTC_OK;
 }
 

@@ -54,20 +54,13 @@ __device__ __forceinline__ void build_bond(const float (*sY)[Paths<LIN, LE, LOUT
   });
 }
 
-template <int LIN, int LE, int LOUT, int NV>
-__global__ void __launch_bounds__(kBlock)
-tp_forward_kernel(const float* __restrict__ x, const float* __restrict__ y,
-                  const float* __restrict__ g, float* __restrict__ out,
-                  const ictc_tp_desc d, int64_t rows) {
-  using PS = Paths<LIN, LE, LOUT>;
-  constexpr int NX = PS::NX, NY = PS::NY;
-  constexpr int NBS = PS::NB > 0 ? PS::NB : 1;
-  __shared__ float sY[kTileEdges][NY];
-  __shared__ float sM[kTileEdges][NBS];
-  const int tid = threadIdx.x;
-  const int lane = tid & (kWave - 1);
-  const int wave = tid / kWave;
-  const int64_t e0 = static_cast<int64_t>(blockIdx.x) * kTileEdges;
+// Stage the tile's harmonics in LDS and build the bond matrices of all tile instances.
+template <int LIN, int LE, int LOUT>
+__device__ __forceinline__ void stage_tile(const float* __restrict__ y, int64_t e0, int64_t rows,
+                                           float (*sY)[Paths<LIN, LE, LOUT>::NY],
+                                           float (*sM)[Paths<LIN, LE, LOUT>::NB > 0 ? Paths<LIN, LE, LOUT>::NB : 1],
+                                           const ictc_tp_desc& d, int tid) {
+  constexpr int NY = Paths<LIN, LE, LOUT>::NY;
   for (int t = tid; t < kTileEdges * NY; t += kBlock) {
     const int e = t / NY;
     sY[e][t - e * NY] = (e0 + e < rows) ? y[(e0 + e) * NY + (t - e * NY)] : 0.f;
@@ -75,42 +68,61 @@ tp_forward_kernel(const float* __restrict__ x, const float* __restrict__ y,
   __syncthreads();
   build_bond<LIN, LE, LOUT>(sY, sM, d, tid);
   __syncthreads();
+}
+
+// Forward.  Per instance the wave issues every feature and gate load up front
+// (NX + P row loads), then streams the NOC output rows; the path loop is fully
+// unrolled with compile-time output offsets, so the instance body is branch-free.
+template <int LIN, int LE, int LOUT, int NV>
+__global__ void __launch_bounds__(kBlock)
+tp_forward_kernel(const float* __restrict__ x, const float* __restrict__ y,
+                  const float* __restrict__ g, float* __restrict__ out,
+                  const ictc_tp_desc d, int64_t rows) {
+  using PS = Paths<LIN, LE, LOUT>;
+  constexpr int NX = PS::NX, NY = PS::NY, NP = PS::N, NOC = PS::NOC;
+  constexpr int NBS = PS::NB > 0 ? PS::NB : 1;
+  __shared__ float sY[kTileEdges][NY];
+  __shared__ float sM[kTileEdges][NBS];
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // wave-uniform (SGPR)
+  const int64_t e0 = static_cast<int64_t>(blockIdx.x) * kTileEdges;
+  stage_tile<LIN, LE, LOUT>(y, e0, rows, sY, sM, d, tid);
 
   const int C = d.channels;
-  const int64_t xw = static_cast<int64_t>(NX) * C;
-  const int64_t gw = static_cast<int64_t>(d.num_paths) * C;
-  const int64_t ow = static_cast<int64_t>(d.out_components) * C;
+  const uint32_t row = static_cast<uint32_t>(C) * 4u;  // bytes of one component row
   for (int le = wave; le < kTileEdges; le += kWavesPerBlock) {
     const int64_t e = e0 + le;
     if (e >= rows) break;
-    const float* __restrict__ xe = x + e * xw;
-    const float* __restrict__ ge = g + e * gw;
-    float* __restrict__ oe = out + e * ow;
+    const rsrc_t rx = make_rsrc(x + e * NX * C, NX * row);
+    const rsrc_t rg = make_rsrc(g + e * NP * C, NP * row);
+    const rsrc_t ro = make_rsrc(out + e * NOC * C, NOC * row);
     for (int c = lane * NV; c < C; c += kWave * NV) {
+      const uint32_t vo = static_cast<uint32_t>(c) * 4u;
+      const float* __restrict__ bond = opaque_lds_row(&sM[le][0]);
       Vec<NV> xr[NX];
+      Vec<NV> gv[NP];
 #pragma unroll
-      for (int m = 0; m < NX; ++m) xr[m] = load_vec<NV>(xe + static_cast<int64_t>(m) * C + c);
-      static_for<0, PS::N>([&](auto P) {
+      for (int m = 0; m < NX; ++m) xr[m] = buf_load<NV>(rx, vo + m * row);
+#pragma unroll
+      for (int p = 0; p < NP; ++p) gv[p] = buf_load<NV>(rg, vo + p * row);
+      static_for<0, NP>([&](auto P) {
         constexpr int p = P;
         constexpr int l1 = PS::tab.l1[p], l3 = PS::tab.l3[p];
         constexpr int ni = 2 * l1 + 1, no = 2 * l3 + 1;
-        constexpr int boff = PS::tab.bond[p];
-        const int gi = d.gate_index[p];
-        if (gi < 0) return;
-        const Vec<NV> gv = load_vec<NV>(ge + static_cast<int64_t>(gi) * C + c);
-        const int oo = d.out_offset[p];
+        constexpr int boff = PS::tab.bond[p], oo = PS::tab.out[p];
         static_for<0, no>([&](auto K) {
           Vec<NV> acc;
 #pragma unroll
           for (int v = 0; v < NV; ++v) acc.v[v] = 0.f;
           static_for<0, ni>([&](auto I) {
-            const float m = sM[le][boff + K * ni + I];
+            const float m = bond[boff + K * ni + I];
 #pragma unroll
             for (int v = 0; v < NV; ++v) acc.v[v] = fmaf(xr[l1 * l1 + I].v[v], m, acc.v[v]);
           });
 #pragma unroll
-          for (int v = 0; v < NV; ++v) acc.v[v] *= gv.v[v];
-          store_vec_nt<NV>(oe + static_cast<int64_t>(oo + K) * C + c, acc);
+          for (int v = 0; v < NV; ++v) acc.v[v] *= gv[p].v[v];
+          buf_store<NV>(ro, vo + (oo + K) * row, acc);
         });
       });
     }
@@ -123,6 +135,8 @@ tp_forward_kernel(const float* __restrict__ x, const float* __restrict__ y,
 //   dY[l2,j]  += s_p * sum_{i,k} Chat_p[i,j,k] * sum_c x_i go_k  (structured_product.py:61-72
 //                                                              composed with the bond adjoint)
 // The dY channel sum is a per-lane partial followed by one wave reduction per instance.
+// Outputs whose pointer is null get an empty buffer descriptor: their stores are
+// dropped by the hardware range check, so the instance body has no branches.
 template <int LIN, int LE, int LOUT, int NV>
 __global__ void __launch_bounds__(kBlock)
 tp_backward_kernel(const float* __restrict__ x, const float* __restrict__ y,
@@ -130,138 +144,107 @@ tp_backward_kernel(const float* __restrict__ x, const float* __restrict__ y,
                    float* __restrict__ dx, float* __restrict__ dy, float* __restrict__ dg,
                    const ictc_tp_desc d, int64_t rows) {
   using PS = Paths<LIN, LE, LOUT>;
-  constexpr int NX = PS::NX, NY = PS::NY;
+  constexpr int NX = PS::NX, NY = PS::NY, NP = PS::N, NOC = PS::NOC;
   constexpr int NBS = PS::NB > 0 ? PS::NB : 1;
   __shared__ float sY[kTileEdges][NY];
   __shared__ float sM[kTileEdges][NBS];
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
-  const int wave = tid / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // wave-uniform (SGPR)
   const int64_t e0 = static_cast<int64_t>(blockIdx.x) * kTileEdges;
-  for (int t = tid; t < kTileEdges * NY; t += kBlock) {
-    const int e = t / NY;
-    sY[e][t - e * NY] = (e0 + e < rows) ? y[(e0 + e) * NY + (t - e * NY)] : 0.f;
-  }
-  __syncthreads();
-  build_bond<LIN, LE, LOUT>(sY, sM, d, tid);
-  __syncthreads();
+  stage_tile<LIN, LE, LOUT>(y, e0, rows, sY, sM, d, tid);
 
-  const bool need_dx = dx != nullptr;
-  const bool need_dy = dy != nullptr;
-  const bool need_dg = dg != nullptr;
-  const bool need_x = need_dy || need_dg;
   const int C = d.channels;
-  const int64_t xw = static_cast<int64_t>(NX) * C;
-  const int64_t gw = static_cast<int64_t>(d.num_paths) * C;
-  const int64_t ow = static_cast<int64_t>(d.out_components) * C;
+  const uint32_t row = static_cast<uint32_t>(C) * 4u;
   for (int le = wave; le < kTileEdges; le += kWavesPerBlock) {
     const int64_t e = e0 + le;
     if (e >= rows) break;
-    const float* __restrict__ xe = x + e * xw;
-    const float* __restrict__ ge = g + e * gw;
-    const float* __restrict__ oe = go + e * ow;
+    const rsrc_t rx = make_rsrc(x ? x + e * NX * C : nullptr, NX * row);
+    const rsrc_t rg = make_rsrc(g + e * NP * C, NP * row);
+    const rsrc_t rgo = make_rsrc(go + e * NOC * C, NOC * row);
+    const rsrc_t rdx = make_rsrc(dx ? dx + e * NX * C : nullptr, NX * row);
+    const rsrc_t rdg = make_rsrc(dg ? dg + e * NP * C : nullptr, NP * row);
     float dyl[NY];
 #pragma unroll
     for (int j = 0; j < NY; ++j) dyl[j] = 0.f;
     for (int c = lane * NV; c < C; c += kWave * NV) {
+      const uint32_t vo = static_cast<uint32_t>(c) * 4u;
+      const float* __restrict__ bond = opaque_lds_row(&sM[le][0]);
       Vec<NV> xr[NX];
       Vec<NV> dxr[NX];
 #pragma unroll
       for (int m = 0; m < NX; ++m) {
-        if (need_x) {
-          xr[m] = load_vec<NV>(xe + static_cast<int64_t>(m) * C + c);
-        } else {
-#pragma unroll
-          for (int v = 0; v < NV; ++v) xr[m].v[v] = 0.f;
-        }
+        xr[m] = buf_load<NV>(rx, vo + m * row);
 #pragma unroll
         for (int v = 0; v < NV; ++v) dxr[m].v[v] = 0.f;
       }
-      static_for<0, PS::N>([&](auto P) {
+      static_for<0, NP>([&](auto P) {
         constexpr int p = P;
         constexpr int l1 = PS::tab.l1[p], l2 = PS::tab.l2[p], l3 = PS::tab.l3[p];
         constexpr int ni = 2 * l1 + 1, nj = 2 * l2 + 1, no = 2 * l3 + 1;
-        constexpr int boff = PS::tab.bond[p];
+        constexpr int boff = PS::tab.bond[p], oo = PS::tab.out[p];
         using CG = CGTab<l1, l2, l3>;
-        const int gi = d.gate_index[p];
-        if (gi < 0) {
-          if (need_dg) return;  // absent path: no gate block to write
-          return;
-        }
-        const Vec<NV> gv = load_vec<NV>(ge + static_cast<int64_t>(gi) * C + c);
-        const int oo = d.out_offset[p];
+        const Vec<NV> gv = buf_load<NV>(rg, vo + p * row);
         Vec<NV> o[no];
+        static_for<0, no>([&](auto K) { o[K] = buf_load<NV>(rgo, vo + (oo + K) * row); });
+        Vec<NV> dgv;
+#pragma unroll
+        for (int v = 0; v < NV; ++v) dgv.v[v] = 0.f;
         static_for<0, no>([&](auto K) {
-          o[K] = load_vec<NV>(oe + static_cast<int64_t>(oo + K) * C + c);
-        });
-        if (need_dg) {
-          Vec<NV> dgv;
+          Vec<NV> base;
 #pragma unroll
-          for (int v = 0; v < NV; ++v) dgv.v[v] = 0.f;
-          static_for<0, no>([&](auto K) {
-            Vec<NV> base;
+          for (int v = 0; v < NV; ++v) base.v[v] = 0.f;
+          static_for<0, ni>([&](auto I) {
+            const float m = bond[boff + K * ni + I];
 #pragma unroll
-            for (int v = 0; v < NV; ++v) base.v[v] = 0.f;
-            static_for<0, ni>([&](auto I) {
-              const float m = sM[le][boff + K * ni + I];
-#pragma unroll
-              for (int v = 0; v < NV; ++v) base.v[v] = fmaf(xr[l1 * l1 + I].v[v], m, base.v[v]);
-            });
-#pragma unroll
-            for (int v = 0; v < NV; ++v) dgv.v[v] = fmaf(base.v[v], o[K].v[v], dgv.v[v]);
+            for (int v = 0; v < NV; ++v) base.v[v] = fmaf(xr[l1 * l1 + I].v[v], m, base.v[v]);
           });
-          store_vec_nt<NV>(dg + e * gw + static_cast<int64_t>(gi) * C + c, dgv);
-        }
+#pragma unroll
+          for (int v = 0; v < NV; ++v) dgv.v[v] = fmaf(base.v[v], o[K].v[v], dgv.v[v]);
+        });
+        buf_store<NV>(rdg, vo + p * row, dgv);
         Vec<NV> gov[no];
         static_for<0, no>([&](auto K) {
 #pragma unroll
           for (int v = 0; v < NV; ++v) gov[K].v[v] = gv.v[v] * o[K].v[v];
         });
-        if (need_dx) {
-          static_for<0, ni>([&](auto I) {
-            static_for<0, no>([&](auto K) {
-              const float m = sM[le][boff + K * ni + I];
+        static_for<0, ni>([&](auto I) {
+          static_for<0, no>([&](auto K) {
+            const float m = bond[boff + K * ni + I];
 #pragma unroll
-              for (int v = 0; v < NV; ++v)
-                dxr[l1 * l1 + I].v[v] = fmaf(m, gov[K].v[v], dxr[l1 * l1 + I].v[v]);
+            for (int v = 0; v < NV; ++v)
+              dxr[l1 * l1 + I].v[v] = fmaf(m, gov[K].v[v], dxr[l1 * l1 + I].v[v]);
+          });
+        });
+        float part[nj];
+#pragma unroll
+        for (int j = 0; j < nj; ++j) part[j] = 0.f;
+        static_for<0, ni>([&](auto I) {
+          static_for<0, no>([&](auto K) {
+            float t = 0.f;
+#pragma unroll
+            for (int v = 0; v < NV; ++v) t = fmaf(xr[l1 * l1 + I].v[v], gov[K].v[v], t);
+            static_for<0, nj>([&](auto J) {
+              constexpr float cg = CG::v[(I * nj + J) * no + K];
+              if constexpr (cg != 0.0f) part[J] = fmaf(cg, t, part[J]);
             });
           });
-        }
-        if (need_dy) {
-          float part[nj];
+        });
+        const float s = d.scale[p];
 #pragma unroll
-          for (int j = 0; j < nj; ++j) part[j] = 0.f;
-          static_for<0, ni>([&](auto I) {
-            static_for<0, no>([&](auto K) {
-              float t = 0.f;
-#pragma unroll
-              for (int v = 0; v < NV; ++v) t = fmaf(xr[l1 * l1 + I].v[v], gov[K].v[v], t);
-              static_for<0, nj>([&](auto J) {
-                constexpr float cg = CG::v[(I * nj + J) * no + K];
-                if constexpr (cg != 0.0f) part[J] = fmaf(cg, t, part[J]);
-              });
-            });
-          });
-          const float s = d.scale[p];
-#pragma unroll
-          for (int j = 0; j < nj; ++j) dyl[l2 * l2 + j] = fmaf(s, part[j], dyl[l2 * l2 + j]);
-        }
+        for (int j = 0; j < nj; ++j) dyl[l2 * l2 + j] = fmaf(s, part[j], dyl[l2 * l2 + j]);
       });
-      if (need_dx) {
-        float* __restrict__ dxe = dx + e * xw;
 #pragma unroll
-        for (int m = 0; m < NX; ++m) store_vec_nt<NV>(dxe + static_cast<int64_t>(m) * C + c, dxr[m]);
-      }
+      for (int m = 0; m < NX; ++m) buf_store<NV>(rdx, vo + m * row, dxr[m]);
     }
-    if (need_dy) {
-      float mine = 0.f;
+    float mine = 0.f;
 #pragma unroll
-      for (int j = 0; j < NY; ++j) {
-        const float tot = wave_sum(dyl[j]);
-        if (lane == j) mine = tot;
-      }
-      if (lane < NY) dy[e * NY + lane] = mine;
+    for (int j = 0; j < NY; ++j) {
+      const float tot = wave_sum(dyl[j]);
+      if (lane == j) mine = tot;
     }
+    const rsrc_t rdy = make_rsrc(dy ? dy + e * NY : nullptr, NY * 4u);
+    if (lane < NY) buf_store<1, 0>(rdy, static_cast<uint32_t>(lane) * 4u, Vec<1>{{mine}});
   }
 }
 

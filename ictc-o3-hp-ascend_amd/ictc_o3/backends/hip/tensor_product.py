@@ -25,8 +25,24 @@ from ...autograd.adjoint_requirements import required_gradients
 from ...basis.ictd_irreps import PathPlan, triangle_paths
 
 
+def _canonical_layout(full):
+    """First output component of each full-set path: ascending l3, enumeration order
+    within one l3 (the owner's path_offset order)."""
+    offsets, acc = [0] * len(full), 0
+    for l in range(max(p[2] for p in full) + 1):
+        for i, p in enumerate(full):
+            if p[2] == l:
+                offsets[i] = acc
+                acc += 2 * l + 1
+    return offsets, acc
+
+
 class TensorProductPlan:
-    """Immutable launch description of one owner (paths, channels, degrees)."""
+    """Immutable launch description of one owner (paths, channels, degrees).
+
+    The kernels are compiled for the full triangle/parity path set of
+    (input_lmax, edge_lmax, output_lmax).  An owner with a path subset runs the full
+    set with zero gates on the absent paths and keeps only its own output rows."""
 
     def __init__(self, paths: Sequence[Tuple[int, int, int]], channels: int, input_lmax: int,
                  edge_lmax: int, lmax: Optional[int] = None):
@@ -44,31 +60,47 @@ class TensorProductPlan:
         self.plan.path_counts_by_l = {l: self.plan.path_counts_by_l.get(l, 0) for l in range(self.lmax + 1)}
         self.paths = self.plan.paths
         full = triangle_paths(self.input_lmax, self.edge_lmax, self.output_lmax)
-        index = {p: i for i, p in enumerate(paths)}
         missing = set(paths) - set(full)
         if missing:
             raise ValueError(f"paths {sorted(missing)} violate the triangle/parity rule")
+        index = {p: i for i, p in enumerate(paths)}
+        offsets, noc = _canonical_layout(full)
         desc = _lib.TpDesc()
         desc.channels = self.channels
         desc.input_lmax, desc.edge_lmax, desc.output_lmax = self.input_lmax, self.edge_lmax, self.output_lmax
-        desc.num_paths = len(paths)
-        desc.out_components = self.plan.output_components
+        desc.num_paths = len(full)
+        desc.out_components = noc
         for s, p in enumerate(full):
-            gi = index.get(p, -1)
-            desc.gate_index[s] = gi
-            desc.out_offset[s] = self.plan.output_component_offset[gi] if gi >= 0 else 0
-            desc.scale[s] = self.plan.scales[gi] if gi >= 0 else 0.0
+            desc.gate_index[s] = s
+            desc.out_offset[s] = offsets[s]
+            desc.scale[s] = self.plan.scales[index[p]] if p in index else 0.0
         self.desc = desc
         self.num_paths = len(paths)
+        self.full_paths = full
+        self.is_full = paths == full
         self.x_width = self.channels * (self.input_lmax + 1) ** 2
         self.y_width = (self.edge_lmax + 1) ** 2
         self.gate_width = self.num_paths * self.channels
         self.out_width = self.plan.output_components * self.channels
+        self.full_gate_width = len(full) * self.channels
+        self.full_out_width = noc * self.channels
+        if not self.is_full:
+            # owner path i -> full slot; owner output rows -> full output rows
+            self.slot_of_path = [full.index(p) for p in paths]
+            rows = []
+            for l in range(self.output_lmax + 1):
+                for s, p in enumerate(full):
+                    if p[2] == l and p in index:
+                        rows.extend(range(offsets[s], offsets[s] + 2 * l + 1))
+            self.output_rows = rows
+
+    def set_scale(self, path_index: int, value: float) -> None:
+        self.desc.scale[self.full_paths.index(self.paths[path_index])] = float(value)
 
 
 def _forward_raw(plan: TensorProductPlan, x, y, g) -> torch.Tensor:
     rows = x.shape[0]
-    out = torch.empty(rows, plan.out_width, device=x.device, dtype=torch.float32)
+    out = torch.empty(rows, plan.full_out_width, device=x.device, dtype=torch.float32)
     _lib.check(_lib.lib().ictc_hip_tp_forward(ctypes.byref(plan.desc), x.data_ptr(), y.data_ptr(),
                                                g.data_ptr(), out.data_ptr(), rows,
                                                _lib.stream_of(x.device)), "ictc_hip_tp_forward")
@@ -80,10 +112,10 @@ def _backward_raw(plan: TensorProductPlan, need, x, y, g, go):
     dev = go.device
     dx = torch.empty(rows, plan.x_width, device=dev, dtype=torch.float32) if need[0] else None
     dy = torch.empty(rows, plan.y_width, device=dev, dtype=torch.float32) if need[1] else None
-    dg = torch.empty(rows, plan.gate_width, device=dev, dtype=torch.float32) if need[2] else None
+    dg = torch.empty(rows, plan.full_gate_width, device=dev, dtype=torch.float32) if need[2] else None
     if any(need):
         _lib.check(_lib.lib().ictc_hip_tp_backward(
-            ctypes.byref(plan.desc), _lib.ptr(x) if (need[1] or need[2]) else None, y.data_ptr(),
+            ctypes.byref(plan.desc), x.data_ptr(), y.data_ptr(),
             g.data_ptr(), go.data_ptr(), _lib.ptr(dx), _lib.ptr(dy), _lib.ptr(dg), rows,
             _lib.stream_of(dev)), "ictc_hip_tp_backward")
     return dx, dy, dg
@@ -174,7 +206,16 @@ def tensor_product(plan: TensorProductPlan, features: torch.Tensor, harmonics: t
                    gates: torch.Tensor) -> torch.Tensor:
     """Packed ir_mul TP: features [E, C(L_in+1)^2], harmonics [E,(L_e+1)^2],
     gates [E, P*C] (path weights already folded in) -> [E, NOC*C]."""
-    return _Forward.apply(plan, features.contiguous(), harmonics.contiguous(), gates.contiguous())
+    if plan.is_full:
+        return _Forward.apply(plan, features.contiguous(), harmonics.contiguous(), gates.contiguous())
+    rows, c = gates.shape[0], plan.channels
+    slots = torch.tensor(plan.slot_of_path, device=gates.device)
+    full_gates = gates.new_zeros(rows, len(plan.full_paths), c).index_copy(
+        1, slots, gates.reshape(rows, plan.num_paths, c))
+    out = _Forward.apply(plan, features.contiguous(), harmonics.contiguous(),
+                         full_gates.reshape(rows, -1))
+    keep = torch.tensor(plan.output_rows, device=gates.device)
+    return out.reshape(rows, -1, c).index_select(1, keep).reshape(rows, -1)
 
 
 def blocks_to_packed(blocks: Dict[int, torch.Tensor], lmax: int) -> torch.Tensor:

@@ -279,10 +279,8 @@ class EdgeWeightedPathPreservingTensorProduct(nn.Module):
         if plan is None:
             from ictc_o3.backends.hip.tensor_product import TensorProductPlan
             plan = TensorProductPlan(self.paths, self.channels, input_lmax, edge_lmax, self.lmax)
-            for s in range(len(plan.desc.scale)):
-                gi = plan.desc.gate_index[s]
-                if gi >= 0:
-                    plan.desc.scale[s] = self.path_scales[gi]
+            for i, scale in enumerate(self.path_scales):
+                plan.set_scale(i, scale)
             self._plans[key] = plan
         return plan
 
