@@ -14,7 +14,11 @@ Also reported on the same JSON line:
   path, ``_forward_index_add`` + autograd) on a bounded sample on the host cores;
 * ``extra``: forward-only throughput at 262,144 instances and its roofline.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+``--kernels-only`` runs a 1 GiB device-to-device copy (the counter calibration
+reference) and three launches of each TP kernel at the benchmark sizes, for
+rocprofv3 --pmc passes.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--kernels-only]
 """
 from __future__ import annotations
 
@@ -102,6 +106,49 @@ def _time_gpu(args, plan, device):
     return elapsed, vjp_ms, fwd_ms
 
 
+def _copy_gbs(device, nbytes: int = 1 << 30, reps: int = 5) -> float:
+    """Device-to-device copy bandwidth (read + write bytes / time)."""
+    src = torch.empty(nbytes // 4, device=device)
+    dst = torch.empty_like(src)
+    src.fill_(1.0)
+    dst.copy_(src)
+    torch.cuda.synchronize(device)
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    e.record()
+    torch.cuda.synchronize(device)
+    return 2 * nbytes * reps / (s.elapsed_time(e) * 1e-3) / 1e9
+
+
+def _kernels_only(plan, device) -> None:
+    from ictc_o3.backends.hip.tensor_product import _backward_raw, _forward_raw
+    src = torch.ones((1 << 30) // 4, device=device)
+    torch.empty_like(src).copy_(src)          # calibration copy: 1 GiB read + 1 GiB written
+    torch.cuda.synchronize(device)
+    del src
+    x, y, g, o = _inputs(ROWS_VJP, device)
+    for _ in range(3):
+        _forward_raw(plan, x, y, g)
+        _backward_raw(plan, (True, True, True), x, y, g, o)
+    torch.cuda.synchronize(device)
+    print("kernels-only pass done", flush=True)
+
+
+def _measured_traffic():
+    """HBM bytes per VJP launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary
+    (calibrated against a 1 GiB copy); None if the summary is absent."""
+    path = os.path.join(ROOT, "profiles", "tp_c128_l3_hbm_traffic.md")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_vjp_launch:"):
+                return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def _cpu_baseline(budget_s: float = 12.0):
     """Oracle fwd+VJP (reference CPU path restated) on a bounded C128/L3 sample."""
     sys.path.insert(0, ROOT)
@@ -139,6 +186,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--kernels-only", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); the hot "
@@ -148,7 +196,11 @@ def main() -> int:
     device = torch.device("cuda", 0)
     from ictc_o3 import EdgeTensorProduct
     op = EdgeTensorProduct.create(channels=C, input_lmax=L, edge_lmax=L, device=device)
+    if args.kernels_only:
+        _kernels_only(op.plan, device)
+        return 0
     elapsed, vjp_ms, fwd_ms = _time_gpu(args, op.plan, device)
+    copy_gbs = _copy_gbs(device)
     value = ROWS_VJP * args.steps / elapsed
     achieved = BYTES_VJP * ROWS_VJP / (vjp_ms * 1e-3) / 1e9
     fwd_achieved = BYTES_FWD * ROWS_FWD / (fwd_ms * 1e-3) / 1e9
@@ -163,10 +215,13 @@ def main() -> int:
                    "lmax": L, "paths": P, "instances": ROWS_VJP, "layout": "ir_mul"},
         "roofline": {"bound": "hbm", "kernel": "tp_backward_kernel<3,3,3,2>", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": None, "algorithmic_bytes_per_launch": BYTES_VJP * ROWS_VJP,
+                     "traffic": _measured_traffic(), "traffic_unit": "bytes/launch",
+                     "algorithmic_bytes_per_launch": BYTES_VJP * ROWS_VJP,
                      "mean_launch_ms": vjp_ms},
         "cpu_baseline": cpu,
-        "extra": {"step_hbm_gbs": (BYTES_FWD + BYTES_VJP) * value / 1e9,
+        "extra": {"copy_gbs_measured": copy_gbs,
+                  "vjp_frac_of_copy": achieved / copy_gbs,
+                  "step_hbm_gbs": (BYTES_FWD + BYTES_VJP) * value / 1e9,
                   "step_hbm_frac": (BYTES_FWD + BYTES_VJP) * value / 1e9 / HBM_PEAK_GBS,
                   "forward_only": {"instances": ROWS_FWD, "instances_per_s": ROWS_FWD / (fwd_ms * 1e-3),
                                    "mean_launch_ms": fwd_ms, "achieved_gbs": fwd_achieved,
