@@ -41,7 +41,7 @@ FLAGS = ["--offload-arch=" + ARCH, "-O3", "-std=c++20", "-fPIC", "-Wno-c99-desig
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
          "-I", INCLUDE, "-I", HERE]
 
-API_SOURCES = ["tp_api.hip", "harmonics_api.hip"]
+API_SOURCES = ["tp_api.hip", "harmonics_api.hip", "message_api.hip"]
 HARM_LMAX = 6
 INSTANCE_KINDS = {
     "fwd": ("tp_kernels.hpp", "template int launch_forward<{a}, {b}, {c}>(const ictc_tp_desc&, "
@@ -49,6 +49,16 @@ INSTANCE_KINDS = {
     "bwd": ("tp_kernels.hpp", "template int launch_backward<{a}, {b}, {c}>(const ictc_tp_desc&, "
             "const float*, const float*, const float*, const float*, float*, float*, float*, "
             "int64_t, hipStream_t);"),
+    "msg": ("message_kernels.hpp",
+            "template int launch_msg_forward<{a}, {b}, {c}>(const ictc_tp_desc&, const float*, "
+            "const float*, const float*, const int64_t*, const int64_t*, const int64_t*, float*, "
+            "int64_t, int64_t, hipStream_t);\n"
+            "template int launch_msg_edge_grad<{a}, {b}, {c}>(const ictc_tp_desc&, const float*, "
+            "const float*, const float*, const float*, const int64_t*, const int64_t*, const int64_t*, "
+            "float*, float*, int64_t, int64_t, hipStream_t);\n"
+            "template int launch_msg_node_grad<{a}, {b}, {c}>(const ictc_tp_desc&, const float*, "
+            "const float*, const float*, const int64_t*, const int64_t*, const int64_t*, float*, "
+            "int64_t, int64_t, hipStream_t);"),
 }
 
 
@@ -69,7 +79,7 @@ def _cost(a: int, b: int, c: int, kind: str) -> int:
     """Rough compile cost (path-set size) to start the biggest TUs first."""
     n = sum((2 * i + 1) * (2 * j + 1) * (2 * k + 1) for i in range(a + 1) for j in range(b + 1)
             for k in range(c + 1) if abs(i - j) <= k <= i + j and (i + j + k) % 2 == 0)
-    return n * (4 if kind == "bwd" else 1)
+    return n * {"fwd": 1, "bwd": 4, "msg": 3}[kind]
 
 
 def _write_if_changed(path: str, text: str) -> None:
@@ -87,7 +97,7 @@ def _generate(combos) -> list:
     units = []
     for a, b, c in combos:
         for kind, (header, line) in INSTANCE_KINDS.items():
-            path = os.path.join(GEN, f"tp_inst_{a}{b}{c}_{kind}.hip")
+            path = os.path.join(GEN, f"{'msg' if kind == 'msg' else 'tp'}_inst_{a}{b}{c}_{kind}.hip")
             _write_if_changed(path, f'#include "{header}"\nnamespace ictc {{\n'
                                     f'{line.format(a=a, b=b, c=c)}\n}}  // namespace ictc\n')
             units.append((_cost(a, b, c, kind), path))

@@ -1,0 +1,119 @@
+// extern "C" entry points of the graph-message family; per-degree instantiations are
+// compiled in generated/msg_inst_*.hip.
+#include "message_kernels.hpp"
+
+namespace ictc {
+
+#define ICTC_DECLARE(A, B, C)                                                                     \
+  extern template int launch_msg_forward<A, B, C>(const ictc_tp_desc&, const float*, const float*, \
+                                                  const float*, const int64_t*, const int64_t*,    \
+                                                  const int64_t*, float*, int64_t, int64_t,        \
+                                                  hipStream_t);                                    \
+  extern template int launch_msg_edge_grad<A, B, C>(const ictc_tp_desc&, const float*, const float*, \
+                                                    const float*, const float*, const int64_t*,    \
+                                                    const int64_t*, const int64_t*, float*, float*, \
+                                                    int64_t, int64_t, hipStream_t);                \
+  extern template int launch_msg_node_grad<A, B, C>(const ictc_tp_desc&, const float*, const float*, \
+                                                    const float*, const int64_t*, const int64_t*,  \
+                                                    const int64_t*, float*, int64_t, int64_t,       \
+                                                    hipStream_t);
+#include "generated/tp_instances.def"
+#undef ICTC_DECLARE
+
+using MsgFwd = int (*)(const ictc_tp_desc&, const float*, const float*, const float*, const int64_t*,
+                       const int64_t*, const int64_t*, float*, int64_t, int64_t, hipStream_t);
+using MsgEdge = int (*)(const ictc_tp_desc&, const float*, const float*, const float*, const float*,
+                        const int64_t*, const int64_t*, const int64_t*, float*, float*, int64_t, int64_t,
+                        hipStream_t);
+using MsgNode = int (*)(const ictc_tp_desc&, const float*, const float*, const float*, const int64_t*,
+                        const int64_t*, const int64_t*, float*, int64_t, int64_t, hipStream_t);
+
+#define ICTC_DECLARE(A, B, C) [A * 16 + B * 4 + C] = &launch_msg_forward<A, B, C>,
+const MsgFwd kMsgFwd[64] = {
+#include "generated/tp_instances.def"
+};
+#undef ICTC_DECLARE
+#define ICTC_DECLARE(A, B, C) [A * 16 + B * 4 + C] = &launch_msg_edge_grad<A, B, C>,
+const MsgEdge kMsgEdge[64] = {
+#include "generated/tp_instances.def"
+};
+#undef ICTC_DECLARE
+#define ICTC_DECLARE(A, B, C) [A * 16 + B * 4 + C] = &launch_msg_node_grad<A, B, C>,
+const MsgNode kMsgNode[64] = {
+#include "generated/tp_instances.def"
+};
+#undef ICTC_DECLARE
+
+int tp_check_desc(const ictc_tp_desc* d);  // tp_api.hip
+
+// Node tensors are gathered through 32-bit buffer offsets.
+inline bool fits_u32(int64_t rows, int64_t width_floats) {
+  return rows >= 0 && rows * width_floats * 4 < (int64_t(1) << 32);
+}
+
+inline int msg_index(const ictc_tp_desc* d) { return d->input_lmax * 16 + d->edge_lmax * 4 + d->output_lmax; }
+
+inline int msg_common(const ictc_tp_desc* d, int64_t nodes_src, int64_t nodes_dst, int64_t edges) {
+  const int st = tp_check_desc(d);
+  if (st != ICTC_OK) return st;
+  if (nodes_src < 0 || nodes_dst < 0 || edges < 0) return ICTC_ERR_INVALID_ARGUMENT;
+  const int nx = (d->input_lmax + 1) * (d->input_lmax + 1);
+  if (!fits_u32(nodes_src, static_cast<int64_t>(nx) * d->channels) ||
+      !fits_u32(nodes_dst, static_cast<int64_t>(d->out_components) * d->channels))
+    return ICTC_ERR_UNSUPPORTED;
+  return ICTC_OK;
+}
+
+}  // namespace ictc
+
+extern "C" {
+
+int ictc_hip_message_chunks(int channels) { return channels < 1 ? -1 : (channels + 63) / 64; }
+
+int ictc_hip_message_forward(const ictc_tp_desc* desc, const float* node_features, const float* harmonics,
+                             const float* gates, const int64_t* src, const int64_t* dst_rowptr,
+                             const int64_t* dst_perm, float* node_out, int64_t nodes_src, int64_t nodes_dst,
+                             int64_t edges, hipStream_t stream) {
+  const int st = ictc::msg_common(desc, nodes_src, nodes_dst, edges);
+  if (st != ICTC_OK) return st;
+  if (nodes_dst == 0) return ICTC_OK;
+  if (!node_out || !dst_rowptr || (edges > 0 && (!node_features || !harmonics || !gates || !src)))
+    return ICTC_ERR_INVALID_ARGUMENT;
+  const ictc::MsgFwd fn = ictc::kMsgFwd[ictc::msg_index(desc)];
+  if (fn == nullptr) return ICTC_ERR_UNSUPPORTED;
+  return fn(*desc, node_features, harmonics, gates, src, dst_rowptr, dst_perm, node_out, nodes_src, nodes_dst,
+            stream);
+}
+
+int ictc_hip_message_edge_grad(const ictc_tp_desc* desc, const float* node_features, const float* harmonics,
+                               const float* gates, const float* grad_out, const int64_t* src,
+                               const int64_t* dst_rowptr, const int64_t* dst_perm,
+                               float* grad_harmonics_partial, float* grad_gates, int64_t nodes_src,
+                               int64_t nodes_dst, int64_t edges, hipStream_t stream) {
+  const int st = ictc::msg_common(desc, nodes_src, nodes_dst, edges);
+  if (st != ICTC_OK) return st;
+  if (edges == 0 || nodes_dst == 0 || (!grad_harmonics_partial && !grad_gates)) return ICTC_OK;
+  if (!node_features || !harmonics || !gates || !grad_out || !src || !dst_rowptr)
+    return ICTC_ERR_INVALID_ARGUMENT;
+  const ictc::MsgEdge fn = ictc::kMsgEdge[ictc::msg_index(desc)];
+  if (fn == nullptr) return ICTC_ERR_UNSUPPORTED;
+  return fn(*desc, node_features, harmonics, gates, grad_out, src, dst_rowptr, dst_perm,
+            grad_harmonics_partial, grad_gates, nodes_src, nodes_dst, stream);
+}
+
+int ictc_hip_message_node_grad(const ictc_tp_desc* desc, const float* harmonics, const float* gates,
+                               const float* grad_out, const int64_t* dst, const int64_t* src_rowptr,
+                               const int64_t* src_perm, float* grad_features, int64_t nodes_src,
+                               int64_t nodes_dst, int64_t edges, hipStream_t stream) {
+  const int st = ictc::msg_common(desc, nodes_src, nodes_dst, edges);
+  if (st != ICTC_OK) return st;
+  if (nodes_src == 0) return ICTC_OK;
+  if (!grad_features || !src_rowptr || (edges > 0 && (!harmonics || !gates || !grad_out || !dst)))
+    return ICTC_ERR_INVALID_ARGUMENT;
+  const ictc::MsgNode fn = ictc::kMsgNode[ictc::msg_index(desc)];
+  if (fn == nullptr) return ICTC_ERR_UNSUPPORTED;
+  return fn(*desc, harmonics, gates, grad_out, dst, src_rowptr, src_perm, grad_features, nodes_src, nodes_dst,
+            stream);
+}
+
+}  // extern "C"

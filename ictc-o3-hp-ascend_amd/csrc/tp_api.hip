@@ -28,7 +28,7 @@ const BwdLaunch kBwdTable[64] = {
 #undef ICTC_DECLARE
 
 // Host-side validation of a descriptor against the compiled path enumeration.
-int check_desc(const ictc_tp_desc* d) {
+int tp_check_desc(const ictc_tp_desc* d) {
   if (d == nullptr) return ICTC_ERR_INVALID_ARGUMENT;
   if (d->channels < 1 || d->num_paths < 0 || d->num_paths > ICTC_MAX_PATHS || d->out_components < 0)
     return ICTC_ERR_INVALID_ARGUMENT;
@@ -73,7 +73,7 @@ int ictc_hip_tp_slot_count(int input_lmax, int edge_lmax, int output_lmax) {
 
 int ictc_hip_tp_forward(const ictc_tp_desc* desc, const float* features, const float* harmonics,
                         const float* gates, float* out, int64_t rows, hipStream_t stream) {
-  const int st = ictc::check_desc(desc);
+  const int st = ictc::tp_check_desc(desc);
   if (st != ICTC_OK) return st;
   if (rows < 0) return ICTC_ERR_INVALID_ARGUMENT;
   if (rows == 0) return ICTC_OK;
@@ -86,7 +86,7 @@ int ictc_hip_tp_forward(const ictc_tp_desc* desc, const float* features, const f
 int ictc_hip_tp_backward(const ictc_tp_desc* desc, const float* features, const float* harmonics,
                          const float* gates, const float* grad_out, float* grad_features,
                          float* grad_harmonics, float* grad_gates, int64_t rows, hipStream_t stream) {
-  const int st = ictc::check_desc(desc);
+  const int st = ictc::tp_check_desc(desc);
   if (st != ICTC_OK) return st;
   if (rows < 0) return ICTC_ERR_INVALID_ARGUMENT;
   if (rows == 0) return ICTC_OK;

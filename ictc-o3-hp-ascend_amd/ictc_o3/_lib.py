@@ -44,6 +44,13 @@ _SIGNATURES = {
                                             _I64, _P]),
     "ictc_hip_direction_harmonics": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, _P, _P, _P, _P, _P,
                                                     _I64, _P]),
+    "ictc_hip_message_chunks": (ctypes.c_int, [ctypes.c_int]),
+    "ictc_hip_message_forward": (ctypes.c_int, [ctypes.POINTER(TpDesc), _P, _P, _P, _P, _P, _P, _P,
+                                                _I64, _I64, _I64, _P]),
+    "ictc_hip_message_edge_grad": (ctypes.c_int, [ctypes.POINTER(TpDesc), _P, _P, _P, _P, _P, _P, _P,
+                                                  _P, _P, _I64, _I64, _I64, _P]),
+    "ictc_hip_message_node_grad": (ctypes.c_int, [ctypes.POINTER(TpDesc), _P, _P, _P, _P, _P, _P, _P,
+                                                  _I64, _I64, _I64, _P]),
 }
 
 _lock = threading.Lock()

@@ -1,0 +1,212 @@
+"""Graph message on the HIP kernels: out[n] = sum_{dst(e)=n} TP(x[src(e)], Y[e], g[e]).
+
+Reference semantics: ``backends/ascend/tensor_product.py:189-218`` (gather -> TP ->
+index_add) and ``channel_message.py:35-216`` (the published performance path).
+
+The map is trilinear in (node features x, edge harmonics Y, edge gates g) for a
+fixed graph, so its VJP and every mixed derivative reuse the same three kernels
+with substituted operands (as for the plain TP):
+
+    forward   : msg_forward  (receiver CSR, per-node register accumulation)
+    dY, dg    : msg_edge_grad (receiver CSR, dout[n] in registers, x[src] gathered)
+    dx        : msg_node_grad (source CSR, dout[dst] gathered)
+
+Graph preprocessing (CSR over receivers and over sources, stable order, index range
+validation) runs once per (src, dst) pair and is cached.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional
+
+import torch
+
+from ... import _lib
+from ...autograd.adjoint_requirements import required_gradients
+from .tensor_product import TensorProductPlan
+
+
+class MessageGraph:
+    """Receiver and source CSR of an edge list (stable order: ties keep edge order)."""
+
+    def __init__(self, src: torch.Tensor, dst: torch.Tensor, nodes_src: int, nodes_dst: int):
+        if src.ndim != 1 or dst.ndim != 1 or src.dtype != torch.int64 or dst.dtype != torch.int64:
+            raise ValueError("Graph indices must be int64 vectors")
+        if src.shape != dst.shape:
+            raise ValueError("Source and destination index shapes must match")
+        self.src, self.dst = src.contiguous(), dst.contiguous()
+        self.edges = int(src.numel())
+        self.nodes_src, self.nodes_dst = int(nodes_src), int(nodes_dst)
+        if self.edges:
+            lo = torch.stack([self.src.min(), self.dst.min()]).cpu()
+            hi = torch.stack([self.src.max(), self.dst.max()]).cpu()
+            if int(lo.min()) < 0 or int(hi[0]) >= self.nodes_src or int(hi[1]) >= self.nodes_dst:
+                raise ValueError("Graph indices are out of range")
+        self.rowptr_dst, self.perm_dst = self._csr(self.dst, self.nodes_dst)
+        self.rowptr_src, self.perm_src = self._csr(self.src, self.nodes_src)
+
+    def _csr(self, index: torch.Tensor, nodes: int):
+        dev = index.device
+        counts = torch.bincount(index, minlength=nodes) if self.edges else torch.zeros(
+            nodes, dtype=torch.int64, device=dev)
+        rowptr = torch.zeros(nodes + 1, dtype=torch.int64, device=dev)
+        torch.cumsum(counts, 0, out=rowptr[1:])
+        if self.edges and bool((index[1:] >= index[:-1]).all()):
+            return rowptr, None                      # already sorted: identity permutation
+        perm = torch.sort(index, stable=True).indices if self.edges else None
+        return rowptr, perm
+
+
+_GRAPH_CACHE: dict = {}
+
+
+def message_graph(src: torch.Tensor, dst: torch.Tensor, nodes_src: int, nodes_dst: int) -> MessageGraph:
+    """Cached CSR build; the key includes tensor identity and version counters."""
+    key = (src.data_ptr(), dst.data_ptr(), src._version, dst._version, src.numel(), str(src.device),
+           int(nodes_src), int(nodes_dst))
+    graph = _GRAPH_CACHE.get(key)
+    if graph is None or graph.src.data_ptr() != src.data_ptr():
+        if len(_GRAPH_CACHE) > 8:
+            _GRAPH_CACHE.clear()
+        graph = MessageGraph(src, dst, nodes_src, nodes_dst)
+        _GRAPH_CACHE[key] = graph
+    return graph
+
+
+def _p(t: Optional[torch.Tensor]):
+    return None if t is None else t.data_ptr()
+
+
+def _forward_raw(plan: TensorProductPlan, graph: MessageGraph, x, y, g) -> torch.Tensor:
+    out = torch.empty(graph.nodes_dst, plan.full_out_width, device=x.device, dtype=torch.float32)
+    _lib.check(_lib.lib().ictc_hip_message_forward(
+        ctypes.byref(plan.desc), x.data_ptr(), _p(y), _p(g), graph.src.data_ptr(),
+        graph.rowptr_dst.data_ptr(), _p(graph.perm_dst), out.data_ptr(), graph.nodes_src,
+        graph.nodes_dst, graph.edges, _lib.stream_of(x.device)), "ictc_hip_message_forward")
+    return out
+
+
+def _backward_raw(plan: TensorProductPlan, graph: MessageGraph, need, x, y, g, go):
+    dev = go.device
+    lib = _lib.lib()
+    stream = _lib.stream_of(dev)
+    dx = dy = dg = None
+    if need[1] or need[2]:
+        nch = lib.ictc_hip_message_chunks(plan.channels)
+        dyp = (torch.empty(graph.edges, nch, plan.y_width, device=dev, dtype=torch.float32)
+               if need[1] else None)
+        dg = (torch.empty(graph.edges, plan.full_gate_width, device=dev, dtype=torch.float32)
+              if need[2] else None)
+        _lib.check(lib.ictc_hip_message_edge_grad(
+            ctypes.byref(plan.desc), x.data_ptr(), _p(y), _p(g), go.data_ptr(), graph.src.data_ptr(),
+            graph.rowptr_dst.data_ptr(), _p(graph.perm_dst), _p(dyp), _p(dg), graph.nodes_src,
+            graph.nodes_dst, graph.edges, stream), "ictc_hip_message_edge_grad")
+        if dyp is not None:
+            dy = dyp[:, 0] if nch == 1 else dyp.sum(1)
+    if need[0]:
+        dx = torch.empty(graph.nodes_src, plan.x_width, device=dev, dtype=torch.float32)
+        _lib.check(lib.ictc_hip_message_node_grad(
+            ctypes.byref(plan.desc), _p(y), _p(g), go.data_ptr(), graph.dst.data_ptr(),
+            graph.rowptr_src.data_ptr(), _p(graph.perm_src), dx.data_ptr(), graph.nodes_src,
+            graph.nodes_dst, graph.edges, stream), "ictc_hip_message_node_grad")
+    return dx, dy, dg
+
+
+def _add(acc, value):
+    if value is None:
+        return acc
+    return value if acc is None else acc + value
+
+
+class _Forward(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, plan, graph, x, y, g):
+        ctx.plan, ctx.graph = plan, graph
+        ctx.save_for_backward(x, y, g)
+        return _forward_raw(plan, graph, x, y, g)
+
+    @staticmethod
+    def backward(ctx, go):
+        x, y, g = ctx.saved_tensors
+        need = required_gradients((x, y, g), ctx.needs_input_grad[2:])
+        if go is None or not any(need):
+            return None, None, None, None, None
+        dx, dy, dg = vjp(ctx.plan, ctx.graph, need, x, y, g, go.contiguous())
+        return None, None, dx, dy, dg
+
+
+class _Backward(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, plan, graph, need, x, y, g, go):
+        ctx.plan, ctx.graph, ctx.need = plan, graph, need
+        ctx.set_materialize_grads(False)
+        ctx.save_for_backward(x, y, g, go)
+        outs = _backward_raw(plan, graph, need, x, y, g, go)
+        empty = go.new_empty(0)
+        outs = tuple(t if t is not None else empty for t in outs)
+        for t, n in zip(outs, need):
+            if not n:
+                ctx.mark_non_differentiable(t)
+        return outs
+
+    @staticmethod
+    def backward(ctx, hx, hy, hg):
+        plan, graph, need_out = ctx.plan, ctx.graph, ctx.need
+        x, y, g, go = ctx.saved_tensors
+        hx = hx if need_out[0] else None
+        hy = hy if need_out[1] else None
+        hg = hg if need_out[2] else None
+        nx, ny, ng, no = required_gradients((x, y, g, go), ctx.needs_input_grad[3:])
+        gx = gy = gg = ggo = None
+        if hx is not None:
+            hx = hx.contiguous()
+            if ny or ng:
+                _, a, b = vjp(plan, graph, (False, ny, ng), hx, y, g, go)
+                gy, gg = _add(gy, a), _add(gg, b)
+            if no:
+                ggo = _add(ggo, _Forward.apply(plan, graph, hx, y, g))
+        if hy is not None:
+            hy = hy.contiguous()
+            if nx or ng:
+                a, _, b = vjp(plan, graph, (nx, False, ng), x, hy, g, go)
+                gx, gg = _add(gx, a), _add(gg, b)
+            if no:
+                ggo = _add(ggo, _Forward.apply(plan, graph, x, hy, g))
+        if hg is not None:
+            hg = hg.contiguous()
+            if nx or ny:
+                a, b, _ = vjp(plan, graph, (nx, ny, False), x, y, hg, go)
+                gx, gy = _add(gx, a), _add(gy, b)
+            if no:
+                ggo = _add(ggo, _Forward.apply(plan, graph, x, y, hg))
+        return None, None, None, gx, gy, gg, ggo
+
+
+def vjp(plan, graph, need, x, y, g, go):
+    need = tuple(bool(n) for n in need)
+    if not any(need):
+        return None, None, None
+    outs = _Backward.apply(plan, graph, need, x, y, g, go)
+    return tuple(o if n else None for o, n in zip(outs, need))
+
+
+def graph_message(plan: TensorProductPlan, features: torch.Tensor, harmonics: torch.Tensor,
+                  gates: torch.Tensor, src: torch.Tensor, dst: torch.Tensor, *,
+                  nodes_dst: Optional[int] = None, mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Packed ir_mul message: features [N_src, C(L_in+1)^2], harmonics [E,(L_e+1)^2],
+    gates [E, P*C] (path weights folded in), src/dst int64 [E] -> [N_dst, NOC*C]."""
+    nodes_src = features.shape[0]
+    nodes_dst = nodes_src if nodes_dst is None else int(nodes_dst)
+    graph = message_graph(src, dst, nodes_src, nodes_dst)
+    rows, c = gates.shape[0], plan.channels
+    if mask is not None:
+        gates = gates * mask.reshape(rows, 1).to(gates.dtype)
+    if not plan.is_full:
+        slots = torch.tensor(plan.slot_of_path, device=gates.device)
+        gates = gates.new_zeros(rows, len(plan.full_paths), c).index_copy(
+            1, slots, gates.reshape(rows, plan.num_paths, c)).reshape(rows, -1)
+    out = _Forward.apply(plan, graph, features.contiguous(), harmonics.contiguous(), gates.contiguous())
+    if not plan.is_full:
+        keep = torch.tensor(plan.output_rows, device=gates.device)
+        out = out.reshape(nodes_dst, -1, c).index_select(1, keep).reshape(nodes_dst, -1)
+    return out

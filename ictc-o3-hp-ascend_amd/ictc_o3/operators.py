@@ -158,6 +158,83 @@ class EdgeTensorProduct(torch.nn.Module):
         return self._from_ir_mul_output(out)
 
 
+class PackedGraphMessage(EdgeTensorProduct):
+    """Packed node gather, per-edge TP and receiver segmented sum in one HIP kernel
+    family (reference ``operators.py:141-163``).
+
+    ``forward(features [N,C(L_in+1)^2], harmonics [E,(L_e+1)^2], gates [E,P*C] or
+    [E,P,C], src, dst int64 [E], mask [E] or [E,1] | None) -> [N_dst, output_width]``.
+    ``edge_chunk_size`` is accepted for API compatibility; the kernels never
+    materialise per-edge messages, so no chunking is needed.  ``N_dst`` defaults to
+    the node count and can be lowered through ``tp._destination_nodes`` (owned
+    destinations of a larger source halo, reference tensor_product.py:151-156)."""
+
+    def __init__(self, *args, edge_chunk_size=16384, **kwargs):
+        super().__init__(*args, **kwargs)
+        _positive_integer(edge_chunk_size, "edge_chunk_size")
+        self.edge_chunk_size = edge_chunk_size
+
+    @classmethod
+    def create(cls, *, edge_chunk_size=16384, **kwargs):
+        op = EdgeTensorProduct.create(**kwargs)
+        return cls(op.tp, input_lmax=op.input_lmax, edge_lmax=op.edge_lmax,
+                   layout=op.layout, edge_chunk_size=edge_chunk_size)
+
+    def _destination_nodes(self, source_nodes):
+        nodes = getattr(self.tp, "_destination_nodes",
+                        getattr(self.tp, "_ascend_destination_nodes", source_nodes))
+        if not isinstance(nodes, int) or isinstance(nodes, bool) or not 0 <= nodes <= source_nodes:
+            raise ValueError("Destination node count must be between zero and the source node count")
+        return nodes
+
+    def _message(self, features, harmonics, gates, src, dst, mask):
+        from ictc_o3.backends.hip.graph_message import graph_message
+        for value in (src, dst):
+            if value.ndim != 1 or value.dtype != torch.int64 or value.device != features.device:
+                raise ValueError("Graph indices must be int64 vectors on the GPU")
+        if dst.shape != src.shape:
+            raise ValueError("Source and destination index shapes must match")
+        edges = src.numel()
+        require_gpu_fp32(features, harmonics, gates, self.tp.weight)
+        if features.ndim != 2 or features.shape[1] != self.tp.channels * (self.input_lmax + 1) ** 2:
+            raise ValueError("Packed features must have shape [E,C*(L_in+1)^2]")
+        if harmonics.shape != (edges, (self.edge_lmax + 1) ** 2):
+            raise ValueError("Harmonics must have shape [E,(L_edge+1)^2]")
+        if gates.shape not in ((edges, self.gate_width), (edges, self.tp.num_paths, self.tp.channels)):
+            raise ValueError("External gates must have shape [E,P*C] or [E,P,C]")
+        if mask is not None:
+            if mask.shape not in ((edges,), (edges, 1)):
+                raise ValueError("Edge mask must have shape [E] or [E,1]")
+            require_gpu_fp32(mask)
+        nodes = self._destination_nodes(features.shape[0])
+        return graph_message(self.plan, self._to_ir_mul_features(features), harmonics,
+                             self.tp.effective_gates(gates, edges), src, dst, nodes_dst=nodes, mask=mask)
+
+    def forward(self, features, harmonics, gates, src, dst, mask=None):
+        return self._from_ir_mul_output(self._message(features, harmonics, gates, src, dst, mask))
+
+
+class GraphMessage(PackedGraphMessage):
+    """Dictionary block interface for the same message map (reference ``operators.py:166-170``):
+    features {l: [N,C,2l+1]}, harmonics {l: [E,1,2l+1]} -> {l: [N_dst, count_l*C, 2l+1]}."""
+
+    def forward(self, features, harmonics, gates, src, dst, mask=None):
+        from ictc_o3.backends.hip.tensor_product import blocks_to_packed, packed_to_blocks
+        sample = next(iter(features.values()))
+        rows = src.numel()
+        feats = {l: features[l] if l in features else sample.new_zeros(sample.shape[0], self.tp.channels, 2 * l + 1)
+                 for l in range(self.input_lmax + 1)}
+        harms = torch.cat([harmonics[l].reshape(rows, 2 * l + 1) if l in harmonics
+                           else sample.new_zeros(rows, 2 * l + 1) for l in range(self.edge_lmax + 1)], -1)
+        packed = blocks_to_packed(feats, self.input_lmax)
+        saved, self.layout = self.layout, "ir_mul"
+        try:
+            out = self._message(packed, harms, gates, src, dst, mask)
+        finally:
+            self.layout = saved
+        return packed_to_blocks(self.plan, out)
+
+
 def direction_harmonics(directions, lmax, *, policy="auto"):
     """Direction harmonics Y_0..Y_lmax in the ICTC basis, returned as a list of
     [..., 2l+1] tensors (reference ``operators.py:173-186``).  Computed by the HIP
@@ -178,4 +255,5 @@ def normalized_silu(features, scale=1.):
     return torch.nn.functional.silu(features) * float(scale)
 
 
-__all__ = ["EdgeTensorProduct", "direction_harmonics", "normalized_silu", "strict_fp32"]
+__all__ = ["EdgeTensorProduct", "PackedGraphMessage", "GraphMessage", "direction_harmonics",
+           "normalized_silu", "strict_fp32"]

@@ -107,6 +107,56 @@ int ictc_hip_tp_backward(const ictc_tp_desc* desc,
                          int64_t rows, hipStream_t stream);
 
 /*
+ * Graph message:  node_out[n] = sum_{e : dst(e) = n} TP(features[src(e)], harmonics[e], gates[e])
+ * with the TP above (same descriptor; node rows use the features / output layouts).
+ * Edges are visited through a CSR over the receivers: dst_rowptr [nodes_dst+1] and
+ * dst_perm [edges] (CSR slot -> edge id; null when edges are already sorted by dst).
+ * Each destination node is accumulated in registers by one wave per 64-channel chunk,
+ * so per-edge messages never reach HBM and the sum order is deterministic (no atomics).
+ * node_out [nodes_dst, NOC*C] is fully overwritten (zeros for nodes without edges).
+ * Indices must lie in [0, nodes_src) / [0, nodes_dst); gathers are range checked by the
+ * hardware (out-of-range reads return zeros).  Node tensors must be < 4 GiB.
+ * Replaces graph_message (reference ictc_o3/backends/ascend/tensor_product.py:159-218),
+ * channel_message.graph_message (channel_message.py:35-216) and the atomic ictc_epilogue
+ * (ascendc/op_kernel/epilogue.cpp:6-212, ascendc/epilogue.py:132-150).
+ */
+int ictc_hip_message_forward(const ictc_tp_desc* desc, const float* node_features,
+                             const float* harmonics, const float* gates, const int64_t* src,
+                             const int64_t* dst_rowptr, const int64_t* dst_perm, float* node_out,
+                             int64_t nodes_src, int64_t nodes_dst, int64_t edges,
+                             hipStream_t stream);
+
+/* Number of 64-channel chunks a message kernel splits the channels into. */
+int ictc_hip_message_chunks(int channels);
+
+/*
+ * Message VJP, per-edge part (receiver CSR): for every edge
+ *   grad_gates[e]               = d<grad_out, node_out>/d gates[e]            [edges, P*C]
+ *   grad_harmonics_partial[e,q] = the harmonics gradient of edge e summed over the
+ *                                 channels of chunk q                 [edges, chunks, NY]
+ * (the caller sums the chunk axis).  Either output may be null.  Replaces the
+ * dr/dg terms of ictc_epilogue_adjoint (ascendc/op_kernel/epilogue_adjoint.cpp:6-208).
+ */
+int ictc_hip_message_edge_grad(const ictc_tp_desc* desc, const float* node_features,
+                               const float* harmonics, const float* gates, const float* grad_out,
+                               const int64_t* src, const int64_t* dst_rowptr,
+                               const int64_t* dst_perm, float* grad_harmonics_partial,
+                               float* grad_gates, int64_t nodes_src, int64_t nodes_dst,
+                               int64_t edges, hipStream_t stream);
+
+/*
+ * Message VJP, per-source-node part (source CSR: src_rowptr [nodes_src+1], src_perm
+ * [edges] or null): grad_features[s] = sum over edges with src(e) = s of the TP feature
+ * adjoint with grad_out[dst(e)]  [nodes_src, C*(L_in+1)^2], fully overwritten.  Replaces
+ * the mode-1 scatter of ictc_weighted_map (ascendc/op_kernel/weighted_map.cpp:225-233)
+ * without atomics.
+ */
+int ictc_hip_message_node_grad(const ictc_tp_desc* desc, const float* harmonics, const float* gates,
+                               const float* grad_out, const int64_t* dst, const int64_t* src_rowptr,
+                               const int64_t* src_perm, float* grad_features, int64_t nodes_src,
+                               int64_t nodes_dst, int64_t edges, hipStream_t stream);
+
+/*
  * Direction harmonics (ICTC basis, component-normalised) and their analytic
  * derivative contractions, one thread per direction.
  *   directions [rows, 3]; Y has (lmax+1)^2 components Y_0 | Y_1 | ...
