@@ -41,7 +41,7 @@ FLAGS = ["--offload-arch=" + ARCH, "-O3", "-std=c++20", "-fPIC", "-Wno-c99-desig
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
          "-I", INCLUDE, "-I", HERE]
 
-API_SOURCES = ["tp_api.hip", "harmonics_api.hip", "message_api.hip"]
+API_SOURCES = ["tp_api.hip", "harmonics_api.hip", "message_api.hip", "sc_api.hip"]
 HARM_LMAX = 6
 INSTANCE_KINDS = {
     "fwd": ("tp_kernels.hpp", "template int launch_forward<{a}, {b}, {c}>(const ictc_tp_desc&, "
@@ -73,6 +73,14 @@ def _combos():
             out.append(tuple(int(ch) for ch in tok))
         return sorted(set(out))
     return [(a, b, c) for a in range(4) for b in range(4) for c in range(4)]
+
+
+def _sc_configs():
+    """(lmax, target_lmax, correlation) of the symmetric-contraction plans to compile."""
+    spec = os.environ.get("ICTC_HIP_SC", "").strip()
+    if spec:
+        return sorted({tuple(int(ch) for ch in tok.strip()) for tok in spec.split(",")})
+    return [(l, t, k) for l in range(4) for t in range(l + 1) for k in (1, 2, 3)]
 
 
 def _cost(a: int, b: int, c: int, kind: str) -> int:
@@ -108,6 +116,21 @@ def _generate(combos) -> list:
                                 'const float*, const float*, float*, int64_t, hipStream_t);\n'
                                 '}  // namespace ictc\n')
         units.append((60 * (l + 1) ** 3, path))
+    # symmetric contraction: generated straight-line plans, one TU per configuration
+    sys.path.insert(0, HERE)
+    import gen_sc
+    sc_cfgs = _sc_configs()
+    gen_sc.main(GEN, sc_cfgs)
+    _write_if_changed(os.path.join(GEN, "sc_instances.def"),
+                      "".join(f"ICTC_SC({l}, {t}, {k}, {gen_sc.weight_columns(l, t, k)})\n"
+                              for l, t, k in sc_cfgs))
+    for l, t, k in sc_cfgs:
+        path = os.path.join(GEN, f"sc_inst_{l}{t}{k}.hip")
+        _write_if_changed(path, f'#include "sc_kernels.hpp"\n#include "generated/sc_{l}{t}{k}.hpp"\n'
+                                f'namespace ictc {{\ntemplate int launch_sc<{l}, {t}, {k}>(int, const float*, '
+                                'const int64_t*, const float*, const float*, float*, int, int64_t, int, '
+                                'hipStream_t);\n}  // namespace ictc\n')
+        units.append((os.path.getsize(os.path.join(GEN, f"sc_{l}{t}{k}.hpp")) // 20, path))
     units.sort(reverse=True)
     return [p for _, p in units]
 

@@ -1,0 +1,107 @@
+// Correlation <= 3 symmetric contraction with species-selected weights (gfx950).
+//
+//   out[n, c, l_out, m] = sum_p W[s_n, p, c] * chain_p(x[n, c, :])_m
+// the MACE contraction recursion of reference
+// ictc_o3/ops/_mace_symmetric_contraction.py:298-346 (_forward_selected_elements),
+// evaluated through shared pair prefixes instead of dense U tensors (the factorisation
+// idea of ictc_o3/ops/factorized_contraction.py:51-149).  One lane per (node, channel):
+// the whole polynomial of a channel lives in registers, the weights of the node's
+// species are read along the channel axis (coalesced), and nodes are independent.
+//
+// Layouts (mul_ir, the module's flat layout): x [N, C*(L+1)^2] with degree blocks
+// [C, 2l+1]; out [N, C*(T+1)^2] with blocks [C, 2l+1]; W [S, KTOT, C].
+#pragma once
+#include "ictc_common.hpp"
+#include "sc_plan.hpp"
+
+namespace ictc {
+
+constexpr int kScBlock = 256;
+constexpr int kScWaves = kScBlock / kWave;
+
+// Loads always read a valid channel (cc = c, or 0 for lanes past C) and are then
+// selected, so the loads need no exec-mask branches.
+template <int L>
+__device__ __forceinline__ void sc_load_mul_ir(const float* __restrict__ row, int C, int cc, bool live,
+                                               float* v) {
+#pragma unroll
+  for (int l = 0; l <= L; ++l) {
+#pragma unroll
+    for (int m = 0; m < 2 * l + 1; ++m) {
+      const float t = row[C * l * l + cc * (2 * l + 1) + m];
+      v[l * l + m] = live ? t : 0.f;
+    }
+  }
+}
+
+template <int L>
+__device__ __forceinline__ void sc_store_mul_ir(float* __restrict__ row, int C, int c, const float* v) {
+#pragma unroll
+  for (int l = 0; l <= L; ++l) {
+#pragma unroll
+    for (int m = 0; m < 2 * l + 1; ++m) row[C * l * l + c * (2 * l + 1) + m] = v[l * l + m];
+  }
+}
+
+// mode 0: forward (u unused); mode 1: VJP to the node features;
+// mode 2: weight features phi[n, p, c] = <u[n,c], chain_p(x[n,c])>  (out: [N, KTOT, C])
+template <int L, int T, int K, int MODE>
+__global__ void __launch_bounds__(kScBlock)
+sc_kernel(const float* __restrict__ x, const int64_t* __restrict__ species, const float* __restrict__ w,
+          const float* __restrict__ u, float* __restrict__ out, int C, int64_t nodes, int num_species,
+          int nchunks) {
+  using PL = sc::Plan<L, T, K>;
+  constexpr int D = PL::D, NO = PL::NO;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * kScWaves + wave;
+  const int64_t node = item / nchunks;
+  if (node >= nodes) return;
+  const int chunk = static_cast<int>(item - node * nchunks);
+  const int c = chunk * kWave + lane;
+  const bool live = c < C;
+  const int cc = live ? c : 0;
+  int64_t s = species[node];
+  if (s < 0 || s >= num_species) s = 0;  // host validates; never read outside W
+  const float* __restrict__ wr = w + s * PL::KTOT * C + cc;
+  float xv[D];
+  sc_load_mul_ir<L>(x + node * D * C, C, cc, live, xv);
+  if constexpr (MODE == 0) {
+    float o[NO];
+#pragma unroll
+    for (int i = 0; i < NO; ++i) o[i] = 0.f;
+    PL::forward(xv, wr, C, o);
+    if (live) sc_store_mul_ir<T>(out + node * NO * C, C, c, o);
+  } else if constexpr (MODE == 1) {
+    float uv[NO];
+    sc_load_mul_ir<T>(u + node * NO * C, C, cc, live, uv);
+    float dx[D];
+    PL::vjp(xv, wr, C, uv, dx);
+    if (live) sc_store_mul_ir<L>(out + node * D * C, C, c, dx);
+  } else {
+    float uv[NO];
+    sc_load_mul_ir<T>(u + node * NO * C, C, cc, live, uv);
+    // only lanes with a real channel store (the per-node block is [KTOT, C])
+    float* __restrict__ phi = out + node * PL::KTOT * C + cc;
+    if (live) PL::weight_features(xv, C, uv, phi);
+  }
+}
+
+template <int L, int T, int K>
+int launch_sc(int mode, const float* x, const int64_t* species, const float* w, const float* u, float* out,
+              int C, int64_t nodes, int num_species, hipStream_t stream) {
+  const int nchunks = (C + kWave - 1) / kWave;
+  const dim3 grid(static_cast<unsigned>((nodes * nchunks + kScWaves - 1) / kScWaves));
+  if (mode == 0)
+    hipLaunchKernelGGL((sc_kernel<L, T, K, 0>), grid, dim3(kScBlock), 0, stream, x, species, w, u, out, C,
+                       nodes, num_species, nchunks);
+  else if (mode == 1)
+    hipLaunchKernelGGL((sc_kernel<L, T, K, 1>), grid, dim3(kScBlock), 0, stream, x, species, w, u, out, C,
+                       nodes, num_species, nchunks);
+  else
+    hipLaunchKernelGGL((sc_kernel<L, T, K, 2>), grid, dim3(kScBlock), 0, stream, x, species, w, u, out, C,
+                       nodes, num_species, nchunks);
+  return hipGetLastError() == hipSuccess ? ICTC_OK : ICTC_ERR_LAUNCH;
+}
+
+}  // namespace ictc

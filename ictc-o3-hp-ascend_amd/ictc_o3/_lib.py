@@ -45,6 +45,12 @@ _SIGNATURES = {
     "ictc_hip_direction_harmonics": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, _P, _P, _P, _P, _P,
                                                     _I64, _P]),
     "ictc_hip_message_chunks": (ctypes.c_int, [ctypes.c_int]),
+    "ictc_hip_sc_weight_columns": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+    "ictc_hip_sc_forward": (ctypes.c_int, [ctypes.c_int] * 4 + [_P, _P, _P, ctypes.c_int, _P, _I64, _P]),
+    "ictc_hip_sc_backward": (ctypes.c_int, [ctypes.c_int] * 4 + [_P, _P, _P, ctypes.c_int, _P, _P, _I64,
+                                                                   _P]),
+    "ictc_hip_sc_weight_features": (ctypes.c_int, [ctypes.c_int] * 4 + [_P, _P, ctypes.c_int, _P, _P, _I64,
+                                                                          _P]),
     "ictc_hip_message_forward": (ctypes.c_int, [ctypes.POINTER(TpDesc), _P, _P, _P, _P, _P, _P, _P,
                                                 _I64, _I64, _I64, _P]),
     "ictc_hip_message_edge_grad": (ctypes.c_int, [ctypes.POINTER(TpDesc), _P, _P, _P, _P, _P, _P, _P,

@@ -1,0 +1,90 @@
+"""Symmetric contraction on the HIP kernels (correlation <= 3, species-selected weights).
+
+    out[n, c, l, m] = sum_p W[s_n, p, c] * chain_p(x[n, c, :])_m
+
+The kernels evaluate the U-tensor columns as coupling chains with shared pair
+prefixes (see ictc_o3/basis/symmetric_u.py).  Gradients:
+
+* node features: the ``ictc_hip_sc_backward`` kernel;
+* weights: the map is linear in W, so dW[s] is the sum over the nodes of species s
+  of the per-node chain features <u, chain_p(x)> (``ictc_hip_sc_weight_features``),
+  reduced by species with a deterministic index_add.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from ... import _lib
+from ...autograd.adjoint_requirements import required_gradients
+
+
+class ContractionPlan:
+    def __init__(self, lmax: int, target_lmax: int, correlation: int, channels: int, num_elements: int):
+        self.lmax, self.target_lmax, self.correlation = int(lmax), int(target_lmax), int(correlation)
+        self.channels, self.num_elements = int(channels), int(num_elements)
+        ktot = _lib.lib().ictc_hip_sc_weight_columns(self.lmax, self.target_lmax, self.correlation)
+        if ktot < 0:
+            raise ValueError(f"symmetric contraction (lmax={lmax}, target_lmax={target_lmax}, "
+                             f"correlation={correlation}) is not compiled into libictc_hip.so")
+        self.ktot = ktot
+        self.in_width = self.channels * (self.lmax + 1) ** 2
+        self.out_width = self.channels * (self.target_lmax + 1) ** 2
+
+
+def _forward_raw(plan: ContractionPlan, x, species, w):
+    out = torch.empty(x.shape[0], plan.out_width, device=x.device, dtype=torch.float32)
+    _lib.check(_lib.lib().ictc_hip_sc_forward(
+        plan.lmax, plan.target_lmax, plan.correlation, plan.channels, x.data_ptr(), species.data_ptr(),
+        w.data_ptr(), plan.num_elements, out.data_ptr(), x.shape[0], _lib.stream_of(x.device)),
+        "ictc_hip_sc_forward")
+    return out
+
+
+def _vjp_raw(plan: ContractionPlan, x, species, w, go):
+    dx = torch.empty(x.shape[0], plan.in_width, device=x.device, dtype=torch.float32)
+    _lib.check(_lib.lib().ictc_hip_sc_backward(
+        plan.lmax, plan.target_lmax, plan.correlation, plan.channels, x.data_ptr(), species.data_ptr(),
+        w.data_ptr(), plan.num_elements, go.data_ptr(), dx.data_ptr(), x.shape[0],
+        _lib.stream_of(x.device)), "ictc_hip_sc_backward")
+    return dx
+
+
+def _weight_grad(plan: ContractionPlan, x, species, go):
+    """dW[s,p,c] = sum_{n: s_n = s} <go[n,c], chain_p(x[n,c])>."""
+    phi = torch.empty(x.shape[0], plan.ktot, plan.channels, device=x.device, dtype=torch.float32)
+    _lib.check(_lib.lib().ictc_hip_sc_weight_features(
+        plan.lmax, plan.target_lmax, plan.correlation, plan.channels, x.data_ptr(), species.data_ptr(),
+        plan.num_elements, go.data_ptr(), phi.data_ptr(), x.shape[0], _lib.stream_of(x.device)),
+        "ictc_hip_sc_weight_features")
+    return torch.zeros(plan.num_elements, plan.ktot, plan.channels, device=x.device,
+                       dtype=torch.float32).index_add(0, species, phi)
+
+
+class _Forward(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, plan, x, species, w):
+        ctx.plan = plan
+        ctx.save_for_backward(x, species, w)
+        return _forward_raw(plan, x, species, w)
+
+    @staticmethod
+    def backward(ctx, go):
+        x, species, w = ctx.saved_tensors
+        nx, nw = required_gradients((x, w), (ctx.needs_input_grad[1], ctx.needs_input_grad[3]))
+        if go is None:
+            return None, None, None, None
+        go = go.contiguous()
+        if torch.is_grad_enabled() and (nx or nw):
+            raise NotImplementedError(
+                "second derivatives through the symmetric contraction are not provided yet")
+        dx = _vjp_raw(ctx.plan, x, species, w, go) if nx else None
+        dw = _weight_grad(ctx.plan, x, species, go) if nw else None
+        return None, dx, None, dw
+
+
+def symmetric_contraction(plan: ContractionPlan, x: torch.Tensor, species: torch.Tensor,
+                          weights: torch.Tensor) -> torch.Tensor:
+    """x [N, C*(L+1)^2] (mul_ir), species int64 [N], weights [S, KTOT, C] -> [N, C*(T+1)^2]."""
+    return _Forward.apply(plan, x.contiguous(), species.contiguous(), weights.contiguous())

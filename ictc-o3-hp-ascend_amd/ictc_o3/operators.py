@@ -248,6 +248,43 @@ def direction_harmonics(directions, lmax, *, policy="auto"):
     return [packed[..., l * l:(l + 1) ** 2] for l in range(lmax + 1)]
 
 
+def configure_symmetric_contraction(module, *, policy="auto", training=False):
+    """Select the HIP contraction for a module (reference ``operators.py:189-201``)."""
+    from ictc_o3.ops.symmetric_contraction import ICTDPureUSymmetricContractionSO3
+    if not isinstance(module, ICTDPureUSymmetricContractionSO3):
+        raise TypeError("Expected an ICTC symmetric contraction")
+    if policy not in ("auto", "generated", "reference"):
+        raise ValueError("policy must be auto, generated or reference")
+    if policy == "reference":
+        raise ValueError("the reference (eager CPU) contraction is not part of this library")
+    require_gpu_fp32(*module.parameters())
+    if module.correlation not in (1, 2, 3):
+        raise ValueError("symmetric contraction supports correlation 1, 2 and 3")
+    strict_fp32()
+    module.plan  # compiled configuration check
+    return {"backend": "hip", "selected": "generated"}
+
+
+def create_symmetric_contraction(*, num_elements, lmax, target_lmax=None, channels=64, correlation=3,
+                                 device="cuda", policy="generated", training=False):
+    """Factory (reference ``operators.py:204-218``).  U tensors are the ICTC coupling
+    chains of the reference's e3nn-free generator (``ictd_irreps.py:1387-1517``)."""
+    for value, name in ((num_elements, "num_elements"), (channels, "channels"), (correlation, "correlation")):
+        _positive_integer(value, name)
+    if correlation not in (1, 2, 3):
+        raise ValueError("symmetric contraction supports correlation 1, 2 and 3")
+    _degree(lmax, "lmax")
+    target_lmax = lmax if target_lmax is None else target_lmax
+    _degree(target_lmax, "target_lmax")
+    device = _require_gpu_device(device)
+    from ictc_o3.ops.symmetric_contraction import ICTDPureUSymmetricContractionSO3
+    module = ICTDPureUSymmetricContractionSO3(num_elements=num_elements, channels=channels, lmax=lmax,
+                                              target_lmax=target_lmax, correlation=correlation
+                                              ).to(device=device, dtype=torch.float32)
+    configure_symmetric_contraction(module, policy=policy, training=training)
+    return module
+
+
 def normalized_silu(features, scale=1.):
     require_gpu_fp32(features)
     if not isinstance(scale, (int, float)) or isinstance(scale, bool):
@@ -256,4 +293,5 @@ def normalized_silu(features, scale=1.):
 
 
 __all__ = ["EdgeTensorProduct", "PackedGraphMessage", "GraphMessage", "direction_harmonics",
-           "normalized_silu", "strict_fp32"]
+           "create_symmetric_contraction", "configure_symmetric_contraction", "normalized_silu",
+           "strict_fp32"]

@@ -40,19 +40,20 @@ typedef enum ictc_status {
 /*
  * Path-preserving channelwise tensor-product descriptor.
  *
- * The kernels enumerate the full triangle/parity path set of
+ * The kernels are compiled for the full triangle/parity path set of
  * (input_lmax, edge_lmax, output_lmax) in ascending (l1,l2,l3) order -- the
- * order of reference ictc_o3/operators.py:54-55 and ictd_irreps.py:2161-2175.
- * slot s of that enumeration is described by:
- *   gate_index[s]  index p of the path in the owner's path list (gates row block
- *                  p), or -1 when the owner does not contain that path;
- *   out_offset[s]  first output component of the path
- *                  (o_offset[l3] + path_offset[p]*(2 l3+1), reference
+ * order of reference ictc_o3/operators.py:54-55 and ictd_irreps.py:2161-2175 --
+ * with its canonical layout, and the descriptor must state exactly that:
+ *   num_paths      = ictc_hip_tp_slot_count(...), out_components = sum (2 l3 + 1);
+ *   gate_index[s]  = s (gates row block of slot s);
+ *   out_offset[s]  first output component of slot s: ascending l3, enumeration order
+ *                  within one l3 (the owner's path_offset, reference
  *                  ictd_irreps.py:2514-2526 and operators.py:107-115);
- *   scale[s]       'element' path normalisation 1/sqrt(#paths with this l3)
- *                  (reference ictd_irreps.py:101-133).  The CG tensors compiled
- *                  into the library carry the 'component' normalisation
- *                  (ictd_irreps.py:136-142).
+ *   scale[s]       per-path normalisation, e.g. 'element' 1/sqrt(#paths with this l3)
+ *                  (reference ictd_irreps.py:101-133).  The CG tensors compiled into
+ *                  the library carry the 'component' normalisation (ictd_irreps.py:136-142).
+ * An owner with a path subset runs the full set with zero gates on the absent paths
+ * and keeps its own output rows.
  */
 typedef struct ictc_tp_desc {
     int32_t channels;          /* C >= 1 */
@@ -155,6 +156,46 @@ int ictc_hip_message_node_grad(const ictc_tp_desc* desc, const float* harmonics,
                                const float* grad_out, const int64_t* dst, const int64_t* src_rowptr,
                                const int64_t* src_perm, float* grad_features, int64_t nodes_src,
                                int64_t nodes_dst, int64_t edges, hipStream_t stream);
+
+/*
+ * Symmetric contraction (correlation <= 3) with species-selected weights:
+ *   out[n, c, l_out, m] = sum_p W[species[n], p, c] * chain_p(x[n, c, :])_m
+ * for every target degree l_out <= target_lmax, where the columns p are the coupling
+ * chains of the pure-ICTC U tensors (reference ictc_o3/basis/ictd_irreps.py:1387-1517,
+ * ICTDPureUSymmetricContractionSO3 at mace_ictc/models/pure_cartesian_ictd_fix.py:1310)
+ * and the polynomial is the MACE recursion of _forward_selected_elements
+ * (ictc_o3/ops/_mace_symmetric_contraction.py:298-346).  Replaces the factorised NPU
+ * schedule (backends/ascend/contraction.py:8-45, ops/factorized_contraction.py:51-149)
+ * and the banked ictc_weighted_map (ascendc/op_kernel/weighted_map.cpp:9-276).
+ * Layouts: node_features [nodes, C*(lmax+1)^2] with degree blocks [C, 2l+1] (mul_ir);
+ * out [nodes, C*(target_lmax+1)^2] likewise; weights [num_elements, KTOT, C] with KTOT =
+ * ictc_hip_sc_weight_columns(...), columns per target degree in the order
+ * [order correlation, correlation-1, ..., 1] (weights_max, weights[0], ...).
+ * species [nodes] int64 in [0, num_elements) (validated by the caller; the kernels
+ * clamp out-of-range values to 0 to stay in bounds).  lmax <= 3.
+ */
+int ictc_hip_sc_weight_columns(int lmax, int target_lmax, int correlation);
+
+int ictc_hip_sc_forward(int lmax, int target_lmax, int correlation, int channels,
+                        const float* node_features, const int64_t* species, const float* weights,
+                        int num_elements, float* out, int64_t nodes, hipStream_t stream);
+
+/* VJP to the node features: grad_features [nodes, C*(lmax+1)^2] (mul_ir, overwritten). */
+int ictc_hip_sc_backward(int lmax, int target_lmax, int correlation, int channels,
+                         const float* node_features, const int64_t* species, const float* weights,
+                         int num_elements, const float* grad_out, float* grad_features,
+                         int64_t nodes, hipStream_t stream);
+
+/*
+ * Weight adjoint per node: features_out[n, p, c] = <grad_out[n, c, :], chain_p(x[n, c, :])>
+ * [nodes, KTOT, C] (overwritten); the weight gradient is its sum over the nodes of each
+ * species (the gradient of the index_select in _forward_selected_elements,
+ * _mace_symmetric_contraction.py:316-317).
+ */
+int ictc_hip_sc_weight_features(int lmax, int target_lmax, int correlation, int channels,
+                                const float* node_features, const int64_t* species,
+                                int num_elements, const float* grad_out, float* features_out,
+                                int64_t nodes, hipStream_t stream);
 
 /*
  * Direction harmonics (ICTC basis, component-normalised) and their analytic

@@ -211,11 +211,33 @@ def full_cg_tensor(l1: int, l2: int, l3: int) -> torch.Tensor:
         rows.append(torch.kron(j3, torch.eye(d1 * d2, dtype=_F64))
                     - torch.kron(torch.eye(d3, dtype=_F64), jin.T.contiguous()))
     a = torch.cat(rows, 0)
-    _, _, vh = np.linalg.svd(a.numpy(), full_matrices=True)
-    c = torch.from_numpy(vh[-1].copy()).reshape(d3, d1 * d2).T.reshape(d1, d2, d3).contiguous()
-    if c.flatten()[int(c.abs().argmax())] < 0:
-        c = -c
-    return c
+    c = torch.from_numpy(null_vector(a.numpy())).reshape(d3, d1 * d2).T.reshape(d1, d2, d3).contiguous()
+    return fix_sign(c)
+
+
+def null_vector(a: np.ndarray) -> np.ndarray:
+    """Right singular vector of the smallest singular value; LAPACK gesdd, falling back to
+    gesvd and then to the eigenvector of A^T A (``_robust_svd_vh``, ictd_irreps.py:1322-1342)."""
+    try:
+        return np.linalg.svd(a, full_matrices=True)[2][-1].copy()
+    except np.linalg.LinAlgError:
+        pass
+    try:
+        import scipy.linalg
+        return scipy.linalg.svd(a, full_matrices=True, lapack_driver="gesvd")[2][-1].copy()
+    except (np.linalg.LinAlgError, ValueError):
+        w, v = np.linalg.eigh(a.T @ a)
+        return v[:, 0].copy()
+
+
+def fix_sign(c: torch.Tensor) -> torch.Tensor:
+    """Largest-magnitude entry positive (``ictd_irreps.py:1369-1372``); among entries within
+    1e-9 of the maximum magnitude the first in row-major order decides, so round-off
+    cannot flip the sign between machines."""
+    flat = c.flatten()
+    mag = flat.abs()
+    first = int(torch.nonzero(mag >= mag.max() * (1 - 1e-9))[0])
+    return -c if flat[first] < 0 else c
 
 
 # --------------------------------------------------------------------------- harmonics
