@@ -128,7 +128,8 @@ def _generate(combos) -> list:
         path = os.path.join(GEN, f"sc_inst_{l}{t}{k}.hip")
         _write_if_changed(path, f'#include "sc_kernels.hpp"\n#include "generated/sc_{l}{t}{k}.hpp"\n'
                                 f'namespace ictc {{\ntemplate int launch_sc<{l}, {t}, {k}>(int, const float*, '
-                                'const int64_t*, const float*, const float*, float*, int, int64_t, int, '
+                                'const float*, const int64_t*, const float*, const float*, float*, int, '
+                                'int64_t, int, '
                                 'hipStream_t);\n}  // namespace ictc\n')
         units.append((os.path.getsize(os.path.join(GEN, f"sc_{l}{t}{k}.hpp")) // 20, path))
     units.sort(reverse=True)

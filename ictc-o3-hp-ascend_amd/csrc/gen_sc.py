@@ -10,7 +10,10 @@ P_{la,lb,L1}[q] = sum_ij CG(la,lb,L1)[i,j,q] x_la,i x_lb,j, evaluated once per
 (la <= lb, L1) group; the swapped pair uses the exchange sign of the intertwiner and
 symmetric groups (la == lb) whose prefix vanishes identically are skipped.
 
-Emitted per configuration (struct ``ictc::sc::Plan<L, T, K>``):
+Emitted per configuration (struct ``ictc::sc::Plan<L, T, K>``), each a template over
+the scalar V of x (float, or the dual number ictc::sc::Dual of sc_plan.hpp, whose
+tangent part turns forward into a JVP, vjp into a Hessian-vector product and
+weight_features into its directional derivative):
   forward(x, w, C, o)     o[T-packed] += sum_p w_p chain_p(x)
   vjp(x, w, C, u, dx)     dx = d/dx <u, forward(x)>
   weight_features(x, C, u, phi)   phi[p*C] = <u, chain_p(x)> (the weight adjoint per node)
@@ -108,10 +111,10 @@ def emit(lmax: int, target: int, corr: int) -> str:
     for lo, p in order1:
         terms = []
         for m in range(2 * lo + 1):
-            fw.append(f"  o[{lo * lo + m}] = fmaf(w[{p} * C], x[{lo * lo + m}], o[{lo * lo + m}]);")
-            bw.append(f"  dx[{lo * lo + m}] = fmaf(w[{p} * C], u[{lo * lo + m}], dx[{lo * lo + m}]);")
+            fw.append(f"  o[{lo * lo + m}] = sfma(w[{p} * C], x[{lo * lo + m}], o[{lo * lo + m}]);")
+            bw.append(f"  dx[{lo * lo + m}] = sfma(w[{p} * C], u[{lo * lo + m}], dx[{lo * lo + m}]);")
             terms.append(f"u[{lo * lo + m}] * x[{lo * lo + m}]")
-        aw.append(f"  phi[{p} * C] = {' + '.join(terms)};")
+        aw.append(f"  phi[{p} * C] = part({' + '.join(terms)});")
     for p in vanishing:
         aw.append(f"  phi[{p} * C] = 0.0f;   // chain with an identically vanishing prefix")
     # ---- pair groups as a sequence of small steps (switch cases of a loop that is not
@@ -128,7 +131,7 @@ def emit(lmax: int, target: int, corr: int) -> str:
             expr = "0.0f"
             for i, j, qq, v in terms:
                 if qq == q:
-                    expr = f"fmaf({_f(v)}, {X(a, i)} * {X(b, j)}, {expr})"
+                    expr = f"sfma({_f(v)}, {X(a, i)} * {X(b, j)}, {expr})"
             pre.append(f"    P[{q}] = {expr};")
         fsteps.append(pre)
         asteps.append(pre)
@@ -139,9 +142,9 @@ def emit(lmax: int, target: int, corr: int) -> str:
             b_.append(f"    const float wv = {sign}.0f * w[{p} * Cs];")
             if order == 2:
                 for m in range(2 * lo + 1):
-                    f.append(f"    o[{lo * lo + m}] = fmaf(wv, P[{m}], o[{lo * lo + m}]);")
-                    b_.append(f"    G[{m}] = fmaf(wv, u[{lo * lo + m}], G[{m}]);")
-                ad.append(f"    phi[{p} * Cs] = {sign}.0f * (" +
+                    f.append(f"    o[{lo * lo + m}] = sfma(wv, P[{m}], o[{lo * lo + m}]);")
+                    b_.append(f"    G[{m}] = sfma(wv, u[{lo * lo + m}], G[{m}]);")
+                ad.append(f"    phi[{p} * Cs] = {sign}.0f * part(" +
                           " + ".join(f"u[{lo * lo + m}] * P[{m}]" for m in range(2 * lo + 1)) + ");")
             else:
                 lc = ch.lc
@@ -152,25 +155,25 @@ def emit(lmax: int, target: int, corr: int) -> str:
                     expr = "0.0f"
                     for aa, k, mm, v in ent:
                         if mm == m:
-                            expr = f"fmaf({_f(v)}, P[{aa}] * {X(lc, k)}, {expr})"
-                    f.append(f"    o[{lo * lo + m}] = fmaf(wv, {expr}, o[{lo * lo + m}]);")
+                            expr = f"sfma({_f(v)}, P[{aa}] * {X(lc, k)}, {expr})"
+                    f.append(f"    o[{lo * lo + m}] = sfma(wv, {expr}, o[{lo * lo + m}]);")
                     b_.append(f"    const float um{m} = wv * u[{lo * lo + m}];")
-                    ad.append(f"    const float t{m} = {expr};")
-                ad.append(f"    phi[{p} * Cs] = {sign}.0f * (" +
+                    ad.append(f"    const V t{m} = {expr};")
+                ad.append(f"    phi[{p} * Cs] = {sign}.0f * part(" +
                           " + ".join(f"u[{lo * lo + m}] * t{m}" for m in range(2 * lo + 1)) + ");")
                 for aa, k, m, v in ent:
-                    b_.append(f"    G[{aa}] = fmaf({_f(v)} * um{m}, {X(lc, k)}, G[{aa}]);")
-                    b_.append(f"    dx[{lc * lc + k}] = fmaf({_f(v)} * um{m}, P[{aa}], dx[{lc * lc + k}]);")
+                    b_.append(f"    G[{aa}] = sfma({_f(v)} * um{m}, {X(lc, k)}, G[{aa}]);")
+                    b_.append(f"    dx[{lc * lc + k}] = sfma({_f(v)} * um{m}, P[{aa}], dx[{lc * lc + k}]);")
             fsteps.append(f)
             bsteps.append(b_)
             asteps.append(ad)
         adj = []
         for i, j, q, v in terms:
             if a == b and i == j:
-                adj.append(f"    dx[{a * a + i}] = fmaf({_f(2 * v)} * G[{q}], {X(a, i)}, dx[{a * a + i}]);")
+                adj.append(f"    dx[{a * a + i}] = sfma({_f(2 * v)} * G[{q}], {X(a, i)}, dx[{a * a + i}]);")
             else:
-                adj.append(f"    dx[{a * a + i}] = fmaf({_f(v)} * G[{q}], {X(b, j)}, dx[{a * a + i}]);")
-                adj.append(f"    dx[{b * b + j}] = fmaf({_f(v)} * G[{q}], {X(a, i)}, dx[{b * b + j}]);")
+                adj.append(f"    dx[{a * a + i}] = sfma({_f(v)} * G[{q}], {X(b, j)}, dx[{a * a + i}]);")
+                adj.append(f"    dx[{b * b + j}] = sfma({_f(v)} * G[{q}], {X(a, i)}, dx[{b * b + j}]);")
         bsteps.append(adj)
 
     def loop(steps, decl):
@@ -179,7 +182,7 @@ def emit(lmax: int, target: int, corr: int) -> str:
         out = [f"  {decl}", "  #pragma clang loop unroll(disable)",
                f"  for (int step = 0; step < {len(steps)}; ++step) {{",
                '    int Cs = C;', '    asm volatile("" : "+s"(Cs));',
-               f"    #pragma unroll\n    for (int i = 0; i < {D}; ++i) asm volatile(\"\" : \"+v\"(xl[i]));",
+               f"    #pragma unroll\n    for (int i = 0; i < {D}; ++i) launder(xl[i]);",
                "    switch (step) {"]
         for k, body in enumerate(steps):
             out.append(f"    case {k}: {{")
@@ -188,10 +191,10 @@ def emit(lmax: int, target: int, corr: int) -> str:
         out += ["    default: break;", "    }", "  }"]
         return out
     if fsteps:
-        copy = f"float xl[{D}];\n  for (int i = 0; i < {D}; ++i) xl[i] = x[i];\n  "
-        fw += loop(fsteps, copy + f"float P[{maxq}];")
-        bw += loop(bsteps, copy + f"float P[{maxq}], G[{maxq}];")
-        aw += loop(asteps, copy + f"float P[{maxq}];")
+        copy = f"V xl[{D}];\n  for (int i = 0; i < {D}; ++i) xl[i] = x[i];\n  "
+        fw += loop(fsteps, copy + f"V P[{maxq}];")
+        bw += loop(bsteps, copy + f"V P[{maxq}], G[{maxq}];")
+        aw += loop(asteps, copy + f"V P[{maxq}];")
     off_lines = ", ".join(str(offsets[(lo, o)]) for lo in range(target + 1) for o in range(corr, 0, -1))
     return "\n".join([
         f"// Generated by csrc/gen_sc.py for lmax={lmax}, target_lmax={target}, correlation={corr}.",
@@ -204,18 +207,22 @@ def emit(lmax: int, target: int, corr: int) -> str:
         f"  static constexpr int KTOT = {ktot};",
         f"  // first W column of (l_out, order), l_out ascending, order descending",
         f"  static constexpr int offsets[{(target + 1) * corr}] = {{{off_lines}}};",
-        "  // x: the channel's input components; w: weight row of (species, channel).",
-        "  __device__ static __forceinline__ void forward(const float* x, const float* __restrict__ w, int C,",
-        "                                                 float* o) {",
+        "  // x: the channel's input components (float, or Dual carrying a tangent);",
+        "  // w: weight row of (species, channel).",
+        "  template <typename V>",
+        "  __device__ static __forceinline__ void forward(const V* x, const float* __restrict__ w, int C, V* o) {",
         *fw,
         "  }",
-        "  __device__ static __forceinline__ void vjp(const float* x, const float* __restrict__ w, int C,",
-        "                                             const float* u, float* dx) {",
+        "  template <typename V>",
+        "  __device__ static __forceinline__ void vjp(const V* x, const float* __restrict__ w, int C,",
+        "                                             const float* u, V* dx) {",
         f"    for (int i = 0; i < {D}; ++i) dx[i] = 0.0f;",
         *bw,
         "  }",
-        "  // phi[p*C] = sum_m u_m chain_p(x)_m for every weight column p (weight adjoint)",
-        "  __device__ static __forceinline__ void weight_features(const float* x, int C, const float* u,",
+        "  // phi[p*C] = part(sum_m u_m chain_p(x)_m) for every weight column p (weight adjoint;",
+        "  // part() is the value for float and the tangent for Dual)",
+        "  template <typename V>",
+        "  __device__ static __forceinline__ void weight_features(const V* x, int C, const float* u,",
         "                                                         float* __restrict__ phi) {",
         *aw,
         "  }",

@@ -4,13 +4,13 @@
 
 namespace ictc {
 #define ICTC_SC(L, T, K, KTOT)                                                                     \
-  extern template int launch_sc<L, T, K>(int, const float*, const int64_t*, const float*, const float*, \
-                                         float*, int, int64_t, int, hipStream_t);
+  extern template int launch_sc<L, T, K>(int, const float*, const float*, const int64_t*, const float*,   \
+                                         const float*, float*, int, int64_t, int, hipStream_t);
 #include "generated/sc_instances.def"
 #undef ICTC_SC
 
-using ScLaunch = int (*)(int, const float*, const int64_t*, const float*, const float*, float*, int, int64_t,
-                         int, hipStream_t);
+using ScLaunch = int (*)(int, const float*, const float*, const int64_t*, const float*, const float*, float*,
+                         int, int64_t, int, hipStream_t);
 struct ScEntry {
   ScLaunch fn;
   int ktot;
@@ -27,15 +27,18 @@ inline const ScEntry* sc_entry(int lmax, int target, int corr) {
   return e->fn ? e : nullptr;
 }
 
-inline int sc_call(int mode, int lmax, int target, int corr, int channels, const float* x,
+// modes: 0 forward, 1 VJP, 2 weight features, 3 JVP, 4 Hessian-vector, 5 weight-feature JVP
+inline int sc_call(int mode, int lmax, int target, int corr, int channels, const float* x, const float* t,
                    const int64_t* species, const float* w, int num_species, const float* u, float* out,
                    int64_t nodes, hipStream_t stream) {
   const ScEntry* e = sc_entry(lmax, target, corr);
   if (e == nullptr) return ICTC_ERR_UNSUPPORTED;
   if (channels < 1 || nodes < 0 || num_species < 1) return ICTC_ERR_INVALID_ARGUMENT;
   if (nodes == 0) return ICTC_OK;
-  if (!x || !species || !out || (mode != 2 && !w) || (mode != 0 && !u)) return ICTC_ERR_INVALID_ARGUMENT;
-  return e->fn(mode, x, species, w, u, out, channels, nodes, num_species, stream);
+  const bool needs_w = mode != 2 && mode != 5, needs_u = mode != 0 && mode != 3, needs_t = mode >= 3;
+  if (!x || !species || !out || (needs_w && !w) || (needs_u && !u) || (needs_t && !t))
+    return ICTC_ERR_INVALID_ARGUMENT;
+  return e->fn(mode, x, t, species, w, u, out, channels, nodes, num_species, stream);
 }
 
 }  // namespace ictc
@@ -50,14 +53,14 @@ int ictc_hip_sc_weight_columns(int lmax, int target_lmax, int correlation) {
 int ictc_hip_sc_forward(int lmax, int target_lmax, int correlation, int channels, const float* node_features,
                         const int64_t* species, const float* weights, int num_elements, float* out,
                         int64_t nodes, hipStream_t stream) {
-  return ictc::sc_call(0, lmax, target_lmax, correlation, channels, node_features, species, weights,
+  return ictc::sc_call(0, lmax, target_lmax, correlation, channels, node_features, nullptr, species, weights,
                        num_elements, nullptr, out, nodes, stream);
 }
 
 int ictc_hip_sc_backward(int lmax, int target_lmax, int correlation, int channels, const float* node_features,
                          const int64_t* species, const float* weights, int num_elements, const float* grad_out,
                          float* grad_features, int64_t nodes, hipStream_t stream) {
-  return ictc::sc_call(1, lmax, target_lmax, correlation, channels, node_features, species, weights,
+  return ictc::sc_call(1, lmax, target_lmax, correlation, channels, node_features, nullptr, species, weights,
                        num_elements, grad_out, grad_features, nodes, stream);
 }
 
@@ -65,7 +68,29 @@ int ictc_hip_sc_weight_features(int lmax, int target_lmax, int correlation, int 
                                 const float* node_features, const int64_t* species, int num_elements,
                                 const float* grad_out, float* features_out, int64_t nodes,
                                 hipStream_t stream) {
-  return ictc::sc_call(2, lmax, target_lmax, correlation, channels, node_features, species, nullptr,
+  return ictc::sc_call(2, lmax, target_lmax, correlation, channels, node_features, nullptr, species, nullptr,
+                       num_elements, grad_out, features_out, nodes, stream);
+}
+
+int ictc_hip_sc_jvp(int lmax, int target_lmax, int correlation, int channels, const float* node_features,
+                    const int64_t* species, const float* weights, int num_elements, const float* tangent,
+                    float* out, int64_t nodes, hipStream_t stream) {
+  return ictc::sc_call(3, lmax, target_lmax, correlation, channels, node_features, tangent, species, weights,
+                       num_elements, nullptr, out, nodes, stream);
+}
+
+int ictc_hip_sc_hvp(int lmax, int target_lmax, int correlation, int channels, const float* node_features,
+                    const int64_t* species, const float* weights, int num_elements, const float* grad_out,
+                    const float* tangent, float* grad_features, int64_t nodes, hipStream_t stream) {
+  return ictc::sc_call(4, lmax, target_lmax, correlation, channels, node_features, tangent, species, weights,
+                       num_elements, grad_out, grad_features, nodes, stream);
+}
+
+int ictc_hip_sc_weight_features_jvp(int lmax, int target_lmax, int correlation, int channels,
+                                    const float* node_features, const int64_t* species, int num_elements,
+                                    const float* grad_out, const float* tangent, float* features_out,
+                                    int64_t nodes, hipStream_t stream) {
+  return ictc::sc_call(5, lmax, target_lmax, correlation, channels, node_features, tangent, species, nullptr,
                        num_elements, grad_out, features_out, nodes, stream);
 }
 

@@ -43,14 +43,21 @@ __device__ __forceinline__ void sc_store_mul_ir(float* __restrict__ row, int C, 
   }
 }
 
-// mode 0: forward (u unused); mode 1: VJP to the node features;
-// mode 2: weight features phi[n, p, c] = <u[n,c], chain_p(x[n,c])>  (out: [N, KTOT, C])
+// Directional modes take a tangent t [N, C*(L+1)^2] (mul_ir, like x) and evaluate the
+// generated code on x + eps t:
+//   mode 0: forward                           out [N, C*(T+1)^2]
+//   mode 1: VJP to the node features          out [N, C*(L+1)^2]   = J(x)^T u
+//   mode 2: weight features                   out [N, KTOT, C]     phi_p = <u, chain_p(x)>
+//   mode 3: JVP                               out [N, C*(T+1)^2]   = J(x) t
+//   mode 4: Hessian-vector product            out [N, C*(L+1)^2]   = d/dx <u, J(x) t>
+//   mode 5: weight-feature JVP                out [N, KTOT, C]     <u, d chain_p(x)[t]>
 template <int L, int T, int K, int MODE>
 __global__ void __launch_bounds__(kScBlock)
-sc_kernel(const float* __restrict__ x, const int64_t* __restrict__ species, const float* __restrict__ w,
-          const float* __restrict__ u, float* __restrict__ out, int C, int64_t nodes, int num_species,
-          int nchunks) {
+sc_kernel(const float* __restrict__ x, const float* __restrict__ t, const int64_t* __restrict__ species,
+          const float* __restrict__ w, const float* __restrict__ u, float* __restrict__ out, int C,
+          int64_t nodes, int num_species, int nchunks) {
   using PL = sc::Plan<L, T, K>;
+  using sc::Dual;
   constexpr int D = PL::D, NO = PL::NO;
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -66,41 +73,74 @@ sc_kernel(const float* __restrict__ x, const int64_t* __restrict__ species, cons
   const float* __restrict__ wr = w + s * PL::KTOT * C + cc;
   float xv[D];
   sc_load_mul_ir<L>(x + node * D * C, C, cc, live, xv);
-  if constexpr (MODE == 0) {
-    float o[NO];
+  float uv[NO];
+  if constexpr (MODE != 0 && MODE != 3) sc_load_mul_ir<T>(u + node * NO * C, C, cc, live, uv);
+  if constexpr (MODE <= 2) {
+    if constexpr (MODE == 0) {
+      float o[NO];
 #pragma unroll
-    for (int i = 0; i < NO; ++i) o[i] = 0.f;
-    PL::forward(xv, wr, C, o);
-    if (live) sc_store_mul_ir<T>(out + node * NO * C, C, c, o);
-  } else if constexpr (MODE == 1) {
-    float uv[NO];
-    sc_load_mul_ir<T>(u + node * NO * C, C, cc, live, uv);
-    float dx[D];
-    PL::vjp(xv, wr, C, uv, dx);
-    if (live) sc_store_mul_ir<L>(out + node * D * C, C, c, dx);
+      for (int i = 0; i < NO; ++i) o[i] = 0.f;
+      PL::forward(xv, wr, C, o);
+      if (live) sc_store_mul_ir<T>(out + node * NO * C, C, c, o);
+    } else if constexpr (MODE == 1) {
+      float dx[D];
+      PL::vjp(xv, wr, C, uv, dx);
+      if (live) sc_store_mul_ir<L>(out + node * D * C, C, c, dx);
+    } else {
+      // only lanes with a real channel store (the per-node block is [KTOT, C])
+      float* __restrict__ phi = out + node * PL::KTOT * C + cc;
+      if (live) PL::weight_features(xv, C, uv, phi);
+    }
   } else {
-    float uv[NO];
-    sc_load_mul_ir<T>(u + node * NO * C, C, cc, live, uv);
-    // only lanes with a real channel store (the per-node block is [KTOT, C])
-    float* __restrict__ phi = out + node * PL::KTOT * C + cc;
-    if (live) PL::weight_features(xv, C, uv, phi);
+    float tv[D];
+    sc_load_mul_ir<L>(t + node * D * C, C, cc, live, tv);
+    Dual xd[D];
+#pragma unroll
+    for (int i = 0; i < D; ++i) xd[i] = Dual(xv[i], tv[i]);
+    if constexpr (MODE == 3) {
+      Dual o[NO];
+#pragma unroll
+      for (int i = 0; i < NO; ++i) o[i] = 0.f;
+      PL::forward(xd, wr, C, o);
+      float r[NO];
+#pragma unroll
+      for (int i = 0; i < NO; ++i) r[i] = o[i].d;
+      if (live) sc_store_mul_ir<T>(out + node * NO * C, C, c, r);
+    } else if constexpr (MODE == 4) {
+      Dual dx[D];
+      PL::vjp(xd, wr, C, uv, dx);
+      float r[D];
+#pragma unroll
+      for (int i = 0; i < D; ++i) r[i] = dx[i].d;
+      if (live) sc_store_mul_ir<L>(out + node * D * C, C, c, r);
+    } else {
+      float* __restrict__ phi = out + node * PL::KTOT * C + cc;
+      if (live) PL::weight_features(xd, C, uv, phi);
+    }
   }
 }
 
 template <int L, int T, int K>
-int launch_sc(int mode, const float* x, const int64_t* species, const float* w, const float* u, float* out,
-              int C, int64_t nodes, int num_species, hipStream_t stream) {
+int launch_sc(int mode, const float* x, const float* t, const int64_t* species, const float* w,
+              const float* u, float* out, int C, int64_t nodes, int num_species, hipStream_t stream) {
   const int nchunks = (C + kWave - 1) / kWave;
   const dim3 grid(static_cast<unsigned>((nodes * nchunks + kScWaves - 1) / kScWaves));
-  if (mode == 0)
-    hipLaunchKernelGGL((sc_kernel<L, T, K, 0>), grid, dim3(kScBlock), 0, stream, x, species, w, u, out, C,
-                       nodes, num_species, nchunks);
-  else if (mode == 1)
-    hipLaunchKernelGGL((sc_kernel<L, T, K, 1>), grid, dim3(kScBlock), 0, stream, x, species, w, u, out, C,
-                       nodes, num_species, nchunks);
-  else
-    hipLaunchKernelGGL((sc_kernel<L, T, K, 2>), grid, dim3(kScBlock), 0, stream, x, species, w, u, out, C,
-                       nodes, num_species, nchunks);
+  switch (mode) {
+#define ICTC_SC_MODE(M)                                                                                   \
+  case M:                                                                                                 \
+    hipLaunchKernelGGL((sc_kernel<L, T, K, M>), grid, dim3(kScBlock), 0, stream, x, t, species, w, u, out, \
+                       C, nodes, num_species, nchunks);                                                   \
+    break;
+    ICTC_SC_MODE(0)
+    ICTC_SC_MODE(1)
+    ICTC_SC_MODE(2)
+    ICTC_SC_MODE(3)
+    ICTC_SC_MODE(4)
+    ICTC_SC_MODE(5)
+#undef ICTC_SC_MODE
+    default:
+      return ICTC_ERR_INVALID_ARGUMENT;
+  }
   return hipGetLastError() == hipSuccess ? ICTC_OK : ICTC_ERR_LAUNCH;
 }
 

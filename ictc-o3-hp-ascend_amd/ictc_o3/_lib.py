@@ -51,6 +51,10 @@ _SIGNATURES = {
                                                                    _P]),
     "ictc_hip_sc_weight_features": (ctypes.c_int, [ctypes.c_int] * 4 + [_P, _P, ctypes.c_int, _P, _P, _I64,
                                                                           _P]),
+    "ictc_hip_sc_jvp": (ctypes.c_int, [ctypes.c_int] * 4 + [_P, _P, _P, ctypes.c_int, _P, _P, _I64, _P]),
+    "ictc_hip_sc_hvp": (ctypes.c_int, [ctypes.c_int] * 4 + [_P, _P, _P, ctypes.c_int, _P, _P, _P, _I64, _P]),
+    "ictc_hip_sc_weight_features_jvp": (ctypes.c_int, [ctypes.c_int] * 4 + [_P, _P, ctypes.c_int, _P, _P, _P,
+                                                                              _I64, _P]),
     "ictc_hip_message_forward": (ctypes.c_int, [ctypes.POINTER(TpDesc), _P, _P, _P, _P, _P, _P, _P,
                                                 _I64, _I64, _I64, _P]),
     "ictc_hip_message_edge_grad": (ctypes.c_int, [ctypes.POINTER(TpDesc), _P, _P, _P, _P, _P, _P, _P,

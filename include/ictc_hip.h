@@ -198,6 +198,35 @@ int ictc_hip_sc_weight_features(int lmax, int target_lmax, int correlation, int 
                                 int64_t nodes, hipStream_t stream);
 
 /*
+ * Second-order pieces of the contraction (the double backward used by force
+ * training), each a directional derivative along tangent [nodes, C*(lmax+1)^2]
+ * (mul_ir, like node_features).  They replace the recursive autograd through the
+ * reference's dense restatement for second derivatives (ictc_o3/sparse_product.py:190-204,
+ * 232-250; the reference's create_graph path of _forward_selected_elements).
+ *   jvp:                  out[n]  = J(x_n) tangent_n                  [nodes, C*(target+1)^2]
+ *   hvp:                  grad_features[n] = d/dx <grad_out_n, J(x_n) tangent_n>
+ *                                                                      [nodes, C*(lmax+1)^2]
+ *   weight_features_jvp:  features_out[n, p, c] = <grad_out[n,c], d chain_p(x[n,c])[tangent[n,c]]>
+ *                                                                      [nodes, KTOT, C]
+ * (J = d forward / d node_features at the node's species weights.)  All outputs are
+ * overwritten.
+ */
+int ictc_hip_sc_jvp(int lmax, int target_lmax, int correlation, int channels,
+                    const float* node_features, const int64_t* species, const float* weights,
+                    int num_elements, const float* tangent, float* out, int64_t nodes,
+                    hipStream_t stream);
+
+int ictc_hip_sc_hvp(int lmax, int target_lmax, int correlation, int channels,
+                    const float* node_features, const int64_t* species, const float* weights,
+                    int num_elements, const float* grad_out, const float* tangent,
+                    float* grad_features, int64_t nodes, hipStream_t stream);
+
+int ictc_hip_sc_weight_features_jvp(int lmax, int target_lmax, int correlation, int channels,
+                                    const float* node_features, const int64_t* species,
+                                    int num_elements, const float* grad_out, const float* tangent,
+                                    float* features_out, int64_t nodes, hipStream_t stream);
+
+/*
  * Direction harmonics (ICTC basis, component-normalised) and their analytic
  * derivative contractions, one thread per direction.
  *   directions [rows, 3]; Y has (lmax+1)^2 components Y_0 | Y_1 | ...

@@ -101,3 +101,43 @@ def test_full_size_equivariance_and_weight_linearity(gpu):
     w2 = torch.randn_like(w1)
     f = lambda w: symmetric_contraction(mod.plan, x, species, w)  # noqa: E731
     assert_rel(f(w1 + w2), f(w1) + f(w2), rtol=2e-5, what="weight linearity")
+
+
+@pytest.mark.parametrize("lmax,target,corr,c,with_weights",
+                         [(3, 1, 3, 128, True), (3, 3, 3, 64, True), (3, 0, 3, 32, False), (2, 2, 2, 48, True),
+                          (1, 0, 3, 96, False)])
+def test_second_derivatives(gpu, lmax, target, corr, c, with_weights):
+    """Double backward: d/d(x, go, W) of <a, dx> + <B, dW> with dx, dW from create_graph=True
+    (with_weights=False is the force-training pattern: only dx is differentiated)."""
+    ref = SymmetricContractionOracle(4, c, lmax, target, corr, seed=lmax * 7 + target + corr)
+    mod = _module(ref, gpu)
+    n = 19
+    x, species = _inputs(ref, n, 21)
+    g = torch.Generator().manual_seed(22)
+    go = torch.randn(n, c * (target + 1) ** 2, generator=g)
+    a = torch.randn(n, c * (lmax + 1) ** 2, generator=g)
+    keys = [(l, nu) for l in range(target + 1) for nu in range(corr, 0, -1)]
+    bs = [torch.randn(ref.weights[k].shape, generator=g, dtype=torch.float64) for k in keys]
+
+    params = [p for con in mod.contractions for p in con.columns()]
+    xd, god = x.to(gpu).requires_grad_(), go.to(gpu).requires_grad_()
+    out = mod(xd, node_type_idx=species.to(gpu))
+    wrt = [xd, *params] if with_weights else [xd]
+    first = torch.autograd.grad(out, wrt, god, create_graph=True)
+    loss = (first[0] * a.to(gpu)).sum()
+    if with_weights:
+        loss = loss + sum((d * b.float().to(gpu)).sum() for d, b in zip(first[1:], bs))
+    got = torch.autograd.grad(loss, [xd, god, *params])
+
+    xc, goc = x.double().requires_grad_(), go.double().requires_grad_()
+    wref = {k: v.clone().requires_grad_() for k, v in ref.weights.items()}
+    expect = ref.forward(xc, species, wref)
+    ewrt = [xc, *[wref[k] for k in keys]] if with_weights else [xc]
+    efirst = torch.autograd.grad(expect, ewrt, goc, create_graph=True)
+    eloss = (efirst[0] * a.double()).sum()
+    if with_weights:
+        eloss = eloss + sum((d * b).sum() for d, b in zip(efirst[1:], bs))
+    want = torch.autograd.grad(eloss, [xc, goc, *[wref[k] for k in keys]])
+    names = ["x", "grad_out"] + [f"W{k}" for k in keys]
+    for name, u, v in zip(names, got, want):
+        assert_rel(u, v, what=f"sc second derivative wrt {name}")
