@@ -1,0 +1,255 @@
+"""MACE-style ICTC model (the baseline route of the reference's PureCartesianICTDFix)
+running its equivariant operators on the HIP kernels of ``ictc_o3``.
+
+Architecture (reference ``mace_ictc/models/pure_cartesian_ictd_fix.py``; factory
+``mace_ictc/hp/runtime.py:7-81`` with ``freeze_conv_tp_weight=True``, Bessel basis of 8,
+``radial_sqrt_num_basis=False``, polynomial cutoff p = 5):
+
+  h_0 = node_embedding[species]                                   (:3008-3011)
+  for t in 0..T-1:
+    interaction_t (:1452-2055):
+      x1    = linear_up(h_t)                     per-l C x C, identity init
+      gates = fc(bessel(r))                      8 -> 64 -> 64 -> 64 -> P*C, normalised SiLU
+      m     = sum_{e -> n} mask_e TP(x1[src_e], Y_e, gates_e)   (fused message, HIP)
+      msg   = message_linear(m) / avg_num_neighbors             (per-l, path-preserving)
+      sc    = self_connection(h_t l=0 block, species)           (element-conditioned)
+    product_t (:1145-1195):  h_{t+1} = Linear(SC(msg, species)) + sc   (SC on HIP)
+    energy  += readout_t(h_{t+1})                                (:3095-3101)
+  layer 0 has input degree 0 (paths (0,l,l)); the last product targets l = 0.
+
+Layouts.  Node features between blocks are the reference's flat mul_ir layout
+``[N, C*(L+1)^2]`` (degree blocks ``[C, 2l+1]``), which the symmetric-contraction
+kernels read directly.  ``linear_up`` writes the channel-contiguous ir_mul layout the
+message kernels read (the transpose is folded into its GEMM), and ``message_linear``
+reads the message kernel's packed ir_mul output and writes mul_ir (again folded).
+The product's symmetric contraction uses the pure-ICTC coupling basis
+(``ICTDPureUProductBasisBlockSO3``, the reference's ``ictd-pure-u`` backend, :1397-1431)
+because the bridge basis needs e3nn; the surrounding ``o3.Linear`` is restated as a
+per-degree C x C map with weights ~ N(0, 1) scaled by 1/sqrt(C) (e3nn's element
+normalisation for one path).
+"""
+from __future__ import annotations
+
+import math
+from typing import Dict, List, Optional
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from ictc_o3.backends.hip.graph_message import graph_message
+from ictc_o3.backends.hip.harmonics import direction_harmonics_packed
+from ictc_o3.basis.ictd_irreps import EdgeWeightedPathPreservingTensorProduct
+from ictc_o3.ops.symmetric_contraction import ICTDPureUSymmetricContractionSO3
+
+from .radial import bessel_embedding
+
+SILU_SCALE = 1.6791767923989418   # _Normalize2MomSiLU (pure_cartesian_ictd_fix.py:610-619)
+
+
+def split_mul_ir(x: torch.Tensor, channels: int, lmax: int) -> Dict[int, torch.Tensor]:
+    widths = [channels * (2 * l + 1) for l in range(lmax + 1)]
+    parts = x.split([*widths, x.shape[-1] - sum(widths)], dim=-1)
+    return {l: parts[l].reshape(x.shape[0], channels, 2 * l + 1) for l in range(lmax + 1)}
+
+
+def merge_mul_ir(blocks: Dict[int, torch.Tensor]) -> torch.Tensor:
+    n = next(iter(blocks.values())).shape[0]
+    return torch.cat([blocks[l].reshape(n, -1) for l in sorted(blocks)], dim=-1)
+
+
+def tp_paths(input_lmax: int, edge_lmax: int, target_lmax: int):
+    """_tp_allowed_paths_from_target_lmax (pure_cartesian_ictd_fix.py:298-319)."""
+    return [(a, b, c) for a in range(input_lmax + 1) for b in range(edge_lmax + 1)
+            for c in range(abs(a - b), a + b + 1) if c <= target_lmax and (a + b + c) % 2 == 0]
+
+
+class NormalizedSiLU(nn.Module):
+    def forward(self, x):
+        return F.silu(x) * SILU_SCALE
+
+
+def _mace_linear(fan_in: int, fan_out: int) -> nn.Linear:
+    lin = nn.Linear(fan_in, fan_out, bias=False)
+    nn.init.normal_(lin.weight, mean=0.0, std=1.0 / math.sqrt(fan_in))
+    return lin
+
+
+class ChannelLinear(nn.Module):
+    """EquivariantChannelLinearSO3 (ictd_irreps.py:187-207): per-degree C x C, identity init."""
+
+    def __init__(self, channels: int, lmax: int):
+        super().__init__()
+        self.channels, self.lmax = channels, lmax
+        self.weights = nn.ParameterList([nn.Parameter(torch.eye(channels)) for _ in range(lmax + 1)])
+
+    def to_ir_mul(self, x: torch.Tensor) -> torch.Tensor:
+        """mul_ir [N, C(L+1)^2] -> ir_mul [N, sum_l (2l+1) C]: out[n, m, o] = sum_c W[o,c] x[n,c,m]."""
+        blocks = split_mul_ir(x, self.channels, self.lmax)
+        return torch.cat([torch.matmul(blocks[l].transpose(1, 2), self.weights[l].t()).reshape(x.shape[0], -1)
+                          for l in range(self.lmax + 1)], dim=-1)
+
+
+class MessageLinear(nn.Module):
+    """PathPreservingLinearSO3 (pure_cartesian_ictd_fix.py:629-661) reading the packed ir_mul
+    message (per degree: [count_l paths][2l+1][C]) and writing mul_ir [N, C(L+1)^2]."""
+
+    def __init__(self, counts: Dict[int, int], channels: int, lmax: int):
+        super().__init__()
+        self.channels, self.lmax = channels, lmax
+        self.counts = [int(counts.get(l, 0)) for l in range(lmax + 1)]
+        self.weights = nn.ParameterList()
+        for l in range(lmax + 1):
+            fan_in = channels * self.counts[l]
+            w = torch.empty(channels, fan_in)
+            if fan_in:
+                nn.init.normal_(w, mean=0.0, std=1.0 / math.sqrt(fan_in))
+            self.weights.append(nn.Parameter(w))
+
+    def forward(self, m: torch.Tensor) -> torch.Tensor:
+        n, c, out, off = m.shape[0], self.channels, [], 0
+        for l in range(self.lmax + 1):
+            k, d = self.counts[l], 2 * l + 1
+            if k == 0:
+                out.append(m.new_zeros(n, c * d))
+                continue
+            blk = m[:, off:off + k * d * c].reshape(n, k, d, c).transpose(1, 2).reshape(n, d, k * c)
+            out.append(torch.matmul(blk, self.weights[l].t()).transpose(1, 2).reshape(n, c * d))
+            off += k * d * c
+        return torch.cat(out, dim=-1)
+
+
+class SpeciesLinear(nn.Module):
+    """ElementConditionedLinearSO3 on a scalar block [N, C] (identity init,
+    pure_cartesian_ictd_fix.py:335-390, 140-158): out[n] = W[s_n] x[n]."""
+
+    def __init__(self, num_elements: int, channels: int):
+        super().__init__()
+        self.num_elements, self.channels = num_elements, channels
+        self.weight = nn.Parameter(torch.eye(channels).unsqueeze(0).repeat(num_elements, 1, 1))
+
+    def forward(self, x: torch.Tensor, species: torch.Tensor) -> torch.Tensor:
+        s, c = self.num_elements, self.channels
+        # all species at once (one GEMM), then pick each node's own block
+        y = torch.matmul(x, self.weight.reshape(s * c, c).t()).reshape(-1, s, c)
+        return y.gather(1, species.view(-1, 1, 1).expand(-1, 1, c)).squeeze(1)
+
+
+class IrrepsLinear(nn.Module):
+    """e3nn o3.Linear on C x (0..L): per degree out = W x / sqrt(C), W ~ N(0, 1)."""
+
+    def __init__(self, channels: int, lmax: int):
+        super().__init__()
+        self.channels, self.lmax = channels, lmax
+        self.weights = nn.ParameterList([nn.Parameter(torch.randn(channels, channels)) for _ in range(lmax + 1)])
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        blocks = split_mul_ir(x, self.channels, self.lmax)
+        scale = 1.0 / math.sqrt(self.channels)
+        return merge_mul_ir({l: torch.matmul(self.weights[l], blocks[l]) * scale for l in blocks})
+
+
+class Interaction(nn.Module):
+    def __init__(self, *, channels: int, input_lmax: int, edge_lmax: int, num_elements: int, num_basis: int,
+                 avg_num_neighbors: float):
+        super().__init__()
+        self.channels, self.input_lmax, self.edge_lmax = channels, input_lmax, edge_lmax
+        self.avg_num_neighbors = float(avg_num_neighbors)
+        self.linear_up = ChannelLinear(channels, input_lmax)
+        self.tp = EdgeWeightedPathPreservingTensorProduct(channels, edge_lmax,
+                                                          allowed_paths=tp_paths(input_lmax, edge_lmax, edge_lmax))
+        with torch.no_grad():
+            self.tp.weight.fill_(1.0)          # _init_path_tp_weight_to_one_, then frozen
+        self.tp.weight.requires_grad_(False)
+        self.fc = nn.Sequential(_mace_linear(num_basis, 64), NormalizedSiLU(), _mace_linear(64, 64),
+                                NormalizedSiLU(), _mace_linear(64, 64), NormalizedSiLU(),
+                                _mace_linear(64, self.tp.num_paths * channels))
+        self.message_linear = MessageLinear(self.tp.path_counts_by_l, channels, edge_lmax)
+        self.self_connection = SpeciesLinear(num_elements, channels)
+
+    def forward(self, h, harmonics, edge_feats, src, dst, mask, species):
+        n = h.shape[0]
+        x1 = self.linear_up.to_ir_mul(h)
+        gates = self.tp.effective_gates(self.fc(edge_feats), edge_feats.shape[0])
+        plan = self.tp.hip_plan(self.input_lmax, self.edge_lmax)
+        m = graph_message(plan, x1, harmonics, gates, src, dst, nodes_dst=n, mask=mask)
+        message = self.message_linear(m) / max(self.avg_num_neighbors, 1e-8)
+        sc = self.self_connection(h[:, :self.channels], species)
+        return message, sc
+
+
+class Product(nn.Module):
+    def __init__(self, *, channels: int, lmax: int, target_lmax: int, correlation: int, num_elements: int):
+        super().__init__()
+        self.channels, self.target_lmax = channels, target_lmax
+        self.symmetric_contractions = ICTDPureUSymmetricContractionSO3(
+            num_elements=num_elements, channels=channels, lmax=lmax, target_lmax=target_lmax,
+            correlation=correlation)
+        self.linear = IrrepsLinear(channels, target_lmax)
+
+    def forward(self, message, sc, species):
+        out = self.linear(self.symmetric_contractions(message, node_type_idx=species))
+        # _add_product_self_connection (:94-118): an l = 0 skip lands on the scalar block
+        return torch.cat([out[:, :self.channels] + sc, out[:, self.channels:]], dim=-1)
+
+
+class MaceICTC(nn.Module):
+    def __init__(self, *, channels: int = 128, lmax: int = 3, num_interactions: int = 2, correlation: int = 3,
+                 atomic_numbers=tuple(range(1, 11)), cutoff: float = 5.0, avg_num_neighbors: float = 50.0,
+                 num_basis: int = 8, cutoff_p: int = 5, readout_hidden: int = 16):
+        super().__init__()
+        self.channels, self.lmax, self.cutoff = int(channels), int(lmax), float(cutoff)
+        self.num_basis, self.cutoff_p = int(num_basis), int(cutoff_p)
+        self.atomic_numbers = [int(z) for z in atomic_numbers]
+        self.num_elements = len(self.atomic_numbers)
+        table = torch.full((max(self.atomic_numbers) + 1,), -1, dtype=torch.int64)
+        for i, z in enumerate(self.atomic_numbers):
+            table[z] = i
+        self.register_buffer("atomic_number_to_index", table, persistent=False)
+        self.node_embedding = nn.Linear(self.num_elements, self.channels, bias=False)
+        targets = [self.lmax if t < num_interactions - 1 else 0 for t in range(num_interactions)]
+        self.interactions = nn.ModuleList()
+        self.products = nn.ModuleList()
+        for t, target in enumerate(targets):
+            self.interactions.append(Interaction(channels=self.channels, input_lmax=0 if t == 0 else self.lmax,
+                                                 edge_lmax=self.lmax, num_elements=self.num_elements,
+                                                 num_basis=self.num_basis, avg_num_neighbors=avg_num_neighbors))
+            self.products.append(Product(channels=self.channels, lmax=self.lmax, target_lmax=target,
+                                         correlation=correlation, num_elements=self.num_elements))
+        # EquivariantScalarReadoutSO3 (pure_cartesian_ictd_layers.py:46-70) per inner layer and the
+        # MACE-style MLP readout (pure_cartesian_ictd_fix.py:1434-1449) after the last one
+        self.layer_readouts = nn.ModuleList([_mace_linear(self.channels, 1) for _ in range(num_interactions - 1)])
+        self.last_readout = nn.Sequential(_mace_linear(self.channels, readout_hidden), NormalizedSiLU(),
+                                          _mace_linear(readout_hidden, 1))
+
+    def species_index(self, atomic_numbers: torch.Tensor) -> torch.Tensor:
+        a = atomic_numbers.long()
+        if int(a.max()) >= self.atomic_number_to_index.numel() or int(a.min()) < 0:
+            raise ValueError(f"atomic numbers outside the configured set {self.atomic_numbers}")
+        idx = self.atomic_number_to_index[a]
+        if bool((idx < 0).any()):
+            raise ValueError(f"atomic numbers outside the configured set {self.atomic_numbers}")
+        return idx
+
+    def forward(self, pos, atomic_numbers, batch, edge_src, edge_dst, edge_shifts, cell, species=None):
+        """Atomic energies [N] (reference forward :2879-3106, baseline route)."""
+        shift_vecs = torch.einsum("ni,nij->nj", edge_shifts.to(pos.dtype), cell[batch[edge_src]].to(pos.dtype))
+        vec = pos[edge_dst] - pos[edge_src] + shift_vecs
+        length = vec.norm(dim=1)
+        directions = vec / length.clamp(min=1e-8).unsqueeze(-1)
+        mask = (length <= self.cutoff).to(pos.dtype)
+        harmonics = direction_harmonics_packed(directions, self.lmax)
+        edge_feats = bessel_embedding(length, r_max=self.cutoff, num_basis=self.num_basis, cutoff_p=self.cutoff_p)
+        if species is None:
+            species = self.species_index(atomic_numbers)
+        h = self.node_embedding.weight.t().index_select(0, species)
+        energy = None
+        for t, (interaction, product) in enumerate(zip(self.interactions, self.products)):
+            message, sc = interaction(h, harmonics, edge_feats, edge_src, edge_dst, mask, species)
+            h = product(message, sc, species)
+            if t < len(self.interactions) - 1:
+                e = self.layer_readouts[t](h[:, :self.channels])
+            else:
+                e = self.last_readout(h)
+            energy = e if energy is None else energy + e
+        return energy.reshape(-1)
