@@ -12,13 +12,26 @@ Also reported on the same JSON line:
   launch stream, against the 8 TB/s HBM3E peak;
 * ``cpu_baseline``: the CPU oracle (a PyTorch restatement of the reference's CPU
   path, ``_forward_index_add`` + autograd) on a bounded sample on the host cores;
-* ``extra``: forward-only throughput at 262,144 instances and its roofline.
+* ``extra``: forward-only throughput at 262,144 instances and its roofline, and the
+  other configurations of BASELINE.json, each with its own roofline and a bounded
+  CPU-oracle sample:
+    - cfg 2, graph message (C=64, lmax 2, 16,384 atoms at 0.1 A^-3, r_c 5 A, gates from
+      a random-init 8-Bessel radial MLP): fused gather -> TP -> receiver sum forward, and
+      its VJP (edge + node kernels);
+    - cfg 3, symmetric contraction (C=128, lmax 3 -> 0e+1o, correlation 3, 65,536 nodes,
+      10 species): forward and VJP to the node features (VALU-bound: FLOPs counted on the
+      generated code);
+    - cfg 4, MACE-style energy + forces (C=128, lmax 3, 2 interactions, correlation 3,
+      2,048 atoms at 0.1 A^-3 with 1.5 A minimum separation, r_c 5 A, 10 species):
+      inference and one force-loss training step (AdamW), atom-steps/s, reference timing
+      protocol (>= 2 s and 3 warmup calls, median of 5 synchronised calls).
 
 ``--kernels-only`` runs a 1 GiB device-to-device copy (the counter calibration
 reference) and three launches of each TP kernel at the benchmark sizes, for
 rocprofv3 --pmc passes.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--kernels-only]
+                      [--only tp|message|sc|mace]
 """
 from __future__ import annotations
 
@@ -180,6 +193,242 @@ def _cpu_baseline(budget_s: float = 12.0):
                       f"C128/lmax3, {rows} instances x {done} steps in {dt:.1f}s"}
 
 
+VALU_PEAK_TFLOPS = 157.3                    # MI355X fp32 vector (published)
+
+
+def _median_call_ms(fn, device, *, warmup_s: float = 2.0, warmup_calls: int = 3, calls: int = 5):
+    """Reference protocol: >= 2 s and 3 warmup calls, then the median of synchronised calls."""
+    t_end = time.time() + warmup_s
+    for _ in range(warmup_calls):
+        fn()
+    while time.time() < t_end:
+        fn()
+    torch.cuda.synchronize(device)
+    times = []
+    for _ in range(calls):
+        t0 = time.perf_counter()
+        fn()
+        torch.cuda.synchronize(device)
+        times.append((time.perf_counter() - t0) * 1e3)
+    return sorted(times)[len(times) // 2]
+
+
+def _event_ms(fn, device, reps: int = 10, warmup: int = 3) -> float:
+    """Mean duration of fn's launches between HIP events on the current stream."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize(device)
+    stream = torch.cuda.current_stream(device)
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record(stream)
+    for _ in range(reps):
+        fn()
+    e.record(stream)
+    torch.cuda.synchronize(device)
+    return s.elapsed_time(e) / reps
+
+
+MSG_C, MSG_L, MSG_P, MSG_ATOMS = 64, 2, 11, 16384
+
+
+def _message_inputs(device):
+    """cfg 2 structure, features, harmonics and radial-MLP gates (all resident on the GPU)."""
+    from mace_hip.radial import bessel_embedding
+    from mace_hip.structures import radius_graph, uniform_box
+    st = uniform_box(MSG_ATOMS, 0.1, seed=4)
+    pos, cell = st.positions.to(device), st.cell.to(device)
+    src, dst, shifts = radius_graph(pos, cell, 5.0)
+    vec = pos[dst] - pos[src] + shifts @ cell
+    r = vec.norm(dim=1)
+    from ictc_o3.backends.hip.harmonics import direction_harmonics_packed
+    y = direction_harmonics_packed((vec / r[:, None]).contiguous(), MSG_L).contiguous()
+    gen = torch.Generator(device="cpu").manual_seed(0)
+    x = torch.randn(MSG_ATOMS, MSG_C * (MSG_L + 1) ** 2, generator=gen).to(device)
+    gen_w = torch.Generator(device="cpu").manual_seed(2)
+    w = [torch.randn(o, i, generator=gen_w) / math.sqrt(i) for i, o in ((8, 64), (64, 64), (64, MSG_P * MSG_C))]
+    with torch.no_grad():
+        h = bessel_embedding(r, r_max=5.0, num_basis=8, cutoff_p=5)
+        for k, wk in enumerate(w):
+            h = h @ wk.to(device).t()
+            if k < len(w) - 1:
+                h = torch.nn.functional.silu(h) * 1.6791767923989418
+    go = torch.randn(MSG_ATOMS, 35 * MSG_C, generator=gen).to(device)
+    return src, dst, x, y, h.contiguous(), go
+
+
+def _bench_message(device):
+    from ictc_o3 import EdgeTensorProduct
+    from ictc_o3.backends.hip.graph_message import _backward_raw, _forward_raw, message_graph
+    op = EdgeTensorProduct.create(channels=MSG_C, input_lmax=MSG_L, edge_lmax=MSG_L, device=device)
+    plan = op.plan
+    src, dst, x, y, g, go = _message_inputs(device)
+    edges = src.numel()
+    graph = message_graph(src, dst, MSG_ATOMS, MSG_ATOMS)
+    fwd_ms = _event_ms(lambda: _forward_raw(plan, graph, x, y, g), device)
+    need = (True, True, True)
+    bwd_ms = _event_ms(lambda: _backward_raw(plan, graph, need, x, y, g, go), device)
+    # unique-byte model: per edge Y, gates, src index; per node x read once, out written once
+    fwd_bytes = edges * (4 * (9 + MSG_P * MSG_C) + 8) + MSG_ATOMS * 4 * (576 + 35 * MSG_C)
+    # VJP: per edge Y, gates, index read + dY, dgates written; per node x, go, dx
+    bwd_bytes = edges * (4 * 2 * (9 + MSG_P * MSG_C) + 8) + MSG_ATOMS * 4 * (2 * 576 + 35 * MSG_C)
+    fwd_gbs, bwd_gbs = fwd_bytes / (fwd_ms * 1e-3) / 1e9, bwd_bytes / (bwd_ms * 1e-3) / 1e9
+    return {"workload": "cfg2 graph message C64/lmax2, 16,384 atoms, r_c 5 A", "edges": edges,
+            "edges_per_atom": edges / MSG_ATOMS,
+            "forward": {"mean_ms": fwd_ms, "edges_per_s": edges / (fwd_ms * 1e-3),
+                        "algorithmic_bytes": fwd_bytes, "achieved_gbs": fwd_gbs,
+                        "frac": fwd_gbs / HBM_PEAK_GBS, "kernel": "msg_forward_kernel<2,2,2>"},
+            "vjp": {"mean_ms": bwd_ms, "edges_per_s": edges / (bwd_ms * 1e-3), "algorithmic_bytes": bwd_bytes,
+                    "achieved_gbs": bwd_gbs, "frac": bwd_gbs / HBM_PEAK_GBS,
+                    "kernels": "msg_edge_grad_kernel + msg_node_grad_kernel"}}
+
+
+SC_C, SC_L, SC_T, SC_K, SC_NODES, SC_S = 128, 3, 1, 3, 65536, 10
+
+
+def _sc_inputs(device, nodes=SC_NODES):
+    gen = torch.Generator(device="cpu").manual_seed(0)
+    x = torch.randn(nodes, SC_C * (SC_L + 1) ** 2, generator=gen)
+    species = torch.randint(0, SC_S, (nodes,), generator=torch.Generator().manual_seed(5))
+    go = torch.randn(nodes, SC_C * (SC_T + 1) ** 2, generator=torch.Generator().manual_seed(3))
+    return x.to(device), species.to(device), go.to(device)
+
+
+def _bench_sc(device):
+    sys.path.insert(0, os.path.join(ROOT, "ictc-o3-hp-ascend_amd", "csrc"))
+    import gen_sc
+    from ictc_o3.backends.hip.symmetric_contraction import ContractionPlan, _forward_raw, _vjp_raw
+    plan = ContractionPlan(SC_L, SC_T, SC_K, SC_C, SC_S)
+    x, species, go = _sc_inputs(device)
+    # per-element weights ~ N(0,1)/sqrt(n_paths) per (degree, order) block (BASELINE.json cfg 3)
+    gen = torch.Generator(device="cpu").manual_seed(6)
+    from ictc_o3.basis.symmetric_u import chains
+    blocks = []
+    for lo in range(SC_T + 1):
+        for nu in range(SC_K, 0, -1):
+            k = len(chains(SC_L, lo, nu))
+            blocks.append(torch.randn(SC_S, k, SC_C, generator=gen) / math.sqrt(k))
+    w = torch.cat(blocks, 1).to(device).contiguous()
+    fwd_ms = _event_ms(lambda: _forward_raw(plan, x, species, w), device)
+    vjp_ms = _event_ms(lambda: _vjp_raw(plan, x, species, w, go), device)
+    flops = gen_sc.flop_counts(SC_L, SC_T, SC_K)
+    d, o = (SC_L + 1) ** 2, (SC_T + 1) ** 2
+    fwd_bytes = SC_NODES * (4 * SC_C * (d + o) + 8)
+    vjp_bytes = SC_NODES * (4 * SC_C * (o + 2 * d) + 8)
+
+    def leg(ms, nbytes, nflops, kernel):
+        tflops = nflops * SC_C * SC_NODES / (ms * 1e-3) / 1e12
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        return {"mean_ms": ms, "nodes_per_s": SC_NODES / (ms * 1e-3), "kernel": kernel,
+                "bound": "valu", "flops_per_node": nflops * SC_C, "achieved_tflops": tflops,
+                "peak_tflops": VALU_PEAK_TFLOPS, "frac": tflops / VALU_PEAK_TFLOPS,
+                "algorithmic_bytes": nbytes, "achieved_gbs": gbs, "hbm_frac": gbs / HBM_PEAK_GBS}
+    return {"workload": "cfg3 symmetric contraction C128, lmax 3 -> 0e+1o, correlation 3, 65,536 nodes",
+            "weight_columns": plan.ktot,
+            "forward": leg(fwd_ms, fwd_bytes, flops["forward"], "sc_kernel<3,1,3,0>"),
+            "vjp": leg(vjp_ms, vjp_bytes, flops["vjp"], "sc_kernel<3,1,3,1>")}
+
+
+MACE_ATOMS, MACE_ZS, MACE_CPU_ATOMS = 2048, tuple(range(1, 11)), 128
+
+
+def _mace_graph(device, atoms=MACE_ATOMS):
+    from mace_hip import radius_graph, sequential_insertion
+    st = sequential_insertion(atoms, 0.1, min_separation=1.5, num_species=10, seed=4)
+    pos, cell = st.positions.to(device), st.cell.to(device)
+    src, dst, shifts = radius_graph(pos, cell, 5.0)
+    return st, dict(positions=pos, atomic_numbers=torch.tensor(MACE_ZS, device=device)[st.species.to(device)],
+                    batch=torch.zeros(atoms, dtype=torch.int64, device=device), edge_src=src, edge_dst=dst,
+                    edge_shifts=shifts, cell=cell[None])
+
+
+def _bench_mace(device):
+    from mace_hip import create_model, energy_and_forces, training_step
+    _, graph = _mace_graph(device)
+    model = create_model(channels=128, lmax=3, num_interactions=2, correlation=3, atomic_numbers=MACE_ZS,
+                         cutoff=5.0, device=device, seed=0)
+    species = model.species_index(graph["atomic_numbers"])
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-3, foreach=False)
+    train_ms = _median_call_ms(lambda: training_step(model, opt, graph, species=species), device)
+    model.eval().requires_grad_(False)
+    infer_ms = _median_call_ms(lambda: energy_and_forces(model, **graph, species=species), device)
+    return {"workload": "cfg4 MACE C128/lmax3, 2 interactions, correlation 3, 2,048 atoms, r_c 5 A",
+            "edges": graph["edge_src"].numel(),
+            "inference": {"median_ms": infer_ms, "atom_steps_per_s": MACE_ATOMS / (infer_ms * 1e-3),
+                          "vs_published_11.0k": MACE_ATOMS / (infer_ms * 1e-3) / 11.0e3},
+            "training": {"median_ms": train_ms, "atom_steps_per_s": MACE_ATOMS / (train_ms * 1e-3),
+                         "vs_published_3.81k": MACE_ATOMS / (train_ms * 1e-3) / 3.81e3}}
+
+
+def _cpu_time(fn, budget_s: float):
+    fn()
+    done, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < budget_s or done == 0:
+        fn()
+        done += 1
+    return done, time.perf_counter() - t0
+
+
+def _cpu_message(budget_s: float = 8.0):
+    """Oracle gather -> TP -> index_add on the edges of the first 512 receivers of cfg 2."""
+    sys.path.insert(0, ROOT)
+    from oracle.tensor_product import TensorProductOracle
+    from mace_hip.structures import radius_graph, uniform_box
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    st = uniform_box(MSG_ATOMS, 0.1, seed=4)
+    src, dst, shifts = radius_graph(st.positions, st.cell, 5.0, rows_per_chunk=512)
+    keep = dst < 512
+    src, dst, shifts = src[keep], dst[keep], shifts[keep]
+    from oracle import ictc_basis as B
+    vec = (st.positions[dst] - st.positions[src] + shifts @ st.cell).double()
+    y = B.direction_harmonics_packed(vec / vec.norm(dim=1, keepdim=True), MSG_L).float()
+    gen = torch.Generator().manual_seed(0)
+    x = torch.randn(MSG_ATOMS, 576, generator=gen)
+    g = torch.randn(src.numel(), MSG_P * MSG_C, generator=gen) / math.sqrt(MSG_P)
+    op = TensorProductOracle(MSG_C, MSG_L, MSG_L, MSG_L, dtype=torch.float32)
+    done, dt = _cpu_time(lambda: op.graph_message(x, y, g, src, dst, nodes=MSG_ATOMS), budget_s)
+    return {"value": src.numel() * done / dt, "unit": "edges/s", "cores": threads, "kind": "port",
+            "sample": f"oracle message forward (gather -> _forward_index_add -> index_add, fp32), "
+                      f"{src.numel()} edges of 512 receivers x {done} calls in {dt:.1f}s"}
+
+
+def _cpu_sc(budget_s: float = 8.0):
+    """Oracle _forward_selected_elements recursion + autograd VJP on 256 nodes of cfg 3."""
+    sys.path.insert(0, ROOT)
+    from oracle.symmetric_contraction import SymmetricContractionOracle
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    ref = SymmetricContractionOracle(SC_S, SC_C, SC_L, SC_T, SC_K, seed=1, dtype=torch.float32)
+    x, species, go = (t.cpu() for t in _sc_inputs("cpu", 256))
+
+    def step():
+        xx = x.clone().requires_grad_()
+        torch.autograd.grad(ref.forward(xx, species), xx, go)
+    done, dt = _cpu_time(step, budget_s)
+    return {"value": 256 * done / dt, "unit": "nodes/s (fwd+VJP)", "cores": threads, "kind": "port",
+            "sample": f"oracle contraction recursion + autograd VJP (fp32), 256 nodes x {done} calls in {dt:.1f}s"}
+
+
+def _cpu_mace(budget_s: float = 10.0):
+    """Float32 oracle model E + F on a smaller cell (same density and cutoff as cfg 4)."""
+    sys.path.insert(0, ROOT)
+    from oracle.mace import MaceOracle
+    from mace_hip.model import MaceICTC
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    torch.manual_seed(0)
+    model = MaceICTC(channels=128, lmax=3, num_interactions=2, correlation=3, atomic_numbers=MACE_ZS, cutoff=5.0)
+    oracle = MaceOracle({k: v.detach() for k, v in model.named_parameters()}, channels=128, lmax=3,
+                        num_interactions=2, correlation=3, num_elements=10, cutoff=5.0, avg_num_neighbors=50.0)
+    st, g = _mace_graph("cpu", atoms=MACE_CPU_ATOMS)
+    args = dict(pos=g["positions"], species=st.species, src=g["edge_src"], dst=g["edge_dst"],
+                shifts=g["edge_shifts"], cell=g["cell"], batch=g["batch"])
+    done, dt = _cpu_time(lambda: oracle.energy_and_forces(**args), budget_s)
+    return {"value": MACE_CPU_ATOMS * done / dt, "unit": "atom-steps/s (E+F inference)", "cores": threads, "kind": "port",
+            "sample": f"oracle MACE restatement fp32 E+F, {MACE_CPU_ATOMS} atoms ({g['edge_src'].numel()} edges) x {done} "
+                      f"calls in {dt:.1f}s"}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -187,6 +436,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--kernels-only", action="store_true")
+    ap.add_argument("--only", choices=("tp", "message", "sc", "mace"), default=None,
+                    help="run one section and print its JSON (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); the hot "
@@ -199,12 +450,24 @@ def main() -> int:
     if args.kernels_only:
         _kernels_only(op.plan, device)
         return 0
+    if args.only in ("message", "sc", "mace"):
+        fn = {"message": _bench_message, "sc": _bench_sc, "mace": _bench_mace}[args.only]
+        print(json.dumps({args.only: fn(device)}), flush=True)
+        return 0
     elapsed, vjp_ms, fwd_ms = _time_gpu(args, op.plan, device)
     copy_gbs = _copy_gbs(device)
     value = ROWS_VJP * args.steps / elapsed
     achieved = BYTES_VJP * ROWS_VJP / (vjp_ms * 1e-3) / 1e9
     fwd_achieved = BYTES_FWD * ROWS_FWD / (fwd_ms * 1e-3) / 1e9
     cpu = None if args.no_cpu else _cpu_baseline()
+    others = {}
+    if args.only is None:
+        others = {"message_cfg2": _bench_message(device), "sc_cfg3": _bench_sc(device),
+                  "mace_cfg4": _bench_mace(device)}
+        if not args.no_cpu:
+            others["message_cfg2"]["cpu_baseline"] = _cpu_message()
+            others["sc_cfg3"]["cpu_baseline"] = _cpu_sc()
+            others["mace_cfg4"]["cpu_baseline"] = _cpu_mace()
     line = {
         "metric": "TP instances/s fwd+VJP C128/lmax3; MACE E+F atom-steps/s; % HBM peak",
         "value": value, "unit": "instances/s", "n_gpus": 1, "steps": args.steps,
@@ -226,7 +489,8 @@ def main() -> int:
                   "forward_only": {"instances": ROWS_FWD, "instances_per_s": ROWS_FWD / (fwd_ms * 1e-3),
                                    "mean_launch_ms": fwd_ms, "achieved_gbs": fwd_achieved,
                                    "frac": fwd_achieved / HBM_PEAK_GBS,
-                                   "vs_published_2.70M": ROWS_FWD / (fwd_ms * 1e-3) / 2.70e6}},
+                                   "vs_published_2.70M": ROWS_FWD / (fwd_ms * 1e-3) / 2.70e6},
+                  **others},
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -236,6 +236,16 @@ def weight_columns(lmax: int, target: int, corr: int) -> int:
     return _columns(lmax, target, corr)[2]
 
 
+def flop_counts(lmax: int, target: int, corr: int) -> Dict[str, int]:
+    """Floating-point operations per (node, channel) of the emitted forward and VJP, counted
+    on the emitted code: an fma counts 2, a multiply or an add 1."""
+    import re
+    text = emit(lmax, target, corr)
+    bodies = {"forward": text[text.index("void forward"):text.index("void vjp")],
+              "vjp": text[text.index("void vjp"):text.index("void weight_features")]}
+    return {k: 2 * b.count("sfma(") + len(re.findall(r" [*+] ", b)) for k, b in bodies.items()}
+
+
 def configs():
     return [(l, t, k) for l in range(4) for t in range(l + 1) for k in (1, 2, 3)]
 
