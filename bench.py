@@ -279,7 +279,7 @@ def _bench_message(device):
                         "frac": fwd_gbs / HBM_PEAK_GBS, "kernel": "msg_forward_kernel<2,2,2>"},
             "vjp": {"mean_ms": bwd_ms, "edges_per_s": edges / (bwd_ms * 1e-3), "algorithmic_bytes": bwd_bytes,
                     "achieved_gbs": bwd_gbs, "frac": bwd_gbs / HBM_PEAK_GBS,
-                    "kernels": "msg_edge_grad_kernel + msg_node_grad_kernel"}}
+                    "kernels": "msg_bond_kernel + msg_edge_grad_kernel (dg/dY pass, dxe pass) + msg_node_grad_kernel"}}
 
 
 SC_C, SC_L, SC_T, SC_K, SC_NODES, SC_S = 128, 3, 1, 3, 65536, 10

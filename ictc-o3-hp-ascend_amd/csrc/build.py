@@ -50,15 +50,14 @@ INSTANCE_KINDS = {
             "const float*, const float*, const float*, const float*, float*, float*, float*, "
             "int64_t, hipStream_t);"),
     "msg": ("message_kernels.hpp",
+            "template int launch_msg_bonds<{a}, {b}, {c}>(const ictc_tp_desc&, const float*, float*, "
+            "int64_t, hipStream_t);\n"
             "template int launch_msg_forward<{a}, {b}, {c}>(const ictc_tp_desc&, const float*, "
             "const float*, const float*, const int64_t*, const int64_t*, const int64_t*, float*, "
             "int64_t, int64_t, hipStream_t);\n"
             "template int launch_msg_edge_grad<{a}, {b}, {c}>(const ictc_tp_desc&, const float*, "
             "const float*, const float*, const float*, const int64_t*, const int64_t*, const int64_t*, "
-            "float*, float*, int64_t, int64_t, hipStream_t);\n"
-            "template int launch_msg_node_grad<{a}, {b}, {c}>(const ictc_tp_desc&, const float*, "
-            "const float*, const float*, const int64_t*, const int64_t*, const int64_t*, float*, "
-            "int64_t, int64_t, hipStream_t);"),
+            "float*, float*, float*, int64_t, int64_t, hipStream_t);"),
 }
 
 

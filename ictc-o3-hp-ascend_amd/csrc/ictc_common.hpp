@@ -171,6 +171,14 @@ __device__ __forceinline__ Vec<NV> buf_load(rsrc_t r, uint32_t off) {
   return out;
 }
 
+// One float at voffset + soffset, with a wave-uniform soffset (an SGPR, so no per-load
+// VGPR).  The range check covers voffset only: callers keep voffset + soffset inside
+// the descriptor's range themselves (soffset below a row, lanes clamped to a real
+// channel) and put anything data-dependent in voffset.
+__device__ __forceinline__ float buf_load_vs(rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+}
+
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
@@ -186,6 +194,14 @@ __device__ __forceinline__ void buf_store(rsrc_t r, uint32_t off, const Vec<NV>&
     const f32x4 t = {v.v[0], v.v[1], v.v[2], v.v[3]};
     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, t), r, voff, soff, policy);
   }
+}
+
+// Branch-free per-lane row store: value v of channel c in row r of a [rows][C] block at
+// rsrc r (num_records = rows * C * 4).  Lanes past C get an offset beyond num_records, so
+// the hardware drops their store; no divergent branch (into which the compiler would sink
+// the arithmetic feeding the store) is needed.
+__device__ __forceinline__ void buf_store_lane(rsrc_t r, bool live, uint32_t off, float v) {
+  buf_store<1>(r, live ? off : 0xFFFFFFF0u, Vec<1>{{v}});
 }
 
 // Sum over the 64 lanes of a wave; every lane receives the total.

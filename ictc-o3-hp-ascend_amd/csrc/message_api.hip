@@ -1,33 +1,37 @@
-// extern "C" entry points of the graph-message family; per-degree instantiations are
-// compiled in generated/msg_inst_*.hip.
+// extern "C" entry points of the graph-message family; per-degree instantiations of the
+// bond, forward and edge-adjoint kernels are compiled in generated/msg_inst_*.hip, the
+// source-node segmented sum (which depends on the input degree only) here.
 #include "message_kernels.hpp"
 
 namespace ictc {
 
-#define ICTC_DECLARE(A, B, C)                                                                     \
-  extern template int launch_msg_forward<A, B, C>(const ictc_tp_desc&, const float*, const float*, \
-                                                  const float*, const int64_t*, const int64_t*,    \
-                                                  const int64_t*, float*, int64_t, int64_t,        \
-                                                  hipStream_t);                                    \
+#define ICTC_DECLARE(A, B, C)                                                                      \
+  extern template int launch_msg_bonds<A, B, C>(const ictc_tp_desc&, const float*, float*, int64_t, \
+                                                hipStream_t);                                       \
+  extern template int launch_msg_forward<A, B, C>(const ictc_tp_desc&, const float*, const float*,  \
+                                                  const float*, const int64_t*, const int64_t*,     \
+                                                  const int64_t*, float*, int64_t, int64_t,         \
+                                                  hipStream_t);                                     \
   extern template int launch_msg_edge_grad<A, B, C>(const ictc_tp_desc&, const float*, const float*, \
-                                                    const float*, const float*, const int64_t*,    \
-                                                    const int64_t*, const int64_t*, float*, float*, \
-                                                    int64_t, int64_t, hipStream_t);                \
-  extern template int launch_msg_node_grad<A, B, C>(const ictc_tp_desc&, const float*, const float*, \
-                                                    const float*, const int64_t*, const int64_t*,  \
-                                                    const int64_t*, float*, int64_t, int64_t,       \
-                                                    hipStream_t);
+                                                    const float*, const float*, const int64_t*,     \
+                                                    const int64_t*, const int64_t*, float*, float*,  \
+                                                    float*, int64_t, int64_t, hipStream_t);
 #include "generated/tp_instances.def"
 #undef ICTC_DECLARE
 
+using MsgBonds = int (*)(const ictc_tp_desc&, const float*, float*, int64_t, hipStream_t);
 using MsgFwd = int (*)(const ictc_tp_desc&, const float*, const float*, const float*, const int64_t*,
                        const int64_t*, const int64_t*, float*, int64_t, int64_t, hipStream_t);
 using MsgEdge = int (*)(const ictc_tp_desc&, const float*, const float*, const float*, const float*,
-                        const int64_t*, const int64_t*, const int64_t*, float*, float*, int64_t, int64_t,
-                        hipStream_t);
-using MsgNode = int (*)(const ictc_tp_desc&, const float*, const float*, const float*, const int64_t*,
-                        const int64_t*, const int64_t*, float*, int64_t, int64_t, hipStream_t);
+                        const int64_t*, const int64_t*, const int64_t*, float*, float*, float*, int64_t,
+                        int64_t, hipStream_t);
+using MsgNode = int (*)(int, const float*, const int64_t*, const int64_t*, float*, int64_t, hipStream_t);
 
+#define ICTC_DECLARE(A, B, C) [A * 16 + B * 4 + C] = &launch_msg_bonds<A, B, C>,
+const MsgBonds kMsgBonds[64] = {
+#include "generated/tp_instances.def"
+};
+#undef ICTC_DECLARE
 #define ICTC_DECLARE(A, B, C) [A * 16 + B * 4 + C] = &launch_msg_forward<A, B, C>,
 const MsgFwd kMsgFwd[64] = {
 #include "generated/tp_instances.def"
@@ -38,11 +42,8 @@ const MsgEdge kMsgEdge[64] = {
 #include "generated/tp_instances.def"
 };
 #undef ICTC_DECLARE
-#define ICTC_DECLARE(A, B, C) [A * 16 + B * 4 + C] = &launch_msg_node_grad<A, B, C>,
-const MsgNode kMsgNode[64] = {
-#include "generated/tp_instances.def"
-};
-#undef ICTC_DECLARE
+const MsgNode kMsgNode[4] = {&launch_msg_node_grad<0>, &launch_msg_node_grad<1>, &launch_msg_node_grad<2>,
+                             &launch_msg_node_grad<3>};
 
 int tp_check_desc(const ictc_tp_desc* d);  // tp_api.hip
 
@@ -52,6 +53,19 @@ inline bool fits_u32(int64_t rows, int64_t width_floats) {
 }
 
 inline int msg_index(const ictc_tp_desc* d) { return d->input_lmax * 16 + d->edge_lmax * 4 + d->output_lmax; }
+
+// floats per edge of the bond row: sum over the paths of (2 l1 + 1)(2 l3 + 1)
+inline int bond_width(const ictc_tp_desc* d) {
+  int nb = 0;
+  for (int a = 0; a <= d->input_lmax; ++a)
+    for (int b = 0; b <= d->edge_lmax; ++b)
+      for (int c = 0; c <= d->output_lmax; ++c) {
+        const int lo = a > b ? a - b : b - a;
+        if (c < lo || c > a + b || ((a + b + c) & 1)) continue;
+        nb += (2 * a + 1) * (2 * c + 1);
+      }
+  return nb;
+}
 
 inline int msg_common(const ictc_tp_desc* d, int64_t nodes_src, int64_t nodes_dst, int64_t edges) {
   const int st = tp_check_desc(d);
@@ -70,50 +84,64 @@ extern "C" {
 
 int ictc_hip_message_chunks(int channels) { return channels < 1 ? -1 : (channels + 63) / 64; }
 
-int ictc_hip_message_forward(const ictc_tp_desc* desc, const float* node_features, const float* harmonics,
+int ictc_hip_message_bond_width(const ictc_tp_desc* desc) {
+  if (ictc::tp_check_desc(desc) != ICTC_OK) return -1;
+  return ictc::bond_width(desc);
+}
+
+int ictc_hip_message_bonds(const ictc_tp_desc* desc, const float* harmonics, float* bonds, int64_t edges,
+                           hipStream_t stream) {
+  const int st = ictc::tp_check_desc(desc);
+  if (st != ICTC_OK) return st;
+  if (edges < 0) return ICTC_ERR_INVALID_ARGUMENT;
+  if (edges == 0) return ICTC_OK;
+  if (!harmonics || !bonds) return ICTC_ERR_INVALID_ARGUMENT;
+  const ictc::MsgBonds fn = ictc::kMsgBonds[ictc::msg_index(desc)];
+  if (fn == nullptr) return ICTC_ERR_UNSUPPORTED;
+  return fn(*desc, harmonics, bonds, edges, stream);
+}
+
+int ictc_hip_message_forward(const ictc_tp_desc* desc, const float* node_features, const float* bonds,
                              const float* gates, const int64_t* src, const int64_t* dst_rowptr,
                              const int64_t* dst_perm, float* node_out, int64_t nodes_src, int64_t nodes_dst,
                              int64_t edges, hipStream_t stream) {
   const int st = ictc::msg_common(desc, nodes_src, nodes_dst, edges);
   if (st != ICTC_OK) return st;
   if (nodes_dst == 0) return ICTC_OK;
-  if (!node_out || !dst_rowptr || (edges > 0 && (!node_features || !harmonics || !gates || !src)))
+  if (!node_out || !dst_rowptr || (edges > 0 && (!node_features || !bonds || !gates || !src)))
     return ICTC_ERR_INVALID_ARGUMENT;
   const ictc::MsgFwd fn = ictc::kMsgFwd[ictc::msg_index(desc)];
   if (fn == nullptr) return ICTC_ERR_UNSUPPORTED;
-  return fn(*desc, node_features, harmonics, gates, src, dst_rowptr, dst_perm, node_out, nodes_src, nodes_dst,
+  return fn(*desc, node_features, bonds, gates, src, dst_rowptr, dst_perm, node_out, nodes_src, nodes_dst,
             stream);
 }
 
-int ictc_hip_message_edge_grad(const ictc_tp_desc* desc, const float* node_features, const float* harmonics,
+int ictc_hip_message_edge_grad(const ictc_tp_desc* desc, const float* node_features, const float* bonds,
                                const float* gates, const float* grad_out, const int64_t* src,
                                const int64_t* dst_rowptr, const int64_t* dst_perm,
-                               float* grad_harmonics_partial, float* grad_gates, int64_t nodes_src,
-                               int64_t nodes_dst, int64_t edges, hipStream_t stream) {
+                               float* grad_harmonics_partial, float* grad_gates, float* edge_grad_features,
+                               int64_t nodes_src, int64_t nodes_dst, int64_t edges, hipStream_t stream) {
   const int st = ictc::msg_common(desc, nodes_src, nodes_dst, edges);
   if (st != ICTC_OK) return st;
-  if (edges == 0 || nodes_dst == 0 || (!grad_harmonics_partial && !grad_gates)) return ICTC_OK;
-  if (!node_features || !harmonics || !gates || !grad_out || !src || !dst_rowptr)
-    return ICTC_ERR_INVALID_ARGUMENT;
+  if (edges == 0 || nodes_dst == 0 || (!grad_harmonics_partial && !grad_gates && !edge_grad_features))
+    return ICTC_OK;
+  if (!bonds || !gates || !grad_out || !src || !dst_rowptr) return ICTC_ERR_INVALID_ARGUMENT;
+  if ((grad_harmonics_partial || grad_gates) && !node_features) return ICTC_ERR_INVALID_ARGUMENT;
   const ictc::MsgEdge fn = ictc::kMsgEdge[ictc::msg_index(desc)];
   if (fn == nullptr) return ICTC_ERR_UNSUPPORTED;
-  return fn(*desc, node_features, harmonics, gates, grad_out, src, dst_rowptr, dst_perm,
-            grad_harmonics_partial, grad_gates, nodes_src, nodes_dst, stream);
+  return fn(*desc, node_features, bonds, gates, grad_out, src, dst_rowptr, dst_perm, grad_harmonics_partial,
+            grad_gates, edge_grad_features, nodes_src, nodes_dst, stream);
 }
 
-int ictc_hip_message_node_grad(const ictc_tp_desc* desc, const float* harmonics, const float* gates,
-                               const float* grad_out, const int64_t* dst, const int64_t* src_rowptr,
-                               const int64_t* src_perm, float* grad_features, int64_t nodes_src,
-                               int64_t nodes_dst, int64_t edges, hipStream_t stream) {
-  const int st = ictc::msg_common(desc, nodes_src, nodes_dst, edges);
+int ictc_hip_message_node_grad(const ictc_tp_desc* desc, const float* edge_grad_features,
+                               const int64_t* src_rowptr, const int64_t* src_perm, float* grad_features,
+                               int64_t nodes_src, int64_t edges, hipStream_t stream) {
+  const int st = ictc::msg_common(desc, nodes_src, 0, edges);
   if (st != ICTC_OK) return st;
   if (nodes_src == 0) return ICTC_OK;
-  if (!grad_features || !src_rowptr || (edges > 0 && (!harmonics || !gates || !grad_out || !dst)))
-    return ICTC_ERR_INVALID_ARGUMENT;
-  const ictc::MsgNode fn = ictc::kMsgNode[ictc::msg_index(desc)];
-  if (fn == nullptr) return ICTC_ERR_UNSUPPORTED;
-  return fn(*desc, harmonics, gates, grad_out, dst, src_rowptr, src_perm, grad_features, nodes_src, nodes_dst,
-            stream);
+  if (!grad_features || !src_rowptr || (edges > 0 && !edge_grad_features)) return ICTC_ERR_INVALID_ARGUMENT;
+  return ictc::kMsgNode[desc->input_lmax](desc->channels, edge_grad_features, src_rowptr, src_perm,
+                                          grad_features, nodes_src, stream);
 }
 
 }  // extern "C"

@@ -3,20 +3,28 @@
 //   out[n] = sum_{e : dst(e) = n} TP(x[src(e)], Y[e], g[e])
 // which is the CPU semantics of reference backends/ascend/tensor_product.py:189-218
 // (index_select(src) -> TP -> index_add(dst)) and of the MACE interaction
-// (mace_ictc/models/pure_cartesian_ictd_fix.py:1801-1917), with the per-edge TP of
-// tp_kernels.hpp.  An optional edge mask is folded into the gates by the caller.
+// (mace_ictc/models/pure_cartesian_ictd_fix.py:1801-1917).  An optional edge mask is
+// folded into the gates by the caller.
 //
-// No atomics, deterministic order: edges are visited through a CSR over the
-// receivers (rowptr_dst + slot->edge permutation), each destination node is owned by
-// one wave per 64-channel chunk and accumulated in registers, so per-edge messages
-// never touch HBM.  The VJP splits into
-//   * msg_edge_grad_kernel (receiver CSR): per edge dY and dg, reading dout[n] once
-//     per node (held in registers) and gathering x[src];
-//   * msg_node_grad_kernel (source CSR): dx[s] = sum over the out-edges of s of the TP
-//     feature adjoint, gathering dout[dst].
-// Node-feature and cotangent gathers go through buffer descriptors spanning the whole
-// node tensor, so an out-of-range index reads zeros instead of faulting; the host
-// validates indices before launch.
+// Kernels (no atomics, deterministic order):
+//   * msg_bond_kernel: per-edge bond matrices M_p[e][k][i] = s_p sum_j Y[e,j] C_p[i,j,k]
+//     for every path (the reference's Y @ P bond projection, backends/ascend/
+//     tensor_product.py:9-57 and structured_product.py:7-22), computed once per edge and
+//     shared by every kernel below and by every channel chunk;
+//   * msg_forward_kernel (receiver CSR): one wave per (node, 64-channel chunk)
+//     accumulates the node's output in registers; per edge, the x[src] row, the gates and
+//     the bond row are requested together (one round trip), the bond row is staged in
+//     the wave's LDS row, and the kernel is kept small enough in registers that several
+//     waves per SIMD hide the latency;
+//   * msg_edge_grad_kernel (receiver CSR): one block per (node, 64-channel chunk) stages
+//     dout[n] in LDS once and its waves split the node's edges; per edge dg, dY partials
+//     per chunk, or the edge's contribution to the source-feature adjoint
+//     dxe[e] = sum_p g_p M_p^T dout[dst(e)] (so dout is never gathered per edge);
+//   * msg_node_grad_kernel (source CSR): dx[s] = sum over the out-edges of s of dxe[e],
+//     a streaming segmented sum.
+// Node-feature gathers go through buffer descriptors spanning the whole node tensor,
+// so an out-of-range index reads zeros instead of faulting; the host validates indices
+// before launch.
 #pragma once
 #include "ictc_common.hpp"
 #include "generated/ictc_cg_table.hpp"
@@ -31,42 +39,123 @@ __device__ __forceinline__ void wave_lds_sync() {
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 }
 
-// Bond matrices of one edge, built by the 64 lanes of a wave into its LDS row.
-// yv: wave-uniform harmonics of the edge.
+// Offset of CG(l1,l2,l3) in kCGFlat (generated table order: l1, l2, l3 ascending over
+// the allowed triples with every degree <= 3).
+constexpr int cg_flat_offset(int a, int b, int c) {
+  int off = 0;
+  for (int l1 = 0; l1 <= 3; ++l1)
+    for (int l2 = 0; l2 <= 3; ++l2)
+      for (int l3 = (l1 > l2 ? l1 - l2 : l2 - l1); l3 <= (l1 + l2 < 3 ? l1 + l2 : 3); ++l3) {
+        if ((l1 + l2 + l3) & 1) continue;
+        if (l1 == a && l2 == b && l3 == c) return off;
+        off += (2 * l1 + 1) * (2 * l2 + 1) * (2 * l3 + 1);
+      }
+  return -1;
+}
+static_assert(cg_flat_offset(1, 2, 3) == CGTab<1, 2, 3>::offset, "CG table order");
+static_assert(cg_flat_offset(3, 3, 2) == CGTab<3, 3, 2>::offset, "CG table order");
+
+// Per bond entry (path p, row k, column i): the kCGFlat index of C_p[i, 0, k] and
+// meta = p | nj << 6 | no << 9 | l2^2 << 12.
 template <int LIN, int LE, int LOUT>
-__device__ __forceinline__ void wave_bond(const float* yv, float* __restrict__ row,
-                                          const ictc_tp_desc& d, int lane) {
-  using PS = Paths<LIN, LE, LOUT>;
-  static_for<0, PS::N>([&](auto P) {
-    constexpr int p = P;
-    constexpr int l1 = PS::tab.l1[p], l2 = PS::tab.l2[p], l3 = PS::tab.l3[p];
-    constexpr int ni = 2 * l1 + 1, nj = 2 * l2 + 1, no = 2 * l3 + 1;
-    constexpr int boff = PS::tab.bond[p];
-    constexpr int cgo = CGTab<l1, l2, l3>::offset;
-    if (lane < ni * no) {
-      const int k = lane / ni;
-      const int i = lane - k * ni;
-      float acc = 0.f;
-      static_for<0, nj>([&](auto J) {
-        acc = fmaf(yv[l2 * l2 + J], kCGFlat[cgo + (i * nj + J) * no + k], acc);
-      });
-      row[boff + lane] = acc * d.scale[p];
+struct BondMap {
+  static constexpr int NB = Paths<LIN, LE, LOUT>::NB;
+  uint16_t cg[NB > 0 ? NB : 1];
+  uint16_t meta[NB > 0 ? NB : 1];
+};
+
+template <int LIN, int LE, int LOUT>
+constexpr BondMap<LIN, LE, LOUT> make_bond_map() {
+  BondMap<LIN, LE, LOUT> m{};
+  constexpr PathTable t = Paths<LIN, LE, LOUT>::tab;
+  for (int p = 0; p < t.n; ++p) {
+    const int ni = 2 * t.l1[p] + 1, nj = 2 * t.l2[p] + 1, no = 2 * t.l3[p] + 1;
+    const int cgo = cg_flat_offset(t.l1[p], t.l2[p], t.l3[p]);
+    for (int q = 0; q < ni * no; ++q) {
+      const int k = q / ni, i = q - k * ni;
+      m.cg[t.bond[p] + q] = static_cast<uint16_t>(cgo + i * nj * no + k);
+      m.meta[t.bond[p] + q] = static_cast<uint16_t>(p | nj << 6 | no << 9 | (t.l2[p] * t.l2[p]) << 12);
     }
-  });
+  }
+  return m;
+}
+
+template <int LIN, int LE, int LOUT>
+__constant__ BondMap<LIN, LE, LOUT> kBondMap = make_bond_map<LIN, LE, LOUT>();
+
+// ----------------------------------------------------------------------------- bonds
+// bonds[e, :] = Y[e, :] @ P with the constant projection P[j][entry] = s_p C_p[i, j - l2^2, k]
+// on the entry's own degree block (zero elsewhere): a GEMM with K = (L_e+1)^2.  Each block
+// builds P in LDS once, stages a tile of kBondEdges harmonics rows, and writes the tile's
+// bond rows contiguously (coalesced).
+constexpr int kBondEdges = 64;
+
+template <int LIN, int LE, int LOUT>
+__global__ void __launch_bounds__(256)
+msg_bond_kernel(const float* __restrict__ y, float* __restrict__ bonds, const ictc_tp_desc d, int64_t edges) {
+  using PS = Paths<LIN, LE, LOUT>;
+  constexpr int NB = PS::NB, NY = PS::NY;
+  __shared__ float sP[NY][NB];
+  __shared__ float sY[kBondEdges * NY];
+  const int tid = threadIdx.x;
+  for (int idx = tid; idx < NB; idx += 256) {
+    const int cg = kBondMap<LIN, LE, LOUT>.cg[idx];
+    const int meta = kBondMap<LIN, LE, LOUT>.meta[idx];
+    const int p = meta & 63, nj = (meta >> 6) & 7, no = (meta >> 9) & 7, y0 = meta >> 12;
+    const float sc = d.scale[p];
+#pragma unroll
+    for (int j = 0; j < NY; ++j) {
+      const int jj = j - y0;
+      sP[j][idx] = (jj >= 0 && jj < nj) ? kCGFlat[cg + jj * no] * sc : 0.f;
+    }
+  }
+  const int64_t e0 = static_cast<int64_t>(blockIdx.x) * kBondEdges;
+  const int ne = static_cast<int>(edges - e0 < kBondEdges ? edges - e0 : kBondEdges);
+  for (int t = tid; t < ne * NY; t += 256) sY[t] = y[e0 * NY + t];
+  __syncthreads();
+  float* __restrict__ out = bonds + e0 * NB;
+  for (int t = tid; t < ne * NB; t += 256) {
+    const int le = t / NB, idx = t - le * NB;
+    float acc = 0.f;
+#pragma unroll
+    for (int j = 0; j < NY; ++j) acc = fmaf(sY[le * NY + j], sP[j][idx], acc);
+    out[t] = acc;
+  }
+}
+
+// Bond row of one edge staged by the wave: lane l holds entries l, l + 64, ...
+template <int NB>
+struct BondStage {
+  static constexpr int NV = NB > 0 ? (NB + kWave - 1) / kWave : 1;
+  float v[NV];
+};
+
+template <int NB>
+__device__ __forceinline__ void bond_fetch(const float* __restrict__ bonds, int64_t e, int lane,
+                                           BondStage<NB>& s) {
+  const rsrc_t rb = make_rsrc(bonds + e * NB, NB * 4u);
+#pragma unroll
+  for (int r = 0; r < BondStage<NB>::NV; ++r) s.v[r] = buf_load<1>(rb, (lane + r * kWave) * 4u).v[0];
+}
+
+template <int NB>
+__device__ __forceinline__ void bond_commit(const BondStage<NB>& s, float* __restrict__ row, int lane) {
+#pragma unroll
+  for (int r = 0; r < BondStage<NB>::NV; ++r) row[lane + r * kWave] = s.v[r];
   wave_lds_sync();
 }
 
 // ----------------------------------------------------------------------------- forward
 template <int LIN, int LE, int LOUT>
 __global__ void __launch_bounds__(kMsgBlock)
-msg_forward_kernel(const float* __restrict__ x, const float* __restrict__ y, const float* __restrict__ g,
+msg_forward_kernel(const float* __restrict__ x, const float* __restrict__ bonds, const float* __restrict__ g,
                    const int64_t* __restrict__ src, const int64_t* __restrict__ rowptr,
                    const int64_t* __restrict__ perm, float* __restrict__ out, const ictc_tp_desc d,
                    int64_t nodes_src, int64_t nodes_dst, int nchunks) {
   using PS = Paths<LIN, LE, LOUT>;
-  constexpr int NX = PS::NX, NY = PS::NY, NP = PS::N, NOC = PS::NOC;
-  constexpr int NBS = PS::NB > 0 ? PS::NB : 1;
-  __shared__ float sB[kMsgWaves][NBS];
+  constexpr int NX = PS::NX, NP = PS::N, NOC = PS::NOC, NB = PS::NB;
+  constexpr int NBS = BondStage<NB>::NV * kWave;
+  __shared__ float sB[kMsgWaves][1][NBS];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int64_t item = static_cast<int64_t>(blockIdx.x) * kMsgWaves + wave;
@@ -76,142 +165,179 @@ msg_forward_kernel(const float* __restrict__ x, const float* __restrict__ y, con
   const int C = d.channels;
   const int c = chunk * kWave + lane;
   const uint32_t row = static_cast<uint32_t>(C) * 4u;
-  const uint32_t vo = static_cast<uint32_t>(c) * 4u;
   const bool live = c < C;
-  // whole-tensor descriptors: gathers are range checked
-  const rsrc_t rx = make_rsrc(x, static_cast<uint32_t>(nodes_src * NX * row));
-  float* bond = &sB[wave][0];
+  const rsrc_t rx = make_rsrc(x, static_cast<uint32_t>(nodes_src * NX * row));  // range-checked gathers
   float acc[NOC];
 #pragma unroll
   for (int r = 0; r < NOC; ++r) acc[r] = 0.f;
-  const int64_t s0 = rowptr[node], s1 = rowptr[node + 1];
-  for (int64_t slot = s0; slot < s1; ++slot) {
+
+  // lanes past C read channel 0 (discarded): every access stays inside its row, so the
+  // uniform row offsets can ride in soffset
+  const uint32_t vc = static_cast<uint32_t>(live ? c : 0) * 4u;
+  // bond row first: staging it into LDS then waits for those loads only, while the x and
+  // gate loads issued after it are still in flight
+  auto fetch = [&](int64_t slot, float* xo, float* gvo, BondStage<NB>& bo) {
     const int64_t e = perm ? perm[slot] : slot;
-    const int64_t s = src[e];
-    float yv[NY];
+    bond_fetch<NB>(bonds, e, lane, bo);
+    const uint32_t xoff = static_cast<uint32_t>(src[e]) * NX * row + vc;   // range-checked gather
 #pragma unroll
-    for (int j = 0; j < NY; ++j) yv[j] = y[e * NY + j];
-    wave_bond<LIN, LE, LOUT>(yv, bond, d, lane);
-    const uint32_t xoff = static_cast<uint32_t>(s) * NX * row + vo;
-    float xr[NX];
-#pragma unroll
-    for (int m = 0; m < NX; ++m) {
-      const float v = buf_load<1>(rx, xoff + m * row).v[0];
-      xr[m] = live ? v : 0.f;
-    }
+    for (int m = 0; m < NX; ++m) xo[m] = buf_load_vs(rx, xoff, m * row);
     const rsrc_t rg = make_rsrc(g + e * NP * C, NP * row);
-    float gv[NP];
 #pragma unroll
-    for (int p = 0; p < NP; ++p) {
-      const float v = buf_load<1>(rg, vo + p * row).v[0];
-      gv[p] = live ? v : 0.f;
-    }
+    for (int p = 0; p < NP; ++p) gvo[p] = buf_load_vs(rg, vc, p * row);
+  };
+
+  auto compute = [&](const float* xr, const float* gv, const float* bond) {
     static_for<0, NP>([&](auto P) {
       constexpr int p = P;
       constexpr int l1 = PS::tab.l1[p], l3 = PS::tab.l3[p];
       constexpr int ni = 2 * l1 + 1, no = 2 * l3 + 1;
       constexpr int boff = PS::tab.bond[p], oo = PS::tab.out[p];
+      // an opaque base per path plus a scheduling barrier keep the path's LDS reads next to
+      // their use (otherwise the reads of the whole row are merged and hoisted into registers)
+      const float* bp = opaque_lds_row(bond + boff);
+      __builtin_amdgcn_sched_barrier(0);
       static_for<0, no>([&](auto K) {
         float t = 0.f;
-        static_for<0, ni>([&](auto I) { t = fmaf(xr[l1 * l1 + I], bond[boff + K * ni + I], t); });
+        static_for<0, ni>([&](auto I) { t = fmaf(xr[l1 * l1 + I], bp[K * ni + I], t); });
         acc[oo + K] = fmaf(t, gv[p], acc[oo + K]);
       });
     });
+  };
+
+  // One round trip per edge, every load of the edge issued together; latency is hidden by
+  // the other resident waves (the kernel stays small enough for several per SIMD).
+  const int64_t s0 = rowptr[node], s1 = rowptr[node + 1];
+#pragma clang loop unroll(disable)
+  for (int64_t slot = s0; slot < s1; ++slot) {
+    float xr[NX], gv[NP];
+    BondStage<NB> bs;
+    fetch(slot, xr, gv, bs);
+    bond_commit<NB>(bs, &sB[wave][0][0], lane);
+    compute(xr, gv, &sB[wave][0][0]);
   }
-  if (live) {
-    float* __restrict__ on = out + node * NOC * C;
+  const rsrc_t ro = make_rsrc(out + node * NOC * C, NOC * row);
 #pragma unroll
-    for (int r = 0; r < NOC; ++r) __builtin_nontemporal_store(acc[r], on + r * C + c);
-  }
+  for (int r = 0; r < NOC; ++r) buf_store_lane(ro, live, c * 4u + r * row, acc[r]);
 }
 
 // ----------------------------------------------------------------------------- VJP: per edge
-// dg[e] (raw, unmasked) and dY partials per (edge, chunk): dyp[e*nchunks + chunk][NY].
-template <int LIN, int LE, int LOUT>
+// Optional outputs (null = skip): dyp[e*nchunks + chunk][NY] dY partials, dg[e] raw gate
+// adjoint, dxe[e] [NX][C] the edge's source-feature adjoint.  XDEP instantiations read x and
+// produce dY / dg; the others produce dxe only (two lean passes instead of one kernel whose
+// live state would not fit in registers at lmax 3).
+template <int LIN, int LE, int LOUT, bool XDEP>
 __global__ void __launch_bounds__(kMsgBlock)
-msg_edge_grad_kernel(const float* __restrict__ x, const float* __restrict__ y, const float* __restrict__ g,
+msg_edge_grad_kernel(const float* __restrict__ x, const float* __restrict__ bonds, const float* __restrict__ g,
                      const float* __restrict__ go, const int64_t* __restrict__ src,
                      const int64_t* __restrict__ rowptr, const int64_t* __restrict__ perm,
-                     float* __restrict__ dyp, float* __restrict__ dg, const ictc_tp_desc d,
-                     int64_t nodes_src, int64_t nodes_dst, int nchunks) {
+                     float* __restrict__ dyp, float* __restrict__ dg, float* __restrict__ dxe,
+                     const ictc_tp_desc d, int64_t nodes_src, int64_t nodes_dst, int nchunks) {
   using PS = Paths<LIN, LE, LOUT>;
-  constexpr int NX = PS::NX, NY = PS::NY, NP = PS::N, NOC = PS::NOC;
-  constexpr int NBS = PS::NB > 0 ? PS::NB : 1;
-  __shared__ float sB[kMsgWaves][NBS];
+  constexpr int NX = PS::NX, NY = PS::NY, NP = PS::N, NOC = PS::NOC, NB = PS::NB;
+  constexpr int NBS = BondStage<NB>::NV * kWave;
+  __shared__ float sB[kMsgWaves][1][NBS];
+  __shared__ float sO[NOC * kWave];   // the node's dout chunk, shared by the block's waves
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const int64_t item = static_cast<int64_t>(blockIdx.x) * kMsgWaves + wave;
-  const int64_t node = item / nchunks;
-  if (node >= nodes_dst) return;
-  const int chunk = static_cast<int>(item - node * nchunks);
+  // one block per (node, chunk); its waves take every kMsgWaves-th edge of the node
+  const int64_t node = static_cast<int64_t>(blockIdx.x) / nchunks;
+  const int chunk = static_cast<int>(blockIdx.x - node * nchunks);
   const int C = d.channels;
   const int c = chunk * kWave + lane;
   const uint32_t row = static_cast<uint32_t>(C) * 4u;
-  const uint32_t vo = static_cast<uint32_t>(c) * 4u;
   const bool live = c < C;
   const rsrc_t rx = make_rsrc(x, static_cast<uint32_t>(nodes_src * NX * row));
-  float* bond = &sB[wave][0];
-  float o[NOC];
+  // lanes past C read channel 0 and zero it (dY sums over lanes); uniform row offsets in soffset
+  const uint32_t vc = static_cast<uint32_t>(live ? c : 0) * 4u;
   {
     const rsrc_t ron = make_rsrc(go + node * NOC * C, NOC * row);
-#pragma unroll
-    for (int r = 0; r < NOC; ++r) {
-      const float v = buf_load<1>(ron, vo + r * row).v[0];
-      o[r] = live ? v : 0.f;
+    for (int r = wave; r < NOC; r += kMsgWaves) {
+      const float v = buf_load_vs(ron, vc, r * row);
+      sO[r * kWave + lane] = live ? v : 0.f;
     }
   }
-  const int64_t s0 = rowptr[node], s1 = rowptr[node + 1];
-  for (int64_t slot = s0; slot < s1; ++slot) {
+  __syncthreads();
+  const float* __restrict__ o = sO + lane;   // o[r * kWave]: this lane's channel of dout row r
+
+  auto fetch = [&](int64_t slot, int64_t& eo, float* xo, float* gvo, BondStage<NB>& bo) {
     const int64_t e = perm ? perm[slot] : slot;
-    const int64_t s = src[e];
-    float yv[NY];
+    eo = e;
+    bond_fetch<NB>(bonds, e, lane, bo);   // first, as in the forward
+    const uint32_t xoff = static_cast<uint32_t>(src[e]) * NX * row + vc;   // range-checked gather
+    if constexpr (XDEP) {
 #pragma unroll
-    for (int j = 0; j < NY; ++j) yv[j] = y[e * NY + j];
-    wave_bond<LIN, LE, LOUT>(yv, bond, d, lane);
-    const uint32_t xoff = static_cast<uint32_t>(s) * NX * row + vo;
-    float xr[NX];
-#pragma unroll
-    for (int m = 0; m < NX; ++m) {
-      const float v = buf_load<1>(rx, xoff + m * row).v[0];
-      xr[m] = live ? v : 0.f;
+      for (int m = 0; m < NX; ++m) {
+        const float v = buf_load_vs(rx, xoff, m * row);
+        xo[m] = live ? v : 0.f;
+      }
     }
     const rsrc_t rg = make_rsrc(g + e * NP * C, NP * row);
-    float* __restrict__ dge = dg ? dg + e * NP * C : nullptr;
-    float dyl[NY];
+#pragma unroll
+    for (int p = 0; p < NP; ++p) gvo[p] = buf_load_vs(rg, vc, p * row);
+  };
+
+  auto compute = [&](int64_t e, const float* xr, const float* gv, const float* bond) {
+    const rsrc_t rdg = make_rsrc(dg ? dg + e * NP * C : nullptr, NP * row);
+    float dyl[NY], dxl[NX];   // dY partials (XDEP) / source-feature adjoint (otherwise)
 #pragma unroll
     for (int j = 0; j < NY; ++j) dyl[j] = 0.f;
+#pragma unroll
+    for (int m = 0; m < NX; ++m) dxl[m] = 0.f;
     static_for<0, NP>([&](auto P) {
       constexpr int p = P;
       constexpr int l1 = PS::tab.l1[p], l2 = PS::tab.l2[p], l3 = PS::tab.l3[p];
       constexpr int ni = 2 * l1 + 1, nj = 2 * l2 + 1, no = 2 * l3 + 1;
       constexpr int boff = PS::tab.bond[p], oo = PS::tab.out[p];
       using CG = CGTab<l1, l2, l3>;
-      const float gl = buf_load<1>(rg, vo + p * row).v[0];
-      const float gv = live ? gl : 0.f;
-      float dgv = 0.f;
-      static_for<0, no>([&](auto K) {
-        float base = 0.f;
-        static_for<0, ni>([&](auto I) { base = fmaf(xr[l1 * l1 + I], bond[boff + K * ni + I], base); });
-        dgv = fmaf(base, o[oo + K], dgv);
-      });
-      if (dge != nullptr && live) __builtin_nontemporal_store(dgv, dge + p * C + c);
-      float part[nj];
-#pragma unroll
-      for (int j = 0; j < nj; ++j) part[j] = 0.f;
-      static_for<0, ni>([&](auto I) {
-        static_for<0, no>([&](auto K) {
-          const float t = xr[l1 * l1 + I] * (gv * o[oo + K]);
-          static_for<0, nj>([&](auto J) {
-            constexpr float cg = CG::v[(I * nj + J) * no + K];
-            if constexpr (cg != 0.0f) part[J] = fmaf(cg, t, part[J]);
-          });
+      // per-path opaque bases keep the bond and dout reads of a path next to their use
+      // instead of hoisting every path's reads; products with the gate come after them
+      // (g_p o_k for every path would hold NOC extra registers)
+      const float* bp = opaque_lds_row(bond + boff);
+      const float* op = XDEP ? o + oo * kWave : opaque_lds_row(o + oo * kWave);
+      __builtin_amdgcn_sched_barrier(0);
+      const float gp = live ? gv[p] : 0.f;
+      if constexpr (!XDEP) {   // source-feature adjoint: dxl_i += g_p sum_k M_p[k][i] o_k
+        static_for<0, ni>([&](auto I) {
+          float t = 0.f;
+          static_for<0, no>([&](auto K) { t = fmaf(bp[K * ni + I], op[K * kWave], t); });
+          dxl[l1 * l1 + I] = fmaf(gp, t, dxl[l1 * l1 + I]);
         });
-      });
-      const float sc = d.scale[p];
+      }
+      if constexpr (XDEP) {
+        float dgv = 0.f;
+        static_for<0, no>([&](auto K) {
+          float base = 0.f;
+          static_for<0, ni>([&](auto I) { base = fmaf(xr[l1 * l1 + I], bp[K * ni + I], base); });
+          dgv = fmaf(base, o[(oo + K) * kWave], dgv);
+        });
+        buf_store_lane(rdg, live, c * 4u + p * row, dgv);   // null dg: empty descriptor
+        if (dyp != nullptr) {
+          float part[nj];
 #pragma unroll
-      for (int j = 0; j < nj; ++j) dyl[l2 * l2 + j] = fmaf(sc, part[j], dyl[l2 * l2 + j]);
+          for (int j = 0; j < nj; ++j) part[j] = 0.f;
+          static_for<0, ni>([&](auto I) {
+            const float xg = xr[l1 * l1 + I] * gp;
+            static_for<0, no>([&](auto K) {
+              const float t = xg * o[(oo + K) * kWave];
+              static_for<0, nj>([&](auto J) {
+                constexpr float cg = CG::v[(I * nj + J) * no + K];
+                if constexpr (cg != 0.0f) part[J] = fmaf(cg, t, part[J]);
+              });
+            });
+          });
+          const float sc = d.scale[p];
+#pragma unroll
+          for (int j = 0; j < nj; ++j) dyl[l2 * l2 + j] = fmaf(sc, part[j], dyl[l2 * l2 + j]);
+        }
+      }
     });
-    if (dyp != nullptr) {
+    if constexpr (!XDEP) {
+      const rsrc_t rde = make_rsrc(dxe ? dxe + e * NX * C : nullptr, NX * row);
+#pragma unroll
+      for (int m = 0; m < NX; ++m) buf_store_lane(rde, live, c * 4u + m * row, dxl[m]);
+    }
+    if (XDEP && dyp != nullptr) {
       float mine = 0.f;
 #pragma unroll
       for (int j = 0; j < NY; ++j) {
@@ -220,69 +346,66 @@ msg_edge_grad_kernel(const float* __restrict__ x, const float* __restrict__ y, c
       }
       if (lane < NY) dyp[(e * nchunks + chunk) * NY + lane] = mine;
     }
+  };
+
+  const int64_t s0 = rowptr[node], s1 = rowptr[node + 1];
+#pragma clang loop unroll(disable)
+  for (int64_t slot = s0 + wave; slot < s1; slot += kMsgWaves) {
+    float xr[NX], gv[NP];
+    int64_t e;
+    BondStage<NB> bs;
+    fetch(slot, e, xr, gv, bs);
+    bond_commit<NB>(bs, &sB[wave][0][0], lane);
+    compute(e, xr, gv, &sB[wave][0][0]);
   }
 }
 
 // ----------------------------------------------------------------------------- VJP: per source node
-// dx[s] = sum over edges with src(e) = s of sum_p sum_k M_p[e](:,k) g[e,p] dout[dst(e)]_k.
-template <int LIN, int LE, int LOUT>
+// dx[s] = sum over edges with src(e) = s of dxe[e]  ([NX][C] rows, streamed four edges at a time).
+template <int NX>
 __global__ void __launch_bounds__(kMsgBlock)
-msg_node_grad_kernel(const float* __restrict__ y, const float* __restrict__ g,
-                     const float* __restrict__ go, const int64_t* __restrict__ dst,
-                     const int64_t* __restrict__ rowptr_src, const int64_t* __restrict__ perm_src,
-                     float* __restrict__ dx, const ictc_tp_desc d, int64_t nodes_src, int64_t nodes_dst,
+msg_node_grad_kernel(const float* __restrict__ dxe, const int64_t* __restrict__ rowptr_src,
+                     const int64_t* __restrict__ perm_src, float* __restrict__ dx, int C, int64_t nodes_src,
                      int nchunks) {
-  using PS = Paths<LIN, LE, LOUT>;
-  constexpr int NX = PS::NX, NY = PS::NY, NP = PS::N, NOC = PS::NOC;
-  constexpr int NBS = PS::NB > 0 ? PS::NB : 1;
-  __shared__ float sB[kMsgWaves][NBS];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int64_t item = static_cast<int64_t>(blockIdx.x) * kMsgWaves + wave;
   const int64_t node = item / nchunks;
   if (node >= nodes_src) return;
   const int chunk = static_cast<int>(item - node * nchunks);
-  const int C = d.channels;
   const int c = chunk * kWave + lane;
   const uint32_t row = static_cast<uint32_t>(C) * 4u;
-  const uint32_t vo = static_cast<uint32_t>(c) * 4u;
   const bool live = c < C;
-  const rsrc_t rgo = make_rsrc(go, static_cast<uint32_t>(nodes_dst * NOC * row));
-  float* bond = &sB[wave][0];
-  float dxr[NX];
+  const uint32_t vc = static_cast<uint32_t>(live ? c : 0) * 4u;   // lanes past C re-read channel 0
+  float acc[NX];
 #pragma unroll
-  for (int m = 0; m < NX; ++m) dxr[m] = 0.f;
+  for (int m = 0; m < NX; ++m) acc[m] = 0.f;
   const int64_t s0 = rowptr_src[node], s1 = rowptr_src[node + 1];
-  for (int64_t slot = s0; slot < s1; ++slot) {
+  constexpr int U = 4;
+  int64_t slot = s0;
+  for (; slot + U <= s1; slot += U) {
+    float v[U][NX];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t e = perm_src ? perm_src[slot + u] : slot + u;
+      const rsrc_t r = make_rsrc(dxe + e * NX * C, NX * row);
+#pragma unroll
+      for (int m = 0; m < NX; ++m) v[u][m] = buf_load_vs(r, vc, m * row);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int m = 0; m < NX; ++m) acc[m] += v[u][m];
+  }
+  for (; slot < s1; ++slot) {
     const int64_t e = perm_src ? perm_src[slot] : slot;
-    const int64_t t = dst[e];
-    float yv[NY];
+    const rsrc_t r = make_rsrc(dxe + e * NX * C, NX * row);
 #pragma unroll
-    for (int j = 0; j < NY; ++j) yv[j] = y[e * NY + j];
-    wave_bond<LIN, LE, LOUT>(yv, bond, d, lane);
-    const uint32_t ooff = static_cast<uint32_t>(t) * NOC * row + vo;
-    const rsrc_t rg = make_rsrc(g + e * NP * C, NP * row);
-    static_for<0, NP>([&](auto P) {
-      constexpr int p = P;
-      constexpr int l1 = PS::tab.l1[p], l3 = PS::tab.l3[p];
-      constexpr int ni = 2 * l1 + 1, no = 2 * l3 + 1;
-      constexpr int boff = PS::tab.bond[p], oo = PS::tab.out[p];
-      const float gl = buf_load<1>(rg, vo + p * row).v[0];
-      const float gv = live ? gl : 0.f;
-      float gov[no];
-      static_for<0, no>([&](auto K) { gov[K] = gv * buf_load<1>(rgo, ooff + (oo + K) * row).v[0]; });
-      static_for<0, ni>([&](auto I) {
-        static_for<0, no>([&](auto K) {
-          dxr[l1 * l1 + I] = fmaf(bond[boff + K * ni + I], gov[K], dxr[l1 * l1 + I]);
-        });
-      });
-    });
+    for (int m = 0; m < NX; ++m) acc[m] += buf_load_vs(r, vc, m * row);
   }
-  if (live) {
-    float* __restrict__ dxn = dx + node * NX * C;
+  const rsrc_t rdx = make_rsrc(dx + node * NX * C, NX * row);
 #pragma unroll
-    for (int m = 0; m < NX; ++m) __builtin_nontemporal_store(dxr[m], dxn + m * C + c);
-  }
+  for (int m = 0; m < NX; ++m) buf_store_lane(rdx, live, c * 4u + m * row, acc[m]);
 }
 
 // ----------------------------------------------------------------------------- launchers
@@ -293,32 +416,47 @@ inline dim3 msg_grid(int64_t nodes, int nchunks) {
 }
 
 template <int LIN, int LE, int LOUT>
-int launch_msg_forward(const ictc_tp_desc& d, const float* x, const float* y, const float* g,
+int launch_msg_bonds(const ictc_tp_desc& d, const float* y, float* bonds, int64_t edges, hipStream_t stream) {
+  constexpr int NB = Paths<LIN, LE, LOUT>::NB;
+  if (NB == 0 || edges == 0) return ICTC_OK;
+  hipLaunchKernelGGL((msg_bond_kernel<LIN, LE, LOUT>),
+                     dim3(static_cast<unsigned>((edges + kBondEdges - 1) / kBondEdges)), dim3(256), 0, stream, y,
+                     bonds, d, edges);
+  return msg_launch_status();
+}
+
+template <int LIN, int LE, int LOUT>
+int launch_msg_forward(const ictc_tp_desc& d, const float* x, const float* bonds, const float* g,
                        const int64_t* src, const int64_t* rowptr, const int64_t* perm, float* out,
                        int64_t nodes_src, int64_t nodes_dst, hipStream_t stream) {
   const int nchunks = (d.channels + kWave - 1) / kWave;
   hipLaunchKernelGGL((msg_forward_kernel<LIN, LE, LOUT>), msg_grid(nodes_dst, nchunks), dim3(kMsgBlock), 0,
-                     stream, x, y, g, src, rowptr, perm, out, d, nodes_src, nodes_dst, nchunks);
+                     stream, x, bonds, g, src, rowptr, perm, out, d, nodes_src, nodes_dst, nchunks);
   return msg_launch_status();
 }
 
 template <int LIN, int LE, int LOUT>
-int launch_msg_edge_grad(const ictc_tp_desc& d, const float* x, const float* y, const float* g,
+int launch_msg_edge_grad(const ictc_tp_desc& d, const float* x, const float* bonds, const float* g,
                          const float* go, const int64_t* src, const int64_t* rowptr, const int64_t* perm,
-                         float* dyp, float* dg, int64_t nodes_src, int64_t nodes_dst, hipStream_t stream) {
+                         float* dyp, float* dg, float* dxe, int64_t nodes_src, int64_t nodes_dst,
+                         hipStream_t stream) {
   const int nchunks = (d.channels + kWave - 1) / kWave;
-  hipLaunchKernelGGL((msg_edge_grad_kernel<LIN, LE, LOUT>), msg_grid(nodes_dst, nchunks), dim3(kMsgBlock),
-                     0, stream, x, y, g, go, src, rowptr, perm, dyp, dg, d, nodes_src, nodes_dst, nchunks);
+  const dim3 grid(static_cast<unsigned>(nodes_dst * nchunks));   // one block per (node, chunk)
+  if (dyp != nullptr || dg != nullptr)
+    hipLaunchKernelGGL((msg_edge_grad_kernel<LIN, LE, LOUT, true>), grid, dim3(kMsgBlock), 0, stream, x, bonds, g, go, src, rowptr, perm, dyp, dg, nullptr, d,
+                       nodes_src, nodes_dst, nchunks);
+  if (dxe != nullptr)
+    hipLaunchKernelGGL((msg_edge_grad_kernel<LIN, LE, LOUT, false>), grid, dim3(kMsgBlock), 0, stream, nullptr, bonds, g, go, src, rowptr, perm, nullptr, nullptr, dxe,
+                       d, nodes_src, nodes_dst, nchunks);
   return msg_launch_status();
 }
 
-template <int LIN, int LE, int LOUT>
-int launch_msg_node_grad(const ictc_tp_desc& d, const float* y, const float* g, const float* go,
-                         const int64_t* dst, const int64_t* rowptr_src, const int64_t* perm_src, float* dx,
-                         int64_t nodes_src, int64_t nodes_dst, hipStream_t stream) {
-  const int nchunks = (d.channels + kWave - 1) / kWave;
-  hipLaunchKernelGGL((msg_node_grad_kernel<LIN, LE, LOUT>), msg_grid(nodes_src, nchunks), dim3(kMsgBlock),
-                     0, stream, y, g, go, dst, rowptr_src, perm_src, dx, d, nodes_src, nodes_dst, nchunks);
+template <int LIN>
+int launch_msg_node_grad(int channels, const float* dxe, const int64_t* rowptr_src, const int64_t* perm_src,
+                         float* dx, int64_t nodes_src, hipStream_t stream) {
+  const int nchunks = (channels + kWave - 1) / kWave;
+  hipLaunchKernelGGL((msg_node_grad_kernel<(LIN + 1) * (LIN + 1)>), msg_grid(nodes_src, nchunks),
+                     dim3(kMsgBlock), 0, stream, dxe, rowptr_src, perm_src, dx, channels, nodes_src, nchunks);
   return msg_launch_status();
 }
 

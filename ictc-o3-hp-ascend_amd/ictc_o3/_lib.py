@@ -15,7 +15,7 @@ import torch  # noqa: F401  (must precede CDLL, see module docstring)
 
 MAX_PATHS = 64
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libictc_hip.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 
 class TpDesc(ctypes.Structure):
@@ -55,12 +55,13 @@ _SIGNATURES = {
     "ictc_hip_sc_hvp": (ctypes.c_int, [ctypes.c_int] * 4 + [_P, _P, _P, ctypes.c_int, _P, _P, _P, _I64, _P]),
     "ictc_hip_sc_weight_features_jvp": (ctypes.c_int, [ctypes.c_int] * 4 + [_P, _P, ctypes.c_int, _P, _P, _P,
                                                                               _I64, _P]),
+    "ictc_hip_message_bond_width": (ctypes.c_int, [ctypes.POINTER(TpDesc)]),
+    "ictc_hip_message_bonds": (ctypes.c_int, [ctypes.POINTER(TpDesc), _P, _P, _I64, _P]),
     "ictc_hip_message_forward": (ctypes.c_int, [ctypes.POINTER(TpDesc), _P, _P, _P, _P, _P, _P, _P,
                                                 _I64, _I64, _I64, _P]),
     "ictc_hip_message_edge_grad": (ctypes.c_int, [ctypes.POINTER(TpDesc), _P, _P, _P, _P, _P, _P, _P,
-                                                  _P, _P, _I64, _I64, _I64, _P]),
-    "ictc_hip_message_node_grad": (ctypes.c_int, [ctypes.POINTER(TpDesc), _P, _P, _P, _P, _P, _P, _P,
-                                                  _I64, _I64, _I64, _P]),
+                                                  _P, _P, _P, _I64, _I64, _I64, _P]),
+    "ictc_hip_message_node_grad": (ctypes.c_int, [ctypes.POINTER(TpDesc), _P, _P, _P, _P, _I64, _I64, _P]),
 }
 
 _lock = threading.Lock()

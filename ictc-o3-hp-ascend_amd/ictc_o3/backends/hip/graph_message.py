@@ -7,9 +7,11 @@ The map is trilinear in (node features x, edge harmonics Y, edge gates g) for a
 fixed graph, so its VJP and every mixed derivative reuse the same three kernels
 with substituted operands (as for the plain TP):
 
+    bonds     : msg_bond     (per-edge bond matrices from Y, once per edge)
     forward   : msg_forward  (receiver CSR, per-node register accumulation)
     dY, dg    : msg_edge_grad (receiver CSR, dout[n] in registers, x[src] gathered)
-    dx        : msg_node_grad (source CSR, dout[dst] gathered)
+    dx        : msg_edge_grad writes each edge's feature adjoint, msg_node_grad sums
+                them per source node (source CSR), so dout is never gathered per edge
 
 Graph preprocessing (CSR over receivers and over sources, stable order, index range
 validation) runs once per (src, dst) pair and is cached.
@@ -77,38 +79,72 @@ def _p(t: Optional[torch.Tensor]):
     return None if t is None else t.data_ptr()
 
 
-def _forward_raw(plan: TensorProductPlan, graph: MessageGraph, x, y, g) -> torch.Tensor:
+def bond_width(plan: TensorProductPlan) -> int:
+    width = getattr(plan, "_bond_width", None)
+    if width is None:
+        width = _lib.lib().ictc_hip_message_bond_width(ctypes.byref(plan.desc))
+        if width < 0:
+            raise ValueError("invalid tensor-product descriptor")
+        plan._bond_width = width
+    return width
+
+
+def _bonds(plan: TensorProductPlan, graph: MessageGraph, y) -> Optional[torch.Tensor]:
+    """Per-edge bond matrices [E, NB] of harmonics y (None for an empty graph)."""
+    if graph.edges == 0:
+        return None
+    out = torch.empty(graph.edges, bond_width(plan), device=y.device, dtype=torch.float32)
+    _lib.check(_lib.lib().ictc_hip_message_bonds(
+        ctypes.byref(plan.desc), y.data_ptr(), out.data_ptr(), graph.edges, _lib.stream_of(y.device)),
+        "ictc_hip_message_bonds")
+    return out
+
+
+def _forward_raw(plan: TensorProductPlan, graph: MessageGraph, x, y, g, bonds=None) -> torch.Tensor:
+    if bonds is None:
+        bonds = _bonds(plan, graph, y)
     out = torch.empty(graph.nodes_dst, plan.full_out_width, device=x.device, dtype=torch.float32)
     _lib.check(_lib.lib().ictc_hip_message_forward(
-        ctypes.byref(plan.desc), x.data_ptr(), _p(y), _p(g), graph.src.data_ptr(),
+        ctypes.byref(plan.desc), x.data_ptr(), _p(bonds), _p(g), graph.src.data_ptr(),
         graph.rowptr_dst.data_ptr(), _p(graph.perm_dst), out.data_ptr(), graph.nodes_src,
         graph.nodes_dst, graph.edges, _lib.stream_of(x.device)), "ictc_hip_message_forward")
     return out
 
 
-def _backward_raw(plan: TensorProductPlan, graph: MessageGraph, need, x, y, g, go):
+def _backward_raw(plan: TensorProductPlan, graph: MessageGraph, need, x, y, g, go, bonds=None):
     dev = go.device
     lib = _lib.lib()
     stream = _lib.stream_of(dev)
+    if bonds is None:
+        bonds = _bonds(plan, graph, y)
     dx = dy = dg = None
-    if need[1] or need[2]:
+    dyp = dxe = None
+    if graph.edges:
         nch = lib.ictc_hip_message_chunks(plan.channels)
-        dyp = (torch.empty(graph.edges, nch, plan.y_width, device=dev, dtype=torch.float32)
-               if need[1] else None)
-        dg = (torch.empty(graph.edges, plan.full_gate_width, device=dev, dtype=torch.float32)
-              if need[2] else None)
-        _lib.check(lib.ictc_hip_message_edge_grad(
-            ctypes.byref(plan.desc), x.data_ptr(), _p(y), _p(g), go.data_ptr(), graph.src.data_ptr(),
-            graph.rowptr_dst.data_ptr(), _p(graph.perm_dst), _p(dyp), _p(dg), graph.nodes_src,
-            graph.nodes_dst, graph.edges, stream), "ictc_hip_message_edge_grad")
+        if need[1]:
+            dyp = torch.empty(graph.edges, nch, plan.y_width, device=dev, dtype=torch.float32)
+        if need[2]:
+            dg = torch.empty(graph.edges, plan.full_gate_width, device=dev, dtype=torch.float32)
+        if need[0]:
+            dxe = torch.empty(graph.edges, plan.x_width, device=dev, dtype=torch.float32)
+        if need[0] or need[1] or need[2]:
+            xp = x.data_ptr() if (need[1] or need[2]) else None
+            _lib.check(lib.ictc_hip_message_edge_grad(
+                ctypes.byref(plan.desc), xp, _p(bonds), _p(g), go.data_ptr(), graph.src.data_ptr(),
+                graph.rowptr_dst.data_ptr(), _p(graph.perm_dst), _p(dyp), _p(dg), _p(dxe), graph.nodes_src,
+                graph.nodes_dst, graph.edges, stream), "ictc_hip_message_edge_grad")
         if dyp is not None:
             dy = dyp[:, 0] if nch == 1 else dyp.sum(1)
+    else:
+        if need[1]:
+            dy = torch.empty(0, plan.y_width, device=dev, dtype=torch.float32)
+        if need[2]:
+            dg = torch.empty(0, plan.full_gate_width, device=dev, dtype=torch.float32)
     if need[0]:
         dx = torch.empty(graph.nodes_src, plan.x_width, device=dev, dtype=torch.float32)
         _lib.check(lib.ictc_hip_message_node_grad(
-            ctypes.byref(plan.desc), _p(y), _p(g), go.data_ptr(), graph.dst.data_ptr(),
-            graph.rowptr_src.data_ptr(), _p(graph.perm_src), dx.data_ptr(), graph.nodes_src,
-            graph.nodes_dst, graph.edges, stream), "ictc_hip_message_node_grad")
+            ctypes.byref(plan.desc), _p(dxe), graph.rowptr_src.data_ptr(), _p(graph.perm_src), dx.data_ptr(),
+            graph.nodes_src, graph.edges, stream), "ictc_hip_message_node_grad")
     return dx, dy, dg
 
 
@@ -119,29 +155,37 @@ def _add(acc, value):
 
 
 class _Forward(torch.autograd.Function):
+    """bonds: the bond rows of y when the caller has them (derived data, not an input)."""
+
     @staticmethod
-    def forward(ctx, plan, graph, x, y, g):
+    def forward(ctx, plan, graph, x, y, g, bonds=None):
         ctx.plan, ctx.graph = plan, graph
+        if bonds is None:
+            bonds = _bonds(plan, graph, y)
+        ctx.bonds = bonds
         ctx.save_for_backward(x, y, g)
-        return _forward_raw(plan, graph, x, y, g)
+        return _forward_raw(plan, graph, x, y, g, bonds)
 
     @staticmethod
     def backward(ctx, go):
         x, y, g = ctx.saved_tensors
-        need = required_gradients((x, y, g), ctx.needs_input_grad[2:])
+        need = required_gradients((x, y, g), ctx.needs_input_grad[2:5])
         if go is None or not any(need):
-            return None, None, None, None, None
-        dx, dy, dg = vjp(ctx.plan, ctx.graph, need, x, y, g, go.contiguous())
-        return None, None, dx, dy, dg
+            return None, None, None, None, None, None
+        dx, dy, dg = vjp(ctx.plan, ctx.graph, need, x, y, g, go.contiguous(), ctx.bonds)
+        return None, None, dx, dy, dg, None
 
 
 class _Backward(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, plan, graph, need, x, y, g, go):
+    def forward(ctx, plan, graph, need, x, y, g, go, bonds=None):
         ctx.plan, ctx.graph, ctx.need = plan, graph, need
         ctx.set_materialize_grads(False)
+        if bonds is None:
+            bonds = _bonds(plan, graph, y)
+        ctx.bonds = bonds
         ctx.save_for_backward(x, y, g, go)
-        outs = _backward_raw(plan, graph, need, x, y, g, go)
+        outs = _backward_raw(plan, graph, need, x, y, g, go, bonds)
         empty = go.new_empty(0)
         outs = tuple(t if t is not None else empty for t in outs)
         for t, n in zip(outs, need):
@@ -153,18 +197,19 @@ class _Backward(torch.autograd.Function):
     def backward(ctx, hx, hy, hg):
         plan, graph, need_out = ctx.plan, ctx.graph, ctx.need
         x, y, g, go = ctx.saved_tensors
+        bonds = ctx.bonds
         hx = hx if need_out[0] else None
         hy = hy if need_out[1] else None
         hg = hg if need_out[2] else None
-        nx, ny, ng, no = required_gradients((x, y, g, go), ctx.needs_input_grad[3:])
+        nx, ny, ng, no = required_gradients((x, y, g, go), ctx.needs_input_grad[3:7])
         gx = gy = gg = ggo = None
         if hx is not None:
             hx = hx.contiguous()
             if ny or ng:
-                _, a, b = vjp(plan, graph, (False, ny, ng), hx, y, g, go)
+                _, a, b = vjp(plan, graph, (False, ny, ng), hx, y, g, go, bonds)
                 gy, gg = _add(gy, a), _add(gg, b)
             if no:
-                ggo = _add(ggo, _Forward.apply(plan, graph, hx, y, g))
+                ggo = _add(ggo, _Forward.apply(plan, graph, hx, y, g, bonds))
         if hy is not None:
             hy = hy.contiguous()
             if nx or ng:
@@ -175,18 +220,18 @@ class _Backward(torch.autograd.Function):
         if hg is not None:
             hg = hg.contiguous()
             if nx or ny:
-                a, b, _ = vjp(plan, graph, (nx, ny, False), x, y, hg, go)
+                a, b, _ = vjp(plan, graph, (nx, ny, False), x, y, hg, go, bonds)
                 gx, gy = _add(gx, a), _add(gy, b)
             if no:
-                ggo = _add(ggo, _Forward.apply(plan, graph, x, y, hg))
-        return None, None, None, gx, gy, gg, ggo
+                ggo = _add(ggo, _Forward.apply(plan, graph, x, y, hg, bonds))
+        return None, None, None, gx, gy, gg, ggo, None
 
 
-def vjp(plan, graph, need, x, y, g, go):
+def vjp(plan, graph, need, x, y, g, go, bonds=None):
     need = tuple(bool(n) for n in need)
     if not any(need):
         return None, None, None
-    outs = _Backward.apply(plan, graph, need, x, y, g, go)
+    outs = _Backward.apply(plan, graph, need, x, y, g, go, bonds)
     return tuple(o if n else None for o, n in zip(outs, need))
 
 

@@ -110,6 +110,13 @@ int ictc_hip_tp_backward(const ictc_tp_desc* desc,
 /*
  * Graph message:  node_out[n] = sum_{e : dst(e) = n} TP(features[src(e)], harmonics[e], gates[e])
  * with the TP above (same descriptor; node rows use the features / output layouts).
+ *
+ * The harmonics enter through per-edge bond matrices, computed once per edge by
+ * ictc_hip_message_bonds into a caller-owned buffer [edges, ictc_hip_message_bond_width]:
+ *   bonds[e][bond_p + k*(2 l1 + 1) + i] = scale_p * sum_j harmonics[e][l2^2 + j] C_p[i, j, k]
+ * (the reference's bond projection Y @ P: backends/ascend/tensor_product.py:9-57,
+ * structured_product.py:7-22).  The same buffer serves the forward and both VJP kernels.
+ *
  * Edges are visited through a CSR over the receivers: dst_rowptr [nodes_dst+1] and
  * dst_perm [edges] (CSR slot -> edge id; null when edges are already sorted by dst).
  * Each destination node is accumulated in registers by one wave per 64-channel chunk,
@@ -121,8 +128,13 @@ int ictc_hip_tp_backward(const ictc_tp_desc* desc,
  * channel_message.graph_message (channel_message.py:35-216) and the atomic ictc_epilogue
  * (ascendc/op_kernel/epilogue.cpp:6-212, ascendc/epilogue.py:132-150).
  */
+int ictc_hip_message_bond_width(const ictc_tp_desc* desc);
+
+int ictc_hip_message_bonds(const ictc_tp_desc* desc, const float* harmonics, float* bonds,
+                           int64_t edges, hipStream_t stream);
+
 int ictc_hip_message_forward(const ictc_tp_desc* desc, const float* node_features,
-                             const float* harmonics, const float* gates, const int64_t* src,
+                             const float* bonds, const float* gates, const int64_t* src,
                              const int64_t* dst_rowptr, const int64_t* dst_perm, float* node_out,
                              int64_t nodes_src, int64_t nodes_dst, int64_t edges,
                              hipStream_t stream);
@@ -131,31 +143,36 @@ int ictc_hip_message_forward(const ictc_tp_desc* desc, const float* node_feature
 int ictc_hip_message_chunks(int channels);
 
 /*
- * Message VJP, per-edge part (receiver CSR): for every edge
+ * Message VJP, per-edge part (receiver CSR, grad_out[n] read once per node): for every edge
  *   grad_gates[e]               = d<grad_out, node_out>/d gates[e]            [edges, P*C]
  *   grad_harmonics_partial[e,q] = the harmonics gradient of edge e summed over the
  *                                 channels of chunk q                 [edges, chunks, NY]
- * (the caller sums the chunk axis).  Either output may be null.  Replaces the
- * dr/dg terms of ictc_epilogue_adjoint (ascendc/op_kernel/epilogue_adjoint.cpp:6-208).
+ *                                 (the caller sums the chunk axis)
+ *   edge_grad_features[e]       = sum_p gates[e,p] M_p[e]^T grad_out[dst(e)], the edge's
+ *                                 contribution to the source-feature gradient
+ *                                 [edges, C*(L_in+1)^2] (features layout)
+ * Any output may be null; node_features may be null when only edge_grad_features is
+ * requested.  Replaces the dr/dg terms of ictc_epilogue_adjoint
+ * (ascendc/op_kernel/epilogue_adjoint.cpp:6-208).
  */
 int ictc_hip_message_edge_grad(const ictc_tp_desc* desc, const float* node_features,
-                               const float* harmonics, const float* gates, const float* grad_out,
+                               const float* bonds, const float* gates, const float* grad_out,
                                const int64_t* src, const int64_t* dst_rowptr,
                                const int64_t* dst_perm, float* grad_harmonics_partial,
-                               float* grad_gates, int64_t nodes_src, int64_t nodes_dst,
-                               int64_t edges, hipStream_t stream);
+                               float* grad_gates, float* edge_grad_features, int64_t nodes_src,
+                               int64_t nodes_dst, int64_t edges, hipStream_t stream);
 
 /*
  * Message VJP, per-source-node part (source CSR: src_rowptr [nodes_src+1], src_perm
- * [edges] or null): grad_features[s] = sum over edges with src(e) = s of the TP feature
- * adjoint with grad_out[dst(e)]  [nodes_src, C*(L_in+1)^2], fully overwritten.  Replaces
- * the mode-1 scatter of ictc_weighted_map (ascendc/op_kernel/weighted_map.cpp:225-233)
- * without atomics.
+ * [edges] or null): grad_features[s] = sum over edges with src(e) = s of
+ * edge_grad_features[e]  [nodes_src, C*(L_in+1)^2], fully overwritten; a deterministic
+ * segmented sum.  Replaces the mode-1 scatter of ictc_weighted_map
+ * (ascendc/op_kernel/weighted_map.cpp:225-233) without atomics.
  */
-int ictc_hip_message_node_grad(const ictc_tp_desc* desc, const float* harmonics, const float* gates,
-                               const float* grad_out, const int64_t* dst, const int64_t* src_rowptr,
-                               const int64_t* src_perm, float* grad_features, int64_t nodes_src,
-                               int64_t nodes_dst, int64_t edges, hipStream_t stream);
+int ictc_hip_message_node_grad(const ictc_tp_desc* desc, const float* edge_grad_features,
+                               const int64_t* src_rowptr, const int64_t* src_perm,
+                               float* grad_features, int64_t nodes_src, int64_t edges,
+                               hipStream_t stream);
 
 /*
  * Symmetric contraction (correlation <= 3) with species-selected weights:
