@@ -144,9 +144,11 @@ class IrrepsLinear(nn.Module):
         self.weights = nn.ParameterList([nn.Parameter(torch.randn(channels, channels)) for _ in range(lmax + 1)])
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        # one GEMM per degree over all (node, m) rows: [N (2l+1), C] @ W^T
         blocks = split_mul_ir(x, self.channels, self.lmax)
         scale = 1.0 / math.sqrt(self.channels)
-        return merge_mul_ir({l: torch.matmul(self.weights[l], blocks[l]) * scale for l in blocks})
+        return merge_mul_ir({l: torch.matmul(b.transpose(1, 2), self.weights[l].t() * scale).transpose(1, 2)
+                             for l, b in blocks.items()})
 
 
 class Interaction(nn.Module):
@@ -168,11 +170,15 @@ class Interaction(nn.Module):
         self.self_connection = SpeciesLinear(num_elements, channels)
 
     def forward(self, h, harmonics, edge_feats, src, dst, mask, species):
+        """mask: the reference multiplies the gates by (r <= r_max) (:1801-1808).  The radial
+        features carry the cutoff envelope, exactly 0 from r_max on, and fc has no biases, so
+        the gates are already exactly 0 wherever the mask is 0: the product is an identity and
+        is skipped (mask is accepted for the signature)."""
         n = h.shape[0]
         x1 = self.linear_up.to_ir_mul(h)
         gates = self.tp.effective_gates(self.fc(edge_feats), edge_feats.shape[0])
         plan = self.tp.hip_plan(self.input_lmax, self.edge_lmax)
-        m = graph_message(plan, x1, harmonics, gates, src, dst, nodes_dst=n, mask=mask)
+        m = graph_message(plan, x1, harmonics, gates, src, dst, nodes_dst=n)
         message = self.message_linear(m) / max(self.avg_num_neighbors, 1e-8)
         sc = self.self_connection(h[:, :self.channels], species)
         return message, sc
