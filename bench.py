@@ -347,7 +347,7 @@ def _bench_mace(device):
     model = create_model(channels=128, lmax=3, num_interactions=2, correlation=3, atomic_numbers=MACE_ZS,
                          cutoff=5.0, device=device, seed=0)
     species = model.species_index(graph["atomic_numbers"])
-    opt = torch.optim.AdamW(model.parameters(), lr=1e-3, foreach=False)
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-3)
     train_ms = _median_call_ms(lambda: training_step(model, opt, graph, species=species), device)
     model.eval().requires_grad_(False)
     infer_ms = _median_call_ms(lambda: energy_and_forces(model, **graph, species=species), device)

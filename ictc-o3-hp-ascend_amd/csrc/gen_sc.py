@@ -1,14 +1,25 @@
 """Emit generated/sc_<lmax><target><corr>.hpp: straight-line device code of the
 symmetric contraction for one (lmax, target_lmax, correlation) configuration.
 
-For every U column (a coupling chain, see ictc_o3/basis/symmetric_u.py) of every
-target degree and order, the emitted code adds  w_p * chain_p(x)  to the output,
-where w_p = W[species, p, channel] is read at ``w[p*C]`` (W columns concatenated per
-target degree as [order corr, corr-1, ..., 1], the reference's weights_max,
-weights[0], ... order).  Chains share their pair prefixes
-P_{la,lb,L1}[q] = sum_ij CG(la,lb,L1)[i,j,q] x_la,i x_lb,j, evaluated once per
-(la <= lb, L1) group; the swapped pair uses the exchange sign of the intertwiner and
-symmetric groups (la == lb) whose prefix vanishes identically are skipped.
+Every U column (a coupling chain, see ictc_o3/basis/symmetric_u.py) of every target
+degree and order contributes  w_p * chain_p(x)  to the output, where
+w_p = W[species, p, channel] is read at ``w[p*C]`` (W columns concatenated per target
+degree as [order corr, corr-1, ..., 1], the reference's weights_max, weights[0], ...
+order).  The chains are evaluated in two shared stages:
+
+* pair prefixes P_{la,lb,mid}[q] = sum_ij CG(la,lb,mid)[i,j,q] x_la,i x_lb,j, once per
+  (la <= lb, mid) group; the swapped pair uses the exchange sign of the intertwiner and
+  symmetric groups (la == lb) whose prefix vanishes identically are skipped;
+* the final coupling of an order-3 chain, CG(mid,lc,l_out)[P, x_lc], is linear in P, so
+  the chains that share (mid, lc, l_out) first accumulate  Q = sum_p w_p sign_p P_p  and
+  are then coupled once:  o_l_out += CG(mid,lc,l_out)[Q, x_lc].  At lmax 3 -> 0e+1o this
+  is 13 couplings instead of 69.  The accumulators of one mid are live together, split
+  into batches of at most QMAX floats (register bound).
+
+The VJP runs the same schedule backwards per batch: accumulate Q, couple's adjoint to x_lc
+(reading Q), Q := the coupling's adjoint to the prefix, then per group the prefix adjoint
+G = sum_p w_p sign_p Q_p (plus order-2 members) and its adjoint to x.  The weight
+features are <P_p, adjoint of p's coupling>, one dot per chain.
 
 Emitted per configuration (struct ``ictc::sc::Plan<L, T, K>``), each a template over
 the scalar V of x (float, or the dual number ictc::sc::Dual of sc_plan.hpp, whose
@@ -90,12 +101,23 @@ def _pair_terms(a: int, b: int, mid: int) -> List[Tuple[int, int, int, float]]:
     return terms
 
 
-def emit(lmax: int, target: int, corr: int) -> str:
-    D, NO = (lmax + 1) ** 2, (target + 1) ** 2
-    cols, offsets, ktot = _columns(lmax, target, corr)
-    # group the chains of order >= 2 by their pair prefix
-    groups: Dict[Tuple[int, int, int], List] = {}
-    order1, vanishing = [], []
+# accumulator floats live per batch (the Q array below); bounds register pressure
+QMAX = 21
+
+
+def _schedule(lmax: int, target: int, corr: int):
+    """Chains grouped for evaluation.
+
+    Returns (order1, vanishing, groups, batches, o2_only):
+      groups[key] = {"o2": [(l_out, p, sign)], "o3": [(triple, p, sign)]} per pair prefix
+        key = (la <= lb, mid); triple = (mid, lc, l_out);
+      batches = [{"triples": [(triple, q_offset)], "groups": [key], "o2": {key: [...]}}]
+        per mid (ascending), triples packed greedily so that sum(2 mid + 1) <= QMAX; a group's
+        order-2 members ride with the first batch that evaluates the group's prefix;
+      o2_only = groups without order-3 members (evaluated on their own).
+    """
+    cols, _, _ = _columns(lmax, target, corr)
+    order1, vanishing, groups, triples = [], [], {}, set()
     for lo, order, ch, p in cols:
         if order == 1:
             order1.append((lo, p))
@@ -104,8 +126,41 @@ def emit(lmax: int, target: int, corr: int) -> str:
         if sign == 0:
             vanishing.append(p)
             continue
-        groups.setdefault(key, []).append((lo, order, ch, p, sign))
+        g = groups.setdefault(key, {"o2": [], "o3": []})
+        if order == 2:
+            g["o2"].append((lo, p, sign))
+        else:
+            t = (ch.mid, ch.lc, lo)
+            g["o3"].append((t, p, sign))
+            triples.add(t)
+    batches = []
+    for mid in sorted({t[0] for t in triples}):
+        cur, size = [], 0
+        for t in sorted(t for t in triples if t[0] == mid):
+            n = 2 * mid + 1
+            if cur and size + n > QMAX:
+                batches.append(cur)
+                cur, size = [], 0
+            cur.append((t, size))
+            size += n
+        batches.append(cur)
+    placed, out = set(), []
+    for trip in batches:
+        ts = {t for t, _ in trip}
+        keys = sorted(k for k, g in groups.items() if any(t in ts for t, _, _ in g["o3"]))
+        o2 = {k: groups[k]["o2"] for k in keys if k not in placed and groups[k]["o2"]}
+        placed.update(keys)
+        out.append({"triples": trip, "groups": keys, "o2": o2})
+    o2_only = sorted(k for k, g in groups.items() if not g["o3"])
+    return order1, vanishing, groups, out, o2_only
+
+
+def emit(lmax: int, target: int, corr: int) -> str:
+    D, NO = (lmax + 1) ** 2, (target + 1) ** 2
+    _, offsets, ktot = _columns(lmax, target, corr)
+    order1, vanishing, groups, batches, o2_only = _schedule(lmax, target, corr)
     X = lambda l, m: f"xl[{l * l + m}]"           # noqa: E731
+    U = lambda l, m: f"ul[{l * l + m}]"           # noqa: E731
     fw, bw, aw = [], [], []
     # ---- order 1
     for lo, p in order1:
@@ -117,73 +172,179 @@ def emit(lmax: int, target: int, corr: int) -> str:
         aw.append(f"  phi[{p} * C] = part({' + '.join(terms)});")
     for p in vanishing:
         aw.append(f"  phi[{p} * C] = 0.0f;   // chain with an identically vanishing prefix")
-    # ---- pair groups as a sequence of small steps (switch cases of a loop that is not
-    # unrolled: every step is its own basic block, so register pressure and scheduling
-    # regions stay bounded).  P (prefix) and G (its adjoint) are loop-carried arrays.
-    fsteps, bsteps, asteps = [], [], []
-    maxq = 1
-    for (a, b, mid), members in sorted(groups.items()):
-        terms = _pair_terms(a, b, mid)
-        nq = 2 * mid + 1
-        maxq = max(maxq, nq)
-        pre = [f"    // pair group ({a},{b})->{mid}"]
-        for q in range(nq):
-            expr = "0.0f"
-            for i, j, qq, v in terms:
-                if qq == q:
-                    expr = f"sfma({_f(v)}, {X(a, i)} * {X(b, j)}, {expr})"
-            pre.append(f"    P[{q}] = {expr};")
-        fsteps.append(pre)
-        asteps.append(pre)
-        bsteps.append(pre + [f"    G[{q}] = 0.0f;" for q in range(nq)])
-        for lo, order, ch, p, sign in members:
-            f, b_, ad = [], [], []
-            f.append(f"    const float wv = {sign}.0f * w[{p} * Cs];")
-            b_.append(f"    const float wv = {sign}.0f * w[{p} * Cs];")
-            if order == 2:
-                for m in range(2 * lo + 1):
-                    f.append(f"    o[{lo * lo + m}] = sfma(wv, P[{m}], o[{lo * lo + m}]);")
-                    b_.append(f"    G[{m}] = sfma(wv, u[{lo * lo + m}], G[{m}]);")
-                ad.append(f"    phi[{p} * Cs] = {sign}.0f * part(" +
-                          " + ".join(f"u[{lo * lo + m}] * P[{m}]" for m in range(2 * lo + 1)) + ");")
-            else:
-                lc = ch.lc
-                c2 = coupling(mid, lc, lo)
-                ent = [(aa, k, m, c2[aa, k, m]) for aa in range(nq) for k in range(2 * lc + 1)
-                       for m in range(2 * lo + 1) if abs(c2[aa, k, m]) > EPS]
-                for m in range(2 * lo + 1):
-                    expr = "0.0f"
-                    for aa, k, mm, v in ent:
-                        if mm == m:
-                            expr = f"sfma({_f(v)}, P[{aa}] * {X(lc, k)}, {expr})"
-                    f.append(f"    o[{lo * lo + m}] = sfma(wv, {expr}, o[{lo * lo + m}]);")
-                    b_.append(f"    const float um{m} = wv * u[{lo * lo + m}];")
-                    ad.append(f"    const V t{m} = {expr};")
-                ad.append(f"    phi[{p} * Cs] = {sign}.0f * part(" +
-                          " + ".join(f"u[{lo * lo + m}] * t{m}" for m in range(2 * lo + 1)) + ");")
-                for aa, k, m, v in ent:
-                    b_.append(f"    G[{aa}] = sfma({_f(v)} * um{m}, {X(lc, k)}, G[{aa}]);")
-                    b_.append(f"    dx[{lc * lc + k}] = sfma({_f(v)} * um{m}, P[{aa}], dx[{lc * lc + k}]);")
-            fsteps.append(f)
-            bsteps.append(b_)
-            asteps.append(ad)
-        adj = []
-        for i, j, q, v in terms:
-            if a == b and i == j:
-                adj.append(f"    dx[{a * a + i}] = sfma({_f(2 * v)} * G[{q}], {X(a, i)}, dx[{a * a + i}]);")
-            else:
-                adj.append(f"    dx[{a * a + i}] = sfma({_f(v)} * G[{q}], {X(b, j)}, dx[{a * a + i}]);")
-                adj.append(f"    dx[{b * b + j}] = sfma({_f(v)} * G[{q}], {X(a, i)}, dx[{b * b + j}]);")
-        bsteps.append(adj)
 
-    def loop(steps, decl):
-        # C is re-laundered every iteration so that weight addresses are formed inside their
-        # step instead of being hoisted (all at once) out of the loop
-        out = [f"  {decl}", "  #pragma clang loop unroll(disable)",
-               f"  for (int step = 0; step < {len(steps)}; ++step) {{",
-               '    int Cs = C;', '    asm volatile("" : "+s"(Cs));',
-               f"    #pragma unroll\n    for (int i = 0; i < {D}; ++i) launder(xl[i]);",
-               "    switch (step) {"]
+    maxq = max([1] + [2 * k[2] + 1 for k in groups])
+    qn = max([1] + [off + 2 * t[0] + 1 for b in batches for t, off in b["triples"]])
+
+    def nested(pairs):
+        """sum of coef * operand as one nested sfma chain ([(coef, operand)], coef a literal)."""
+        expr = "0.0f"
+        for v, operand in pairs:
+            expr = f"sfma({_f(v)}, {operand}, {expr})"
+        return expr
+
+    def by_pair(terms):
+        pairs = {}
+        for i, j, q, v in terms:
+            pairs.setdefault((i, j), []).append((q, v))
+        return pairs
+
+    def prefix(key):
+        """P[q] = sum v x_a,i x_b,j, pair-major: one product live at a time."""
+        a, b, mid = key
+        lines = [f"    // pair prefix ({a},{b})->{mid}"] + [f"    P[{q}] = 0.0f;" for q in range(2 * mid + 1)]
+        for (i, j), qs in by_pair(_pair_terms(a, b, mid)).items():
+            lines.append(f"    {{ const V pr = {X(a, i)} * {X(b, j)};")
+            lines += [f"      P[{q}] = sfma({_f(v)}, pr, P[{q}]);" for q, v in qs]
+            lines.append("    }")
+        return lines
+
+    def prefix_adjoint(key):
+        """dx from the prefix adjoint G: h_ij = sum_q v G[q] per pair, then two FMAs."""
+        a, b, _ = key
+        lines = []
+        for (i, j), qs in by_pair(_pair_terms(*key)).items():
+            h = nested([(v, f"G[{q}]") for q, v in qs])
+            lines.append(f"    {{ const V h = {h};")
+            if a == b and i == j:
+                lines.append(f"      dx[{a * a + i}] = sfma(h + h, {X(a, i)}, dx[{a * a + i}]); }}")
+            else:
+                lines.append(f"      dx[{a * a + i}] = sfma(h, {X(b, j)}, dx[{a * a + i}]);")
+                lines.append(f"      dx[{b * b + j}] = sfma(h, {X(a, i)}, dx[{b * b + j}]); }}")
+        return lines
+
+    def weight(p, sign, name):
+        return f"    const float {name} = {sign}.0f * w[{p} * Cs];"
+
+    def entries(t):
+        mid, lc, lo = t
+        c2 = coupling(mid, lc, lo)
+        return [(q, k, m, c2[q, k, m]) for q in range(2 * mid + 1) for k in range(2 * lc + 1)
+                for m in range(2 * lo + 1) if abs(c2[q, k, m]) > EPS]
+
+    def coupling_lines(t, off):
+        """o_m += sum_k x_k (sum_q c[q,k,m] Q[q])."""
+        mid, lc, lo = t
+        km = {}
+        for q, k, m, v in entries(t):
+            km.setdefault((k, m), []).append((v, f"Q[{off + q}]"))
+        return [f"    o[{lo * lo + m}] = sfma({X(lc, k)}, {nested(terms)}, o[{lo * lo + m}]);"
+                for (k, m), terms in sorted(km.items(), key=lambda kv: (kv[0][1], kv[0][0]))]
+
+    def coupling_adjoint_x(t, off):
+        """dx_k += sum_m u_m (sum_q c[q,k,m] Q[q])  (reads the accumulated prefix)."""
+        mid, lc, lo = t
+        km = {}
+        for q, k, m, v in entries(t):
+            km.setdefault((k, m), []).append((v, f"Q[{off + q}]"))
+        return [f"    dx[{lc * lc + k}] = sfma({U(lo, m)}, {nested(terms)}, dx[{lc * lc + k}]);"
+                for (k, m), terms in sorted(km.items())]
+
+    def dual_coupling(t, off):
+        """Q[off + q] = sum_m u_m (sum_k c[q,k,m] x_k): the adjoint of the triple's coupling
+        with respect to its accumulated prefix."""
+        mid, lc, lo = t
+        qm = {}
+        for q, k, m, v in entries(t):
+            qm.setdefault(q, {}).setdefault(m, []).append((v, X(lc, k)))
+        lines = []
+        for q in range(2 * mid + 1):
+            expr = "0.0f"
+            for m, terms in sorted(qm.get(q, {}).items()):
+                expr = f"sfma({U(lo, m)}, {nested(terms)}, {expr})"
+            lines.append(f"    Q[{off + q}] = {expr};")
+        return lines
+
+    fsteps, bsteps, asteps = [], [], []
+    for batch in batches:
+        offs = dict(batch["triples"])
+        # forward / VJP phase A: accumulate the weighted prefixes of each triple
+        for key in batch["groups"]:
+            g = groups[key]
+            nq = 2 * key[2] + 1
+            f = prefix(key)
+            acc = []
+            for r, (t, p, sign) in enumerate(m for m in g["o3"] if m[0] in offs):
+                acc.append(weight(p, sign, f"wq{r}"))
+                acc += [f"    Q[{offs[t] + q}] = sfma(wq{r}, P[{q}], Q[{offs[t] + q}]);" for q in range(nq)]
+            f += acc
+            for r, (lo, p, sign) in enumerate(batch["o2"].get(key, [])):
+                f.append(weight(p, sign, f"wo{r}"))
+                f += [f"    o[{lo * lo + m}] = sfma(wo{r}, P[{m}], o[{lo * lo + m}]);" for m in range(2 * lo + 1)]
+            fsteps.append(f)
+            bsteps.append(prefix(key) + acc)
+        # forward: one coupling per triple on the accumulated prefix (then clear its slots)
+        for t, off in batch["triples"]:
+            mid, lc, lo = t
+            f = [f"    // coupling ({mid},{lc})->{lo}"] + coupling_lines(t, off)
+            f += [f"    Q[{off + q}] = 0.0f;" for q in range(2 * mid + 1)]
+            fsteps.append(f)
+        # VJP phase B: coupling adjoint to x_lc (reads Q), then Q := adjoint to the prefix
+        for t, off in batch["triples"]:
+            mid, lc, lo = t
+            b_ = [f"    // coupling adjoint ({mid},{lc})->{lo}"] + coupling_adjoint_x(t, off)
+            b_ += dual_coupling(t, off)
+            bsteps.append(b_)
+        # VJP phase C: prefix adjoint G = sum_p w_p (adjoint of p's triple) per group
+        for n, key in enumerate(batch["groups"]):
+            g = groups[key]
+            nq = 2 * key[2] + 1
+            b_ = [f"    // prefix adjoint ({key[0]},{key[1]})->{key[2]}"] + [f"    G[{q}] = 0.0f;" for q in range(nq)]
+            for r, (t, p, sign) in enumerate(m for m in g["o3"] if m[0] in offs):
+                b_.append(weight(p, sign, f"wq{r}"))
+                b_ += [f"    G[{q}] = sfma(wq{r}, Q[{offs[t] + q}], G[{q}]);" for q in range(nq)]
+            for r, (lo, p, sign) in enumerate(batch["o2"].get(key, [])):
+                b_.append(weight(p, sign, f"wo{r}"))
+                b_ += [f"    G[{q}] = sfma(wo{r}, {U(lo, q)}, G[{q}]);" for q in range(nq)]
+            b_ += prefix_adjoint(key)
+            if n == len(batch["groups"]) - 1:
+                b_ += [f"    Q[{i}] = 0.0f;" for i in range(qn)]
+            bsteps.append(b_)
+        # weight features: Q := prefix adjoints of the triples, then one dot per chain
+        for t, off in batch["triples"]:
+            asteps.append([f"    // coupling adjoint ({t[0]},{t[1]})->{t[2]}"] + dual_coupling(t, off))
+        for key in batch["groups"]:
+            g = groups[key]
+            nq = 2 * key[2] + 1
+            ad = prefix(key)
+            for t, p, sign in g["o3"]:
+                if t in offs:
+                    dot = " + ".join(f"P[{q}] * Q[{offs[t] + q}]" for q in range(nq))
+                    ad.append(f"    phi[{p} * Cs] = {sign}.0f * part({dot});")
+            for lo, p, sign in batch["o2"].get(key, []):
+                dot = " + ".join(f"{U(lo, m)} * P[{m}]" for m in range(2 * lo + 1))
+                ad.append(f"    phi[{p} * Cs] = {sign}.0f * part({dot});")
+            asteps.append(ad)
+    for key in o2_only:
+        g = groups[key]
+        nq = 2 * key[2] + 1
+        f, ad = prefix(key), prefix(key)
+        b_ = [f"    // order-2 prefix adjoint ({key[0]},{key[1]})->{key[2]}"] + [f"    G[{q}] = 0.0f;" for q in range(nq)]
+        for r, (lo, p, sign) in enumerate(g["o2"]):
+            f.append(weight(p, sign, f"wo{r}"))
+            f += [f"    o[{lo * lo + m}] = sfma(wo{r}, P[{m}], o[{lo * lo + m}]);" for m in range(2 * lo + 1)]
+            b_.append(weight(p, sign, f"wo{r}"))
+            b_ += [f"    G[{q}] = sfma(wo{r}, {U(lo, q)}, G[{q}]);" for q in range(nq)]
+            dot = " + ".join(f"{U(lo, m)} * P[{m}]" for m in range(2 * lo + 1))
+            ad.append(f"    phi[{p} * Cs] = {sign}.0f * part({dot});")
+        fsteps.append(f)
+        bsteps.append(b_ + prefix_adjoint(key))
+        asteps.append(ad)
+
+    def loop(steps, decl, with_u=False):
+        # C, the input copy and (when used) the cotangent copy are re-laundered every
+        # iteration, so that weight addresses and products of x or u with constants are
+        # formed inside their step instead of being hoisted (all at once) out of the loop
+        out = [f"  {decl}"]
+        if with_u:
+            out.append(f"float ul[{NO}];\n  for (int i = 0; i < {NO}; ++i) ul[i] = u[i];")
+        out += ["  #pragma clang loop unroll(disable)",
+                f"  for (int step = 0; step < {len(steps)}; ++step) {{",
+                '    int Cs = C;', '    asm volatile("" : "+s"(Cs));',
+                f"    #pragma unroll\n    for (int i = 0; i < {D}; ++i) launder(xl[i]);"]
+        if with_u:
+            out.append(f"    #pragma unroll\n    for (int i = 0; i < {NO}; ++i) launder(ul[i]);")
+        out.append("    switch (step) {")
         for k, body in enumerate(steps):
             out.append(f"    case {k}: {{")
             out.extend("  " + line for line in body)
@@ -192,9 +353,10 @@ def emit(lmax: int, target: int, corr: int) -> str:
         return out
     if fsteps:
         copy = f"V xl[{D}];\n  for (int i = 0; i < {D}; ++i) xl[i] = x[i];\n  "
-        fw += loop(fsteps, copy + f"V P[{maxq}];")
-        bw += loop(bsteps, copy + f"V P[{maxq}], G[{maxq}];")
-        aw += loop(asteps, copy + f"V P[{maxq}];")
+        zq = f"V Q[{qn}];\n  for (int i = 0; i < {qn}; ++i) Q[i] = 0.0f;\n  "
+        fw += loop(fsteps, copy + zq + f"V P[{maxq}];")
+        bw += loop(bsteps, copy + zq + f"V P[{maxq}], G[{maxq}];", with_u=True)
+        aw += loop(asteps, copy + f"V Q[{qn}];\n  V P[{maxq}];", with_u=True)
     off_lines = ", ".join(str(offsets[(lo, o)]) for lo in range(target + 1) for o in range(corr, 0, -1))
     return "\n".join([
         f"// Generated by csrc/gen_sc.py for lmax={lmax}, target_lmax={target}, correlation={corr}.",

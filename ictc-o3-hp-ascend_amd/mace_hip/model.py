@@ -58,6 +58,13 @@ def merge_mul_ir(blocks: Dict[int, torch.Tensor]) -> torch.Tensor:
     return torch.cat([blocks[l].reshape(n, -1) for l in sorted(blocks)], dim=-1)
 
 
+def degree_rows(block: torch.Tensor) -> torch.Tensor:
+    """mul_ir degree block [N, C, 2l+1] -> rows [N (2l+1), C] (one row per (node, m)), so that a
+    per-degree channel map is one plain GEMM; torch.matmul on the strided [N, 2l+1, C] view can
+    fall back to a batched GEMM over N tiny matrices."""
+    return block.transpose(1, 2).reshape(-1, block.shape[1])
+
+
 def tp_paths(input_lmax: int, edge_lmax: int, target_lmax: int):
     """_tp_allowed_paths_from_target_lmax (pure_cartesian_ictd_fix.py:298-319)."""
     return [(a, b, c) for a in range(input_lmax + 1) for b in range(edge_lmax + 1)
@@ -86,7 +93,7 @@ class ChannelLinear(nn.Module):
     def to_ir_mul(self, x: torch.Tensor) -> torch.Tensor:
         """mul_ir [N, C(L+1)^2] -> ir_mul [N, sum_l (2l+1) C]: out[n, m, o] = sum_c W[o,c] x[n,c,m]."""
         blocks = split_mul_ir(x, self.channels, self.lmax)
-        return torch.cat([torch.matmul(blocks[l].transpose(1, 2), self.weights[l].t()).reshape(x.shape[0], -1)
+        return torch.cat([F.linear(degree_rows(blocks[l]), self.weights[l]).reshape(x.shape[0], -1)
                           for l in range(self.lmax + 1)], dim=-1)
 
 
@@ -113,8 +120,8 @@ class MessageLinear(nn.Module):
             if k == 0:
                 out.append(m.new_zeros(n, c * d))
                 continue
-            blk = m[:, off:off + k * d * c].reshape(n, k, d, c).transpose(1, 2).reshape(n, d, k * c)
-            out.append(torch.matmul(blk, self.weights[l].t()).transpose(1, 2).reshape(n, c * d))
+            blk = m[:, off:off + k * d * c].reshape(n, k, d, c).transpose(1, 2).reshape(n * d, k * c)
+            out.append(F.linear(blk, self.weights[l]).reshape(n, d, c).transpose(1, 2).reshape(n, c * d))
             off += k * d * c
         return torch.cat(out, dim=-1)
 
@@ -144,11 +151,11 @@ class IrrepsLinear(nn.Module):
         self.weights = nn.ParameterList([nn.Parameter(torch.randn(channels, channels)) for _ in range(lmax + 1)])
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        # one GEMM per degree over all (node, m) rows: [N (2l+1), C] @ W^T
         blocks = split_mul_ir(x, self.channels, self.lmax)
         scale = 1.0 / math.sqrt(self.channels)
-        return merge_mul_ir({l: torch.matmul(b.transpose(1, 2), self.weights[l].t() * scale).transpose(1, 2)
-                             for l, b in blocks.items()})
+        n = x.shape[0]
+        return merge_mul_ir({l: F.linear(degree_rows(b), self.weights[l] * scale)
+                             .reshape(n, 2 * l + 1, self.channels).transpose(1, 2) for l, b in blocks.items()})
 
 
 class Interaction(nn.Module):
@@ -239,7 +246,8 @@ class MaceICTC(nn.Module):
 
     def forward(self, pos, atomic_numbers, batch, edge_src, edge_dst, edge_shifts, cell, species=None):
         """Atomic energies [N] (reference forward :2879-3106, baseline route)."""
-        shift_vecs = torch.einsum("ni,nij->nj", edge_shifts.to(pos.dtype), cell[batch[edge_src]].to(pos.dtype))
+        # shift_e @ cell_e as three multiply-adds per edge (not a batched GEMM of 3 x 3 matrices)
+        shift_vecs = (edge_shifts.to(pos.dtype).unsqueeze(-1) * cell[batch[edge_src]].to(pos.dtype)).sum(1)
         vec = pos[edge_dst] - pos[edge_src] + shift_vecs
         length = vec.norm(dim=1)
         directions = vec / length.clamp(min=1e-8).unsqueeze(-1)

@@ -104,7 +104,7 @@ def test_full_size_rotation_and_training_step(gpu):
     assert_rel(out_r["atomic_energy"], out["atomic_energy"], rtol=2e-5, what="atomic energy invariance")
     assert_rel(out_r["forces"], out["forces"] @ rot.T, rtol=RTOL_FORCE, what="force covariance")
     assert math.isfinite(float(out["energy"]))
-    opt = torch.optim.AdamW(model.parameters(), lr=1e-3, foreach=False)
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-3)
     before = {n: p.detach().clone() for n, p in model.named_parameters() if p.requires_grad}
     loss = training_step(model, opt, dict(positions=st.positions.to(gpu), cell=st.cell[None].to(gpu), **base))
     assert math.isfinite(float(loss))
