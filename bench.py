@@ -342,21 +342,40 @@ def _mace_graph(device, atoms=MACE_ATOMS):
 
 
 def _bench_mace(device):
-    from mace_hip import create_model, energy_and_forces, training_step
+    """Eager steps (the reference's execution mode) and the same steps captured into HIP graphs
+    and replayed on the same inputs (positions re-copied into the graph's buffer every call)."""
+    from mace_hip import (CapturedEnergyAndForces, CapturedTrainingStep, create_model, energy_and_forces,
+                          training_step)
     _, graph = _mace_graph(device)
-    model = create_model(channels=128, lmax=3, num_interactions=2, correlation=3, atomic_numbers=MACE_ZS,
-                         cutoff=5.0, device=device, seed=0)
-    species = model.species_index(graph["atomic_numbers"])
+
+    def fresh():
+        model = create_model(channels=128, lmax=3, num_interactions=2, correlation=3, atomic_numbers=MACE_ZS,
+                             cutoff=5.0, device=device, seed=0)
+        return model, model.species_index(graph["atomic_numbers"])
+    model, species = fresh()
     opt = torch.optim.AdamW(model.parameters(), lr=1e-3)
     train_ms = _median_call_ms(lambda: training_step(model, opt, graph, species=species), device)
     model.eval().requires_grad_(False)
     infer_ms = _median_call_ms(lambda: energy_and_forces(model, **graph, species=species), device)
+    captured = CapturedEnergyAndForces(model, **graph, species=species)
+    infer_graph_ms = _median_call_ms(lambda: captured(graph["positions"]), device)
+    del captured
+    model, species = fresh()
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-3, capturable=True)
+    step = CapturedTrainingStep(model, opt, graph, species=species)
+    train_graph_ms = _median_call_ms(lambda: step(graph["positions"]), device)
+    del step
+
+    def leg(ms, published, mode):
+        rate = MACE_ATOMS / (ms * 1e-3)
+        return {"median_ms": ms, "atom_steps_per_s": rate, f"vs_published_{published / 1e3:.2f}k": rate / published,
+                "execution": mode}
     return {"workload": "cfg4 MACE C128/lmax3, 2 interactions, correlation 3, 2,048 atoms, r_c 5 A",
             "edges": graph["edge_src"].numel(),
-            "inference": {"median_ms": infer_ms, "atom_steps_per_s": MACE_ATOMS / (infer_ms * 1e-3),
-                          "vs_published_11.0k": MACE_ATOMS / (infer_ms * 1e-3) / 11.0e3},
-            "training": {"median_ms": train_ms, "atom_steps_per_s": MACE_ATOMS / (train_ms * 1e-3),
-                         "vs_published_3.81k": MACE_ATOMS / (train_ms * 1e-3) / 3.81e3}}
+            "inference": leg(infer_ms, 11.0e3, "eager"),
+            "training": leg(train_ms, 3.81e3, "eager"),
+            "inference_hip_graph": leg(infer_graph_ms, 11.0e3, "HIP graph replay"),
+            "training_hip_graph": leg(train_graph_ms, 3.81e3, "HIP graph replay")}
 
 
 def _cpu_time(fn, budget_s: float):

@@ -11,11 +11,12 @@
 //     for every path (the reference's Y @ P bond projection, backends/ascend/
 //     tensor_product.py:9-57 and structured_product.py:7-22), computed once per edge and
 //     shared by every kernel below and by every channel chunk;
-//   * msg_forward_kernel (receiver CSR): one wave per (node, 64-channel chunk)
-//     accumulates the node's output in registers; per edge, the x[src] row, the gates and
-//     the bond row are requested together (one round trip), the bond row is staged in
-//     the wave's LDS row, and the kernel is kept small enough in registers that several
-//     waves per SIMD hide the latency;
+//   * msg_forward_kernel (receiver CSR): one block per (node, 64-channel chunk); its waves
+//     split the node's edges and accumulate in registers, then sum their partials in a
+//     fixed order through LDS; per edge, the x[src] row, the gates and the bond row are
+//     requested together (one round trip), the bond row is staged in the wave's LDS row,
+//     and the kernel is kept small enough in registers that several waves per SIMD hide
+//     the latency;
 //   * msg_edge_grad_kernel (receiver CSR): one block per (node, 64-channel chunk) stages
 //     dout[n] in LDS once and its waves split the node's edges; per edge dg, dY partials
 //     per chunk, or the edge's contribution to the source-feature adjoint
@@ -146,6 +147,13 @@ __device__ __forceinline__ void bond_commit(const BondStage<NB>& s, float* __res
 }
 
 // ----------------------------------------------------------------------------- forward
+// One block per (receiver node, 64-channel chunk): its waves take every kMsgWaves-th edge
+// of the node and accumulate partial outputs in registers, then the partials are summed
+// in a fixed order (wave 0 + 1 + 2 + 3) through LDS, kMsgReduceRows output rows at a time.
+// Four waves per receiver fill the GPU even for a few thousand receivers (the per-node
+// wave count is what a one-wave-per-receiver launch is limited by).
+constexpr int kMsgReduceRows = 16;
+
 template <int LIN, int LE, int LOUT>
 __global__ void __launch_bounds__(kMsgBlock)
 msg_forward_kernel(const float* __restrict__ x, const float* __restrict__ bonds, const float* __restrict__ g,
@@ -155,13 +163,13 @@ msg_forward_kernel(const float* __restrict__ x, const float* __restrict__ bonds,
   using PS = Paths<LIN, LE, LOUT>;
   constexpr int NX = PS::NX, NP = PS::N, NOC = PS::NOC, NB = PS::NB;
   constexpr int NBS = BondStage<NB>::NV * kWave;
+  constexpr int R = kMsgReduceRows;
   __shared__ float sB[kMsgWaves][1][NBS];
+  __shared__ float sR[kMsgWaves - 1][R][kWave];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const int64_t item = static_cast<int64_t>(blockIdx.x) * kMsgWaves + wave;
-  const int64_t node = item / nchunks;
-  if (node >= nodes_dst) return;
-  const int chunk = static_cast<int>(item - node * nchunks);
+  const int64_t node = static_cast<int64_t>(blockIdx.x) / nchunks;
+  const int chunk = static_cast<int>(blockIdx.x - node * nchunks);
   const int C = d.channels;
   const int c = chunk * kWave + lane;
   const uint32_t row = static_cast<uint32_t>(C) * 4u;
@@ -170,7 +178,6 @@ msg_forward_kernel(const float* __restrict__ x, const float* __restrict__ bonds,
   float acc[NOC];
 #pragma unroll
   for (int r = 0; r < NOC; ++r) acc[r] = 0.f;
-
   // lanes past C read channel 0 (discarded): every access stays inside its row, so the
   // uniform row offsets can ride in soffset
   const uint32_t vc = static_cast<uint32_t>(live ? c : 0) * 4u;
@@ -209,7 +216,7 @@ msg_forward_kernel(const float* __restrict__ x, const float* __restrict__ bonds,
   // the other resident waves (the kernel stays small enough for several per SIMD).
   const int64_t s0 = rowptr[node], s1 = rowptr[node + 1];
 #pragma clang loop unroll(disable)
-  for (int64_t slot = s0; slot < s1; ++slot) {
+  for (int64_t slot = s0 + wave; slot < s1; slot += kMsgWaves) {
     float xr[NX], gv[NP];
     BondStage<NB> bs;
     fetch(slot, xr, gv, bs);
@@ -217,8 +224,25 @@ msg_forward_kernel(const float* __restrict__ x, const float* __restrict__ bonds,
     compute(xr, gv, &sB[wave][0][0]);
   }
   const rsrc_t ro = make_rsrc(out + node * NOC * C, NOC * row);
+  static_for<0, (NOC + R - 1) / R>([&](auto PIECE) {
+    constexpr int r0 = PIECE * R;
+    constexpr int nr = NOC - r0 < R ? NOC - r0 : R;
+    if (wave > 0) {
 #pragma unroll
-  for (int r = 0; r < NOC; ++r) buf_store_lane(ro, live, c * 4u + r * row, acc[r]);
+      for (int r = 0; r < nr; ++r) sR[wave - 1][r][lane] = acc[r0 + r];
+    }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+      for (int r = 0; r < nr; ++r) {
+        float v = acc[r0 + r];
+#pragma unroll
+        for (int w = 0; w < kMsgWaves - 1; ++w) v += sR[w][r][lane];
+        buf_store_lane(ro, live, c * 4u + (r0 + r) * row, v);
+      }
+    }
+    __syncthreads();
+  });
 }
 
 // ----------------------------------------------------------------------------- VJP: per edge
@@ -430,7 +454,8 @@ int launch_msg_forward(const ictc_tp_desc& d, const float* x, const float* bonds
                        const int64_t* src, const int64_t* rowptr, const int64_t* perm, float* out,
                        int64_t nodes_src, int64_t nodes_dst, hipStream_t stream) {
   const int nchunks = (d.channels + kWave - 1) / kWave;
-  hipLaunchKernelGGL((msg_forward_kernel<LIN, LE, LOUT>), msg_grid(nodes_dst, nchunks), dim3(kMsgBlock), 0,
+  const dim3 grid(static_cast<unsigned>(nodes_dst * nchunks));   // one block per (node, chunk)
+  hipLaunchKernelGGL((msg_forward_kernel<LIN, LE, LOUT>), grid, dim3(kMsgBlock), 0,
                      stream, x, bonds, g, src, rowptr, perm, out, d, nodes_src, nodes_dst, nchunks);
   return msg_launch_status();
 }

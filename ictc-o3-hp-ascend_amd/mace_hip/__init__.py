@@ -1,7 +1,8 @@
 """MACE-style energy + force model on the ictc_o3 HIP operators (caller side)."""
 from .model import MaceICTC
-from .runtime import create_model, energy_and_forces, force_loss, training_step
+from .runtime import (CapturedEnergyAndForces, CapturedTrainingStep, create_model, energy_and_forces,
+                      force_loss, training_step)
 from .structures import radius_graph, sequential_insertion, uniform_box
 
-__all__ = ["MaceICTC", "create_model", "energy_and_forces", "force_loss", "training_step", "radius_graph",
+__all__ = ["MaceICTC", "CapturedEnergyAndForces", "CapturedTrainingStep", "create_model", "energy_and_forces", "force_loss", "training_step", "radius_graph",
            "sequential_insertion", "uniform_box"]

@@ -17,6 +17,9 @@ Architecture (reference ``mace_ictc/models/pure_cartesian_ictd_fix.py``; factory
     energy  += readout_t(h_{t+1})                                (:3095-3101)
   layer 0 has input degree 0 (paths (0,l,l)); the last product targets l = 0.
 
+Dense layers (radial MLP, channel linears, readouts) go through ``mace_hip.linear`` (one GEMM
+per layer and degree; weight gradients reduced in row blocks).
+
 Layouts.  Node features between blocks are the reference's flat mul_ir layout
 ``[N, C*(L+1)^2]`` (degree blocks ``[C, 2l+1]``), which the symmetric-contraction
 kernels read directly.  ``linear_up`` writes the channel-contiguous ir_mul layout the
@@ -42,6 +45,7 @@ from ictc_o3.backends.hip.harmonics import direction_harmonics_packed
 from ictc_o3.basis.ictd_irreps import EdgeWeightedPathPreservingTensorProduct
 from ictc_o3.ops.symmetric_contraction import ICTDPureUSymmetricContractionSO3
 
+from .linear import Linear, linear
 from .radial import bessel_embedding
 
 SILU_SCALE = 1.6791767923989418   # _Normalize2MomSiLU (pure_cartesian_ictd_fix.py:610-619)
@@ -76,8 +80,8 @@ class NormalizedSiLU(nn.Module):
         return F.silu(x) * SILU_SCALE
 
 
-def _mace_linear(fan_in: int, fan_out: int) -> nn.Linear:
-    lin = nn.Linear(fan_in, fan_out, bias=False)
+def _mace_linear(fan_in: int, fan_out: int) -> Linear:
+    lin = Linear(fan_in, fan_out)
     nn.init.normal_(lin.weight, mean=0.0, std=1.0 / math.sqrt(fan_in))
     return lin
 
@@ -93,7 +97,7 @@ class ChannelLinear(nn.Module):
     def to_ir_mul(self, x: torch.Tensor) -> torch.Tensor:
         """mul_ir [N, C(L+1)^2] -> ir_mul [N, sum_l (2l+1) C]: out[n, m, o] = sum_c W[o,c] x[n,c,m]."""
         blocks = split_mul_ir(x, self.channels, self.lmax)
-        return torch.cat([F.linear(degree_rows(blocks[l]), self.weights[l]).reshape(x.shape[0], -1)
+        return torch.cat([linear(degree_rows(blocks[l]), self.weights[l]).reshape(x.shape[0], -1)
                           for l in range(self.lmax + 1)], dim=-1)
 
 
@@ -121,7 +125,7 @@ class MessageLinear(nn.Module):
                 out.append(m.new_zeros(n, c * d))
                 continue
             blk = m[:, off:off + k * d * c].reshape(n, k, d, c).transpose(1, 2).reshape(n * d, k * c)
-            out.append(F.linear(blk, self.weights[l]).reshape(n, d, c).transpose(1, 2).reshape(n, c * d))
+            out.append(linear(blk, self.weights[l]).reshape(n, d, c).transpose(1, 2).reshape(n, c * d))
             off += k * d * c
         return torch.cat(out, dim=-1)
 
@@ -138,7 +142,7 @@ class SpeciesLinear(nn.Module):
     def forward(self, x: torch.Tensor, species: torch.Tensor) -> torch.Tensor:
         s, c = self.num_elements, self.channels
         # all species at once (one GEMM), then pick each node's own block
-        y = torch.matmul(x, self.weight.reshape(s * c, c).t()).reshape(-1, s, c)
+        y = linear(x, self.weight.reshape(s * c, c)).reshape(-1, s, c)
         return y.gather(1, species.view(-1, 1, 1).expand(-1, 1, c)).squeeze(1)
 
 
@@ -154,7 +158,7 @@ class IrrepsLinear(nn.Module):
         blocks = split_mul_ir(x, self.channels, self.lmax)
         scale = 1.0 / math.sqrt(self.channels)
         n = x.shape[0]
-        return merge_mul_ir({l: F.linear(degree_rows(b), self.weights[l] * scale)
+        return merge_mul_ir({l: linear(degree_rows(b), self.weights[l] * scale)
                              .reshape(n, 2 * l + 1, self.channels).transpose(1, 2) for l, b in blocks.items()})
 
 

@@ -6,6 +6,12 @@ num_interactions, correlation 1-3, atomic_numbers, cutoff, avg_num_neighbors) an
 when training, detached results otherwise, zero-edge graphs keep the coordinate
 dependency).  ``training_step`` is the pattern of ``examples/model.py:35-41``: energy and
 forces with ``training=True``, loss = mean((E/N)^2) + mean(F^2), backward, AdamW step.
+
+``CapturedEnergyAndForces`` / ``CapturedTrainingStep`` record one fixed-shape step into a
+HIP graph and replay it (the reference runs eager only: its graph capture is not qualified,
+``mace_ictc/ascend/runtime.py:28-29``).  Every operator of the step launches on the current
+stream, allocates through torch and performs no host synchronisation once its per-graph
+checks are cached, which the warmup calls do.
 """
 from __future__ import annotations
 
@@ -54,7 +60,9 @@ def energy_and_forces(model, positions, atomic_numbers, batch, edge_src, edge_ds
         pos = positions if positions.requires_grad else positions.detach().requires_grad_(True)
         atomic = model(pos, atomic_numbers, batch, edge_src, edge_dst, edge_shifts, cell, species=species)
         energy = atomic.new_zeros(cell.shape[0]).index_add(0, batch, atomic)
-        force = -torch.autograd.grad(energy.sum() + pos.sum() * 0.0, pos, create_graph=training,
+        # keep the coordinate dependency for zero-edge graphs (a 3-element sum: no multi-block
+        # reduction, so the step stays capturable into a HIP graph)
+        force = -torch.autograd.grad(energy.sum() + pos[:1].sum() * 0.0, pos, create_graph=training,
                                      retain_graph=training)[0]
     result = {"energy": energy, "forces": force, "atomic_energy": atomic}
     return result if training else {k: v.detach() for k, v in result.items()}
@@ -72,3 +80,83 @@ def training_step(model, optimizer, graph: dict, *, species=None):
     optimizer.step()
     optimizer.zero_grad(set_to_none=True)
     return loss.detach()
+
+
+def _warm_up(fn, calls: int, device) -> None:
+    """Run fn on a side stream (default priority) before capture, as graph capture requires."""
+    side = torch.cuda.Stream(device=device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(side):
+        for _ in range(calls):
+            fn()
+    torch.cuda.current_stream(device).wait_stream(side)
+    torch.cuda.synchronize(device)
+
+
+class CapturedEnergyAndForces:
+    """energy_and_forces of one fixed structure graph, captured once and replayed.
+
+    Atomic numbers, batch, edges and shifts are fixed at capture; each call copies new
+    positions (and optionally a new cell) into the captured input buffers and replays.
+    The returned tensors are the graph's own output buffers, overwritten by the next call
+    (clone them to keep them).  A different edge count needs a new capture."""
+
+    def __init__(self, model, positions, atomic_numbers, batch, edge_src, edge_dst, edge_shifts, cell, *,
+                 species=None, warmup: int = 3):
+        self.model = model
+        self._pos = positions.detach().clone()
+        self._cell = cell.detach().clone()
+        self._fixed = dict(atomic_numbers=atomic_numbers, batch=batch, edge_src=edge_src, edge_dst=edge_dst,
+                           edge_shifts=edge_shifts)
+        self._species = model.species_index(atomic_numbers) if species is None else species
+        dev = positions.device
+        _warm_up(self._step, warmup, dev)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self._out = self._step()
+
+    def _step(self):
+        return energy_and_forces(self.model, positions=self._pos, cell=self._cell, species=self._species,
+                                 **self._fixed)
+
+    def __call__(self, positions: torch.Tensor, cell=None) -> dict:
+        if positions.shape != self._pos.shape:
+            raise ValueError("positions must keep the captured shape")
+        self._pos.copy_(positions)
+        if cell is not None:
+            self._cell.copy_(cell)
+        self.graph.replay()
+        return self._out
+
+
+class CapturedTrainingStep:
+    """One force-loss training step (energy + forces with create_graph, loss backward, optimizer
+    step) captured once and replayed on new positions.  The optimizer must keep its state on
+    the device (``torch.optim.AdamW(..., capturable=True)``); gradients are released before
+    capture so that backward writes them into the graph's own buffers on every replay."""
+
+    def __init__(self, model, optimizer, graph: dict, *, species=None, warmup: int = 3):
+        if not all(group.get("capturable", False) for group in optimizer.param_groups):
+            raise ValueError("the optimizer must be created with capturable=True")
+        self.model, self.optimizer = model, optimizer
+        self._graph = {k: (v.detach().clone() if k in ("positions", "cell") else v) for k, v in graph.items()}
+        self._species = model.species_index(graph["atomic_numbers"]) if species is None else species
+        dev = self._graph["positions"].device
+        _warm_up(lambda: training_step(model, optimizer, self._graph, species=self._species), warmup, dev)
+        optimizer.zero_grad(set_to_none=True)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            prediction = energy_and_forces(model, **self._graph, training=True, species=self._species)
+            self._loss = force_loss(prediction, self._graph["positions"].shape[0])
+            self._loss.backward()
+            optimizer.step()
+
+    def __call__(self, positions: torch.Tensor, cell=None) -> torch.Tensor:
+        """Replays the step on these positions; returns the loss buffer (device, not synchronised)."""
+        if positions.shape != self._graph["positions"].shape:
+            raise ValueError("positions must keep the captured shape")
+        self._graph["positions"].copy_(positions)
+        if cell is not None:
+            self._graph["cell"].copy_(cell)
+        self.graph.replay()
+        return self._loss
