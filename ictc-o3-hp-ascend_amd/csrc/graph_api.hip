@@ -1,0 +1,56 @@
+// C ABI of the periodic radius-graph builder (graph_kernels.hpp).
+#include "graph_kernels.hpp"
+
+namespace ictc {
+namespace {
+
+constexpr int kMaxReach = 64;
+
+int grid_status(const ictc_cell_grid* g, const double* wpos, const int32_t* abin, const int64_t* bin_start,
+                const int64_t* bin_atoms, int64_t atoms) {
+  if (g == nullptr || atoms < 0) return ICTC_ERR_INVALID_ARGUMENT;
+  if (!(g->cutoff_sq > 0.0)) return ICTC_ERR_INVALID_ARGUMENT;
+  for (int a = 0; a < 3; ++a) {
+    if (g->bins[a] < 1 || g->reach[a] < 0 || g->reach[a] > kMaxReach) return ICTC_ERR_INVALID_ARGUMENT;
+    if (g->periodic[a] != 0 && g->periodic[a] != 1) return ICTC_ERR_INVALID_ARGUMENT;
+  }
+  const int64_t nbins = static_cast<int64_t>(g->bins[0]) * g->bins[1] * g->bins[2];
+  if (nbins > (int64_t{1} << 31)) return ICTC_ERR_INVALID_ARGUMENT;
+  if (atoms > 0 && (!wpos || !abin || !bin_start || !bin_atoms)) return ICTC_ERR_INVALID_ARGUMENT;
+  return ICTC_OK;
+}
+
+dim3 grid_blocks(int64_t atoms) { return dim3(static_cast<unsigned>((atoms + 255) / 256)); }
+
+}  // namespace
+}  // namespace ictc
+
+extern "C" {
+
+int ictc_hip_radius_graph_count(const ictc_cell_grid* grid, const double* wrapped_positions,
+                                const int32_t* atom_bins, const int64_t* bin_start, const int64_t* bin_atoms,
+                                int64_t atoms, int64_t* counts, hipStream_t stream) {
+  const int st = ictc::grid_status(grid, wrapped_positions, atom_bins, bin_start, bin_atoms, atoms);
+  if (st != ICTC_OK) return st;
+  if (atoms == 0) return ICTC_OK;
+  if (!counts) return ICTC_ERR_INVALID_ARGUMENT;
+  hipLaunchKernelGGL((ictc::radius_graph_kernel<false>), ictc::grid_blocks(atoms), dim3(256), 0, stream,
+                     wrapped_positions, atom_bins, bin_start, bin_atoms, atoms, *grid, counts, nullptr, nullptr,
+                     nullptr);
+  return hipGetLastError() == hipSuccess ? ICTC_OK : ICTC_ERR_LAUNCH;
+}
+
+int ictc_hip_radius_graph_fill(const ictc_cell_grid* grid, const double* wrapped_positions,
+                               const int32_t* atom_bins, const int64_t* bin_start, const int64_t* bin_atoms,
+                               int64_t atoms, const int64_t* rowptr, int64_t* src, int32_t* images,
+                               hipStream_t stream) {
+  const int st = ictc::grid_status(grid, wrapped_positions, atom_bins, bin_start, bin_atoms, atoms);
+  if (st != ICTC_OK) return st;
+  if (atoms == 0) return ICTC_OK;
+  if (!rowptr || !src || !images) return ICTC_ERR_INVALID_ARGUMENT;
+  hipLaunchKernelGGL((ictc::radius_graph_kernel<true>), ictc::grid_blocks(atoms), dim3(256), 0, stream,
+                     wrapped_positions, atom_bins, bin_start, bin_atoms, atoms, *grid, nullptr, rowptr, src, images);
+  return hipGetLastError() == hipSuccess ? ICTC_OK : ICTC_ERR_LAUNCH;
+}
+
+}  // extern "C"

@@ -8,7 +8,8 @@
 // first, as the reference's bond projection does (backends/ascend/tensor_product.py:30-55,
 // structured_product.py:7-22).
 //
-// Launch shape: one 256-thread workgroup per tile of kTileEdges instances.
+// Launch shape: one 256-thread workgroup per tile of kFwdTile (forward) or kBwdTile (VJP)
+// instances.
 //   1. the tile's harmonics are staged in LDS and the bond matrices M_p of all
 //      tile instances are built cooperatively into LDS (CG read from __constant__);
 //   2. each wave then owns whole instances: lane l covers channels
@@ -24,11 +25,15 @@
 
 namespace ictc {
 
-constexpr int kTileEdges = 8;
+// instances per workgroup: the forward runs one instance per wave (its next instance then
+// starts in a fresh wave instead of behind this wave's output stores), the VJP four per wave
+// (measured best on gfx950 at C128/lmax3)
+constexpr int kFwdTile = 4;
+constexpr int kBwdTile = 16;
 constexpr int kBlock = 256;
 constexpr int kWavesPerBlock = kBlock / kWave;
 
-template <int LIN, int LE, int LOUT>
+template <int LIN, int LE, int LOUT, int TILE>
 __device__ __forceinline__ void build_bond(const float (*sY)[Paths<LIN, LE, LOUT>::NY],
                                            float (*sM)[Paths<LIN, LE, LOUT>::NB > 0 ? Paths<LIN, LE, LOUT>::NB : 1],
                                            const ictc_tp_desc& d, int tid) {
@@ -40,7 +45,7 @@ __device__ __forceinline__ void build_bond(const float (*sY)[Paths<LIN, LE, LOUT
     constexpr int boff = PS::tab.bond[p];
     constexpr int cgo = CGTab<l1, l2, l3>::offset;
     const float s = d.scale[p];
-    for (int t = tid; t < kTileEdges * ni * no; t += kBlock) {
+    for (int t = tid; t < TILE * ni * no; t += kBlock) {
       const int e = t / (ni * no);
       const int r = t - e * (ni * no);  // M_p stored [k][i]: r = k*ni + i
       const int k = r / ni;
@@ -55,18 +60,18 @@ __device__ __forceinline__ void build_bond(const float (*sY)[Paths<LIN, LE, LOUT
 }
 
 // Stage the tile's harmonics in LDS and build the bond matrices of all tile instances.
-template <int LIN, int LE, int LOUT>
+template <int LIN, int LE, int LOUT, int TILE>
 __device__ __forceinline__ void stage_tile(const float* __restrict__ y, int64_t e0, int64_t rows,
                                            float (*sY)[Paths<LIN, LE, LOUT>::NY],
                                            float (*sM)[Paths<LIN, LE, LOUT>::NB > 0 ? Paths<LIN, LE, LOUT>::NB : 1],
                                            const ictc_tp_desc& d, int tid) {
   constexpr int NY = Paths<LIN, LE, LOUT>::NY;
-  for (int t = tid; t < kTileEdges * NY; t += kBlock) {
+  for (int t = tid; t < TILE * NY; t += kBlock) {
     const int e = t / NY;
     sY[e][t - e * NY] = (e0 + e < rows) ? y[(e0 + e) * NY + (t - e * NY)] : 0.f;
   }
   __syncthreads();
-  build_bond<LIN, LE, LOUT>(sY, sM, d, tid);
+  build_bond<LIN, LE, LOUT, TILE>(sY, sM, d, tid);
   __syncthreads();
 }
 
@@ -81,17 +86,17 @@ tp_forward_kernel(const float* __restrict__ x, const float* __restrict__ y,
   using PS = Paths<LIN, LE, LOUT>;
   constexpr int NX = PS::NX, NY = PS::NY, NP = PS::N, NOC = PS::NOC;
   constexpr int NBS = PS::NB > 0 ? PS::NB : 1;
-  __shared__ float sY[kTileEdges][NY];
-  __shared__ float sM[kTileEdges][NBS];
+  __shared__ float sY[kFwdTile][NY];
+  __shared__ float sM[kFwdTile][NBS];
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // wave-uniform (SGPR)
-  const int64_t e0 = static_cast<int64_t>(blockIdx.x) * kTileEdges;
-  stage_tile<LIN, LE, LOUT>(y, e0, rows, sY, sM, d, tid);
+  const int64_t e0 = static_cast<int64_t>(blockIdx.x) * kFwdTile;
+  stage_tile<LIN, LE, LOUT, kFwdTile>(y, e0, rows, sY, sM, d, tid);
 
   const int C = d.channels;
   const uint32_t row = static_cast<uint32_t>(C) * 4u;  // bytes of one component row
-  for (int le = wave; le < kTileEdges; le += kWavesPerBlock) {
+  for (int le = wave; le < kFwdTile; le += kWavesPerBlock) {
     const int64_t e = e0 + le;
     if (e >= rows) break;
     const rsrc_t rx = make_rsrc(x + e * NX * C, NX * row);
@@ -146,17 +151,17 @@ tp_backward_kernel(const float* __restrict__ x, const float* __restrict__ y,
   using PS = Paths<LIN, LE, LOUT>;
   constexpr int NX = PS::NX, NY = PS::NY, NP = PS::N, NOC = PS::NOC;
   constexpr int NBS = PS::NB > 0 ? PS::NB : 1;
-  __shared__ float sY[kTileEdges][NY];
-  __shared__ float sM[kTileEdges][NBS];
+  __shared__ float sY[kBwdTile][NY];
+  __shared__ float sM[kBwdTile][NBS];
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // wave-uniform (SGPR)
-  const int64_t e0 = static_cast<int64_t>(blockIdx.x) * kTileEdges;
-  stage_tile<LIN, LE, LOUT>(y, e0, rows, sY, sM, d, tid);
+  const int64_t e0 = static_cast<int64_t>(blockIdx.x) * kBwdTile;
+  stage_tile<LIN, LE, LOUT, kBwdTile>(y, e0, rows, sY, sM, d, tid);
 
   const int C = d.channels;
   const uint32_t row = static_cast<uint32_t>(C) * 4u;
-  for (int le = wave; le < kTileEdges; le += kWavesPerBlock) {
+  for (int le = wave; le < kBwdTile; le += kWavesPerBlock) {
     const int64_t e = e0 + le;
     if (e >= rows) break;
     const rsrc_t rx = make_rsrc(x ? x + e * NX * C : nullptr, NX * row);
@@ -259,7 +264,7 @@ inline int launch_status() { return hipGetLastError() == hipSuccess ? ICTC_OK : 
 template <int LIN, int LE, int LOUT>
 int launch_forward(const ictc_tp_desc& d, const float* x, const float* y, const float* g, float* out,
                    int64_t rows, hipStream_t stream) {
-  const dim3 grid(static_cast<unsigned>((rows + kTileEdges - 1) / kTileEdges));
+  const dim3 grid(static_cast<unsigned>((rows + kFwdTile - 1) / kFwdTile));
   if (d.channels % (2 * kWave) == 0)
     hipLaunchKernelGGL((tp_forward_kernel<LIN, LE, LOUT, 2>), grid, dim3(kBlock), 0, stream, x, y, g,
                        out, d, rows);
@@ -272,7 +277,7 @@ int launch_forward(const ictc_tp_desc& d, const float* x, const float* y, const 
 template <int LIN, int LE, int LOUT>
 int launch_backward(const ictc_tp_desc& d, const float* x, const float* y, const float* g,
                     const float* go, float* dx, float* dy, float* dg, int64_t rows, hipStream_t stream) {
-  const dim3 grid(static_cast<unsigned>((rows + kTileEdges - 1) / kTileEdges));
+  const dim3 grid(static_cast<unsigned>((rows + kBwdTile - 1) / kBwdTile));
   if (d.channels % (2 * kWave) == 0)
     hipLaunchKernelGGL((tp_backward_kernel<LIN, LE, LOUT, 2>), grid, dim3(kBlock), 0, stream, x, y, g,
                        go, dx, dy, dg, d, rows);

@@ -15,7 +15,7 @@ import torch  # noqa: F401  (must precede CDLL, see module docstring)
 
 MAX_PATHS = 64
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libictc_hip.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 
 class TpDesc(ctypes.Structure):
@@ -30,6 +30,17 @@ class TpDesc(ctypes.Structure):
         ("gate_index", ctypes.c_int32 * MAX_PATHS),
         ("out_offset", ctypes.c_int32 * MAX_PATHS),
         ("scale", ctypes.c_float * MAX_PATHS),
+    ]
+
+
+class CellGrid(ctypes.Structure):
+    """Mirror of ``ictc_cell_grid``."""
+    _fields_ = [
+        ("cell", ctypes.c_double * 9),
+        ("cutoff_sq", ctypes.c_double),
+        ("bins", ctypes.c_int32 * 3),
+        ("reach", ctypes.c_int32 * 3),
+        ("periodic", ctypes.c_int32 * 3),
     ]
 
 
@@ -62,6 +73,9 @@ _SIGNATURES = {
     "ictc_hip_message_edge_grad": (ctypes.c_int, [ctypes.POINTER(TpDesc), _P, _P, _P, _P, _P, _P, _P,
                                                   _P, _P, _P, _I64, _I64, _I64, _P]),
     "ictc_hip_message_node_grad": (ctypes.c_int, [ctypes.POINTER(TpDesc), _P, _P, _P, _P, _I64, _I64, _P]),
+    "ictc_hip_radius_graph_count": (ctypes.c_int, [ctypes.POINTER(CellGrid), _P, _P, _P, _P, _I64, _P, _P]),
+    "ictc_hip_radius_graph_fill": (ctypes.c_int, [ctypes.POINTER(CellGrid), _P, _P, _P, _P, _I64, _P, _P, _P,
+                                                  _P]),
 }
 
 _lock = threading.Lock()

@@ -272,6 +272,40 @@ int ictc_hip_direction_harmonics(int lmax, int mode, const float* directions, co
                                  const float* t, const float* s, float* out, int64_t rows,
                                  hipStream_t stream);
 
+/*
+ * Periodic radius graph (cell list).  Replaces the neighbour-list builder of reference
+ * mace_ictc/utils/graph_utils.py:217-297 (radius_graph_pbc_gpu, one torch_cluster radius
+ * query per lattice image) with an exact search over binned atoms.
+ *   grid: lattice (rows of cell[9] are the lattice vectors a, b, c), cutoff^2, bins per
+ *         axis, bin offsets searched per axis ("reach", <= 64), periodic flags (0/1);
+ *   wrapped_positions [atoms,3] float64: positions wrapped into the cell along periodic
+ *         axes (cartesian); atom_bins [atoms,3] int32: each atom's bin coordinates;
+ *   bin_start [bins+1] int64 and bin_atoms [atoms] int64: atoms grouped by bin
+ *         (bin index (bx * bins[1] + by) * bins[2] + bz).
+ * count: counts[j] = number of (i, t) with |w_j - w_i + t @ cell| < cutoff, (i,t) != (j,0).
+ * fill:  for receiver j, writes its neighbours at rows rowptr[j] .. rowptr[j+1]-1 (rowptr is
+ *        the exclusive scan of counts, rowptr[atoms] = edges): src[e] = i and
+ *        images[e,0:3] = t (integer lattice image in wrapped coordinates), in a fixed order.
+ * The caller converts t to the shift of the unwrapped positions and orders the rows.
+ */
+typedef struct ictc_cell_grid {
+    double cell[9];
+    double cutoff_sq;
+    int32_t bins[3];
+    int32_t reach[3];
+    int32_t periodic[3];
+} ictc_cell_grid;
+
+int ictc_hip_radius_graph_count(const ictc_cell_grid* grid, const double* wrapped_positions,
+                                const int32_t* atom_bins, const int64_t* bin_start,
+                                const int64_t* bin_atoms, int64_t atoms, int64_t* counts,
+                                hipStream_t stream);
+
+int ictc_hip_radius_graph_fill(const ictc_cell_grid* grid, const double* wrapped_positions,
+                               const int32_t* atom_bins, const int64_t* bin_start,
+                               const int64_t* bin_atoms, int64_t atoms, const int64_t* rowptr,
+                               int64_t* src, int32_t* images, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

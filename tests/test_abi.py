@@ -83,3 +83,30 @@ def test_python_guards_reject_cpu_tensors():
     from ictc_o3 import EdgeTensorProduct
     with pytest.raises(ValueError):
         EdgeTensorProduct.create(channels=8, device="cpu")
+
+
+def test_radius_graph_validation_rejects_before_launch():
+    from ictc_o3 import _lib
+    lib = _lib.lib()
+    fake = ctypes.c_void_p(16)  # never dereferenced: every call below fails validation or launches nothing
+    grid = _lib.CellGrid()
+    for i in range(3):
+        grid.cell[4 * i] = 10.0
+        grid.bins[i], grid.reach[i], grid.periodic[i] = 2, 1, 1
+    grid.cutoff_sq = 9.0
+    count = lib.ictc_hip_radius_graph_count
+    assert count(None, fake, fake, fake, fake, 4, fake, None) == 1
+    assert count(ctypes.byref(grid), None, fake, fake, fake, 4, fake, None) == 1
+    assert count(ctypes.byref(grid), fake, fake, fake, fake, -1, fake, None) == 1
+    assert count(ctypes.byref(grid), None, None, None, None, 0, None, None) == 0
+    bad = _lib.CellGrid.from_buffer_copy(grid)
+    bad.bins[1] = 0
+    assert count(ctypes.byref(bad), fake, fake, fake, fake, 4, fake, None) == 1
+    bad = _lib.CellGrid.from_buffer_copy(grid)
+    bad.reach[2] = 65
+    assert count(ctypes.byref(bad), fake, fake, fake, fake, 4, fake, None) == 1
+    bad = _lib.CellGrid.from_buffer_copy(grid)
+    bad.cutoff_sq = 0.0
+    assert count(ctypes.byref(bad), fake, fake, fake, fake, 4, fake, None) == 1
+    fill = lib.ictc_hip_radius_graph_fill
+    assert fill(ctypes.byref(grid), fake, fake, fake, fake, 4, None, fake, fake, None) == 1
