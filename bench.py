@@ -24,14 +24,17 @@ Also reported on the same JSON line:
     - cfg 4, MACE-style energy + forces (C=128, lmax 3, 2 interactions, correlation 3,
       2,048 atoms at 0.1 A^-3 with 1.5 A minimum separation, r_c 5 A, 10 species):
       inference and one force-loss training step (AdamW), atom-steps/s, reference timing
-      protocol (>= 2 s and 3 warmup calls, median of 5 synchronised calls).
+      protocol (>= 2 s and 3 warmup calls, median of 5 synchronised calls), run eager (as
+      the reference does) and as HIP-graph replays of the captured steps;
+    - the HIP periodic radius graph build for the cfg-2 and cfg-4 structures (outside every
+      timed hot-path region).
 
 ``--kernels-only`` runs a 1 GiB device-to-device copy (the counter calibration
 reference) and three launches of each TP kernel at the benchmark sizes, for
 rocprofv3 --pmc passes.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--kernels-only]
-                      [--only tp|message|sc|mace]
+                      [--only tp|message|sc|mace|graph]
 """
 from __future__ import annotations
 
@@ -234,11 +237,11 @@ MSG_C, MSG_L, MSG_P, MSG_ATOMS = 64, 2, 11, 16384
 def _message_inputs(device):
     """cfg 2 structure, features, harmonics and radial-MLP gates (all resident on the GPU)."""
     from mace_hip.radial import bessel_embedding
-    from mace_hip.structures import radius_graph, uniform_box
+    from mace_hip import radius_graph_pbc_gpu, uniform_box
     st = uniform_box(MSG_ATOMS, 0.1, seed=4)
     pos, cell = st.positions.to(device), st.cell.to(device)
-    src, dst, shifts = radius_graph(pos, cell, 5.0)
-    vec = pos[dst] - pos[src] + shifts @ cell
+    src, dst, shifts = radius_graph_pbc_gpu(pos, 5.0, cell)
+    vec = pos[dst] - pos[src] + shifts.to(pos.dtype) @ cell
     r = vec.norm(dim=1)
     from ictc_o3.backends.hip.harmonics import direction_harmonics_packed
     y = direction_harmonics_packed((vec / r[:, None]).contiguous(), MSG_L).contiguous()
@@ -332,10 +335,14 @@ MACE_ATOMS, MACE_ZS, MACE_CPU_ATOMS = 2048, tuple(range(1, 11)), 128
 
 
 def _mace_graph(device, atoms=MACE_ATOMS):
-    from mace_hip import radius_graph, sequential_insertion
+    from mace_hip import radius_graph, radius_graph_pbc_gpu, sequential_insertion
     st = sequential_insertion(atoms, 0.1, min_separation=1.5, num_species=10, seed=4)
     pos, cell = st.positions.to(device), st.cell.to(device)
-    src, dst, shifts = radius_graph(pos, cell, 5.0)
+    if pos.device.type == "cuda":
+        src, dst, shifts = radius_graph_pbc_gpu(pos, 5.0, cell)
+        shifts = shifts.to(pos.dtype)
+    else:                                  # the CPU-oracle sample builds its graph on the host
+        src, dst, shifts = radius_graph(pos, cell, 5.0)
     return st, dict(positions=pos, atomic_numbers=torch.tensor(MACE_ZS, device=device)[st.species.to(device)],
                     batch=torch.zeros(atoms, dtype=torch.int64, device=device), edge_src=src, edge_dst=dst,
                     edge_shifts=shifts, cell=cell[None])
@@ -376,6 +383,21 @@ def _bench_mace(device):
             "training": leg(train_ms, 3.81e3, "eager"),
             "inference_hip_graph": leg(infer_graph_ms, 11.0e3, "HIP graph replay"),
             "training_hip_graph": leg(train_graph_ms, 3.81e3, "HIP graph replay")}
+
+
+def _bench_graph(device):
+    """Periodic radius graph on HIP (cell list) for the cfg-2 and cfg-4 structures: median of
+    synchronised calls (the builder returns edge counts to the host, so calls are synchronous)."""
+    from mace_hip import radius_graph_pbc_gpu, sequential_insertion, uniform_box
+    out = {}
+    for name, st in (("cfg2_16384_atoms", uniform_box(MSG_ATOMS, 0.1, seed=4)),
+                     ("cfg4_2048_atoms", sequential_insertion(MACE_ATOMS, 0.1, min_separation=1.5, num_species=10,
+                                                              seed=4))):
+        pos, cell = st.positions.to(device), st.cell.to(device)
+        edges = radius_graph_pbc_gpu(pos, 5.0, cell)[0].numel()
+        ms = _median_call_ms(lambda: radius_graph_pbc_gpu(pos, 5.0, cell), device, warmup_s=0.5)
+        out[name] = {"atoms": pos.shape[0], "edges": edges, "median_ms": ms, "edges_per_s": edges / (ms * 1e-3)}
+    return out
 
 
 def _cpu_time(fn, budget_s: float):
@@ -455,7 +477,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--kernels-only", action="store_true")
-    ap.add_argument("--only", choices=("tp", "message", "sc", "mace"), default=None,
+    ap.add_argument("--only", choices=("tp", "message", "sc", "mace", "graph"), default=None,
                     help="run one section and print its JSON (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -469,8 +491,8 @@ def main() -> int:
     if args.kernels_only:
         _kernels_only(op.plan, device)
         return 0
-    if args.only in ("message", "sc", "mace"):
-        fn = {"message": _bench_message, "sc": _bench_sc, "mace": _bench_mace}[args.only]
+    if args.only in ("message", "sc", "mace", "graph"):
+        fn = {"message": _bench_message, "sc": _bench_sc, "mace": _bench_mace, "graph": _bench_graph}[args.only]
         print(json.dumps({args.only: fn(device)}), flush=True)
         return 0
     elapsed, vjp_ms, fwd_ms = _time_gpu(args, op.plan, device)
@@ -482,7 +504,7 @@ def main() -> int:
     others = {}
     if args.only is None:
         others = {"message_cfg2": _bench_message(device), "sc_cfg3": _bench_sc(device),
-                  "mace_cfg4": _bench_mace(device)}
+                  "mace_cfg4": _bench_mace(device), "radius_graph": _bench_graph(device)}
         if not args.no_cpu:
             others["message_cfg2"]["cpu_baseline"] = _cpu_message()
             others["sc_cfg3"]["cpu_baseline"] = _cpu_sc()
