@@ -204,6 +204,19 @@ __device__ __forceinline__ void buf_store_lane(rsrc_t r, bool live, uint32_t off
   buf_store<1>(r, live ? off : 0xFFFFFFF0u, Vec<1>{{v}});
 }
 
+// Workgroups are dispatched to the GPU's XCDs (each with its own L2) round-robin by block
+// index.  xcd_block(b, n) renumbers the n blocks of a launch so that each XCD receives one
+// contiguous range of work items (XCD x gets items [start(x), start(x) + count(x))), which
+// keeps neighbouring items -- e.g. receivers of a spatially ordered graph, whose source rows
+// overlap -- in the same L2.  A bijection on [0, n).
+constexpr int kXcds = 8;
+
+__device__ __forceinline__ uint32_t xcd_block(uint32_t b, uint32_t n) {
+  const uint32_t q = n / kXcds, r = n % kXcds;
+  const uint32_t x = b % kXcds, i = b / kXcds;
+  return x * q + (x < r ? x : r) + i;
+}
+
 // Sum over the 64 lanes of a wave; every lane receives the total.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

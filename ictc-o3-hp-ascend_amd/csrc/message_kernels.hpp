@@ -168,8 +168,9 @@ msg_forward_kernel(const float* __restrict__ x, const float* __restrict__ bonds,
   __shared__ float sR[kMsgWaves - 1][R][kWave];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const int64_t node = static_cast<int64_t>(blockIdx.x) / nchunks;
-  const int chunk = static_cast<int>(blockIdx.x - node * nchunks);
+  const uint32_t item = xcd_block(blockIdx.x, gridDim.x);   // receivers contiguous per XCD
+  const int64_t node = static_cast<int64_t>(item) / nchunks;
+  const int chunk = static_cast<int>(item - node * nchunks);
   const int C = d.channels;
   const int c = chunk * kWave + lane;
   const uint32_t row = static_cast<uint32_t>(C) * 4u;
@@ -264,9 +265,11 @@ msg_edge_grad_kernel(const float* __restrict__ x, const float* __restrict__ bond
   __shared__ float sO[NOC * kWave];   // the node's dout chunk, shared by the block's waves
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  // one block per (node, chunk); its waves take every kMsgWaves-th edge of the node
-  const int64_t node = static_cast<int64_t>(blockIdx.x) / nchunks;
-  const int chunk = static_cast<int>(blockIdx.x - node * nchunks);
+  // one block per (node, chunk); its waves take every kMsgWaves-th edge of the node;
+  // receivers contiguous per XCD
+  const uint32_t item = xcd_block(blockIdx.x, gridDim.x);
+  const int64_t node = static_cast<int64_t>(item) / nchunks;
+  const int chunk = static_cast<int>(item - node * nchunks);
   const int C = d.channels;
   const int c = chunk * kWave + lane;
   const uint32_t row = static_cast<uint32_t>(C) * 4u;
@@ -393,7 +396,8 @@ msg_node_grad_kernel(const float* __restrict__ dxe, const int64_t* __restrict__ 
                      int nchunks) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const int64_t item = static_cast<int64_t>(blockIdx.x) * kMsgWaves + wave;
+  // source nodes contiguous per XCD
+  const int64_t item = static_cast<int64_t>(xcd_block(blockIdx.x, gridDim.x)) * kMsgWaves + wave;
   const int64_t node = item / nchunks;
   if (node >= nodes_src) return;
   const int chunk = static_cast<int>(item - node * nchunks);
