@@ -16,6 +16,11 @@ order).  The chains are evaluated in two shared stages:
   is 13 couplings instead of 69.  The accumulators of one mid are live together, split
   into batches of at most QMAX floats (register bound).
 
+The float forward is emitted as straight-line code (fewest instructions: no loop-carried copies,
+every CG literal folded into its FMA); the dual-number forward, the VJP and the weight features run
+the steps as switch cases of a non-unrolled loop (bounded registers; their straight-line forms
+spill).
+
 The VJP runs the same schedule backwards per batch: accumulate Q, couple's adjoint to x_lc
 (reading Q), Q := the coupling's adjoint to the prefix, then per group the prefix adjoint
 G = sum_p w_p sign_p Q_p (plus order-2 members) and its adjoint to x.  The weight
@@ -331,6 +336,15 @@ def emit(lmax: int, target: int, corr: int) -> str:
         bsteps.append(b_ + prefix_adjoint(key))
         asteps.append(ad)
 
+    def straight(steps, decl):
+        # the steps one after another in their own scopes (no loop, nothing laundered)
+        out = [f"  {decl}"]
+        for k, body in enumerate(steps):
+            out.append(f"  {{  // step {k}")
+            out.extend(body)
+            out.append("  }")
+        return [ln.replace("* Cs]", "* C]") for ln in out]
+
     def loop(steps, decl, with_u=False):
         # C, the input copy and (when used) the cotangent copy are re-laundered every
         # iteration, so that weight addresses and products of x or u with constants are
@@ -354,7 +368,10 @@ def emit(lmax: int, target: int, corr: int) -> str:
     if fsteps:
         copy = f"V xl[{D}];\n  for (int i = 0; i < {D}; ++i) xl[i] = x[i];\n  "
         zq = f"V Q[{qn}];\n  for (int i = 0; i < {qn}; ++i) Q[i] = 0.0f;\n  "
-        fw += loop(fsteps, copy + zq + f"V P[{maxq}];")
+        # float forward: straight-line (no loop-carried copies, constants folded into the FMAs;
+        # more registers, fewer instructions); dual-number forward (the JVP): the step loop
+        fw += ["  if constexpr (__is_same(V, float)) {"] + straight(fsteps, copy + zq + f"V P[{maxq}];")
+        fw += ["  } else {"] + loop(fsteps, copy + zq + f"V P[{maxq}];") + ["  }"]
         bw += loop(bsteps, copy + zq + f"V P[{maxq}], G[{maxq}];", with_u=True)
         aw += loop(asteps, copy + f"V Q[{qn}];\n  V P[{maxq}];", with_u=True)
     off_lines = ", ".join(str(offsets[(lo, o)]) for lo in range(target + 1) for o in range(corr, 0, -1))
@@ -399,12 +416,14 @@ def weight_columns(lmax: int, target: int, corr: int) -> int:
 
 
 def flop_counts(lmax: int, target: int, corr: int) -> Dict[str, int]:
-    """Floating-point operations per (node, channel) of the emitted forward and VJP, counted
-    on the emitted code: an fma counts 2, a multiply or an add 1."""
+    """Floating-point operations per (node, channel) of the emitted float forward and VJP,
+    counted on the emitted code: an fma counts 2, a multiply or an add 1."""
     import re
     text = emit(lmax, target, corr)
-    bodies = {"forward": text[text.index("void forward"):text.index("void vjp")],
-              "vjp": text[text.index("void vjp"):text.index("void weight_features")]}
+    forward = text[text.index("void forward"):text.index("void vjp")]
+    if "  } else {" in forward:          # float instantiation: the straight-line branch only
+        forward = forward[:forward.index("  } else {")]
+    bodies = {"forward": forward, "vjp": text[text.index("void vjp"):text.index("void weight_features")]}
     return {k: 2 * b.count("sfma(") + len(re.findall(r" [*+] ", b)) for k, b in bodies.items()}
 
 

@@ -89,16 +89,15 @@ def radius_graph_pbc_gpu(pos: torch.Tensor, r: float, cell: torch.Tensor, max_nu
     span = torch.where(periodic, torch.ones(3, dtype=torch.float64, device=dev),
                        (fw.max(0).values - lo).clamp_min(1e-12))
     span_host = span.cpu().tolist()
-    bins, reach = [], []
+    extents = [span_host[a] * heights[a] for a in range(3)]   # perpendicular extent of the binned region
+    bins = [int(min(MAX_BINS_PER_AXIS, max(1, math.floor(e / r)))) for e in extents]
+    while bins[0] * bins[1] * bins[2] > max(64, 8 * n):          # sparse systems: coarser bins
+        a = max(range(3), key=lambda i: bins[i])
+        bins[a] = max(1, bins[a] // 2)
+    reach = []
     for a in range(3):
-        extent = span_host[a] * heights[a]               # perpendicular extent of the binned region
-        b = int(min(MAX_BINS_PER_AXIS, max(1, math.floor(extent / r))))
-        width = extent / b
-        k = max(1, math.ceil(r / width))
-        if not flags[a]:
-            k = min(k, b - 1)
-        bins.append(b)
-        reach.append(k)
+        k = max(1, math.ceil(r / (extents[a] / bins[a])))         # bins of width extent / bins
+        reach.append(min(k, bins[a] - 1) if not flags[a] else k)
     bins_t = torch.tensor(bins, dtype=torch.float64, device=dev)
     abin = torch.floor((fw - lo) / span * bins_t).clamp(min=0)
     abin = torch.minimum(abin, bins_t - 1).to(torch.int32).contiguous()

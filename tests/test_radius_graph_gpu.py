@@ -98,6 +98,16 @@ def test_empty_single_atom_and_float32(gpu):
     _check(gpu, pos32, cell, 3.5)
 
 
+def test_sparse_system_in_a_large_cell(gpu):
+    """Few atoms in a large cell: the bin grid is coarsened (bounded by the atom count) and the
+    result is still exact."""
+    cell = torch.tensor([[400.0, 0.0, 0.0], [0.0, 300.0, 0.0], [20.0, 0.0, 350.0]], dtype=torch.float64)
+    g = torch.Generator().manual_seed(9)
+    centers = torch.rand(6, 3, generator=g, dtype=torch.float64) @ cell
+    pos = (centers[:, None, :] + 3.0 * torch.randn(6, 7, 3, generator=g, dtype=torch.float64)).reshape(-1, 3)
+    _check(gpu, pos, cell, 5.0)
+
+
 def test_saturation_flag(gpu):
     from mace_hip import radius_graph_pbc_gpu
     cell = torch.eye(3, dtype=torch.float64) * 8.0

@@ -4,7 +4,8 @@ csrc/gen_sc.py emits straight-line C++ (one Plan<L, T, K> per configuration) tha
 kernels instantiate.  Here that exact text is translated statement by statement into
 numpy (float64, vectorised over channels) and run:
 
-* forward(x, w)        == sum_p W_p U_p[x, x, x]           (dense oracle U per (l_out, order))
+* forward(x, w)        == sum_p W_p U_p[x, x, x]           (dense U per (l_out, order); both the
+                                                            straight-line float branch and the step loop)
 * vjp(x, w, u)         == d/dx <u, forward(x)>             (autograd through the dense form)
 * weight_features(x,u) == <u, U_p[x, x, x]> per column p
 
@@ -65,7 +66,27 @@ def _translate(lines):
     return out
 
 
-def _functions(text):
+def _branch(body, which):
+    """Keep one branch of an emitted ``if constexpr (__is_same(V, float)) { ... } else { ... }``:
+    "float" (the straight-line code) or "generic" (the step loop)."""
+    out, mode = [], None
+    for line in body:
+        st = line.strip()
+        if st == "if constexpr (__is_same(V, float)) {":
+            mode = "float"
+            continue
+        if mode == "float" and line == "  } else {":
+            mode = "generic"
+            continue
+        if mode == "generic" and line == "  }":
+            mode = None
+            continue
+        if mode is None or mode == which:
+            out.append(line)
+    return out
+
+
+def _functions(text, which="float"):
     """{name: python source} for forward / vjp / weight_features of one emitted plan."""
     segs = text.split("  template <typename V>\n")[1:]
     funcs = {}
@@ -74,7 +95,7 @@ def _functions(text):
         body = seg[seg.index("{\n") + 2:].split("\n")
         while body and body[-1].strip() in ("", "};", "}}  // namespace ictc::sc") or body[-1].startswith("}"):
             body.pop()
-        body = [b for b in body if not b.startswith("  // ")]
+        body = [b for b in _branch(body, which) if not b.startswith("  // ")]
         funcs[name] = "\n".join(_translate(body))
     return funcs
 
@@ -112,7 +133,8 @@ def _dense(lmax, target, corr, x, w):
 @pytest.mark.parametrize("lmax,target,corr", [(3, 1, 3), (3, 3, 3), (3, 0, 3), (2, 2, 3), (3, 2, 2),
                                               (1, 1, 3), (2, 0, 2), (0, 0, 3)])
 def test_generated_plan_matches_dense_u(lmax, target, corr):
-    funcs = _functions(gen_sc.emit(lmax, target, corr))
+    text = gen_sc.emit(lmax, target, corr)
+    funcs = _functions(text)
     d, no = (lmax + 1) ** 2, (target + 1) ** 2
     ktot = gen_sc.weight_columns(lmax, target, corr)
     chans = 5
@@ -127,10 +149,11 @@ def test_generated_plan_matches_dense_u(lmax, target, corr):
     dxe = torch.autograd.grad((dense * u).sum(), xt)[0]
     scale_f, scale_b = dense.abs().max().item(), dxe.abs().max().item()
 
-    o = [np.zeros(chans) for _ in range(no)]
-    _run(funcs["forward"], x=xs, w=ws, C=chans, o=o)
-    err = np.abs(np.stack(o, 1) - dense.detach().numpy()).max() / scale_f
-    assert err < TOL, f"forward relative error {err:.3e}"
+    for which, fn in (("float", funcs["forward"]), ("generic", _functions(text, "generic")["forward"])):
+        o = [np.zeros(chans) for _ in range(no)]
+        _run(fn, x=xs, w=ws, C=chans, o=o)
+        err = np.abs(np.stack(o, 1) - dense.detach().numpy()).max() / scale_f
+        assert err < TOL, f"forward ({which} branch) relative error {err:.3e}"
 
     dx = [np.zeros(chans) for _ in range(d)]
     _run(funcs["vjp"], x=xs, w=ws, C=chans, u=us, dx=dx)
