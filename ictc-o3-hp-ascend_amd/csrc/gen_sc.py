@@ -18,8 +18,8 @@ order).  The chains are evaluated in two shared stages:
 
 The float forward is emitted as straight-line code (fewest instructions: no loop-carried copies,
 every CG literal folded into its FMA); the dual-number forward, the VJP and the weight features run
-the steps as switch cases of a non-unrolled loop (bounded registers; their straight-line forms
-spill).
+one switch case per accumulator batch inside a non-unrolled loop (straight-line within a batch,
+registers bounded by the batch; their fully straight-line forms spill).
 
 The VJP runs the same schedule backwards per batch: accumulate Q, couple's adjoint to x_lc
 (reading Q), Q := the coupling's adjoint to the prefix, then per group the prefix adjoint
@@ -261,7 +261,9 @@ def emit(lmax: int, target: int, corr: int) -> str:
         return lines
 
     fsteps, bsteps, asteps = [], [], []
+    fgroups, bgroups, agroups = [], [], []     # steps per batch: one loop case per batch
     for batch in batches:
+        nf0, nb0, na0 = len(fsteps), len(bsteps), len(asteps)
         offs = dict(batch["triples"])
         # forward / VJP phase A: accumulate the weighted prefixes of each triple
         for key in batch["groups"]:
@@ -305,6 +307,8 @@ def emit(lmax: int, target: int, corr: int) -> str:
             if n == len(batch["groups"]) - 1:
                 b_ += [f"    Q[{i}] = 0.0f;" for i in range(qn)]
             bsteps.append(b_)
+        fgroups.append(len(fsteps) - nf0)
+        bgroups.append(len(bsteps) - nb0)
         # weight features: Q := prefix adjoints of the triples, then one dot per chain
         for t, off in batch["triples"]:
             asteps.append([f"    // coupling adjoint ({t[0]},{t[1]})->{t[2]}"] + dual_coupling(t, off))
@@ -320,7 +324,11 @@ def emit(lmax: int, target: int, corr: int) -> str:
                 dot = " + ".join(f"{U(lo, m)} * P[{m}]" for m in range(2 * lo + 1))
                 ad.append(f"    phi[{p} * Cs] = {sign}.0f * part({dot});")
             asteps.append(ad)
+        agroups.append(len(asteps) - na0)
     for key in o2_only:
+        fgroups.append(1)
+        bgroups.append(1)
+        agroups.append(1)
         g = groups[key]
         nq = 2 * key[2] + 1
         f, ad = prefix(key), prefix(key)
@@ -344,6 +352,18 @@ def emit(lmax: int, target: int, corr: int) -> str:
             out.extend(body)
             out.append("  }")
         return [ln.replace("* Cs]", "* C]") for ln in out]
+
+    def merged(steps, sizes):
+        """Concatenate consecutive steps into one step per group (sizes sum to len(steps))."""
+        out, k = [], 0
+        for n in sizes:
+            body = []
+            for st in steps[k:k + n]:
+                body += ["    {"] + st + ["    }"]
+            out.append(body)
+            k += n
+        assert k == len(steps)
+        return out
 
     def loop(steps, decl, with_u=False):
         # C, the input copy and (when used) the cotangent copy are re-laundered every
@@ -371,9 +391,9 @@ def emit(lmax: int, target: int, corr: int) -> str:
         # float forward: straight-line (no loop-carried copies, constants folded into the FMAs;
         # more registers, fewer instructions); dual-number forward (the JVP): the step loop
         fw += ["  if constexpr (__is_same(V, float)) {"] + straight(fsteps, copy + zq + f"V P[{maxq}];")
-        fw += ["  } else {"] + loop(fsteps, copy + zq + f"V P[{maxq}];") + ["  }"]
-        bw += loop(bsteps, copy + zq + f"V P[{maxq}], G[{maxq}];", with_u=True)
-        aw += loop(asteps, copy + f"V Q[{qn}];\n  V P[{maxq}];", with_u=True)
+        fw += ["  } else {"] + loop(merged(fsteps, fgroups), copy + zq + f"V P[{maxq}];") + ["  }"]
+        bw += loop(merged(bsteps, bgroups), copy + zq + f"V P[{maxq}], G[{maxq}];", with_u=True)
+        aw += loop(merged(asteps, agroups), copy + f"V Q[{qn}];\n  V P[{maxq}];", with_u=True)
     off_lines = ", ".join(str(offsets[(lo, o)]) for lo in range(target + 1) for o in range(corr, 0, -1))
     return "\n".join([
         f"// Generated by csrc/gen_sc.py for lmax={lmax}, target_lmax={target}, correlation={corr}.",
@@ -424,7 +444,9 @@ def flop_counts(lmax: int, target: int, corr: int) -> Dict[str, int]:
     if "  } else {" in forward:          # float instantiation: the straight-line branch only
         forward = forward[:forward.index("  } else {")]
     bodies = {"forward": forward, "vjp": text[text.index("void vjp"):text.index("void weight_features")]}
-    return {k: 2 * b.count("sfma(") + len(re.findall(r" [*+] ", b)) for k, b in bodies.items()}
+    # an sfma whose accumulator is the literal 0 is a multiply (1 FLOP)
+    return {k: 2 * b.count("sfma(") - len(re.findall(r"sfma\([^()]*, 0\.0f\)", b)) + len(re.findall(r" [*+] ", b))
+            for k, b in bodies.items()}
 
 
 def configs():
