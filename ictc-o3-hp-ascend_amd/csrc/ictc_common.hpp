@@ -224,4 +224,40 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// Sums over the 64 lanes of N values per lane at once (N <= 16), by a transposing butterfly:
+// at each of the first log2(P) exchange distances (32, 16, ...) a lane keeps one half of its
+// values and receives its partner's sums of that half, then plain butterflies finish; P - 1 +
+// 6 - log2(P) exchanges instead of 6 N (P = N rounded up to a power of two).  Returns the total
+// of value index j = (lane >> (6 - log2 P)) & (P - 1) (0 for j >= N); the lanes with
+// lane & ((64 >> log2 P) - 1) == 0 hold each index exactly once.
+template <int N>
+struct WaveSums {
+  static constexpr int P = N <= 1 ? 1 : N <= 2 ? 2 : N <= 4 ? 4 : N <= 8 ? 8 : 16;
+  static constexpr int LOGP = P == 1 ? 0 : P == 2 ? 1 : P == 4 ? 2 : P == 8 ? 3 : 4;
+  static constexpr int SHIFT = 6 - LOGP;
+  static_assert(N >= 1 && N <= 16, "WaveSums: 1 <= N <= 16");
+  __device__ static __forceinline__ int index(int lane) { return (lane >> SHIFT) & (P - 1); }
+  __device__ static __forceinline__ bool owner(int lane) { return (lane & ((1 << SHIFT) - 1)) == 0; }
+  __device__ static __forceinline__ float reduce(const float (&v)[N], int lane) {
+    float t[P];
+#pragma unroll
+    for (int i = 0; i < P; ++i) t[i] = i < N ? v[i] : 0.f;
+    static_for<0, LOGP>([&](auto S) {
+      constexpr int half = P >> (S + 1);
+      constexpr int dist = 32 >> S;
+      const bool upper = (lane & dist) != 0;
+#pragma unroll
+      for (int i = 0; i < half; ++i) {
+        const float send = upper ? t[i] : t[i + half];
+        const float keep = upper ? t[i + half] : t[i];
+        t[i] = keep + __shfl_xor(send, dist, kWave);
+      }
+    });
+    float r = t[0];
+#pragma unroll
+    for (int off = 32 >> LOGP; off > 0; off >>= 1) r += __shfl_xor(r, off, kWave);
+    return r;
+  }
+};
+
 }  // namespace ictc

@@ -364,14 +364,11 @@ msg_edge_grad_kernel(const float* __restrict__ x, const float* __restrict__ bond
 #pragma unroll
       for (int m = 0; m < NX; ++m) buf_store_lane(rde, live, c * 4u + m * row, dxl[m]);
     }
-    if (XDEP && dyp != nullptr) {
-      float mine = 0.f;
-#pragma unroll
-      for (int j = 0; j < NY; ++j) {
-        const float tot = wave_sum(dyl[j]);
-        if (lane == j) mine = tot;
-      }
-      if (lane < NY) dyp[(e * nchunks + chunk) * NY + lane] = mine;
+    if (XDEP && dyp != nullptr) {   // channel sums of the NY partials, one transposing butterfly
+      using WS = WaveSums<NY>;
+      const float tot = WS::reduce(dyl, lane);
+      const int j = WS::index(lane);
+      if (WS::owner(lane) && j < NY) dyp[(e * nchunks + chunk) * NY + j] = tot;
     }
   };
 

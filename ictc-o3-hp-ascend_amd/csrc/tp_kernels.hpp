@@ -242,14 +242,12 @@ tp_backward_kernel(const float* __restrict__ x, const float* __restrict__ y,
 #pragma unroll
       for (int m = 0; m < NX; ++m) buf_store<NV>(rdx, vo + m * row, dxr[m]);
     }
-    float mine = 0.f;
-#pragma unroll
-    for (int j = 0; j < NY; ++j) {
-      const float tot = wave_sum(dyl[j]);
-      if (lane == j) mine = tot;
-    }
+    // channel sums of the NY partials, one transposing butterfly
+    using WS = WaveSums<NY>;
+    const float tot = WS::reduce(dyl, lane);
+    const int j = WS::index(lane);
     const rsrc_t rdy = make_rsrc(dy ? dy + e * NY : nullptr, NY * 4u);
-    if (lane < NY) buf_store<1, 0>(rdy, static_cast<uint32_t>(lane) * 4u, Vec<1>{{mine}});
+    if (WS::owner(lane) && j < NY) buf_store<1, 0>(rdy, static_cast<uint32_t>(j) * 4u, Vec<1>{{tot}});
   }
 }
 
