@@ -8,7 +8,7 @@ prefixes (see ictc_o3/basis/symmetric_u.py).  Gradients:
 * node features: the ``ictc_hip_sc_backward`` kernel;
 * weights: the map is linear in W, so dW[s] is the sum over the nodes of species s
   of the per-node chain features <u, chain_p(x)> (``ictc_hip_sc_weight_features``),
-  reduced by species with a deterministic index_add.
+  reduced by species as one GEMM with the species one-hot matrix.
 
 The backward is itself a differentiable Function (second derivatives, as force
 training needs).  With cotangents (a, B) of (dx, dW):
@@ -60,8 +60,11 @@ def _vjp_raw(plan: ContractionPlan, x, species, w, go):
 
 
 def _species_sum(plan: ContractionPlan, species, phi):
-    return torch.zeros(plan.num_elements, plan.ktot, plan.channels, device=phi.device,
-                       dtype=torch.float32).index_add(0, species, phi)
+    """sum of phi [N, KTOT, C] over the nodes of each species -> [S, KTOT, C], as one GEMM with the
+    species one-hot matrix (a few species rows: atomic adds into them would all contend)."""
+    n = phi.shape[0]
+    onehot = torch.nn.functional.one_hot(species, plan.num_elements).to(torch.float32)
+    return torch.mm(onehot.t(), phi.reshape(n, -1)).reshape(plan.num_elements, plan.ktot, plan.channels)
 
 
 def _weight_grad(plan: ContractionPlan, x, species, go):

@@ -180,6 +180,15 @@ class Interaction(nn.Module):
         self.message_linear = MessageLinear(self.tp.path_counts_by_l, channels, edge_lmax)
         self.self_connection = SpeciesLinear(num_elements, channels)
 
+    def radial_mlp(self, edge_feats):
+        """self.fc on the edge features with each normalised SiLU's constant folded into the next
+        layer's (64 x 64 or 64 x P*C) weight instead of scaling the [E, 64] activations."""
+        layers = [m for m in self.fc if isinstance(m, nn.Linear)]
+        h = layers[0](edge_feats)
+        for lin in layers[1:]:
+            h = linear(F.silu(h), lin.weight * SILU_SCALE)
+        return h
+
     def forward(self, h, harmonics, edge_feats, src, dst, mask, species):
         """mask: the reference multiplies the gates by (r <= r_max) (:1801-1808).  The radial
         features carry the cutoff envelope, exactly 0 from r_max on, and fc has no biases, so
@@ -187,7 +196,7 @@ class Interaction(nn.Module):
         is skipped (mask is accepted for the signature)."""
         n = h.shape[0]
         x1 = self.linear_up.to_ir_mul(h)
-        gates = self.tp.effective_gates(self.fc(edge_feats), edge_feats.shape[0])
+        gates = self.tp.effective_gates(self.radial_mlp(edge_feats), edge_feats.shape[0])
         plan = self.tp.hip_plan(self.input_lmax, self.edge_lmax)
         m = graph_message(plan, x1, harmonics, gates, src, dst, nodes_dst=n)
         message = self.message_linear(m) / max(self.avg_num_neighbors, 1e-8)
@@ -252,7 +261,8 @@ class MaceICTC(nn.Module):
         """Atomic energies [N] (reference forward :2879-3106, baseline route)."""
         # shift_e @ cell_e as three multiply-adds per edge (not a batched GEMM of 3 x 3 matrices)
         shift_vecs = (edge_shifts.to(pos.dtype).unsqueeze(-1) * cell[batch[edge_src]].to(pos.dtype)).sum(1)
-        vec = pos[edge_dst] - pos[edge_src] + shift_vecs
+        # index_select: its backward is a direct index_add (advanced indexing would scatter through a sort)
+        vec = pos.index_select(0, edge_dst) - pos.index_select(0, edge_src) + shift_vecs
         length = vec.norm(dim=1)
         directions = vec / length.clamp(min=1e-8).unsqueeze(-1)
         mask = (length <= self.cutoff).to(pos.dtype)
