@@ -138,6 +138,41 @@ def _copy_gbs(device, nbytes: int = 1 << 30, reps: int = 5) -> float:
     return 2 * nbytes * reps / (s.elapsed_time(e) * 1e-3) / 1e9
 
 
+def _stream_mix_gbs(device, reads: int, writes: int, total_bytes: int, reps: int = 5):
+    """Best bandwidth of an ideal grid-stride float4 streaming kernel (csrc/stream_probe.hip)
+    moving total_bytes in the given read:write mix; None if the probe library is absent."""
+    import ctypes
+    path = os.path.join(ROOT, "ictc-o3-hp-ascend_amd", "ictc_o3", "lib", "libictc_stream_probe.so")
+    if not os.path.exists(path):
+        return None
+    lib = ctypes.CDLL(path)
+    lib.ictc_probe_stream_mix.restype = ctypes.c_int
+    lib.ictc_probe_stream_mix.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+                                          ctypes.c_size_t, ctypes.c_int, ctypes.c_void_p]
+    units = total_bytes // (16 * (reads + writes))
+    a = torch.ones(reads * units * 4, device=device)
+    b = torch.empty(writes * units * 4, device=device)
+    stream = torch.cuda.current_stream(device)
+    best = 0.0
+    for grid in (8192, 65536, min((units + 255) // 256, 2 ** 31 - 1)):
+        def launch():
+            if lib.ictc_probe_stream_mix(reads, writes, a.data_ptr(), b.data_ptr(), units, grid,
+                                         ctypes.c_void_p(stream.cuda_stream)) != 0:
+                raise RuntimeError("stream probe launch failed")
+        for _ in range(2):
+            launch()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record(stream)
+        for _ in range(reps):
+            launch()
+        e.record(stream)
+        torch.cuda.synchronize(device)
+        best = max(best, 16 * (reads + writes) * units * reps / (s.elapsed_time(e) * 1e-3) / 1e9)
+    del a, b
+    torch.cuda.empty_cache()
+    return best
+
+
 def _kernels_only(plan, device) -> None:
     from ictc_o3.backends.hip.tensor_product import _backward_raw, _forward_raw
     src = torch.ones((1 << 30) // 4, device=device)
@@ -497,6 +532,8 @@ def main() -> int:
         return 0
     elapsed, vjp_ms, fwd_ms = _time_gpu(args, op.plan, device)
     copy_gbs = _copy_gbs(device)
+    mix_vjp = _stream_mix_gbs(device, 7, 2, BYTES_VJP * ROWS_VJP)
+    mix_fwd = _stream_mix_gbs(device, 2, 5, BYTES_FWD * ROWS_FWD)
     value = ROWS_VJP * args.steps / elapsed
     achieved = BYTES_VJP * ROWS_VJP / (vjp_ms * 1e-3) / 1e9
     fwd_achieved = BYTES_FWD * ROWS_FWD / (fwd_ms * 1e-3) / 1e9
@@ -525,6 +562,13 @@ def main() -> int:
         "cpu_baseline": cpu,
         "extra": {"copy_gbs_measured": copy_gbs,
                   "vjp_frac_of_copy": achieved / copy_gbs,
+                  "stream_mix_reference": {
+                      "what": "ideal grid-stride float4 streaming kernel moving the same bytes per launch in "
+                              "a matching read:write mix (7:2 for the VJP's 3.53:1, 2:5 for the forward's "
+                              "0.395:1), best of three grid sizes",
+                      "vjp_mix_gbs": mix_vjp, "fwd_mix_gbs": mix_fwd,
+                      "vjp_frac_of_mix": achieved / mix_vjp if mix_vjp else None,
+                      "fwd_frac_of_mix": fwd_achieved / mix_fwd if mix_fwd else None},
                   "step_hbm_gbs": (BYTES_FWD + BYTES_VJP) * value / 1e9,
                   "step_hbm_frac": (BYTES_FWD + BYTES_VJP) * value / 1e9 / HBM_PEAK_GBS,
                   "forward_only": {"instances": ROWS_FWD, "instances_per_s": ROWS_FWD / (fwd_ms * 1e-3),

@@ -6,7 +6,9 @@ Steps:
      kind) with the explicit template instantiation, plus ``tp_instances.def``
      listing the compiled combinations for the dispatch tables;
   3. compile every TU to an object in parallel, largest first;
-  4. link the objects and the API TUs into ``ictc_o3/lib/libictc_hip.so``.
+  4. link the objects and the API TUs into ``ictc_o3/lib/libictc_hip.so``;
+  5. build ``ictc_o3/lib/libictc_stream_probe.so`` from ``stream_probe.hip`` (bench.py's
+     streaming-bandwidth reference; not part of the operator library).
 
 Every HIP TU is compiled with ``-Xclang -target-feature -Xclang -packed-fp32-ops``
 (no packed FP32 VALU instructions are generated).
@@ -33,6 +35,7 @@ GEN = os.path.join(HERE, "generated")
 OBJ = os.path.join(HERE, "_build")
 LIB_DIR = os.path.join(PKG, "ictc_o3", "lib")
 LIB = os.path.join(LIB_DIR, "libictc_hip.so")
+PROBE_LIB = os.path.join(LIB_DIR, "libictc_stream_probe.so")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
@@ -159,6 +162,11 @@ def build(jobs: int | None = None, verbose: bool = True) -> str:
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
     os.replace(tmp, LIB)
+    res = subprocess.run([HIPCC, *FLAGS, "-shared", os.path.join(HERE, "stream_probe.hip"), "-o", PROBE_LIB + ".tmp"],
+                         capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"stream probe build failed:\n{res.stderr}")
+    os.replace(PROBE_LIB + ".tmp", PROBE_LIB)
     if verbose:
         print(f"built {LIB} ({len(combos)} degree combinations, {len(units)} units, "
               f"{time.time() - t0:.0f}s)", flush=True)

@@ -30,6 +30,13 @@ namespace ictc {
 // (measured best on gfx950 at C128/lmax3)
 constexpr int kFwdTile = 4;
 constexpr int kBwdTile = 16;
+// The VJP requests the gate and dout rows of path p + kBwdPrefetch before it computes path p.
+// Without that, each path's loads were issued behind the previous path's dg store and waited
+// for together with it (gfx9's vmcnt counts loads and stores in one in-order counter, and the
+// compiler cannot move a buffer load above a possibly aliasing buffer store), so every path
+// paid a full memory round trip.  Measured at C128/lmax3: 2.45 -> 2.26 ms (distance 1:
+// 2.29 ms, 3 and 4: no further gain).
+constexpr int kBwdPrefetch = 2;
 constexpr int kBlock = 256;
 constexpr int kWavesPerBlock = kBlock / kWave;
 
@@ -140,6 +147,8 @@ tp_forward_kernel(const float* __restrict__ x, const float* __restrict__ y,
 //   dY[l2,j]  += s_p * sum_{i,k} Chat_p[i,j,k] * sum_c x_i go_k  (structured_product.py:61-72
 //                                                              composed with the bond adjoint)
 // The dY channel sum is a per-lane partial followed by one wave reduction per instance.
+// The path loop is software-pipelined: the gate and dout rows of path p + kBwdPrefetch are
+// requested before path p is computed and its dg stored.
 // Outputs whose pointer is null get an empty buffer descriptor: their stores are
 // dropped by the hardware range check, so the instance body has no branches.
 template <int LIN, int LE, int LOUT, int NV>
@@ -183,15 +192,28 @@ tp_backward_kernel(const float* __restrict__ x, const float* __restrict__ y,
 #pragma unroll
         for (int v = 0; v < NV; ++v) dxr[m].v[v] = 0.f;
       }
+      constexpr int D = kBwdPrefetch;
+      Vec<NV> pre_g[D];                    // rows of the next D paths, in flight
+      Vec<NV> pre_o[D][2 * LOUT + 1];
+      auto request = [&](auto Q) {
+        constexpr int q = Q;
+        if constexpr (q < NP) {
+          constexpr int nq = 2 * PS::tab.l3[q] + 1, oq = PS::tab.out[q];
+          pre_g[q % D] = buf_load<NV>(rg, vo + q * row);
+          static_for<0, nq>([&](auto K) { pre_o[q % D][K] = buf_load<NV>(rgo, vo + (oq + K) * row); });
+        }
+      };
+      static_for<0, D>(request);
       static_for<0, NP>([&](auto P) {
         constexpr int p = P;
         constexpr int l1 = PS::tab.l1[p], l2 = PS::tab.l2[p], l3 = PS::tab.l3[p];
         constexpr int ni = 2 * l1 + 1, nj = 2 * l2 + 1, no = 2 * l3 + 1;
-        constexpr int boff = PS::tab.bond[p], oo = PS::tab.out[p];
+        constexpr int boff = PS::tab.bond[p];
         using CG = CGTab<l1, l2, l3>;
-        const Vec<NV> gv = buf_load<NV>(rg, vo + p * row);
+        const Vec<NV> gv = pre_g[p % D];
         Vec<NV> o[no];
-        static_for<0, no>([&](auto K) { o[K] = buf_load<NV>(rgo, vo + (oo + K) * row); });
+        static_for<0, no>([&](auto K) { o[K] = pre_o[p % D][K]; });
+        request(Int<p + D>{});             // issued ahead of this path's dg store
         Vec<NV> dgv;
 #pragma unroll
         for (int v = 0; v < NV; ++v) dgv.v[v] = 0.f;
