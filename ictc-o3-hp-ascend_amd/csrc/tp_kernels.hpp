@@ -25,17 +25,17 @@
 
 namespace ictc {
 
-// instances per workgroup: the forward runs one instance per wave (its next instance then
-// starts in a fresh wave instead of behind this wave's output stores), the VJP four per wave
-// (measured best on gfx950 at C128/lmax3)
+// instances per workgroup: one instance per wave in both kernels (a wave's next instance then
+// starts in a fresh wave instead of behind this wave's output stores; measured best on gfx950
+// at C128/lmax3: VJP 2.16 ms at 4 per workgroup, 2.18 at 8, 2.26 at 16, 2.28 at 32)
 constexpr int kFwdTile = 4;
-constexpr int kBwdTile = 16;
+constexpr int kBwdTile = 4;
 // The VJP requests the gate and dout rows of path p + kBwdPrefetch before it computes path p.
 // Without that, each path's loads were issued behind the previous path's dg store and waited
 // for together with it (gfx9's vmcnt counts loads and stores in one in-order counter, and the
 // compiler cannot move a buffer load above a possibly aliasing buffer store), so every path
-// paid a full memory round trip.  Measured at C128/lmax3: 2.45 -> 2.26 ms (distance 1:
-// 2.29 ms, 3 and 4: no further gain).
+// paid a full memory round trip.  Measured at C128/lmax3 (16 instances per workgroup):
+// 2.45 -> 2.26 ms (distance 1: 2.29 ms, 3 and 4: no further gain).
 constexpr int kBwdPrefetch = 2;
 constexpr int kBlock = 256;
 constexpr int kWavesPerBlock = kBlock / kWave;
