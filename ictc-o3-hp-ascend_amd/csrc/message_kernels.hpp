@@ -373,14 +373,46 @@ msg_edge_grad_kernel(const float* __restrict__ x, const float* __restrict__ bond
   };
 
   const int64_t s0 = rowptr[node], s1 = rowptr[node + 1];
-#pragma clang loop unroll(disable)
-  for (int64_t slot = s0 + wave; slot < s1; slot += kMsgWaves) {
+  if constexpr (XDEP) {
+    // The dg pass stores NP rows per edge; the next edge's loads are requested before them, so
+    // waiting for those loads does not also wait for this edge's stores (one in-order vmcnt).
+    // Measured 4-7 % faster at lmax 2 and 3; the dxe pass (NX stores after the path loop)
+    // gained nothing consistent and stays unpipelined (fewer VGPRs).
+    int64_t slot = s0 + wave;
+    if (slot >= s1) return;
     float xr[NX], gv[NP];
     int64_t e;
     BondStage<NB> bs;
     fetch(slot, e, xr, gv, bs);
-    bond_commit<NB>(bs, &sB[wave][0][0], lane);
-    compute(e, xr, gv, &sB[wave][0][0]);
+#pragma clang loop unroll(disable)
+    for (;;) {
+      const int64_t nslot = slot + kMsgWaves;
+      const bool more = nslot < s1;
+      float xn[NX], gn[NP];
+      int64_t en = e;
+      BondStage<NB> bn;
+      if (more) fetch(nslot, en, xn, gn, bn);
+      bond_commit<NB>(bs, &sB[wave][0][0], lane);
+      compute(e, xr, gv, &sB[wave][0][0]);
+      if (!more) break;
+#pragma unroll
+      for (int m = 0; m < NX; ++m) xr[m] = xn[m];
+#pragma unroll
+      for (int p = 0; p < NP; ++p) gv[p] = gn[p];
+      bs = bn;
+      e = en;
+      slot = nslot;
+    }
+  } else {
+#pragma clang loop unroll(disable)
+    for (int64_t slot = s0 + wave; slot < s1; slot += kMsgWaves) {
+      float xr[NX], gv[NP];
+      int64_t e;
+      BondStage<NB> bs;
+      fetch(slot, e, xr, gv, bs);
+      bond_commit<NB>(bs, &sB[wave][0][0], lane);
+      compute(e, xr, gv, &sB[wave][0][0]);
+    }
   }
 }
 
