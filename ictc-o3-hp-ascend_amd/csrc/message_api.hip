@@ -55,7 +55,7 @@ inline bool fits_u32(int64_t rows, int64_t width_floats) {
 inline int msg_index(const ictc_tp_desc* d) { return d->input_lmax * 16 + d->edge_lmax * 4 + d->output_lmax; }
 
 // floats per edge of the bond row: sum over the paths of (2 l1 + 1)(2 l3 + 1)
-inline int bond_width(const ictc_tp_desc* d) {
+inline int bond_row_floats(const ictc_tp_desc* d) {
   int nb = 0;
   for (int a = 0; a <= d->input_lmax; ++a)
     for (int b = 0; b <= d->edge_lmax; ++b)
@@ -65,6 +65,12 @@ inline int bond_width(const ictc_tp_desc* d) {
         nb += (2 * a + 1) * (2 * c + 1);
       }
   return nb;
+}
+
+// width of the caller's bond buffer: 0 when the kernels build the rows from the harmonics
+inline int bond_width(const ictc_tp_desc* d) {
+  const int nb = bond_row_floats(d), ny = (d->edge_lmax + 1) * (d->edge_lmax + 1);
+  return bond_inline(nb, ny) ? 0 : nb;
 }
 
 inline int msg_common(const ictc_tp_desc* d, int64_t nodes_src, int64_t nodes_dst, int64_t edges) {

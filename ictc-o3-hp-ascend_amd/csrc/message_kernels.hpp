@@ -10,7 +10,8 @@
 //   * msg_bond_kernel: per-edge bond matrices M_p[e][k][i] = s_p sum_j Y[e,j] C_p[i,j,k]
 //     for every path (the reference's Y @ P bond projection, backends/ascend/
 //     tensor_product.py:9-57 and structured_product.py:7-22), computed once per edge and
-//     shared by every kernel below and by every channel chunk;
+//     shared by every kernel below and by every channel chunk (for small degree sets the
+//     kernels below build each row themselves from the harmonics instead: bond_inline);
 //   * msg_forward_kernel (receiver CSR): one block per (node, 64-channel chunk); its waves
 //     split the node's edges and accumulate in registers, then sum their partials in a
 //     fixed order through LDS; per edge, the x[src] row, the gates and the bond row are
@@ -139,6 +140,108 @@ __device__ __forceinline__ void bond_fetch(const float* __restrict__ bonds, int6
   for (int r = 0; r < BondStage<NB>::NV; ++r) s.v[r] = buf_load<1>(rb, (lane + r * kWave) * 4u).v[0];
 }
 
+// In-kernel bond rows.  When a lane's share of the bond row (BondStage::NV entries) times the
+// NY harmonics fits in 32 registers, the kernels form each edge's bond row themselves from its
+// harmonics row, with the products and the accumulation order of msg_bond_kernel (so the rows
+// are bit-identical), and no bond buffer exists: the caller passes the harmonics where the
+// bond rows would go (ictc_hip_message_bond_width reports 0).  This saves the bond kernel and
+// the bond-row traffic (115 floats per edge at lmax 2 against 9 harmonics).
+constexpr bool bond_inline(int nb, int ny) { return nb > 0 && ((nb + kWave - 1) / kWave) * ny <= 32; }
+
+template <int LIN, int LE, int LOUT>
+struct BondInline {
+  static constexpr bool value = bond_inline(Paths<LIN, LE, LOUT>::NB, Paths<LIN, LE, LOUT>::NY);
+};
+
+// Dense per-entry view of the projection for the in-kernel rows: cg[idx][j] = C_p[i, j - l2^2, k]
+// on the entry's l2 block (0 elsewhere) and the entry's path, for every entry slot a wave's
+// lanes own (slots past NB are all zero), so each lane loads its coefficients without branches.
+template <int LIN, int LE, int LOUT>
+struct BondDense {
+  static constexpr int NB = Paths<LIN, LE, LOUT>::NB, NY = Paths<LIN, LE, LOUT>::NY;
+  static constexpr int NS = BondStage<NB>::NV * kWave;
+  float cg[NS][NY];
+  uint8_t path[NS];
+};
+
+template <int LIN, int LE, int LOUT, int P = 0>
+constexpr void fill_bond_dense(BondDense<LIN, LE, LOUT>& t) {
+  if constexpr (P < Paths<LIN, LE, LOUT>::N) {
+    constexpr PathTable tab = Paths<LIN, LE, LOUT>::tab;
+    constexpr int l1 = tab.l1[P], l2 = tab.l2[P], l3 = tab.l3[P];
+    constexpr int ni = 2 * l1 + 1, nj = 2 * l2 + 1, no = 2 * l3 + 1;
+    using CG = CGTab<l1, l2, l3>;
+    for (int q = 0; q < ni * no; ++q) {
+      const int k = q / ni, i = q - k * ni, idx = tab.bond[P] + q;
+      t.path[idx] = static_cast<uint8_t>(P);
+      for (int jj = 0; jj < nj; ++jj) t.cg[idx][l2 * l2 + jj] = CG::v[(i * nj + jj) * no + k];
+    }
+    fill_bond_dense<LIN, LE, LOUT, P + 1>(t);
+  }
+}
+
+template <int LIN, int LE, int LOUT>
+constexpr BondDense<LIN, LE, LOUT> make_bond_dense() {
+  BondDense<LIN, LE, LOUT> t{};
+  fill_bond_dense<LIN, LE, LOUT>(t);
+  return t;
+}
+
+template <int LIN, int LE, int LOUT>
+__constant__ BondDense<LIN, LE, LOUT> kBondDense = make_bond_dense<LIN, LE, LOUT>();
+
+// Per-lane projection coefficients of the lane's bond entries (the columns of Y @ P that the
+// lane owns): c[r][j] = s_p C_p[i, j - l2^2, k] for entry lane + 64 r on its l2 block, +0
+// elsewhere -- the values msg_bond_kernel puts in its LDS projection table.
+template <int LIN, int LE, int LOUT, bool INLINE = BondInline<LIN, LE, LOUT>::value>
+struct BondCoef {
+  __device__ void init(const ictc_tp_desc&, int) {}
+};
+
+template <int LIN, int LE, int LOUT>
+struct BondCoef<LIN, LE, LOUT, true> {
+  static constexpr int NB = Paths<LIN, LE, LOUT>::NB, NY = Paths<LIN, LE, LOUT>::NY;
+  static constexpr int NV = BondStage<NB>::NV;
+  float c[NV][NY];
+  __device__ __forceinline__ void init(const ictc_tp_desc& d, int lane) {
+    const BondDense<LIN, LE, LOUT>& t = kBondDense<LIN, LE, LOUT>;
+    // unconditional loads (issued together); off-block entries are stored zeros, and the path
+    // scales are positive, so they stay +0 like the bond kernel's literal zeros
+#pragma unroll
+    for (int r = 0; r < NV; ++r) {
+      const int idx = lane + r * kWave;
+      const float sc = d.scale[t.path[idx]];
+#pragma unroll
+      for (int j = 0; j < NY; ++j) c[r][j] = t.cg[idx][j] * sc;
+    }
+  }
+};
+
+// Bond row of edge e into the wave's staging registers: fetched from the bond buffer, or
+// formed from the harmonics row (one load, the NY values broadcast from lanes 0..NY-1).
+template <int LIN, int LE, int LOUT>
+__device__ __forceinline__ void bond_row(const float* __restrict__ bonds_or_y, int64_t e, int lane,
+                                         const BondCoef<LIN, LE, LOUT>& bc,
+                                         BondStage<Paths<LIN, LE, LOUT>::NB>& s) {
+  constexpr int NB = Paths<LIN, LE, LOUT>::NB, NY = Paths<LIN, LE, LOUT>::NY;
+  if constexpr (BondInline<LIN, LE, LOUT>::value) {
+    const float yl = bonds_or_y[e * NY + (lane < NY ? lane : NY - 1)];
+    float yv[NY];
+#pragma unroll
+    for (int j = 0; j < NY; ++j)
+      yv[j] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, yl), j));
+#pragma unroll
+    for (int r = 0; r < BondStage<NB>::NV; ++r) {
+      float acc = 0.f;
+#pragma unroll
+      for (int j = 0; j < NY; ++j) acc = fmaf(yv[j], bc.c[r][j], acc);
+      s.v[r] = acc;
+    }
+  } else {
+    bond_fetch<NB>(bonds_or_y, e, lane, s);
+  }
+}
+
 template <int NB>
 __device__ __forceinline__ void bond_commit(const BondStage<NB>& s, float* __restrict__ row, int lane) {
 #pragma unroll
@@ -182,11 +285,13 @@ msg_forward_kernel(const float* __restrict__ x, const float* __restrict__ bonds,
   // lanes past C read channel 0 (discarded): every access stays inside its row, so the
   // uniform row offsets can ride in soffset
   const uint32_t vc = static_cast<uint32_t>(live ? c : 0) * 4u;
+  BondCoef<LIN, LE, LOUT> bc;
+  bc.init(d, lane);
   // bond row first: staging it into LDS then waits for those loads only, while the x and
   // gate loads issued after it are still in flight
   auto fetch = [&](int64_t slot, float* xo, float* gvo, BondStage<NB>& bo) {
     const int64_t e = perm ? perm[slot] : slot;
-    bond_fetch<NB>(bonds, e, lane, bo);
+    bond_row<LIN, LE, LOUT>(bonds, e, lane, bc, bo);
     const uint32_t xoff = static_cast<uint32_t>(src[e]) * NX * row + vc;   // range-checked gather
 #pragma unroll
     for (int m = 0; m < NX; ++m) xo[m] = buf_load_vs(rx, xoff, m * row);
@@ -287,10 +392,12 @@ msg_edge_grad_kernel(const float* __restrict__ x, const float* __restrict__ bond
   __syncthreads();
   const float* __restrict__ o = sO + lane;   // o[r * kWave]: this lane's channel of dout row r
 
+  BondCoef<LIN, LE, LOUT> bc;
+  bc.init(d, lane);
   auto fetch = [&](int64_t slot, int64_t& eo, float* xo, float* gvo, BondStage<NB>& bo) {
     const int64_t e = perm ? perm[slot] : slot;
     eo = e;
-    bond_fetch<NB>(bonds, e, lane, bo);   // first, as in the forward
+    bond_row<LIN, LE, LOUT>(bonds, e, lane, bc, bo);   // first, as in the forward
     const uint32_t xoff = static_cast<uint32_t>(src[e]) * NX * row + vc;   // range-checked gather
     if constexpr (XDEP) {
 #pragma unroll
@@ -475,7 +582,7 @@ inline dim3 msg_grid(int64_t nodes, int nchunks) {
 template <int LIN, int LE, int LOUT>
 int launch_msg_bonds(const ictc_tp_desc& d, const float* y, float* bonds, int64_t edges, hipStream_t stream) {
   constexpr int NB = Paths<LIN, LE, LOUT>::NB;
-  if (NB == 0 || edges == 0) return ICTC_OK;
+  if (NB == 0 || edges == 0 || BondInline<LIN, LE, LOUT>::value) return ICTC_OK;   // rows built in-kernel
   hipLaunchKernelGGL((msg_bond_kernel<LIN, LE, LOUT>),
                      dim3(static_cast<unsigned>((edges + kBondEdges - 1) / kBondEdges)), dim3(256), 0, stream, y,
                      bonds, d, edges);

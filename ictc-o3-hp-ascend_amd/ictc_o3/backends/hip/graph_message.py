@@ -90,9 +90,12 @@ def bond_width(plan: TensorProductPlan) -> int:
 
 
 def _bonds(plan: TensorProductPlan, graph: MessageGraph, y) -> Optional[torch.Tensor]:
-    """Per-edge bond matrices [E, NB] of harmonics y (None for an empty graph)."""
+    """Per-edge bond matrices [E, NB] of harmonics y (None for an empty graph).  For degree
+    sets whose kernels build the bond rows themselves (bond width 0) this is y itself."""
     if graph.edges == 0:
         return None
+    if bond_width(plan) == 0:
+        return y
     out = torch.empty(graph.edges, bond_width(plan), device=y.device, dtype=torch.float32)
     _lib.check(_lib.lib().ictc_hip_message_bonds(
         ctypes.byref(plan.desc), y.data_ptr(), out.data_ptr(), graph.edges, _lib.stream_of(y.device)),

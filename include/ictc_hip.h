@@ -116,6 +116,10 @@ int ictc_hip_tp_backward(const ictc_tp_desc* desc,
  *   bonds[e][bond_p + k*(2 l1 + 1) + i] = scale_p * sum_j harmonics[e][l2^2 + j] C_p[i, j, k]
  * (the reference's bond projection Y @ P: backends/ascend/tensor_product.py:9-57,
  * structured_product.py:7-22).  The same buffer serves the forward and both VJP kernels.
+ * For small degree sets (at most 32 projection coefficients per lane, e.g. lmax 2 or an
+ * input lmax of 0) the kernels form the bond rows from the harmonics themselves:
+ * ictc_hip_message_bond_width then returns 0, ictc_hip_message_bonds does nothing, and the
+ * caller passes the harmonics [edges, (L_e+1)^2] as the `bonds` argument.
  *
  * Edges are visited through a CSR over the receivers: dst_rowptr [nodes_dst+1] and
  * dst_perm [edges] (CSR slot -> edge id; null when edges are already sorted by dst).
