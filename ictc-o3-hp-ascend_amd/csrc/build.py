@@ -60,7 +60,13 @@ INSTANCE_KINDS = {
             "int64_t, int64_t, hipStream_t);\n"
             "template int launch_msg_edge_grad<{a}, {b}, {c}>(const ictc_tp_desc&, const float*, "
             "const float*, const float*, const float*, const int64_t*, const int64_t*, const int64_t*, "
-            "float*, float*, float*, int64_t, int64_t, hipStream_t);"),
+            "float*, float*, float*, int64_t, int64_t, hipStream_t);\n"
+            "template int launch_msg_forward_tangent<{a}, {b}, {c}>(const ictc_tp_desc&, const float*, "
+            "const float*, const float*, const MsgTangent&, const int64_t*, const int64_t*, const int64_t*, "
+            "float*, int64_t, int64_t, hipStream_t);\n"
+            "template int launch_msg_edge_grad_tangent<{a}, {b}, {c}>(const ictc_tp_desc&, const float*, "
+            "const float*, const float*, const MsgTangent&, const float*, const int64_t*, const int64_t*, "
+            "const int64_t*, float*, float*, float*, int64_t, int64_t, hipStream_t);"),
 }
 
 
@@ -89,7 +95,7 @@ def _cost(a: int, b: int, c: int, kind: str) -> int:
     """Rough compile cost (path-set size) to start the biggest TUs first."""
     n = sum((2 * i + 1) * (2 * j + 1) * (2 * k + 1) for i in range(a + 1) for j in range(b + 1)
             for k in range(c + 1) if abs(i - j) <= k <= i + j and (i + j + k) % 2 == 0)
-    return n * {"fwd": 1, "bwd": 4, "msg": 3}[kind]
+    return n * {"fwd": 1, "bwd": 4, "msg": 6}[kind]
 
 
 def _write_if_changed(path: str, text: str) -> None:

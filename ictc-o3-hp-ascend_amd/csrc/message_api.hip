@@ -15,7 +15,14 @@ namespace ictc {
   extern template int launch_msg_edge_grad<A, B, C>(const ictc_tp_desc&, const float*, const float*, \
                                                     const float*, const float*, const int64_t*,     \
                                                     const int64_t*, const int64_t*, float*, float*,  \
-                                                    float*, int64_t, int64_t, hipStream_t);
+                                                    float*, int64_t, int64_t, hipStream_t);          \
+  extern template int launch_msg_forward_tangent<A, B, C>(                                          \
+      const ictc_tp_desc&, const float*, const float*, const float*, const MsgTangent&,             \
+      const int64_t*, const int64_t*, const int64_t*, float*, int64_t, int64_t, hipStream_t);       \
+  extern template int launch_msg_edge_grad_tangent<A, B, C>(                                        \
+      const ictc_tp_desc&, const float*, const float*, const float*, const MsgTangent&,             \
+      const float*, const int64_t*, const int64_t*, const int64_t*, float*, float*, float*,         \
+      int64_t, int64_t, hipStream_t);
 #include "generated/tp_instances.def"
 #undef ICTC_DECLARE
 
@@ -26,6 +33,11 @@ using MsgEdge = int (*)(const ictc_tp_desc&, const float*, const float*, const f
                         const int64_t*, const int64_t*, const int64_t*, float*, float*, float*, int64_t,
                         int64_t, hipStream_t);
 using MsgNode = int (*)(int, const float*, const int64_t*, const int64_t*, float*, int64_t, hipStream_t);
+using MsgFwdT = int (*)(const ictc_tp_desc&, const float*, const float*, const float*, const MsgTangent&,
+                        const int64_t*, const int64_t*, const int64_t*, float*, int64_t, int64_t, hipStream_t);
+using MsgEdgeT = int (*)(const ictc_tp_desc&, const float*, const float*, const float*, const MsgTangent&,
+                         const float*, const int64_t*, const int64_t*, const int64_t*, float*, float*, float*,
+                         int64_t, int64_t, hipStream_t);
 
 #define ICTC_DECLARE(A, B, C) [A * 16 + B * 4 + C] = &launch_msg_bonds<A, B, C>,
 const MsgBonds kMsgBonds[64] = {
@@ -39,6 +51,16 @@ const MsgFwd kMsgFwd[64] = {
 #undef ICTC_DECLARE
 #define ICTC_DECLARE(A, B, C) [A * 16 + B * 4 + C] = &launch_msg_edge_grad<A, B, C>,
 const MsgEdge kMsgEdge[64] = {
+#include "generated/tp_instances.def"
+};
+#undef ICTC_DECLARE
+#define ICTC_DECLARE(A, B, C) [A * 16 + B * 4 + C] = &launch_msg_forward_tangent<A, B, C>,
+const MsgFwdT kMsgFwdT[64] = {
+#include "generated/tp_instances.def"
+};
+#undef ICTC_DECLARE
+#define ICTC_DECLARE(A, B, C) [A * 16 + B * 4 + C] = &launch_msg_edge_grad_tangent<A, B, C>,
+const MsgEdgeT kMsgEdgeT[64] = {
 #include "generated/tp_instances.def"
 };
 #undef ICTC_DECLARE
@@ -136,6 +158,46 @@ int ictc_hip_message_edge_grad(const ictc_tp_desc* desc, const float* node_featu
   const ictc::MsgEdge fn = ictc::kMsgEdge[ictc::msg_index(desc)];
   if (fn == nullptr) return ICTC_ERR_UNSUPPORTED;
   return fn(*desc, node_features, bonds, gates, grad_out, src, dst_rowptr, dst_perm, grad_harmonics_partial,
+            grad_gates, edge_grad_features, nodes_src, nodes_dst, stream);
+}
+
+int ictc_hip_message_forward_tangent(const ictc_tp_desc* desc, const float* node_features, const float* bonds,
+                                     const float* gates, const float* tangent_features, const float* tangent_bonds,
+                                     const float* tangent_gates, const int64_t* src, const int64_t* dst_rowptr,
+                                     const int64_t* dst_perm, float* node_out, int64_t nodes_src,
+                                     int64_t nodes_dst, int64_t edges, hipStream_t stream) {
+  const int st = ictc::msg_common(desc, nodes_src, nodes_dst, edges);
+  if (st != ICTC_OK) return st;
+  if (nodes_dst == 0) return ICTC_OK;
+  if (!node_out || !dst_rowptr ||
+      (edges > 0 && (!node_features || !bonds || !gates || !tangent_features || !tangent_bonds ||
+                     !tangent_gates || !src)))
+    return ICTC_ERR_INVALID_ARGUMENT;
+  const ictc::MsgFwdT fn = ictc::kMsgFwdT[ictc::msg_index(desc)];
+  if (fn == nullptr) return ICTC_ERR_UNSUPPORTED;
+  const ictc::MsgTangent t{tangent_features, tangent_bonds, tangent_gates};
+  return fn(*desc, node_features, bonds, gates, t, src, dst_rowptr, dst_perm, node_out, nodes_src, nodes_dst,
+            stream);
+}
+
+int ictc_hip_message_edge_grad_tangent(const ictc_tp_desc* desc, const float* node_features, const float* bonds,
+                                       const float* gates, const float* tangent_features,
+                                       const float* tangent_bonds, const float* tangent_gates,
+                                       const float* grad_out, const int64_t* src, const int64_t* dst_rowptr,
+                                       const int64_t* dst_perm, float* grad_harmonics_partial, float* grad_gates,
+                                       float* edge_grad_features, int64_t nodes_src, int64_t nodes_dst,
+                                       int64_t edges, hipStream_t stream) {
+  const int st = ictc::msg_common(desc, nodes_src, nodes_dst, edges);
+  if (st != ICTC_OK) return st;
+  if (edges == 0 || nodes_dst == 0 || (!grad_harmonics_partial && !grad_gates && !edge_grad_features))
+    return ICTC_OK;
+  if (!node_features || !bonds || !gates || !tangent_features || !tangent_bonds || !tangent_gates || !grad_out ||
+      !src || !dst_rowptr)
+    return ICTC_ERR_INVALID_ARGUMENT;
+  const ictc::MsgEdgeT fn = ictc::kMsgEdgeT[ictc::msg_index(desc)];
+  if (fn == nullptr) return ICTC_ERR_UNSUPPORTED;
+  const ictc::MsgTangent t{tangent_features, tangent_bonds, tangent_gates};
+  return fn(*desc, node_features, bonds, gates, t, grad_out, src, dst_rowptr, dst_perm, grad_harmonics_partial,
             grad_gates, edge_grad_features, nodes_src, nodes_dst, stream);
 }
 

@@ -257,17 +257,31 @@ __device__ __forceinline__ void bond_commit(const BondStage<NB>& s, float* __res
 // wave count is what a one-wave-per-receiver launch is limited by).
 constexpr int kMsgReduceRows = 16;
 
-template <int LIN, int LE, int LOUT>
+// Direction of the message inputs for the tangent (JVP) kernels: x [nodes_src, NX*C], the bond
+// rows of the harmonics direction (the harmonics direction itself when the rows are built
+// in-kernel) and g [edges, NP*C]; all three are required.
+struct MsgTangent {
+  const float* x;
+  const float* bonds;
+  const float* g;
+};
+
+// JVP = true computes the directional derivative of the message in direction t:
+//   out[n] = sum_e g (.) [TP(tx, M) + TP(x, tM)] + tg (.) TP(x, M)
+// (the sum of the three one-argument substitutions of the reference's bilinear second-order
+// rule, structured_product.py:146-158, in one pass over the edges).
+template <int LIN, int LE, int LOUT, bool JVP = false>
 __global__ void __launch_bounds__(kMsgBlock)
 msg_forward_kernel(const float* __restrict__ x, const float* __restrict__ bonds, const float* __restrict__ g,
-                   const int64_t* __restrict__ src, const int64_t* __restrict__ rowptr,
+                   const MsgTangent t, const int64_t* __restrict__ src, const int64_t* __restrict__ rowptr,
                    const int64_t* __restrict__ perm, float* __restrict__ out, const ictc_tp_desc d,
                    int64_t nodes_src, int64_t nodes_dst, int nchunks) {
   using PS = Paths<LIN, LE, LOUT>;
   constexpr int NX = PS::NX, NP = PS::N, NOC = PS::NOC, NB = PS::NB;
   constexpr int NBS = BondStage<NB>::NV * kWave;
+  constexpr int NT = JVP ? 2 : 1;   // input sets per edge: primal (+ direction)
   constexpr int R = kMsgReduceRows;
-  __shared__ float sB[kMsgWaves][1][NBS];
+  __shared__ float sB[kMsgWaves][NT][NBS];
   __shared__ float sR[kMsgWaves - 1][R][kWave];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -278,7 +292,10 @@ msg_forward_kernel(const float* __restrict__ x, const float* __restrict__ bonds,
   const int c = chunk * kWave + lane;
   const uint32_t row = static_cast<uint32_t>(C) * 4u;
   const bool live = c < C;
-  const rsrc_t rx = make_rsrc(x, static_cast<uint32_t>(nodes_src * NX * row));  // range-checked gathers
+  const uint32_t xbytes = static_cast<uint32_t>(nodes_src * NX * row);
+  const rsrc_t rx[2] = {make_rsrc(x, xbytes), make_rsrc(JVP ? t.x : x, xbytes)};   // range-checked gathers
+  const float* gs[2] = {g, t.g};
+  const float* bs_src[2] = {bonds, t.bonds};
   float acc[NOC];
 #pragma unroll
   for (int r = 0; r < NOC; ++r) acc[r] = 0.f;
@@ -287,20 +304,26 @@ msg_forward_kernel(const float* __restrict__ x, const float* __restrict__ bonds,
   const uint32_t vc = static_cast<uint32_t>(live ? c : 0) * 4u;
   BondCoef<LIN, LE, LOUT> bc;
   bc.init(d, lane);
-  // bond row first: staging it into LDS then waits for those loads only, while the x and
-  // gate loads issued after it are still in flight
-  auto fetch = [&](int64_t slot, float* xo, float* gvo, BondStage<NB>& bo) {
+  // bond rows first: staging them into LDS then waits for those loads only, while the x and
+  // gate loads issued after them are still in flight
+  auto fetch = [&](int64_t slot, float (*xo)[NX], float (*gvo)[NP], BondStage<NB>* bo) {
     const int64_t e = perm ? perm[slot] : slot;
-    bond_row<LIN, LE, LOUT>(bonds, e, lane, bc, bo);
+#pragma unroll
+    for (int q = 0; q < NT; ++q) bond_row<LIN, LE, LOUT>(bs_src[q], e, lane, bc, bo[q]);
     const uint32_t xoff = static_cast<uint32_t>(src[e]) * NX * row + vc;   // range-checked gather
 #pragma unroll
-    for (int m = 0; m < NX; ++m) xo[m] = buf_load_vs(rx, xoff, m * row);
-    const rsrc_t rg = make_rsrc(g + e * NP * C, NP * row);
+    for (int q = 0; q < NT; ++q)
 #pragma unroll
-    for (int p = 0; p < NP; ++p) gvo[p] = buf_load_vs(rg, vc, p * row);
+      for (int m = 0; m < NX; ++m) xo[q][m] = buf_load_vs(rx[q], xoff, m * row);
+#pragma unroll
+    for (int q = 0; q < NT; ++q) {
+      const rsrc_t rg = make_rsrc(gs[q] + e * NP * C, NP * row);
+#pragma unroll
+      for (int p = 0; p < NP; ++p) gvo[q][p] = buf_load_vs(rg, vc, p * row);
+    }
   };
 
-  auto compute = [&](const float* xr, const float* gv, const float* bond) {
+  auto compute = [&](const float (*xr)[NX], const float (*gv)[NP], const float* bond0, const float* bond1) {
     static_for<0, NP>([&](auto P) {
       constexpr int p = P;
       constexpr int l1 = PS::tab.l1[p], l3 = PS::tab.l3[p];
@@ -308,12 +331,22 @@ msg_forward_kernel(const float* __restrict__ x, const float* __restrict__ bonds,
       constexpr int boff = PS::tab.bond[p], oo = PS::tab.out[p];
       // an opaque base per path plus a scheduling barrier keep the path's LDS reads next to
       // their use (otherwise the reads of the whole row are merged and hoisted into registers)
-      const float* bp = opaque_lds_row(bond + boff);
+      const float* bp = opaque_lds_row(bond0 + boff);
+      const float* tp = JVP ? opaque_lds_row(bond1 + boff) : bp;
       __builtin_amdgcn_sched_barrier(0);
       static_for<0, no>([&](auto K) {
-        float t = 0.f;
-        static_for<0, ni>([&](auto I) { t = fmaf(xr[l1 * l1 + I], bp[K * ni + I], t); });
-        acc[oo + K] = fmaf(t, gv[p], acc[oo + K]);
+        float u = 0.f;
+        static_for<0, ni>([&](auto I) { u = fmaf(xr[0][l1 * l1 + I], bp[K * ni + I], u); });
+        if constexpr (JVP) {
+          float v = 0.f;   // TP(tx, M) + TP(x, tM)
+          static_for<0, ni>([&](auto I) {
+            v = fmaf(xr[1][l1 * l1 + I], bp[K * ni + I], v);
+            v = fmaf(xr[0][l1 * l1 + I], tp[K * ni + I], v);
+          });
+          acc[oo + K] = fmaf(v, gv[0][p], fmaf(u, gv[1][p], acc[oo + K]));
+        } else {
+          acc[oo + K] = fmaf(u, gv[0][p], acc[oo + K]);
+        }
       });
     });
   };
@@ -323,11 +356,12 @@ msg_forward_kernel(const float* __restrict__ x, const float* __restrict__ bonds,
   const int64_t s0 = rowptr[node], s1 = rowptr[node + 1];
 #pragma clang loop unroll(disable)
   for (int64_t slot = s0 + wave; slot < s1; slot += kMsgWaves) {
-    float xr[NX], gv[NP];
-    BondStage<NB> bs;
+    float xr[NT][NX], gv[NT][NP];
+    BondStage<NB> bs[NT];
     fetch(slot, xr, gv, bs);
-    bond_commit<NB>(bs, &sB[wave][0][0], lane);
-    compute(xr, gv, &sB[wave][0][0]);
+#pragma unroll
+    for (int q = 0; q < NT; ++q) bond_commit<NB>(bs[q], &sB[wave][q][0], lane);
+    compute(xr, gv, &sB[wave][0][0], &sB[wave][NT - 1][0]);
   }
   const rsrc_t ro = make_rsrc(out + node * NOC * C, NOC * row);
   static_for<0, (NOC + R - 1) / R>([&](auto PIECE) {
@@ -356,17 +390,28 @@ msg_forward_kernel(const float* __restrict__ x, const float* __restrict__ bonds,
 // adjoint, dxe[e] [NX][C] the edge's source-feature adjoint.  XDEP instantiations read x and
 // produce dY / dg; the others produce dxe only (two lean passes instead of one kernel whose
 // live state would not fit in registers at lmax 3).
-template <int LIN, int LE, int LOUT, bool XDEP>
+// JVP = true (XDEP passes) computes the directional derivative of dg and dY in direction t
+// with dout fixed (the mixed second derivatives, reference structured_product.py:146-158 and
+// the mixed-second mode of ascendc/op_kernel/epilogue_adjoint.cpp):
+//   dg[p]  = sum_k dout_k sum_i (tx_i M[k,i] + x_i tM[k,i])
+//   dY     : x_i g_p replaced by tx_i g_p + x_i tg_p
+// The dxe derivative, sum_p (g_p tM_p^T + tg_p M_p^T) dout, is two plain dxe passes, the
+// second with ACC = true (adds to the rows the first wrote): one fused pass held both gate
+// sets and both bond rows live and needed 256 VGPRs at lmax 3.
+template <int LIN, int LE, int LOUT, bool XDEP, bool JVP = false, bool ACC = false>
 __global__ void __launch_bounds__(kMsgBlock)
 msg_edge_grad_kernel(const float* __restrict__ x, const float* __restrict__ bonds, const float* __restrict__ g,
-                     const float* __restrict__ go, const int64_t* __restrict__ src,
+                     const MsgTangent t, const float* __restrict__ go, const int64_t* __restrict__ src,
                      const int64_t* __restrict__ rowptr, const int64_t* __restrict__ perm,
                      float* __restrict__ dyp, float* __restrict__ dg, float* __restrict__ dxe,
                      const ictc_tp_desc d, int64_t nodes_src, int64_t nodes_dst, int nchunks) {
+  static_assert(XDEP || !JVP, "the dxe derivative is two plain dxe passes (ACC on the second)");
+  static_assert(!(XDEP && ACC), "ACC applies to the dxe pass");
   using PS = Paths<LIN, LE, LOUT>;
   constexpr int NX = PS::NX, NY = PS::NY, NP = PS::N, NOC = PS::NOC, NB = PS::NB;
   constexpr int NBS = BondStage<NB>::NV * kWave;
-  __shared__ float sB[kMsgWaves][1][NBS];
+  constexpr int NT = JVP ? 2 : 1;   // input sets per edge: primal (+ direction)
+  __shared__ float sB[kMsgWaves][NT][NBS];
   __shared__ float sO[NOC * kWave];   // the node's dout chunk, shared by the block's waves
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -379,7 +424,10 @@ msg_edge_grad_kernel(const float* __restrict__ x, const float* __restrict__ bond
   const int c = chunk * kWave + lane;
   const uint32_t row = static_cast<uint32_t>(C) * 4u;
   const bool live = c < C;
-  const rsrc_t rx = make_rsrc(x, static_cast<uint32_t>(nodes_src * NX * row));
+  const uint32_t xbytes = static_cast<uint32_t>(nodes_src * NX * row);
+  const rsrc_t rx[2] = {make_rsrc(x, xbytes), make_rsrc(JVP ? t.x : x, xbytes)};
+  const float* gs[2] = {g, t.g};
+  const float* bs_src[2] = {bonds, t.bonds};
   // lanes past C read channel 0 and zero it (dY sums over lanes); uniform row offsets in soffset
   const uint32_t vc = static_cast<uint32_t>(live ? c : 0) * 4u;
   {
@@ -394,24 +442,31 @@ msg_edge_grad_kernel(const float* __restrict__ x, const float* __restrict__ bond
 
   BondCoef<LIN, LE, LOUT> bc;
   bc.init(d, lane);
-  auto fetch = [&](int64_t slot, int64_t& eo, float* xo, float* gvo, BondStage<NB>& bo) {
+  auto fetch = [&](int64_t slot, int64_t& eo, float (*xo)[NX], float (*gvo)[NP], BondStage<NB>* bo) {
     const int64_t e = perm ? perm[slot] : slot;
     eo = e;
-    bond_row<LIN, LE, LOUT>(bonds, e, lane, bc, bo);   // first, as in the forward
+#pragma unroll
+    for (int q = 0; q < NT; ++q) bond_row<LIN, LE, LOUT>(bs_src[q], e, lane, bc, bo[q]);   // first
     const uint32_t xoff = static_cast<uint32_t>(src[e]) * NX * row + vc;   // range-checked gather
     if constexpr (XDEP) {
 #pragma unroll
-      for (int m = 0; m < NX; ++m) {
-        const float v = buf_load_vs(rx, xoff, m * row);
-        xo[m] = live ? v : 0.f;
-      }
-    }
-    const rsrc_t rg = make_rsrc(g + e * NP * C, NP * row);
+      for (int q = 0; q < NT; ++q)
 #pragma unroll
-    for (int p = 0; p < NP; ++p) gvo[p] = buf_load_vs(rg, vc, p * row);
+        for (int m = 0; m < NX; ++m) {
+          const float v = buf_load_vs(rx[q], xoff, m * row);
+          xo[q][m] = live ? v : 0.f;
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < NT; ++q) {
+      const rsrc_t rg = make_rsrc(gs[q] + e * NP * C, NP * row);
+#pragma unroll
+      for (int p = 0; p < NP; ++p) gvo[q][p] = buf_load_vs(rg, vc, p * row);
+    }
   };
 
-  auto compute = [&](int64_t e, const float* xr, const float* gv, const float* bond) {
+  auto compute = [&](int64_t e, const float (*xr)[NX], const float (*gv)[NP], const float* bond0,
+                     const float* bond1) {
     const rsrc_t rdg = make_rsrc(dg ? dg + e * NP * C : nullptr, NP * row);
     float dyl[NY], dxl[NX];   // dY partials (XDEP) / source-feature adjoint (otherwise)
 #pragma unroll
@@ -427,22 +482,27 @@ msg_edge_grad_kernel(const float* __restrict__ x, const float* __restrict__ bond
       // per-path opaque bases keep the bond and dout reads of a path next to their use
       // instead of hoisting every path's reads; products with the gate come after them
       // (g_p o_k for every path would hold NOC extra registers)
-      const float* bp = opaque_lds_row(bond + boff);
+      const float* bp = opaque_lds_row(bond0 + boff);
+      const float* tp = JVP ? opaque_lds_row(bond1 + boff) : bp;
       const float* op = XDEP ? o + oo * kWave : opaque_lds_row(o + oo * kWave);
       __builtin_amdgcn_sched_barrier(0);
-      const float gp = live ? gv[p] : 0.f;
-      if constexpr (!XDEP) {   // source-feature adjoint: dxl_i += g_p sum_k M_p[k][i] o_k
+      const float gp = live ? gv[0][p] : 0.f;
+      const float tgp = JVP && live ? gv[NT - 1][p] : 0.f;
+      if constexpr (!XDEP && !JVP) {   // source-feature adjoint: dxl_i += g_p sum_k M_p[k][i] o_k
         static_for<0, ni>([&](auto I) {
-          float t = 0.f;
-          static_for<0, no>([&](auto K) { t = fmaf(bp[K * ni + I], op[K * kWave], t); });
-          dxl[l1 * l1 + I] = fmaf(gp, t, dxl[l1 * l1 + I]);
+          float u = 0.f;
+          static_for<0, no>([&](auto K) { u = fmaf(bp[K * ni + I], op[K * kWave], u); });
+          dxl[l1 * l1 + I] = fmaf(gp, u, dxl[l1 * l1 + I]);
         });
       }
       if constexpr (XDEP) {
         float dgv = 0.f;
         static_for<0, no>([&](auto K) {
           float base = 0.f;
-          static_for<0, ni>([&](auto I) { base = fmaf(xr[l1 * l1 + I], bp[K * ni + I], base); });
+          static_for<0, ni>([&](auto I) {
+            base = fmaf(xr[NT - 1][l1 * l1 + I], bp[K * ni + I], base);   // x M (tx M under JVP)
+            if constexpr (JVP) base = fmaf(xr[0][l1 * l1 + I], tp[K * ni + I], base);   // + x tM
+          });
           dgv = fmaf(base, o[(oo + K) * kWave], dgv);
         });
         buf_store_lane(rdg, live, c * 4u + p * row, dgv);   // null dg: empty descriptor
@@ -451,12 +511,13 @@ msg_edge_grad_kernel(const float* __restrict__ x, const float* __restrict__ bond
 #pragma unroll
           for (int j = 0; j < nj; ++j) part[j] = 0.f;
           static_for<0, ni>([&](auto I) {
-            const float xg = xr[l1 * l1 + I] * gp;
+            const float xg = JVP ? fmaf(xr[1][l1 * l1 + I], gp, xr[0][l1 * l1 + I] * tgp)
+                                 : xr[0][l1 * l1 + I] * gp;
             static_for<0, no>([&](auto K) {
-              const float t = xg * o[(oo + K) * kWave];
+              const float tt = xg * o[(oo + K) * kWave];
               static_for<0, nj>([&](auto J) {
                 constexpr float cg = CG::v[(I * nj + J) * no + K];
-                if constexpr (cg != 0.0f) part[J] = fmaf(cg, t, part[J]);
+                if constexpr (cg != 0.0f) part[J] = fmaf(cg, tt, part[J]);
               });
             });
           });
@@ -468,6 +529,10 @@ msg_edge_grad_kernel(const float* __restrict__ x, const float* __restrict__ bond
     });
     if constexpr (!XDEP) {
       const rsrc_t rde = make_rsrc(dxe ? dxe + e * NX * C : nullptr, NX * row);
+      if constexpr (ACC) {   // add to the dxe rows an earlier launch wrote
+#pragma unroll
+        for (int m = 0; m < NX; ++m) dxl[m] += buf_load_vs(rde, vc, m * row);
+      }
 #pragma unroll
       for (int m = 0; m < NX; ++m) buf_store_lane(rde, live, c * 4u + m * row, dxl[m]);
     }
@@ -480,45 +545,47 @@ msg_edge_grad_kernel(const float* __restrict__ x, const float* __restrict__ bond
   };
 
   const int64_t s0 = rowptr[node], s1 = rowptr[node + 1];
-  if constexpr (XDEP) {
+  if constexpr (XDEP && !JVP) {
     // The dg pass stores NP rows per edge; the next edge's loads are requested before them, so
     // waiting for those loads does not also wait for this edge's stores (one in-order vmcnt).
     // Measured 4-7 % faster at lmax 2 and 3; the dxe pass (NX stores after the path loop)
-    // gained nothing consistent and stays unpipelined (fewer VGPRs).
+    // gained nothing consistent and stays unpipelined (fewer VGPRs), as do the JVP passes
+    // (twice the per-edge inputs).
     int64_t slot = s0 + wave;
     if (slot >= s1) return;
-    float xr[NX], gv[NP];
+    float xr[1][NX], gv[1][NP];
     int64_t e;
-    BondStage<NB> bs;
+    BondStage<NB> bs[1];
     fetch(slot, e, xr, gv, bs);
 #pragma clang loop unroll(disable)
     for (;;) {
       const int64_t nslot = slot + kMsgWaves;
       const bool more = nslot < s1;
-      float xn[NX], gn[NP];
+      float xn[1][NX], gn[1][NP];
       int64_t en = e;
-      BondStage<NB> bn;
+      BondStage<NB> bn[1];
       if (more) fetch(nslot, en, xn, gn, bn);
-      bond_commit<NB>(bs, &sB[wave][0][0], lane);
-      compute(e, xr, gv, &sB[wave][0][0]);
+      bond_commit<NB>(bs[0], &sB[wave][0][0], lane);
+      compute(e, xr, gv, &sB[wave][0][0], &sB[wave][0][0]);
       if (!more) break;
 #pragma unroll
-      for (int m = 0; m < NX; ++m) xr[m] = xn[m];
+      for (int m = 0; m < NX; ++m) xr[0][m] = xn[0][m];
 #pragma unroll
-      for (int p = 0; p < NP; ++p) gv[p] = gn[p];
-      bs = bn;
+      for (int p = 0; p < NP; ++p) gv[0][p] = gn[0][p];
+      bs[0] = bn[0];
       e = en;
       slot = nslot;
     }
   } else {
 #pragma clang loop unroll(disable)
     for (int64_t slot = s0 + wave; slot < s1; slot += kMsgWaves) {
-      float xr[NX], gv[NP];
+      float xr[NT][NX], gv[NT][NP];
       int64_t e;
-      BondStage<NB> bs;
+      BondStage<NB> bs[NT];
       fetch(slot, e, xr, gv, bs);
-      bond_commit<NB>(bs, &sB[wave][0][0], lane);
-      compute(e, xr, gv, &sB[wave][0][0]);
+#pragma unroll
+      for (int q = 0; q < NT; ++q) bond_commit<NB>(bs[q], &sB[wave][q][0], lane);
+      compute(e, xr, gv, &sB[wave][0][0], &sB[wave][NT - 1][0]);
     }
   }
 }
@@ -596,7 +663,19 @@ int launch_msg_forward(const ictc_tp_desc& d, const float* x, const float* bonds
   const int nchunks = (d.channels + kWave - 1) / kWave;
   const dim3 grid(static_cast<unsigned>(nodes_dst * nchunks));   // one block per (node, chunk)
   hipLaunchKernelGGL((msg_forward_kernel<LIN, LE, LOUT>), grid, dim3(kMsgBlock), 0,
-                     stream, x, bonds, g, src, rowptr, perm, out, d, nodes_src, nodes_dst, nchunks);
+                     stream, x, bonds, g, MsgTangent{}, src, rowptr, perm, out, d, nodes_src, nodes_dst, nchunks);
+  return msg_launch_status();
+}
+
+template <int LIN, int LE, int LOUT>
+int launch_msg_forward_tangent(const ictc_tp_desc& d, const float* x, const float* bonds, const float* g,
+                               const MsgTangent& t, const int64_t* src, const int64_t* rowptr,
+                               const int64_t* perm, float* out, int64_t nodes_src, int64_t nodes_dst,
+                               hipStream_t stream) {
+  const int nchunks = (d.channels + kWave - 1) / kWave;
+  const dim3 grid(static_cast<unsigned>(nodes_dst * nchunks));
+  hipLaunchKernelGGL((msg_forward_kernel<LIN, LE, LOUT, true>), grid, dim3(kMsgBlock), 0,
+                     stream, x, bonds, g, t, src, rowptr, perm, out, d, nodes_src, nodes_dst, nchunks);
   return msg_launch_status();
 }
 
@@ -608,11 +687,33 @@ int launch_msg_edge_grad(const ictc_tp_desc& d, const float* x, const float* bon
   const int nchunks = (d.channels + kWave - 1) / kWave;
   const dim3 grid(static_cast<unsigned>(nodes_dst * nchunks));   // one block per (node, chunk)
   if (dyp != nullptr || dg != nullptr)
-    hipLaunchKernelGGL((msg_edge_grad_kernel<LIN, LE, LOUT, true>), grid, dim3(kMsgBlock), 0, stream, x, bonds, g, go, src, rowptr, perm, dyp, dg, nullptr, d,
-                       nodes_src, nodes_dst, nchunks);
+    hipLaunchKernelGGL((msg_edge_grad_kernel<LIN, LE, LOUT, true>), grid, dim3(kMsgBlock), 0, stream, x, bonds, g,
+                       MsgTangent{}, go, src, rowptr, perm, dyp, dg, nullptr, d, nodes_src, nodes_dst, nchunks);
   if (dxe != nullptr)
-    hipLaunchKernelGGL((msg_edge_grad_kernel<LIN, LE, LOUT, false>), grid, dim3(kMsgBlock), 0, stream, nullptr, bonds, g, go, src, rowptr, perm, nullptr, nullptr, dxe,
-                       d, nodes_src, nodes_dst, nchunks);
+    hipLaunchKernelGGL((msg_edge_grad_kernel<LIN, LE, LOUT, false>), grid, dim3(kMsgBlock), 0, stream, nullptr, bonds,
+                       g, MsgTangent{}, go, src, rowptr, perm, nullptr, nullptr, dxe, d, nodes_src, nodes_dst,
+                       nchunks);
+  return msg_launch_status();
+}
+
+template <int LIN, int LE, int LOUT>
+int launch_msg_edge_grad_tangent(const ictc_tp_desc& d, const float* x, const float* bonds, const float* g,
+                                 const MsgTangent& t, const float* go, const int64_t* src, const int64_t* rowptr,
+                                 const int64_t* perm, float* dyp, float* dg, float* dxe, int64_t nodes_src,
+                                 int64_t nodes_dst, hipStream_t stream) {
+  const int nchunks = (d.channels + kWave - 1) / kWave;
+  const dim3 grid(static_cast<unsigned>(nodes_dst * nchunks));
+  if (dyp != nullptr || dg != nullptr)
+    hipLaunchKernelGGL((msg_edge_grad_kernel<LIN, LE, LOUT, true, true>), grid, dim3(kMsgBlock), 0, stream, x,
+                       bonds, g, t, go, src, rowptr, perm, dyp, dg, nullptr, d, nodes_src, nodes_dst, nchunks);
+  if (dxe != nullptr) {
+    hipLaunchKernelGGL((msg_edge_grad_kernel<LIN, LE, LOUT, false>), grid, dim3(kMsgBlock), 0, stream, nullptr,
+                       t.bonds, g, MsgTangent{}, go, src, rowptr, perm, nullptr, nullptr, dxe, d, nodes_src,
+                       nodes_dst, nchunks);
+    hipLaunchKernelGGL((msg_edge_grad_kernel<LIN, LE, LOUT, false, false, true>), grid, dim3(kMsgBlock), 0, stream,
+                       nullptr, bonds, t.g, MsgTangent{}, go, src, rowptr, perm, nullptr, nullptr, dxe, d, nodes_src,
+                       nodes_dst, nchunks);
+  }
   return msg_launch_status();
 }
 

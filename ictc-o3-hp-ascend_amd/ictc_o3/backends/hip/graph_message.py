@@ -151,6 +151,51 @@ def _backward_raw(plan: TensorProductPlan, graph: MessageGraph, need, x, y, g, g
     return dx, dy, dg
 
 
+def _second_order_raw(plan: TensorProductPlan, graph: MessageGraph, need, x, y, g, go, tx, ty, tg, bonds=None):
+    """Mixed second derivatives of the message for the tangent (tx, ty, tg) with go fixed:
+    (gx, gy, gg, ggo) = the directional derivatives of (node_grad(dxe), dY, dg) and of the
+    forward, each summed over the three one-argument substitutions; two tangent kernel
+    passes and one node_grad instead of a forward and a VJP per tangent argument."""
+    nx, ny, ng, no = (bool(n) for n in need)
+    dev = go.device
+    lib = _lib.lib()
+    stream = _lib.stream_of(dev)
+    if bonds is None:
+        bonds = _bonds(plan, graph, y)
+    tbonds = _bonds(plan, graph, ty)
+    gx = gy = gg = ggo = None
+    if no:
+        ggo = torch.empty(graph.nodes_dst, plan.full_out_width, device=dev, dtype=torch.float32)
+        _lib.check(lib.ictc_hip_message_forward_tangent(
+            ctypes.byref(plan.desc), x.data_ptr(), _p(bonds), _p(g), tx.data_ptr(), _p(tbonds), _p(tg),
+            graph.src.data_ptr(), graph.rowptr_dst.data_ptr(), _p(graph.perm_dst), ggo.data_ptr(),
+            graph.nodes_src, graph.nodes_dst, graph.edges, stream), "ictc_hip_message_forward_tangent")
+    nch = lib.ictc_hip_message_chunks(plan.channels)
+    dyp = torch.empty(graph.edges, nch, plan.y_width, device=dev, dtype=torch.float32) if ny else None
+    gg = torch.empty(graph.edges, plan.full_gate_width, device=dev, dtype=torch.float32) if ng else None
+    dxe = torch.empty(graph.edges, plan.x_width, device=dev, dtype=torch.float32) if nx else None
+    if nx or ny or ng:
+        _lib.check(lib.ictc_hip_message_edge_grad_tangent(
+            ctypes.byref(plan.desc), x.data_ptr(), _p(bonds), _p(g), tx.data_ptr(), _p(tbonds), _p(tg),
+            go.data_ptr(), graph.src.data_ptr(), graph.rowptr_dst.data_ptr(), _p(graph.perm_dst), _p(dyp),
+            _p(gg), _p(dxe), graph.nodes_src, graph.nodes_dst, graph.edges, stream),
+            "ictc_hip_message_edge_grad_tangent")
+    if dyp is not None:
+        gy = dyp[:, 0] if nch == 1 else dyp.sum(1)
+    if nx:
+        gx = torch.empty(graph.nodes_src, plan.x_width, device=dev, dtype=torch.float32)
+        _lib.check(lib.ictc_hip_message_node_grad(
+            ctypes.byref(plan.desc), dxe.data_ptr(), graph.rowptr_src.data_ptr(), _p(graph.perm_src),
+            gx.data_ptr(), graph.nodes_src, graph.edges, stream), "ictc_hip_message_node_grad")
+    return gx, gy, gg, ggo
+
+
+# The double backward uses the fused tangent kernels when no further derivative is recorded
+# (grad mode off inside backward) and all three tangents are present; otherwise it applies the
+# differentiable one-argument substitutions.  Tests switch this off to compare the two.
+FUSED_SECOND_ORDER = True
+
+
 def _add(acc, value):
     if value is None:
         return acc
@@ -205,6 +250,11 @@ class _Backward(torch.autograd.Function):
         hy = hy if need_out[1] else None
         hg = hg if need_out[2] else None
         nx, ny, ng, no = required_gradients((x, y, g, go), ctx.needs_input_grad[3:7])
+        if (FUSED_SECOND_ORDER and not torch.is_grad_enabled() and graph.edges > 0
+                and hx is not None and hy is not None and hg is not None and (nx or ny or ng or no)):
+            gx, gy, gg, ggo = _second_order_raw(plan, graph, (nx, ny, ng, no), x, y, g, go, hx.contiguous(),
+                                                hy.contiguous(), hg.contiguous(), bonds)
+            return None, None, None, gx, gy, gg, ggo, None
         gx = gy = gg = ggo = None
         if hx is not None:
             hx = hx.contiguous()

@@ -167,6 +167,39 @@ int ictc_hip_message_edge_grad(const ictc_tp_desc* desc, const float* node_featu
                                int64_t nodes_dst, int64_t edges, hipStream_t stream);
 
 /*
+ * Mixed second derivatives of the message, as directional derivatives (JVPs) in the
+ * direction (tangent_features [nodes_src, C*(L_in+1)^2], tangent harmonics, tangent_gates
+ * [edges, P*C]); tangent_bonds are the bond rows of the tangent harmonics from
+ * ictc_hip_message_bonds (or the tangent harmonics themselves when the bond width is 0).
+ *   ictc_hip_message_forward_tangent: node_out = d/de message(x + e tx, Y + e tY, g + e tg)
+ *     = sum over each argument replaced by its tangent, the others kept;
+ *   ictc_hip_message_edge_grad_tangent: the same derivative of each edge_grad output with
+ *     grad_out fixed: grad_gates from (tx, Y) + (x, tY), grad_harmonics_partial from
+ *     (tx, g) + (x, tg), edge_grad_features from (tY, g) + (Y, tg).
+ * The double backward of the message is these two calls plus one node_grad, instead of one
+ * forward and one VJP per tangent argument.  All tangent arguments are required.  Replaces
+ * the bilinear substitution of reference backends/ascend/structured_product.py:146-158 and
+ * the mixed-second adjoint mode of ascendc/op_kernel/epilogue_adjoint.cpp:6-208.
+ */
+int ictc_hip_message_forward_tangent(const ictc_tp_desc* desc, const float* node_features,
+                                     const float* bonds, const float* gates,
+                                     const float* tangent_features, const float* tangent_bonds,
+                                     const float* tangent_gates, const int64_t* src,
+                                     const int64_t* dst_rowptr, const int64_t* dst_perm,
+                                     float* node_out, int64_t nodes_src, int64_t nodes_dst,
+                                     int64_t edges, hipStream_t stream);
+
+int ictc_hip_message_edge_grad_tangent(const ictc_tp_desc* desc, const float* node_features,
+                                       const float* bonds, const float* gates,
+                                       const float* tangent_features, const float* tangent_bonds,
+                                       const float* tangent_gates, const float* grad_out,
+                                       const int64_t* src, const int64_t* dst_rowptr,
+                                       const int64_t* dst_perm, float* grad_harmonics_partial,
+                                       float* grad_gates, float* edge_grad_features,
+                                       int64_t nodes_src, int64_t nodes_dst, int64_t edges,
+                                       hipStream_t stream);
+
+/*
  * Message VJP, per-source-node part (source CSR: src_rowptr [nodes_src+1], src_perm
  * [edges] or null): grad_features[s] = sum over edges with src(e) = s of
  * edge_grad_features[e]  [nodes_src, C*(L_in+1)^2], fully overwritten; a deterministic

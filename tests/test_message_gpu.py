@@ -102,8 +102,16 @@ def test_mask_destinations_and_mul_ir(gpu):
         assert_rel(a, b, what=f"masked grad {name}")
 
 
-def test_mixed_second_derivatives(gpu):
-    c, lin, le, lout = 64, 2, 2, 2
+@pytest.mark.parametrize("c,lin,le,lout", [(64, 2, 2, 2), (128, 3, 3, 3), (48, 3, 3, 3), (96, 0, 3, 3),
+                                           (64, 1, 2, 1)])
+@pytest.mark.parametrize("fused", [True, False], ids=["tangent_kernels", "substitution"])
+def test_mixed_second_derivatives(gpu, c, lin, le, lout, fused, monkeypatch):
+    """Second derivatives of <dout, message> contracted with (hx, hY, hg), against the float64
+    oracle: once through the fused tangent kernels (the final backward records nothing, so
+    the message's double backward uses them) and once through the differentiable
+    one-argument substitutions."""
+    from ictc_o3.backends.hip import graph_message as gm
+    monkeypatch.setattr(gm, "FUSED_SECOND_ORDER", fused)
     op = _op(c, lin, le, lout, gpu)
     ref = TensorProductOracle(c, lin, le, lout)
     nodes, edges = 12, 60
