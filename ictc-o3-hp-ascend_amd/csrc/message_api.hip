@@ -122,7 +122,7 @@ int ictc_hip_message_bonds(const ictc_tp_desc* desc, const float* harmonics, flo
   const int st = ictc::tp_check_desc(desc);
   if (st != ICTC_OK) return st;
   if (edges < 0) return ICTC_ERR_INVALID_ARGUMENT;
-  if (edges == 0) return ICTC_OK;
+  if (edges == 0 || ictc::bond_width(desc) == 0) return ICTC_OK;   // width 0: rows built in-kernel
   if (!harmonics || !bonds) return ICTC_ERR_INVALID_ARGUMENT;
   const ictc::MsgBonds fn = ictc::kMsgBonds[ictc::msg_index(desc)];
   if (fn == nullptr) return ICTC_ERR_UNSUPPORTED;

@@ -110,3 +110,32 @@ def test_radius_graph_validation_rejects_before_launch():
     assert count(ctypes.byref(bad), fake, fake, fake, fake, 4, fake, None) == 1
     fill = lib.ictc_hip_radius_graph_fill
     assert fill(ctypes.byref(grid), fake, fake, fake, fake, 4, None, fake, fake, None) == 1
+
+
+def test_message_bond_width_and_tangent_validation():
+    """Bond width 0 marks degree sets whose kernels form the bond rows in-kernel (then
+    ictc_hip_message_bonds launches nothing); the tangent entry points require every
+    primal and tangent operand and reject before any launch."""
+    from ictc_o3 import _lib
+    lib = _lib.lib()
+    fake = ctypes.c_void_p(16)  # never dereferenced: every call below fails validation or launches nothing
+    d2, d3 = _desc(64, 2), _desc(128, 3)
+    assert lib.ictc_hip_message_bond_width(ctypes.byref(d2)) == 0       # lmax 2: 2 entries/lane x 9 harmonics
+    assert lib.ictc_hip_message_bond_width(ctypes.byref(d3)) == 439     # lmax 3 keeps the bond buffer
+    assert lib.ictc_hip_message_bonds(ctypes.byref(d2), fake, None, 8, None) == 0
+    fwd_t = lib.ictc_hip_message_forward_tangent
+    args = [fake] * 10                                       # x, bonds, g, tx, tb, tg, src, rowptr, perm, out
+    for i in (0, 1, 2, 3, 4, 5, 6, 7, 9):                    # perm (index 8) may be null
+        bad = list(args)
+        bad[i] = None
+        assert fwd_t(ctypes.byref(d3), *bad, 4, 4, 8, None) == 1, f"forward_tangent accepted null arg {i}"
+    assert fwd_t(ctypes.byref(d3), *args, 4, 4, -1, None) == 1
+    edge_t = lib.ictc_hip_message_edge_grad_tangent
+    args = [fake] * 13                 # x, bonds, g, tx, tb, tg, dout, src, rowptr, perm, dyp, dg, dxe
+    for i in (0, 1, 2, 3, 4, 5, 6, 7, 8):
+        bad = list(args)
+        bad[i] = None
+        assert edge_t(ctypes.byref(d3), *bad, 4, 4, 8, None) == 1, f"edge_grad_tangent accepted null arg {i}"
+    none_out = list(args)
+    none_out[10] = none_out[11] = none_out[12] = None         # nothing requested: no launch, ok
+    assert edge_t(ctypes.byref(d3), *none_out, 4, 4, 8, None) == 0
