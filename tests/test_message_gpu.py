@@ -135,6 +135,35 @@ def test_mixed_second_derivatives(gpu, c, lin, le, lout, fused, monkeypatch):
         assert_rel(a, b, what=f"message mixed second derivative {name}")
 
 
+def test_mixed_second_derivatives_masked_destinations_mul_ir(gpu):
+    """The tangent-kernel double backward with a mask (with gradient), owned destinations
+    below the source count, unsorted edges (receiver permutation) and the mul_ir layout."""
+    c, lin, le, lout = 96, 3, 3, 3
+    op = _op(c, lin, le, lout, gpu, layout="mul_ir")
+    ref = TensorProductOracle(c, lin, le, lout, layout="mul_ir")
+    nodes, edges = 21, 120
+    src, dst = _graph(nodes, edges, 21)
+    dst = dst % 15
+    op.tp._destination_nodes = 15
+    x, y, g = _edge_inputs(ref, nodes, edges, 22)
+    gen = torch.Generator().manual_seed(23)
+    mask = (torch.rand(edges, generator=gen) > 0.3).float() * torch.rand(edges, generator=gen)
+    go = torch.randn(15, ref.output_width, generator=gen)
+    hs = [torch.randn(*t.shape, generator=gen) for t in (x, y, g, mask)]
+
+    def second(fwd, tensors, dev):
+        leaves = [t.to(dev).requires_grad_() for t in tensors]
+        first = torch.autograd.grad(fwd(*leaves[:4]), leaves[:4], leaves[4], create_graph=True)
+        total = sum((f * h.to(dev)).sum() for f, h in zip(first, hs))
+        return torch.autograd.grad(total, leaves)
+
+    got = second(lambda a, b, cc, m: op(a, b, cc, src.to(gpu), dst.to(gpu), m), (x, y, g, mask, go), gpu)
+    expect = second(lambda a, b, cc, m: ref.graph_message(a, b, cc, src, dst, m, nodes=15),
+                    [t.double() for t in (x, y, g, mask, go)], "cpu")
+    for name, a, b in zip(("x", "Y", "g", "mask", "go"), got, expect):
+        assert_rel(a, b, what=f"masked message mixed second derivative {name}")
+
+
 def test_dict_interface_subset_and_empty(gpu):
     from ictc_o3 import GraphMessage
     from ictc_o3.basis.ictd_irreps import EdgeWeightedPathPreservingTensorProduct
