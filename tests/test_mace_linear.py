@@ -37,3 +37,36 @@ def test_linear_module_keeps_parameter_contract():
     assert [n for n, _ in lin.named_parameters()] == ["weight"] and lin.weight.shape == (5, 8)
     x = torch.randn(7, 3, 8)
     assert torch.allclose(lin(x), x @ lin.weight.t(), atol=1e-6)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n", [64, 512])
+def test_tall_products_on_gpu(n):
+    """Edge-sized products ([E, K] @ [K, N], E above TALL_ROWS) take the rocBLAS route with a
+    column-major right operand; value, first and second derivatives (all through the same
+    Function) against float64, with the right operand both row-major and a transposed weight."""
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    dev = torch.device("cuda", 0)
+    rows = L.TALL_ROWS + 1234
+    g = torch.Generator().manual_seed(n)
+    a64 = torch.randn(rows, 64, generator=g, dtype=torch.float64)
+    w64 = torch.randn(n, 64, generator=g, dtype=torch.float64) / 8
+    go = torch.randn(rows, n, generator=g, dtype=torch.float64)
+    h = torch.randn(rows, 64, generator=g, dtype=torch.float64)
+
+    def run(a, w, transposed):
+        a = a.clone().requires_grad_()
+        w = w.clone().requires_grad_()
+        right = w.t() if transposed else w.t().contiguous()
+        out = L.mm(a, right) if a.is_cuda else a @ right
+        ga, = torch.autograd.grad(out, a, go.to(a.device), create_graph=True)
+        second = torch.autograd.grad((ga * h.to(a.device)).sum(), w)[0]
+        return out, ga, second
+
+    for transposed in (True, False):
+        got = run(a64.float().to(dev), w64.float().to(dev), transposed)
+        expect = run(a64, w64, transposed)
+        for name, x, y in zip(("product", "input grad", "weight grad of input grad"), got, expect):
+            err = (x.double().cpu() - y).abs().max() / y.abs().max()
+            assert err < 1e-5, f"{name} (transposed={transposed}): relative error {err:.2e}"
