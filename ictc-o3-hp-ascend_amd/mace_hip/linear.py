@@ -20,6 +20,13 @@ from ictc_o3.autograd.adjoint_requirements import required_gradients
 SPLIT_ROWS = 2048          # rows per partial product
 SPLIT_MIN_RATIO = 16       # split when K >= 16 * max(M, N) ...
 SPLIT_MAX_OUTPUT = 1 << 18  # ... and the output has at most this many entries
+# Measured on MI355X at K = 105,634 rows: outputs of 2^17 entries or more ([64, 2944] and its
+# transpose) split best into 8,192-row blocks (0.45 / 0.40 ms vs 0.50 / 0.43 ms at 2,048), and outputs
+# of at most 4,096 entries ([64, 64], [8, 64]) are fastest as one rocBLAS GEMM (0.04 ms vs 0.065 ms
+# split); the split at 2,048 rows stays best in between ([64, 512], [512, 64]).
+SPLIT_ROWS_LARGE = 8192
+SPLIT_LARGE_OUTPUT = 1 << 17
+SPLIT_SINGLE_GEMM_OUTPUT = 4096
 
 # Edge-sized products against a weight-sized right operand ([E, K] @ [K, N] with E in the 10^5 range
 # and K, N <= a few thousand: the radial MLP and its adjoints) run on rocBLAS with the right operand
@@ -35,33 +42,39 @@ TALL_MAX_RIGHT = 1 << 22
 warnings.filterwarnings("ignore", message="torch.backends.cuda.preferred_blas_library is an experimental feature")
 
 
-def _rows_view(t: torch.Tensor, blocks: int) -> torch.Tensor:
-    """[K', X] (K' = blocks * SPLIT_ROWS) -> [blocks, SPLIT_ROWS, X] (a view when t is contiguous)."""
-    return t.reshape(blocks, SPLIT_ROWS, t.shape[1])
+def _rows_view(t: torch.Tensor, blocks: int, rows: int) -> torch.Tensor:
+    """[K', X] (K' = blocks * rows) -> [blocks, rows, X] (a view when t is contiguous)."""
+    return t.reshape(blocks, rows, t.shape[1])
 
 
-def _tall_product(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
-    bc = b if b.stride(0) == 1 else b.t().contiguous().t()     # column-major right operand
+def _on_rocblas(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     prev = torch.backends.cuda.preferred_blas_library()
     torch.backends.cuda.preferred_blas_library("cublas")        # rocBLAS on ROCm
     try:
-        return a @ bc
+        return a @ b
     finally:
         torch.backends.cuda.preferred_blas_library(prev)
+
+
+def _tall_product(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    return _on_rocblas(a, b if b.stride(0) == 1 else b.t().contiguous().t())   # column-major right operand
 
 
 def _product(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     m, k = a.shape
     n = b.shape[1]
-    blocks = k // SPLIT_ROWS
+    rows = SPLIT_ROWS_LARGE if m * n >= SPLIT_LARGE_OUTPUT else SPLIT_ROWS
+    blocks = k // rows
     if blocks < 2 or k < SPLIT_MIN_RATIO * max(m, n) or m * n > SPLIT_MAX_OUTPUT:
         if a.is_cuda and m >= TALL_ROWS and k * n <= TALL_MAX_RIGHT:
             return _tall_product(a, b)
         return a @ b
-    main = blocks * SPLIT_ROWS
+    if a.is_cuda and m * n <= SPLIT_SINGLE_GEMM_OUTPUT:
+        return _on_rocblas(a, b)
+    main = blocks * rows
     at = a.t()                                   # [K, M]: contiguous when a is a transposed activation
-    left = _rows_view(at[:main], blocks).transpose(1, 2)          # [blocks, M, rows]
-    right = _rows_view(b[:main], blocks)                           # [blocks, rows, N]
+    left = _rows_view(at[:main], blocks, rows).transpose(1, 2)    # [blocks, M, rows]
+    right = _rows_view(b[:main], blocks, rows)                     # [blocks, rows, N]
     out = torch.bmm(left, right).sum(0)
     if main < k:
         out = out + a[:, main:] @ b[main:]

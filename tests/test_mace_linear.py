@@ -40,7 +40,7 @@ def test_linear_module_keeps_parameter_contract():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("n", [64, 512])
+@pytest.mark.parametrize("n", [64, 512, 2944])
 def test_tall_products_on_gpu(n):
     """Edge-sized products ([E, K] @ [K, N], E above TALL_ROWS) take the rocBLAS route with a
     column-major right operand; value, first and second derivatives (all through the same
