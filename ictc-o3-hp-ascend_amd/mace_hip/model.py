@@ -118,15 +118,18 @@ class MessageLinear(nn.Module):
             self.weights.append(nn.Parameter(w))
 
     def forward(self, m: torch.Tensor) -> torch.Tensor:
-        n, c, out, off = m.shape[0], self.channels, [], 0
+        n, c, out = m.shape[0], self.channels, []
+        # one split (its backward concatenates the block gradients) rather than a slice per degree
+        # (each slice's backward zero-fills a full [N, NOC*C] gradient and the engine adds them)
+        sizes = [self.counts[l] * (2 * l + 1) * c for l in range(self.lmax + 1)]
+        blocks = m.split([*sizes, m.shape[1] - sum(sizes)], dim=-1)
         for l in range(self.lmax + 1):
             k, d = self.counts[l], 2 * l + 1
             if k == 0:
                 out.append(m.new_zeros(n, c * d))
                 continue
-            blk = m[:, off:off + k * d * c].reshape(n, k, d, c).transpose(1, 2).reshape(n * d, k * c)
+            blk = blocks[l].reshape(n, k, d, c).transpose(1, 2).reshape(n * d, k * c)
             out.append(linear(blk, self.weights[l]).reshape(n, d, c).transpose(1, 2).reshape(n, c * d))
-            off += k * d * c
         return torch.cat(out, dim=-1)
 
 
@@ -216,7 +219,8 @@ class Product(nn.Module):
     def forward(self, message, sc, species):
         out = self.linear(self.symmetric_contractions(message, node_type_idx=species))
         # _add_product_self_connection (:94-118): an l = 0 skip lands on the scalar block
-        return torch.cat([out[:, :self.channels] + sc, out[:, self.channels:]], dim=-1)
+        scalar, rest = out.split([self.channels, out.shape[1] - self.channels], dim=-1)
+        return torch.cat([scalar + sc, rest], dim=-1)
 
 
 class MaceICTC(nn.Module):
