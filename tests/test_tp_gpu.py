@@ -51,6 +51,8 @@ CASES = [
     (48, 3, 3, 3, "mul_ir"),     # partial wave, mul_ir layout
     (256, 1, 2, 3, "ir_mul"),
     (32, 3, 1, 0, "ir_mul"),
+    (64, 0, 0, 0, "ir_mul"),     # one path: fewer paths than the VJP's prefetch distance
+    (16, 1, 1, 1, "mul_ir"),     # fewer channels than lanes
 ]
 
 
