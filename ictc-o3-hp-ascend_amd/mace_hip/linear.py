@@ -39,6 +39,7 @@ SPLIT_SINGLE_GEMM_OUTPUT = 4096
 # is issued from the thread that runs the model).
 TALL_ROWS = 32768
 TALL_MAX_RIGHT = 1 << 22
+TALL_ROW_MAJOR_BELOW_K = 16
 warnings.filterwarnings("ignore", message="torch.backends.cuda.preferred_blas_library is an experimental feature")
 
 
@@ -57,7 +58,11 @@ def _on_rocblas(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
 
 
 def _tall_product(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
-    return _on_rocblas(a, b if b.stride(0) == 1 else b.t().contiguous().t())   # column-major right operand
+    # column-major right operand, except for a short reduction ([E, 8] @ [8, 64]: 25 us row-major,
+    # 35 us column-major, 45 us on hipBLASLt)
+    if b.shape[0] < TALL_ROW_MAJOR_BELOW_K:
+        return _on_rocblas(a, b.contiguous())
+    return _on_rocblas(a, b if b.stride(0) == 1 else b.t().contiguous().t())
 
 
 def _product(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:

@@ -40,8 +40,8 @@ def test_linear_module_keeps_parameter_contract():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("n", [64, 512, 2944])
-def test_tall_products_on_gpu(n):
+@pytest.mark.parametrize("k,n", [(64, 64), (64, 512), (64, 2944), (8, 64)])
+def test_tall_products_on_gpu(k, n):
     """Edge-sized products ([E, K] @ [K, N], E above TALL_ROWS) take the rocBLAS route with a
     column-major right operand; value, first and second derivatives (all through the same
     Function) against float64, with the right operand both row-major and a transposed weight."""
@@ -49,11 +49,11 @@ def test_tall_products_on_gpu(n):
         pytest.skip("no GPU")
     dev = torch.device("cuda", 0)
     rows = L.TALL_ROWS + 1234
-    g = torch.Generator().manual_seed(n)
-    a64 = torch.randn(rows, 64, generator=g, dtype=torch.float64)
-    w64 = torch.randn(n, 64, generator=g, dtype=torch.float64) / 8
+    g = torch.Generator().manual_seed(n + k)
+    a64 = torch.randn(rows, k, generator=g, dtype=torch.float64)
+    w64 = torch.randn(n, k, generator=g, dtype=torch.float64) / 8
     go = torch.randn(rows, n, generator=g, dtype=torch.float64)
-    h = torch.randn(rows, 64, generator=g, dtype=torch.float64)
+    h = torch.randn(rows, k, generator=g, dtype=torch.float64)
 
     def run(a, w, transposed):
         a = a.clone().requires_grad_()
