@@ -139,3 +139,21 @@ def test_message_bond_width_and_tangent_validation():
     none_out = list(args)
     none_out[10] = none_out[11] = none_out[12] = None         # nothing requested: no launch, ok
     assert edge_t(ctypes.byref(d3), *none_out, 4, 4, 8, None) == 0
+
+
+def test_message_rejects_node_tensors_beyond_32bit_offsets():
+    """Node tensors are gathered through 32-bit buffer offsets: sizes at or beyond 4 GiB are
+    refused (ICTC_ERR_UNSUPPORTED) before any launch, for the primal and tangent entry points."""
+    from ictc_o3 import _lib
+    lib = _lib.lib()
+    fake = ctypes.c_void_p(16)  # never dereferenced: every call below fails validation
+    d3 = _desc(128, 3)                       # 16 * 128 floats = 8 KiB per node row
+    too_many = (1 << 32) // (16 * 128 * 4)   # exactly 4 GiB of node features
+    assert lib.ictc_hip_message_forward(ctypes.byref(d3), fake, fake, fake, fake, fake, None, fake,
+                                        too_many, 4, 8, None) == 2
+    assert lib.ictc_hip_message_forward(ctypes.byref(d3), fake, fake, fake, fake, fake, None, fake,
+                                        4, too_many, 8, None) == 2   # output rows are 99 * 128 floats
+    assert lib.ictc_hip_message_forward_tangent(ctypes.byref(d3), *([fake] * 8), None, fake,
+                                                too_many, 4, 8, None) == 2
+    assert lib.ictc_hip_message_edge_grad(ctypes.byref(d3), fake, fake, fake, fake, fake, fake, None,
+                                          fake, fake, fake, too_many, 4, 8, None) == 2
