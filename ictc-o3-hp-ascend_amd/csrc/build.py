@@ -44,7 +44,8 @@ FLAGS = ["--offload-arch=" + ARCH, "-O3", "-std=c++20", "-fPIC", "-Wno-c99-desig
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
          "-I", INCLUDE, "-I", HERE]
 
-API_SOURCES = ["tp_api.hip", "harmonics_api.hip", "message_api.hip", "sc_api.hip", "graph_api.hip"]
+API_SOURCES = ["tp_api.hip", "harmonics_api.hip", "message_api.hip", "sc_api.hip", "graph_api.hip",
+               "elementwise_api.hip"]
 HARM_LMAX = 6
 INSTANCE_KINDS = {
     "fwd": ("tp_kernels.hpp", "template int launch_forward<{a}, {b}, {c}>(const ictc_tp_desc&, "

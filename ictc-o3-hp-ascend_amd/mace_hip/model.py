@@ -45,6 +45,7 @@ from ictc_o3.backends.hip.harmonics import direction_harmonics_packed
 from ictc_o3.basis.ictd_irreps import EdgeWeightedPathPreservingTensorProduct
 from ictc_o3.ops.symmetric_contraction import ICTDPureUSymmetricContractionSO3
 
+from .activation import silu
 from .linear import Linear, linear
 from .radial import bessel_embedding
 
@@ -189,7 +190,7 @@ class Interaction(nn.Module):
         layers = [m for m in self.fc if isinstance(m, nn.Linear)]
         h = layers[0](edge_feats)
         for lin in layers[1:]:
-            h = linear(F.silu(h), lin.weight * SILU_SCALE)
+            h = linear(silu(h), lin.weight * SILU_SCALE)
         return h
 
     def forward(self, h, harmonics, edge_feats, src, dst, mask, species):

@@ -343,6 +343,19 @@ int ictc_hip_radius_graph_fill(const ictc_cell_grid* grid, const double* wrapped
                                const int64_t* bin_atoms, int64_t atoms, const int64_t* rowptr,
                                int64_t* src, int32_t* images, hipStream_t stream);
 
+/*
+ * SiLU derivative forms of force training's double backward through the radial MLP: for the
+ * first-order backward y = grad * silu'(x) and a cotangent of y, one elementwise pass over n
+ * floats writes
+ *   grad_grad[i] = cotangent[i] * silu'(x[i])                 (if non-null)
+ *   grad_x[i]    = cotangent[i] * grad[i] * silu''(x[i])      (if non-null; needs grad)
+ * with s = sigmoid(x), silu' = s (1 + x (1 - s)), silu'' = s (1 - s) (2 + x (1 - 2 s)).
+ * Replaces the silu derivative modes of the fp32 elementwise kernel ictc_binary
+ * (ascendc/op_kernel/vector.cpp:6-136, ascendc/elementwise.py:7-97).
+ */
+int ictc_hip_silu_second(const float* x, const float* grad, const float* cotangent,
+                         float* grad_grad, float* grad_x, int64_t n, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
