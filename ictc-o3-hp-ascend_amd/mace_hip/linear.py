@@ -33,8 +33,10 @@ SPLIT_SINGLE_GEMM_OUTPUT = 4096
 # column-major (copied when needed; it is weight-sized).  Measured on MI355X at E = 105,634 against
 # the default hipBLASLt choice: [E,64]@[64,2944] 0.485 vs 0.571 ms, [E,2944]@[2944,64] 0.372 vs
 # 0.393-0.407 ms, [E,64]@[64,64] 0.014 vs 0.028-0.038 ms, [E,64]@[64,512] 0.068 vs 0.102 ms,
-# [E,512]@[512,64] 0.064 vs 0.094 ms.  Other products (split-K weight gradients, node-level layers)
-# keep the default, which is faster for them.
+# [E,512]@[512,64] 0.064 vs 0.094 ms.  The other plain products (node-level layers) also run on
+# rocBLAS: its host cost per call is about half hipBLASLt's (8-9 us vs 18.6 us measured), which
+# matters because an eager energy-and-forces step issues ~60 of them and is bound by host issue
+# time.  The split-K weight gradients (batched products) keep the default, faster for them.
 # The backend is switched per product (a global setting, restored after the call: the product
 # is issued from the thread that runs the model).
 TALL_ROWS = 32768
@@ -73,7 +75,7 @@ def _product(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     if blocks < 2 or k < SPLIT_MIN_RATIO * max(m, n) or m * n > SPLIT_MAX_OUTPUT:
         if a.is_cuda and m >= TALL_ROWS and k * n <= TALL_MAX_RIGHT:
             return _tall_product(a, b)
-        return a @ b
+        return _on_rocblas(a, b) if a.is_cuda else a @ b
     if a.is_cuda and m * n <= SPLIT_SINGLE_GEMM_OUTPUT:
         return _on_rocblas(a, b)
     main = blocks * rows
