@@ -284,6 +284,8 @@ def vjp(plan, graph, need, x, y, g, go, bonds=None):
     need = tuple(bool(n) for n in need)
     if not any(need):
         return None, None, None
+    if not torch.is_grad_enabled():       # nothing recorded: skip the autograd Function
+        return _backward_raw(plan, graph, need, x, y, g, go, bonds)
     outs = _Backward.apply(plan, graph, need, x, y, g, go, bonds)
     return tuple(o if n else None for o, n in zip(outs, need))
 

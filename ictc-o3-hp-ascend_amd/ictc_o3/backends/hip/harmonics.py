@@ -53,6 +53,8 @@ class _Value(torch.autograd.Function):
         (n,) = ctx.saved_tensors
         if gy is None or not ctx.needs_input_grad[0]:
             return None, None
+        if not torch.is_grad_enabled():       # nothing recorded: skip the autograd Function
+            return _raw(VJP, n, ctx.lmax, u=gy), None
         return _Vjp.apply(n, gy, ctx.lmax), None
 
 

@@ -198,6 +198,8 @@ def vjp(plan, need, x, y, g, go):
     need = tuple(bool(n) for n in need)
     if not any(need):
         return None, None, None
+    if not torch.is_grad_enabled():       # nothing recorded: skip the autograd Function
+        return _backward_raw(plan, need, x, y, g, go)
     outs = _Backward.apply(plan, need, x, y, g, go)
     return tuple(o if n else None for o, n in zip(outs, need))
 

@@ -98,8 +98,9 @@ class _MM(torch.autograd.Function):
     def backward(ctx, g):
         a, b = ctx.saved_tensors
         need_a, need_b = required_gradients((a, b), ctx.needs_input_grad)
-        ga = mm(g, b.t()) if need_a else None
-        gb = mm(a.t(), g) if need_b else None
+        prod = mm if torch.is_grad_enabled() else _product   # nothing recorded: no Function needed
+        ga = prod(g, b.t()) if need_a else None
+        gb = prod(a.t(), g) if need_b else None
         return ga, gb
 
 
