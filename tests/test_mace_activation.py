@@ -31,7 +31,9 @@ def test_fused_double_backward_matches_torch_gpu():
     dev = torch.device("cuda", 0)
     g = torch.Generator().manual_seed(1)
     n = 105634 * 64 + 7                               # a radial-MLP activation, not a multiple of 4
-    x0 = (3 * torch.randn(n, generator=g)).to(dev)
+    x0 = 3 * torch.randn(n, generator=g)
+    x0[:8] = torch.tensor([-120.0, -88.0, -30.0, -1e-7, 0.0, 1e-7, 30.0, 120.0])   # exp over/underflow
+    x0 = x0.to(dev)
     go0 = torch.randn(n, generator=g).to(dev)
     h0 = torch.randn(n, generator=g).to(dev)
 
@@ -42,6 +44,7 @@ def test_fused_double_backward_matches_torch_gpu():
         return torch.autograd.grad((first * h0).sum(), (x, go))   # last backward: fused path for silu
 
     for ours, ref, name in zip(second(silu), second(F.silu), ("x", "grad_output")):
+        assert torch.isfinite(ours).all(), f"non-finite silu double backward wrt {name}"
         err = (ours - ref).abs().max() / ref.abs().max()
         assert err < 1e-6, f"silu double backward wrt {name}: relative error {err:.2e}"
     from ictc_o3 import _lib
