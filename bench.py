@@ -200,6 +200,17 @@ def _measured_traffic():
     return None
 
 
+def _cpu_model() -> str:
+    """The host CPU's model name (reported beside every CPU baseline)."""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def _cpu_baseline(budget_s: float = 12.0):
     """Oracle fwd+VJP (reference CPU path restated) on a bounded C128/L3 sample."""
     sys.path.insert(0, ROOT)
@@ -226,7 +237,7 @@ def _cpu_baseline(budget_s: float = 12.0):
         step()
         done += 1
     dt = time.perf_counter() - t0
-    return {"value": rows * done / dt, "unit": "instances/s", "cores": threads, "kind": "port",
+    return {"value": rows * done / dt, "unit": "instances/s", "cores": threads, "cpu_model": _cpu_model(), "kind": "port",
             "sample": f"oracle fwd+VJP (PyTorch CPU fp32, reference _forward_index_add + autograd), "
                       f"C128/lmax3, {rows} instances x {done} steps in {dt:.1f}s"}
 
@@ -463,7 +474,7 @@ def _cpu_message(budget_s: float = 8.0):
     g = torch.randn(src.numel(), MSG_P * MSG_C, generator=gen) / math.sqrt(MSG_P)
     op = TensorProductOracle(MSG_C, MSG_L, MSG_L, MSG_L, dtype=torch.float32)
     done, dt = _cpu_time(lambda: op.graph_message(x, y, g, src, dst, nodes=MSG_ATOMS), budget_s)
-    return {"value": src.numel() * done / dt, "unit": "edges/s", "cores": threads, "kind": "port",
+    return {"value": src.numel() * done / dt, "unit": "edges/s", "cores": threads, "cpu_model": _cpu_model(), "kind": "port",
             "sample": f"oracle message forward (gather -> _forward_index_add -> index_add, fp32), "
                       f"{src.numel()} edges of 512 receivers x {done} calls in {dt:.1f}s"}
 
@@ -481,7 +492,7 @@ def _cpu_sc(budget_s: float = 8.0):
         xx = x.clone().requires_grad_()
         torch.autograd.grad(ref.forward(xx, species), xx, go)
     done, dt = _cpu_time(step, budget_s)
-    return {"value": 256 * done / dt, "unit": "nodes/s (fwd+VJP)", "cores": threads, "kind": "port",
+    return {"value": 256 * done / dt, "unit": "nodes/s (fwd+VJP)", "cores": threads, "cpu_model": _cpu_model(), "kind": "port",
             "sample": f"oracle contraction recursion + autograd VJP (fp32), 256 nodes x {done} calls in {dt:.1f}s"}
 
 
@@ -500,7 +511,7 @@ def _cpu_mace(budget_s: float = 10.0):
     args = dict(pos=g["positions"], species=st.species, src=g["edge_src"], dst=g["edge_dst"],
                 shifts=g["edge_shifts"], cell=g["cell"], batch=g["batch"])
     done, dt = _cpu_time(lambda: oracle.energy_and_forces(**args), budget_s)
-    return {"value": MACE_CPU_ATOMS * done / dt, "unit": "atom-steps/s (E+F inference)", "cores": threads, "kind": "port",
+    return {"value": MACE_CPU_ATOMS * done / dt, "unit": "atom-steps/s (E+F inference)", "cores": threads, "cpu_model": _cpu_model(), "kind": "port",
             "sample": f"oracle MACE restatement fp32 E+F, {MACE_CPU_ATOMS} atoms ({g['edge_src'].numel()} edges) x {done} "
                       f"calls in {dt:.1f}s"}
 
