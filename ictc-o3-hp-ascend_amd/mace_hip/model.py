@@ -265,7 +265,9 @@ class MaceICTC(nn.Module):
     def forward(self, pos, atomic_numbers, batch, edge_src, edge_dst, edge_shifts, cell, species=None):
         """Atomic energies [N] (reference forward :2879-3106, baseline route)."""
         # shift_e @ cell_e as three multiply-adds per edge (not a batched GEMM of 3 x 3 matrices)
-        shift_vecs = (edge_shifts.to(pos.dtype).unsqueeze(-1) * cell[batch[edge_src]].to(pos.dtype)).sum(1)
+        # index_select rather than advanced indexing (cheaper to issue; same gather)
+        edge_cell = cell.index_select(0, batch.index_select(0, edge_src)).to(pos.dtype)
+        shift_vecs = (edge_shifts.to(pos.dtype).unsqueeze(-1) * edge_cell).sum(1)
         # index_select: its backward is a direct index_add (advanced indexing would scatter through a sort)
         vec = pos.index_select(0, edge_dst) - pos.index_select(0, edge_src) + shift_vecs
         length = vec.norm(dim=1)
