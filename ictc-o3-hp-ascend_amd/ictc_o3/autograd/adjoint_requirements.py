@@ -11,8 +11,11 @@ gradient is kept.
 import torch
 
 
+_QUERY = getattr(torch._C, "_will_engine_execute_node", None)
+
+
 def required_gradients(inputs, declared):
-    query = getattr(torch._C, "_will_engine_execute_node", None)
+    query = _QUERY
     if query is None or torch.compiler.is_compiling():
         return tuple(bool(d) for d in declared)
     result = []
@@ -20,9 +23,13 @@ def required_gradients(inputs, declared):
         if not needed or tensor is None:
             result.append(False)
             continue
+        if tensor.grad_fn is None:
+            # a leaf: backward() accumulates into every leaf, and the engine cannot be queried about
+            # leaves under autograd.grad() (it raises, which costs far more than the answer)
+            result.append(True)
+            continue
         try:
-            node = torch.autograd.graph.get_gradient_edge(tensor).node
-            result.append(bool(query(node)))
+            result.append(bool(query(tensor.grad_fn)))       # a non-leaf's gradient edge is its grad_fn
         except (RuntimeError, AttributeError, AssertionError):
             result.append(True)
     return tuple(result)
