@@ -305,6 +305,26 @@ def _message_inputs(device):
     return src, dst, x, y, h.contiguous(), go
 
 
+def _message_traffic():
+    """HBM bytes per dispatch of the cfg-2 message kernels from the committed rocprofv3
+    FETCH_SIZE/WRITE_SIZE summary (2.0 x FETCH + 1.0 x WRITE, calibrated on a 1 GiB copy):
+    (forward, VJP passes summed), or None if the summary is absent."""
+    path = os.path.join(ROOT, "profiles", "msg_c64_l2_cfg2_kernel_trace_and_traffic.md")
+    found = {}
+    try:
+        for line in open(path):
+            if line.startswith("| `ictc::msg_") and line.rstrip().endswith("GB |"):
+                cells = [c.strip() for c in line.strip().strip("|").split("|")]
+                found[cells[0].strip("`")] = float(cells[-1].split()[0]) * 1e9
+    except OSError:
+        return None
+    fwd = [v for k, v in found.items() if k.startswith("ictc::msg_forward_kernel")]
+    vjp = [v for k, v in found.items() if not k.startswith("ictc::msg_forward_kernel")]
+    if len(fwd) != 1 or len(vjp) != 3:
+        return None
+    return fwd[0], sum(vjp)
+
+
 def _bench_message(device):
     from ictc_o3 import EdgeTensorProduct
     from ictc_o3.backends.hip.graph_message import _backward_raw, _forward_raw, message_graph
@@ -321,14 +341,20 @@ def _bench_message(device):
     # VJP: per edge Y, gates, index read + dY, dgates written; per node x, go, dx
     bwd_bytes = edges * (4 * 2 * (9 + MSG_P * MSG_C) + 8) + MSG_ATOMS * 4 * (2 * 576 + 35 * MSG_C)
     fwd_gbs, bwd_gbs = fwd_bytes / (fwd_ms * 1e-3) / 1e9, bwd_bytes / (bwd_ms * 1e-3) / 1e9
+    traffic = _message_traffic()     # measured HBM bytes per call (L2-miss gathers, bond/dxe rows included)
+    real = {} if traffic is None else {
+        "forward": {"traffic_bytes": traffic[0], "traffic_gbs": traffic[0] / (fwd_ms * 1e-3) / 1e9},
+        "vjp": {"traffic_bytes": traffic[1], "traffic_gbs": traffic[1] / (bwd_ms * 1e-3) / 1e9}}
     return {"workload": "cfg2 graph message C64/lmax2, 16,384 atoms, r_c 5 A", "edges": edges,
             "edges_per_atom": edges / MSG_ATOMS,
             "forward": {"mean_ms": fwd_ms, "edges_per_s": edges / (fwd_ms * 1e-3),
                         "algorithmic_bytes": fwd_bytes, "achieved_gbs": fwd_gbs,
-                        "frac": fwd_gbs / HBM_PEAK_GBS, "kernel": "msg_forward_kernel<2,2,2>"},
+                        "frac": fwd_gbs / HBM_PEAK_GBS, "kernel": "msg_forward_kernel<2,2,2> (in-kernel bond rows)",
+                        **real.get("forward", {})},
             "vjp": {"mean_ms": bwd_ms, "edges_per_s": edges / (bwd_ms * 1e-3), "algorithmic_bytes": bwd_bytes,
                     "achieved_gbs": bwd_gbs, "frac": bwd_gbs / HBM_PEAK_GBS,
-                    "kernels": "msg_bond_kernel + msg_edge_grad_kernel (dg/dY pass, dxe pass) + msg_node_grad_kernel"}}
+                    "kernels": "msg_edge_grad_kernel (dg/dY pass, dxe pass) + msg_node_grad_kernel",
+                    **real.get("vjp", {})}}
 
 
 SC_C, SC_L, SC_T, SC_K, SC_NODES, SC_S = 128, 3, 1, 3, 65536, 10
