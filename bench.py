@@ -39,6 +39,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--kernels
 from __future__ import annotations
 
 import argparse
+import itertools
 import json
 import math
 import os
@@ -140,23 +141,24 @@ def _copy_gbs(device, nbytes: int = 1 << 30, reps: int = 5) -> float:
 
 def _stream_mix_gbs(device, reads: int, writes: int, total_bytes: int, reps: int = 5):
     """Best bandwidth of an ideal grid-stride float4 streaming kernel (csrc/stream_probe.hip)
-    moving total_bytes in the given read:write mix; None if the probe library is absent."""
+    moving total_bytes in the given read:write mix, over three grid sizes and both load cache
+    policies (default, non-temporal); None if the probe library is absent."""
     import ctypes
     path = os.path.join(ROOT, "ictc-o3-hp-ascend_amd", "ictc_o3", "lib", "libictc_stream_probe.so")
     if not os.path.exists(path):
         return None
     lib = ctypes.CDLL(path)
     lib.ictc_probe_stream_mix.restype = ctypes.c_int
-    lib.ictc_probe_stream_mix.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
-                                          ctypes.c_size_t, ctypes.c_int, ctypes.c_void_p]
+    lib.ictc_probe_stream_mix.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                          ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_void_p]
     units = total_bytes // (16 * (reads + writes))
     a = torch.ones(reads * units * 4, device=device)
     b = torch.empty(writes * units * 4, device=device)
     stream = torch.cuda.current_stream(device)
     best = 0.0
-    for grid in (8192, 65536, min((units + 255) // 256, 2 ** 31 - 1)):
+    for nt, grid in itertools.product((0, 1), (8192, 65536, min((units + 255) // 256, 2 ** 31 - 1))):
         def launch():
-            if lib.ictc_probe_stream_mix(reads, writes, a.data_ptr(), b.data_ptr(), units, grid,
+            if lib.ictc_probe_stream_mix(reads, writes, nt, a.data_ptr(), b.data_ptr(), units, grid,
                                          ctypes.c_void_p(stream.cuda_stream)) != 0:
                 raise RuntimeError("stream probe launch failed")
         for _ in range(2):
@@ -602,7 +604,7 @@ def main() -> int:
                   "stream_mix_reference": {
                       "what": "ideal grid-stride float4 streaming kernel moving the same bytes per launch in "
                               "a matching read:write mix (7:2 for the VJP's 3.53:1, 2:5 for the forward's "
-                              "0.395:1), best of three grid sizes",
+                              "0.395:1), best of three grid sizes and both load cache policies",
                       "vjp_mix_gbs": mix_vjp, "fwd_mix_gbs": mix_fwd,
                       "vjp_frac_of_mix": achieved / mix_vjp if mix_vjp else None,
                       "fwd_frac_of_mix": fwd_achieved / mix_fwd if mix_fwd else None},

@@ -150,19 +150,20 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
 }
 
 // The whole byte offset goes into the per-lane voffset (soffset = 0): the range check
-// then compares exactly that offset with num_records.
-template <int NV>
+// then compares exactly that offset with num_records.  `policy` is the cache-policy
+// operand (0 = default; kNonTemporal for rows read exactly once).
+template <int NV, int policy = 0>
 __device__ __forceinline__ Vec<NV> buf_load(rsrc_t r, uint32_t off) {
   const uint32_t voff = off, soff = 0;
   Vec<NV> out;
   if constexpr (NV == 1) {
-    out.v[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+    out.v[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, policy));
   } else if constexpr (NV == 2) {
-    const f32x2 t = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
+    const f32x2 t = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, policy));
     out.v[0] = t.x;
     out.v[1] = t.y;
   } else {
-    const f32x4 t = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+    const f32x4 t = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, policy));
     out.v[0] = t.x;
     out.v[1] = t.y;
     out.v[2] = t.z;

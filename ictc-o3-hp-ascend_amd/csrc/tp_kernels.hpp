@@ -166,6 +166,8 @@ tp_forward_kernel(const float* __restrict__ x, const float* __restrict__ y,
 // The dY channel sum is a per-lane partial followed by one wave reduction per instance.
 // The path loop is software-pipelined: the gate and dout rows of path p + kBwdPrefetch are
 // requested before path p is computed and its dg stored.
+// The x, gate and dout rows are read exactly once and loaded with the non-temporal cache policy
+// (measured at C128/lmax3: 2.16 -> 2.10 ms; the forward's loads measure slower with it).
 // Outputs whose pointer is null get an empty buffer descriptor: their stores are
 // dropped by the hardware range check, so the instance body has no branches.
 template <int LIN, int LE, int LOUT, int NV>
@@ -205,7 +207,7 @@ tp_backward_kernel(const float* __restrict__ x, const float* __restrict__ y,
       Vec<NV> dxr[NX];
 #pragma unroll
       for (int m = 0; m < NX; ++m) {
-        xr[m] = buf_load<NV>(rx, vo + m * row);
+        xr[m] = buf_load<NV, kNonTemporal>(rx, vo + m * row);
 #pragma unroll
         for (int v = 0; v < NV; ++v) dxr[m].v[v] = 0.f;
       }
@@ -216,8 +218,8 @@ tp_backward_kernel(const float* __restrict__ x, const float* __restrict__ y,
         constexpr int q = Q;
         if constexpr (q < NP) {
           constexpr int nq = 2 * PS::tab.l3[q] + 1, oq = PS::tab.out[q];
-          pre_g[q % D] = buf_load<NV>(rg, vo + q * row);
-          static_for<0, nq>([&](auto K) { pre_o[q % D][K] = buf_load<NV>(rgo, vo + (oq + K) * row); });
+          pre_g[q % D] = buf_load<NV, kNonTemporal>(rg, vo + q * row);
+          static_for<0, nq>([&](auto K) { pre_o[q % D][K] = buf_load<NV, kNonTemporal>(rgo, vo + (oq + K) * row); });
         }
       };
       static_for<0, D>(request);
