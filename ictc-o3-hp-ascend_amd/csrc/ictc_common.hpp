@@ -176,8 +176,9 @@ __device__ __forceinline__ Vec<NV> buf_load(rsrc_t r, uint32_t off) {
 // VGPR).  The range check covers voffset only: callers keep voffset + soffset inside
 // the descriptor's range themselves (soffset below a row, lanes clamped to a real
 // channel) and put anything data-dependent in voffset.
+template <int policy = 0>
 __device__ __forceinline__ float buf_load_vs(rsrc_t r, uint32_t voff, uint32_t soff) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, policy));
 }
 
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));

@@ -305,7 +305,10 @@ msg_forward_kernel(const float* __restrict__ x, const float* __restrict__ bonds,
   BondCoef<LIN, LE, LOUT> bc;
   bc.init(d, lane);
   // bond rows first: staging them into LDS then waits for those loads only, while the x and
-  // gate loads issued after them are still in flight
+  // gate loads issued after them are still in flight.  Gate rows are read exactly once and use
+  // the non-temporal cache policy, which leaves L2 to the x[src] gathers that other edges of
+  // nearby receivers re-read (C128/lmax-3 forward over 105,634 edges: 0.62 -> 0.55 ms measured,
+  // bit-identical)
   auto fetch = [&](int64_t slot, float (*xo)[NX], float (*gvo)[NP], BondStage<NB>* bo) {
     const int64_t e = perm ? perm[slot] : slot;
 #pragma unroll
@@ -319,7 +322,7 @@ msg_forward_kernel(const float* __restrict__ x, const float* __restrict__ bonds,
     for (int q = 0; q < NT; ++q) {
       const rsrc_t rg = make_rsrc(gs[q] + e * NP * C, NP * row);
 #pragma unroll
-      for (int p = 0; p < NP; ++p) gvo[q][p] = buf_load_vs(rg, vc, p * row);
+      for (int p = 0; p < NP; ++p) gvo[q][p] = buf_load_vs<kNonTemporal>(rg, vc, p * row);
     }
   };
 
@@ -460,8 +463,11 @@ msg_edge_grad_kernel(const float* __restrict__ x, const float* __restrict__ bond
   const uint32_t vc = static_cast<uint32_t>(live ? c : 0) * 4u;
   {
     const rsrc_t ron = make_rsrc(go + node * NOC * C, NOC * row);
+    // read once: non-temporal in the dg/dY pass (measured 1-10 % faster); the dxe pass keeps the
+    // default policy (3 % slower with it at lmax 2)
+    constexpr int kDoutPolicy = XDEP ? kNonTemporal : 0;
     for (int r = wave; r < NOC; r += kMsgWaves) {
-      const float v = buf_load_vs(ron, vc, r * row);
+      const float v = buf_load_vs<kDoutPolicy>(ron, vc, r * row);
       sO[r * kWave + lane] = live ? v : 0.f;
     }
   }
@@ -489,7 +495,7 @@ msg_edge_grad_kernel(const float* __restrict__ x, const float* __restrict__ bond
     for (int q = 0; q < NT; ++q) {
       const rsrc_t rg = make_rsrc(gs[q] + e * NP * C, NP * row);
 #pragma unroll
-      for (int p = 0; p < NP; ++p) gvo[q][p] = buf_load_vs(rg, vc, p * row);
+      for (int p = 0; p < NP; ++p) gvo[q][p] = buf_load_vs<kNonTemporal>(rg, vc, p * row);
     }
   };
 
@@ -619,7 +625,8 @@ msg_edge_grad_kernel(const float* __restrict__ x, const float* __restrict__ bond
 }
 
 // ----------------------------------------------------------------------------- VJP: per source node
-// dx[s] = sum over edges with src(e) = s of dxe[e]  ([NX][C] rows, streamed four edges at a time).
+// dx[s] = sum over edges with src(e) = s of dxe[e]  ([NX][C] rows, streamed four edges at a time;
+// each row is read once, with the non-temporal cache policy: 7-11 % faster measured).
 template <int NX>
 __global__ void __launch_bounds__(kMsgBlock)
 msg_node_grad_kernel(const float* __restrict__ dxe, const int64_t* __restrict__ rowptr_src,
@@ -649,7 +656,7 @@ msg_node_grad_kernel(const float* __restrict__ dxe, const int64_t* __restrict__ 
       const int64_t e = perm_src ? perm_src[slot + u] : slot + u;
       const rsrc_t r = make_rsrc(dxe + e * NX * C, NX * row);
 #pragma unroll
-      for (int m = 0; m < NX; ++m) v[u][m] = buf_load_vs(r, vc, m * row);
+      for (int m = 0; m < NX; ++m) v[u][m] = buf_load_vs<kNonTemporal>(r, vc, m * row);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u)
@@ -660,7 +667,7 @@ msg_node_grad_kernel(const float* __restrict__ dxe, const int64_t* __restrict__ 
     const int64_t e = perm_src ? perm_src[slot] : slot;
     const rsrc_t r = make_rsrc(dxe + e * NX * C, NX * row);
 #pragma unroll
-    for (int m = 0; m < NX; ++m) acc[m] += buf_load_vs(r, vc, m * row);
+    for (int m = 0; m < NX; ++m) acc[m] += buf_load_vs<kNonTemporal>(r, vc, m * row);
   }
   const rsrc_t rdx = make_rsrc(dx + node * NX * C, NX * row);
 #pragma unroll
