@@ -21,6 +21,7 @@ int grid_status(const ictc_cell_grid* g, const double* wpos, const int32_t* abin
 }
 
 dim3 grid_blocks(int64_t atoms) { return dim3(static_cast<unsigned>((atoms + 255) / 256)); }
+dim3 wave_blocks(int64_t atoms) { return dim3(static_cast<unsigned>((atoms + kGraphWaves - 1) / kGraphWaves)); }
 
 }  // namespace
 }  // namespace ictc
@@ -34,9 +35,8 @@ int ictc_hip_radius_graph_count(const ictc_cell_grid* grid, const double* wrappe
   if (st != ICTC_OK) return st;
   if (atoms == 0) return ICTC_OK;
   if (!counts) return ICTC_ERR_INVALID_ARGUMENT;
-  hipLaunchKernelGGL((ictc::radius_graph_kernel<false>), ictc::grid_blocks(atoms), dim3(256), 0, stream,
-                     wrapped_positions, atom_bins, bin_start, bin_atoms, atoms, *grid, counts, nullptr, nullptr,
-                     nullptr);
+  hipLaunchKernelGGL(ictc::radius_count_kernel, ictc::wave_blocks(atoms), dim3(ictc::kGraphWaves * ictc::kWave), 0,
+                     stream, wrapped_positions, atom_bins, bin_start, bin_atoms, atoms, *grid, counts);
   return hipGetLastError() == hipSuccess ? ICTC_OK : ICTC_ERR_LAUNCH;
 }
 
@@ -48,8 +48,24 @@ int ictc_hip_radius_graph_fill(const ictc_cell_grid* grid, const double* wrapped
   if (st != ICTC_OK) return st;
   if (atoms == 0) return ICTC_OK;
   if (!rowptr || !src || !images) return ICTC_ERR_INVALID_ARGUMENT;
-  hipLaunchKernelGGL((ictc::radius_graph_kernel<true>), ictc::grid_blocks(atoms), dim3(256), 0, stream,
-                     wrapped_positions, atom_bins, bin_start, bin_atoms, atoms, *grid, nullptr, rowptr, src, images);
+  hipLaunchKernelGGL(ictc::radius_fill_kernel, ictc::grid_blocks(atoms), dim3(256), 0, stream, wrapped_positions,
+                     atom_bins, bin_start, bin_atoms, atoms, *grid, rowptr, src, images);
+  return hipGetLastError() == hipSuccess ? ICTC_OK : ICTC_ERR_LAUNCH;
+}
+
+int64_t ictc_hip_radius_graph_row_capacity(void) { return ictc::kGraphRowCap; }
+
+int ictc_hip_radius_graph_fill_sorted(const ictc_cell_grid* grid, const double* wrapped_positions,
+                                      const int32_t* atom_bins, const int64_t* bin_start, const int64_t* bin_atoms,
+                                      int64_t atoms, const int64_t* rowptr, const int64_t* image_base, int64_t* src,
+                                      int64_t* dst, double* shifts, hipStream_t stream) {
+  const int st = ictc::grid_status(grid, wrapped_positions, atom_bins, bin_start, bin_atoms, atoms);
+  if (st != ICTC_OK) return st;
+  if (atoms == 0) return ICTC_OK;
+  if (!rowptr || !image_base || !src || !dst || !shifts) return ICTC_ERR_INVALID_ARGUMENT;
+  hipLaunchKernelGGL(ictc::radius_fill_sorted_kernel, ictc::wave_blocks(atoms),
+                     dim3(ictc::kGraphWaves * ictc::kWave), 0, stream, wrapped_positions, atom_bins, bin_start,
+                     bin_atoms, atoms, *grid, rowptr, image_base, src, dst, shifts);
   return hipGetLastError() == hipSuccess ? ICTC_OK : ICTC_ERR_LAUNCH;
 }
 

@@ -15,7 +15,7 @@ import torch  # noqa: F401  (must precede CDLL, see module docstring)
 
 MAX_PATHS = 64
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libictc_hip.so")
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 
 class TpDesc(ctypes.Structure):
@@ -81,6 +81,9 @@ _SIGNATURES = {
     "ictc_hip_radius_graph_count": (ctypes.c_int, [ctypes.POINTER(CellGrid), _P, _P, _P, _P, _I64, _P, _P]),
     "ictc_hip_radius_graph_fill": (ctypes.c_int, [ctypes.POINTER(CellGrid), _P, _P, _P, _P, _I64, _P, _P, _P,
                                                   _P]),
+    "ictc_hip_radius_graph_row_capacity": (_I64, []),
+    "ictc_hip_radius_graph_fill_sorted": (ctypes.c_int, [ctypes.POINTER(CellGrid), _P, _P, _P, _P, _I64, _P, _P, _P,
+                                                         _P, _P, _P]),
 }
 
 _lock = threading.Lock()

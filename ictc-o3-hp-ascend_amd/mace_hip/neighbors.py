@@ -6,7 +6,7 @@ arguments and returns: ``(edge_src, edge_dst, edge_shifts float64)`` with
 ``vec = pos[dst] - pos[src] + shift @ cell``, self pairs excluded, optional saturation flag).
 The reference runs one torch_cluster radius query per lattice image, each capped at
 ``max_num_neighbors``; here one exact search over binned atoms runs on HIP
-(``ictc_hip_radius_graph_count`` / ``_fill``), nothing is truncated, and the edges come
+(``ictc_hip_radius_graph_count`` / ``_fill_sorted``), nothing is truncated, and the edges come
 out ordered by (dst, src, shift): the receiver order the message kernels use, with ties
 resolved deterministically.  ``saturated`` reports whether any receiver has at least
 ``max_num_neighbors`` neighbours (where the reference's per-image queries could truncate).
@@ -14,7 +14,10 @@ resolved deterministically.  ``saturated`` reports whether any receiver has at l
 Host steps (device tensors): fractional coordinates, wrap along periodic axes, bins at
 least one cutoff wide along every face normal (fewer bins and a wider reach when the cell
 is narrower than the cutoff, so every image is enumerated exactly once), atoms grouped by
-bin, count pass, exclusive scan, fill pass, row ordering.
+bin, count pass (one wave per receiver), exclusive scan, one device-to-host read of the edge
+count and the longest row, then the sorted fill: one wave per receiver writes its row already
+ordered by (src, shift), with dst and the float64 shifts.  A row longer than the kernel's LDS
+key capacity (1,024 edges) takes the unsorted fill and two stable sorts here instead.
 """
 from __future__ import annotations
 
@@ -57,6 +60,11 @@ def pbc_image_nmax(cell: torch.Tensor, cutoff: float, pbc=None) -> torch.Tensor:
     flags = _pbc_flags(pbc)
     return torch.tensor([max(1, math.ceil(float(cutoff) / h)) if f else 0 for h, f in zip(heights, flags)],
                         dtype=torch.long, device=cell_mat.device)
+
+
+def _row_capacity() -> int:
+    """Longest receiver row the sorted fill kernel orders in LDS."""
+    return int(_lib.lib().ictc_hip_radius_graph_row_capacity())
 
 
 @torch.no_grad()
@@ -121,16 +129,27 @@ def radius_graph_pbc_gpu(pos: torch.Tensor, r: float, cell: torch.Tensor, max_nu
     _lib.check(lib.ictc_hip_radius_graph_count(*args, counts.data_ptr(), stream), "ictc_hip_radius_graph_count")
     rowptr = torch.zeros(n + 1, dtype=torch.int64, device=dev)
     torch.cumsum(counts, 0, out=rowptr[1:])
-    edges = int(rowptr[-1])
-    saturated = bool((counts >= int(max_num_neighbors)).any()) if max_num_neighbors > 0 else False
+    edges, longest = torch.stack((rowptr[-1], counts.max())).tolist()   # one device-to-host read
+    saturated = max_num_neighbors > 0 and longest >= int(max_num_neighbors)
     if edges == 0:
         return empty + (saturated,) if return_saturation else empty
+    n0i = n0.to(torch.int64).contiguous()
+    if longest <= _row_capacity():
+        # rows written in (dst, src, shift) order by the kernel itself
+        src = torch.empty(edges, dtype=torch.int64, device=dev)
+        dst = torch.empty(edges, dtype=torch.int64, device=dev)
+        shift = torch.empty(edges, 3, dtype=torch.float64, device=dev)
+        _lib.check(lib.ictc_hip_radius_graph_fill_sorted(*args, rowptr.data_ptr(), n0i.data_ptr(), src.data_ptr(),
+                                                         dst.data_ptr(), shift.data_ptr(), stream),
+                   "ictc_hip_radius_graph_fill_sorted")
+        result = (src, dst, shift)
+        return result + (saturated,) if return_saturation else result
+    # a row beyond the kernel's key capacity: fill in visiting order, then order the rows here
     src = torch.empty(edges, dtype=torch.int64, device=dev)
     images = torch.empty(edges, 3, dtype=torch.int32, device=dev)
     _lib.check(lib.ictc_hip_radius_graph_fill(*args, rowptr.data_ptr(), src.data_ptr(), images.data_ptr(), stream),
                "ictc_hip_radius_graph_fill")
     dst = torch.repeat_interleave(torch.arange(n, device=dev), counts)
-    n0i = n0.to(torch.int64)
     shift = images.to(torch.int64) - n0i[dst] + n0i[src]
     # rows are grouped by dst; order each row by (src, shift): stable sort by that key, then by dst
     smax = int(shift.abs().max())

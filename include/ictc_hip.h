@@ -344,6 +344,25 @@ int ictc_hip_radius_graph_fill(const ictc_cell_grid* grid, const double* wrapped
                                int64_t* src, int32_t* images, hipStream_t stream);
 
 /*
+ * Sorted fill (also replaces graph_utils.py:217-297, including the caller's edge ordering):
+ * for every receiver j whose row holds at most ictc_hip_radius_graph_row_capacity() edges
+ * (the caller checks the counts; a longer row is cut to that many), writes rows
+ * rowptr[j] .. rowptr[j+1]-1 in (src, shift) order:
+ *   src[e] = i, dst[e] = j, shifts[e,0:3] = t - image_base[j] + image_base[i] (float64),
+ * where image_base [atoms,3] int64 is each atom's wrap image (position = wrapped position +
+ * image_base @ cell) and t the lattice image of the fill entry point above.  The rows then
+ * form the (dst, src, shift)-ordered edge list of the reference builder's result, with
+ * edge vectors pos[dst] - pos[src] + shift @ cell.
+ */
+int64_t ictc_hip_radius_graph_row_capacity(void);
+
+int ictc_hip_radius_graph_fill_sorted(const ictc_cell_grid* grid, const double* wrapped_positions,
+                                      const int32_t* atom_bins, const int64_t* bin_start,
+                                      const int64_t* bin_atoms, int64_t atoms, const int64_t* rowptr,
+                                      const int64_t* image_base, int64_t* src, int64_t* dst,
+                                      double* shifts, hipStream_t stream);
+
+/*
  * SiLU derivative forms of force training's double backward through the radial MLP: for the
  * first-order backward y = grad * silu'(x) and a cotangent of y, one elementwise pass over n
  * floats writes

@@ -6,8 +6,9 @@ s in [-nmax, nmax]^3 on periodic axes (0 on open ones), (src, s) != (dst, 0), in
 the CPU, sorted by (dst, src, s): the semantics of reference
 mace_ictc/utils/graph_utils.py:217-297 without its per-image neighbour cap.  Cases: cubic,
 skewed triclinic, cells narrower than the cutoff (several images of one pair), an open
-axis, empty and single-atom inputs, and the cfg-4 structure against the minimum-image
-builder the benchmarks also use.
+axis, empty and single-atom inputs, the cfg-4 structure against the minimum-image
+builder the benchmarks also use, rows longer than the sorted fill kernel's key capacity, and
+the host-ordered long-row path forced on small cases and checked against the sorted fill.
 """
 import itertools
 import math
@@ -126,3 +127,41 @@ def test_cfg4_structure_matches_minimum_image_builder(gpu):
     s2, d2, sh2 = radius_graph(pos, cell, 5.0)
     assert src.numel() > 100_000
     assert torch.equal(src, s2) and torch.equal(dst, d2) and torch.equal(shifts.to(sh2.dtype), sh2)
+
+
+def test_rows_beyond_the_sorted_fill_capacity(gpu):
+    """A dense cell (~1,200 neighbours per atom, above the sorted fill's 1,024-key rows) takes the
+    unsorted fill and host-side ordering; still exact against the brute force."""
+    from mace_hip.neighbors import _row_capacity
+    cell = torch.eye(3, dtype=torch.float64) * 10.0
+    src, dst, shifts = _check(gpu, _uniform(400, cell, 6), cell, 9.0)
+    assert int(torch.bincount(dst).max()) > _row_capacity()
+
+
+@pytest.mark.parametrize("case", ["triclinic", "narrow", "open"])
+def test_unsorted_fill_path(gpu, monkeypatch, case):
+    """The long-row path forced on small cases (capacity patched to 2 keys), against the brute force."""
+    from mace_hip import neighbors
+    monkeypatch.setattr(neighbors, "_row_capacity", lambda: 2)
+    if case == "triclinic":
+        cell = torch.tensor([[12.0, 0.0, 0.0], [5.0, 11.0, 0.0], [-3.0, 4.0, 13.0]], dtype=torch.float64)
+        _check(gpu, _uniform(220, cell, 2), cell, 4.5)
+    elif case == "narrow":
+        cell = torch.tensor([[4.0, 0.0, 0.0], [0.3, 4.0, 0.0], [0.0, -0.4, 4.4]], dtype=torch.float64)
+        _check(gpu, _uniform(5, cell, 5), cell, 5.0)
+    else:
+        cell = torch.eye(3, dtype=torch.float64) * 14.0
+        pos = _uniform(180, cell, 3)
+        pos[:, 2] = pos[:, 2] * 2.5 - 6.0
+        _check(gpu, pos, cell, 4.0, pbc=(True, True, False))
+
+
+def test_sorted_and_unsorted_fill_agree_on_cfg4(gpu, monkeypatch):
+    from mace_hip import neighbors, sequential_insertion
+    st = sequential_insertion(2048, 0.1, min_separation=1.5, num_species=10, seed=4)
+    pos, cell = st.positions.to(gpu), st.cell.to(gpu)
+    sorted_fill = neighbors.radius_graph_pbc_gpu(pos, 5.0, cell)
+    monkeypatch.setattr(neighbors, "_row_capacity", lambda: 0)
+    host_ordered = neighbors.radius_graph_pbc_gpu(pos, 5.0, cell)
+    for a, b in zip(sorted_fill, host_ordered):
+        assert a.dtype == b.dtype and torch.equal(a, b)
