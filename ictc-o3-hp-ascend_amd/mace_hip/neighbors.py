@@ -90,13 +90,19 @@ def radius_graph_pbc_gpu(pos: torch.Tensor, r: float, cell: torch.Tensor, max_nu
     heights = _face_heights(cell_cpu)
     c64 = cell_cpu.to(dev)
     frac = pos.double() @ torch.linalg.inv(cell_cpu).to(dev)
-    periodic = torch.tensor(flags, device=dev)
-    n0 = torch.where(periodic, torch.floor(frac), torch.zeros_like(frac))
-    fw = frac - n0
-    lo = torch.where(periodic, torch.zeros(3, dtype=torch.float64, device=dev), fw.min(0).values)
-    span = torch.where(periodic, torch.ones(3, dtype=torch.float64, device=dev),
-                       (fw.max(0).values - lo).clamp_min(1e-12))
-    span_host = span.cpu().tolist()
+    if all(flags):
+        # every axis wraps into [0, 1): the binned region is the cell itself, known on the host
+        n0 = torch.floor(frac)
+        fw = frac - n0
+        lo, span, span_host = None, None, [1.0, 1.0, 1.0]
+    else:
+        periodic = torch.tensor(flags, device=dev)
+        n0 = torch.where(periodic, torch.floor(frac), torch.zeros_like(frac))
+        fw = frac - n0
+        lo = torch.where(periodic, torch.zeros(3, dtype=torch.float64, device=dev), fw.min(0).values)
+        span = torch.where(periodic, torch.ones(3, dtype=torch.float64, device=dev),
+                           (fw.max(0).values - lo).clamp_min(1e-12))
+        span_host = span.cpu().tolist()
     extents = [span_host[a] * heights[a] for a in range(3)]   # perpendicular extent of the binned region
     bins = [int(min(MAX_BINS_PER_AXIS, max(1, math.floor(e / r)))) for e in extents]
     while bins[0] * bins[1] * bins[2] > max(64, 8 * n):          # sparse systems: coarser bins
@@ -107,7 +113,7 @@ def radius_graph_pbc_gpu(pos: torch.Tensor, r: float, cell: torch.Tensor, max_nu
         k = max(1, math.ceil(r / (extents[a] / bins[a])))         # bins of width extent / bins
         reach.append(min(k, bins[a] - 1) if not flags[a] else k)
     bins_t = torch.tensor(bins, dtype=torch.float64, device=dev)
-    abin = torch.floor((fw - lo) / span * bins_t).clamp(min=0)
+    abin = torch.floor((fw if lo is None else (fw - lo) / span) * bins_t).clamp(min=0)
     abin = torch.minimum(abin, bins_t - 1).to(torch.int32).contiguous()
     wpos = (fw @ c64).contiguous()
     ab = abin.to(torch.int64)
