@@ -18,6 +18,7 @@ validation) runs once per (src, dst) pair and is cached.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 from typing import Optional
 
@@ -60,6 +61,23 @@ class MessageGraph:
 
 
 _GRAPH_CACHE: dict = {}
+_PIN_LISTS: list = []          # open pin_graphs() scopes
+
+
+@contextlib.contextmanager
+def pin_graphs():
+    """Collect every MessageGraph handed out inside the scope into the yielded list.
+
+    A HIP graph captured inside the scope records the raw device addresses of those graphs'
+    CSR tensors; the cache below evicts entries, so whoever replays the capture must keep
+    the list (and with it the tensors) alive for as long as the capture exists."""
+    held: list = []
+    _PIN_LISTS.append(held)
+    try:
+        yield held
+    finally:
+        # by identity: two open scopes may hold equal lists
+        del _PIN_LISTS[next(i for i, h in enumerate(_PIN_LISTS) if h is held)]
 
 
 def message_graph(src: torch.Tensor, dst: torch.Tensor, nodes_src: int, nodes_dst: int) -> MessageGraph:
@@ -72,6 +90,9 @@ def message_graph(src: torch.Tensor, dst: torch.Tensor, nodes_src: int, nodes_ds
             _GRAPH_CACHE.clear()
         graph = MessageGraph(src, dst, nodes_src, nodes_dst)
         _GRAPH_CACHE[key] = graph
+    for held in _PIN_LISTS:
+        if not any(g is graph for g in held):
+            held.append(graph)
     return graph
 
 

@@ -284,17 +284,33 @@ class EdgeWeightedPathPreservingTensorProduct(nn.Module):
             self._plans[key] = plan
         return plan
 
+    def invalidate_weight_cache(self) -> None:
+        """Forget that the frozen weight was found to be all ones.  Needed only after writing the
+        weight through ``weight.data`` (such writes bypass the version counter that the cache
+        checks); ``load_state_dict``, in-place updates of the parameter and replacing its
+        storage are detected without it."""
+        self._unit_weight_key = None
+
+    def _load_from_state_dict(self, *args, **kwargs):
+        self._unit_weight_key = None
+        super()._load_from_state_dict(*args, **kwargs)
+
     def effective_gates(self, gates: Optional[torch.Tensor], rows: int) -> torch.Tensor:
-        """gates * weight as [E, P*C] (weight folded only when it is not a frozen all-ones)."""
+        """gates * weight as [E, P*C] (weight folded only when it is not a frozen all-ones).
+
+        Whether a frozen weight is all ones is checked once (a host read) and cached on the
+        weight's identity, storage address and version counter."""
         w = self.weight
         if gates is None:
             return w.reshape(1, -1).expand(rows, -1).contiguous()
         gates = gates.reshape(rows, self.num_paths * self.channels)
-        if not w.requires_grad and getattr(self, "_unit_weight_version", None) == (w._version, w.data_ptr()):
-            return gates
-        if not w.requires_grad and bool(torch.all(w == 1)):
-            self._unit_weight_version = (w._version, w.data_ptr())
-            return gates
+        if not w.requires_grad:
+            key = (id(w), w.data_ptr(), w._version)
+            if getattr(self, "_unit_weight_key", None) == key:
+                return gates
+            if bool(torch.all(w == 1)):
+                self._unit_weight_key = key
+                return gates
         return (gates.reshape(rows, self.num_paths, self.channels) * w[None]).reshape(rows, -1)
 
     def forward(self, x1: Dict[int, torch.Tensor], x2: Dict[int, torch.Tensor],

@@ -19,6 +19,7 @@ import torch
 import torch.nn as nn
 
 from ictc_o3.backends.hip.runtime import require_gpu_fp32
+from ictc_o3.backends.hip.species import validate_species
 
 
 class _Contraction(nn.Module):
@@ -58,7 +59,6 @@ class ICTDPureUSymmetricContractionSO3(nn.Module):
             [_Contraction(self.lmax, l, self.correlation, self.num_elements, self.channels, with_u_buffers)
              for l in range(self.target_lmax + 1)])
         self._plan = None
-        self._checked_species = None
 
     @property
     def plan(self):
@@ -77,12 +77,7 @@ class ICTDPureUSymmetricContractionSO3(nn.Module):
         species = species.to(torch.int64).contiguous()
         if species.shape != (nodes,):
             raise ValueError("species indices must have shape [N]")
-        key = (species.data_ptr(), species._version, nodes)
-        if nodes and self._checked_species != key:
-            lo_hi = torch.stack([species.min(), species.max()]).cpu()
-            if int(lo_hi[0]) < 0 or int(lo_hi[1]) >= self.num_elements:
-                raise ValueError("species index out of range")
-            self._checked_species = key
+        validate_species(species, self.num_elements)
         return species
 
     def forward(self, node_feats: torch.Tensor, node_attrs: Optional[torch.Tensor] = None,

@@ -17,6 +17,7 @@ from __future__ import annotations
 
 import torch
 
+from ictc_o3.backends.hip.graph_message import pin_graphs
 from ictc_o3.backends.hip.runtime import require_gpu_fp32
 
 from .model import MaceICTC
@@ -112,7 +113,8 @@ class CapturedEnergyAndForces:
         dev = positions.device
         _warm_up(self._step, warmup, dev)
         self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph):
+        # the capture records the addresses of the cached message-graph CSR tensors: hold them
+        with pin_graphs() as self._message_graphs, torch.cuda.graph(self.graph):
             self._out = self._step()
 
     def _step(self):
@@ -145,7 +147,7 @@ class CapturedTrainingStep:
         _warm_up(lambda: training_step(model, optimizer, self._graph, species=self._species), warmup, dev)
         optimizer.zero_grad(set_to_none=True)
         self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph):
+        with pin_graphs() as self._message_graphs, torch.cuda.graph(self.graph):
             prediction = energy_and_forces(model, **self._graph, training=True, species=self._species)
             self._loss = force_loss(prediction, self._graph["positions"].shape[0])
             self._loss.backward()

@@ -60,3 +60,31 @@ def test_captured_training_step_replays_match_eager(gpu):
         for (name, pa), (_, pb) in zip(model_a.named_parameters(), model_b.named_parameters()):
             if pa.requires_grad:
                 assert_rel(pb, pa, rtol=1e-4, what=f"replay {step} parameter {name}")
+
+
+def test_captured_replay_after_message_graph_cache_eviction(gpu):
+    """The captured step keeps its message-graph CSR tensors alive after the CSR cache has been
+    cycled and cleared and their memory would otherwise have been reused."""
+    import gc
+    from ictc_o3.backends.hip import graph_message as gm
+    from mace_hip import CapturedEnergyAndForces, energy_and_forces
+    model, graph, _, _ = _setup(gpu, atoms=96)
+    model.eval().requires_grad_(False)
+    captured = CapturedEnergyAndForces(model, **graph)
+    n = graph["positions"].shape[0]
+    for seed in range(12):
+        g = torch.Generator(device=gpu).manual_seed(seed)
+        gm.message_graph(torch.randint(0, n, (4000,), device=gpu, generator=g),
+                         torch.randint(0, n, (4000,), device=gpu, generator=g), n, n)
+    gm._GRAPH_CACHE.clear()
+    gc.collect()
+    junk = [torch.full((1 << 16,), -1, dtype=torch.int64, device=gpu) for _ in range(64)]
+    fixed = {k: v for k, v in graph.items() if k != "positions"}
+    pos = _positions(graph, 7, gpu)
+    eager = energy_and_forces(model, positions=pos, **fixed)
+    torch.cuda.synchronize(gpu)
+    got = captured(pos)
+    torch.cuda.synchronize(gpu)
+    del junk
+    for key in ("atomic_energy", "energy", "forces"):
+        assert_rel(got[key], eager[key], rtol=1e-5, what=f"replay after eviction {key}")
