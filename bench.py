@@ -15,12 +15,15 @@ Also reported on the same JSON line:
 * ``extra``: forward-only throughput at 262,144 instances and its roofline, and the
   other configurations of BASELINE.json, each with its own roofline and a bounded
   CPU-oracle sample:
+    - cfg 0, the TP forward at C=64, lmax 2 (11 paths), 65,536 instances (14,116 algorithmic
+      bytes per instance), beside the CPU reference path (the oracle's _forward_index_add);
     - cfg 2, graph message (C=64, lmax 2, 16,384 atoms at 0.1 A^-3, r_c 5 A, gates from
       a random-init 8-Bessel radial MLP): fused gather -> TP -> receiver sum forward, and
       its VJP (edge + node kernels);
     - cfg 3, symmetric contraction (C=128, lmax 3 -> 0e+1o, correlation 3, 65,536 nodes,
       10 species): forward and VJP to the node features (VALU-bound: FLOPs counted on the
-      generated code);
+      generated code as useful FLOPs, and from the committed VALU counters as executed FLOPs,
+      against the published fp32 vector peak and the measured rate of a non-packed FMA probe);
     - cfg 4, MACE-style energy + forces (C=128, lmax 3, 2 interactions, correlation 3,
       2,048 atoms at 0.1 A^-3 with 1.5 A minimum separation, r_c 5 A, 10 species):
       inference and one force-loss training step (AdamW), atom-steps/s, reference timing
@@ -279,6 +282,89 @@ def _event_ms(fn, device, reps: int = 10, warmup: int = 3) -> float:
     return s.elapsed_time(e) / reps
 
 
+def _probe_lib():
+    import ctypes
+    path = os.path.join(ROOT, "ictc-o3-hp-ascend_amd", "ictc_o3", "lib", "libictc_stream_probe.so")
+    if not os.path.exists(path):
+        return None
+    lib = ctypes.CDLL(path)
+    lib.ictc_probe_valu_fma.restype = ctypes.c_int
+    lib.ictc_probe_valu_fma.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    return lib
+
+
+def _valu_fma_tflops(device, grid: int = 16384, iters: int = 2048, reps: int = 5):
+    """fp32 FMA rate of a register-only kernel of scalar (non-packed) v_fma_f32 chains
+    (csrc/stream_probe.hip): the VALU ceiling this build's code can reach; None if the probe
+    library is absent."""
+    import ctypes
+    lib = _probe_lib()
+    if lib is None:
+        return None
+    out = torch.empty(grid * 256, device=device)
+    stream = torch.cuda.current_stream(device)
+
+    def launch():
+        if lib.ictc_probe_valu_fma(out.data_ptr(), iters, grid, ctypes.c_void_p(stream.cuda_stream)) != 0:
+            raise RuntimeError("VALU probe launch failed")
+    ms = _event_ms(launch, device, reps=reps, warmup=2)
+    return 32.0 * iters * grid * 256 / (ms * 1e-3) / 1e12
+
+
+TP0_C, TP0_L, TP0_P, TP0_ROWS = 64, 2, 11, 65536
+TP0_X, TP0_Y, TP0_O = TP0_C * (TP0_L + 1) ** 2, (TP0_L + 1) ** 2, 35 * TP0_C
+BYTES_TP0 = 4 * (TP0_X + TP0_Y + TP0_P * TP0_C + TP0_O)          # 14,116 B/inst
+
+
+def _tp0_inputs(rows: int, device):
+    """cfg 0: x ~ N(0,1) packed ir_mul [E, 576]; unit directions -> ICTC Y [E, 9]; gates in the
+    API layout [E, P, C] ~ N(0,1)/sqrt(P) (the config's w[N,C,P] transposed to the operator's
+    path-major order); tp.weight = 1."""
+    gen = torch.Generator(device="cpu").manual_seed(0)
+    x = torch.randn(rows, TP0_X, generator=gen)
+    n = torch.nn.functional.normalize(torch.randn(rows, 3, generator=gen), dim=-1)
+    g = torch.randn(rows, TP0_P, TP0_C, generator=gen) / math.sqrt(TP0_P)
+    return x, n, g
+
+
+def _bench_tp_cfg0(device):
+    from ictc_o3 import EdgeTensorProduct
+    from ictc_o3.backends.hip.harmonics import direction_harmonics_packed
+    from ictc_o3.backends.hip.tensor_product import _forward_raw
+    op = EdgeTensorProduct.create(channels=TP0_C, input_lmax=TP0_L, edge_lmax=TP0_L, device=device)
+    assert op.tp.num_paths == TP0_P and op.output_width == TP0_O
+    x, n, g = _tp0_inputs(TP0_ROWS, device)
+    x, g = x.to(device), g.to(device).reshape(TP0_ROWS, -1)
+    y = direction_harmonics_packed(n.to(device), TP0_L).contiguous()
+    ms = _event_ms(lambda: _forward_raw(op.plan, x, y, g), device, reps=20)
+    gbs = BYTES_TP0 * TP0_ROWS / (ms * 1e-3) / 1e9
+    return {"workload": "cfg0 channelwise TP forward C64/lmax2 (11 paths), 65,536 instances, ir_mul",
+            "kernel": "tp_forward_kernel<2,2,2,1>", "mean_launch_ms": ms,
+            "instances_per_s": TP0_ROWS / (ms * 1e-3), "vs_published_11.57M": TP0_ROWS / (ms * 1e-3) / 11.57e6,
+            "roofline": {"bound": "hbm", "algorithmic_bytes_per_instance": BYTES_TP0,
+                         "algorithmic_bytes_per_launch": BYTES_TP0 * TP0_ROWS, "achieved": gbs,
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS}}
+
+
+def _cpu_tp_cfg0(budget_s: float = 10.0, rows: int = 8192):
+    """cfg 0 on the CPU reference path: the oracle's _forward_index_add restatement, fp32, all host
+    threads, on the first `rows` instances of the same seeded inputs."""
+    sys.path.insert(0, ROOT)
+    from oracle import ictc_basis as B
+    from oracle.tensor_product import TensorProductOracle
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    op = TensorProductOracle(TP0_C, TP0_L, TP0_L, TP0_L, dtype=torch.float32)
+    x, n, g = _tp0_inputs(TP0_ROWS, "cpu")
+    x, n, g = x[:rows], n[:rows], g[:rows].reshape(rows, -1)
+    y = B.direction_harmonics_packed(n.double(), TP0_L).float()
+    with torch.no_grad():
+        done, dt = _cpu_time(lambda: op.forward(x, y, g), budget_s)
+    return {"value": rows * done / dt, "unit": "instances/s", "cores": threads, "cpu_model": _cpu_model(),
+            "kind": "port", "sample": f"oracle TP forward (reference _forward_index_add restated, PyTorch CPU "
+                                      f"fp32), C64/lmax2, {rows} of the 65,536 instances x {done} calls in {dt:.1f}s"}
+
+
 MSG_C, MSG_L, MSG_P, MSG_ATOMS = 64, 2, 11, 16384
 
 
@@ -387,22 +473,48 @@ def _bench_sc(device):
     w = torch.cat(blocks, 1).to(device).contiguous()
     fwd_ms = _event_ms(lambda: _forward_raw(plan, x, species, w), device)
     vjp_ms = _event_ms(lambda: _vjp_raw(plan, x, species, w, go), device)
-    flops = gen_sc.flop_counts(SC_L, SC_T, SC_K)
+    flops = gen_sc.flop_counts(SC_L, SC_T, SC_K)          # useful FLOPs per (node, channel)
+    executed = _sc_executed_flops()                        # per lane, from the committed VALU counters
+    probe = _valu_fma_tflops(device)
     d, o = (SC_L + 1) ** 2, (SC_T + 1) ** 2
     fwd_bytes = SC_NODES * (4 * SC_C * (d + o) + 8)
     vjp_bytes = SC_NODES * (4 * SC_C * (o + 2 * d) + 8)
 
-    def leg(ms, nbytes, nflops, kernel):
-        tflops = nflops * SC_C * SC_NODES / (ms * 1e-3) / 1e12
+    def leg(ms, nbytes, nflops, kernel, mode):
+        lanes = SC_C * SC_NODES
+        tflops = nflops * lanes / (ms * 1e-3) / 1e12
         gbs = nbytes / (ms * 1e-3) / 1e9
-        return {"mean_ms": ms, "nodes_per_s": SC_NODES / (ms * 1e-3), "kernel": kernel,
-                "bound": "valu", "flops_per_node": nflops * SC_C, "achieved_tflops": tflops,
-                "peak_tflops": VALU_PEAK_TFLOPS, "frac": tflops / VALU_PEAK_TFLOPS,
-                "algorithmic_bytes": nbytes, "achieved_gbs": gbs, "hbm_frac": gbs / HBM_PEAK_GBS}
+        out = {"mean_ms": ms, "nodes_per_s": SC_NODES / (ms * 1e-3), "kernel": kernel,
+               "bound": "valu", "useful_flops_per_node": nflops * SC_C, "achieved_tflops": tflops,
+               "peak_tflops": VALU_PEAK_TFLOPS, "frac": tflops / VALU_PEAK_TFLOPS,
+               "algorithmic_bytes": nbytes, "achieved_gbs": gbs, "hbm_frac": gbs / HBM_PEAK_GBS}
+        if probe:
+            out["frac_of_measured_fma_rate"] = tflops / probe
+        if executed and mode in executed:
+            ex = executed[mode] * lanes / (ms * 1e-3) / 1e12
+            out.update({"executed_flops_per_node": executed[mode] * SC_C, "executed_tflops": ex,
+                        "executed_frac": ex / VALU_PEAK_TFLOPS})
+        return out
     return {"workload": "cfg3 symmetric contraction C128, lmax 3 -> 0e+1o, correlation 3, 65,536 nodes",
-            "weight_columns": plan.ktot,
-            "forward": leg(fwd_ms, fwd_bytes, flops["forward"], "sc_kernel<3,1,3,0>"),
-            "vjp": leg(vjp_ms, vjp_bytes, flops["vjp"], "sc_kernel<3,1,3,1>")}
+            "weight_columns": plan.ktot, "measured_valu_fma_tflops": probe,
+            "forward": leg(fwd_ms, fwd_bytes, flops["forward"], "sc_kernel<3,1,3,0>", "forward"),
+            "vjp": leg(vjp_ms, vjp_bytes, flops["vjp"], "sc_kernel<3,1,3,1>", "vjp")}
+
+
+def _sc_executed_flops():
+    """Executed fp32 FLOPs per (node, channel) lane of the cfg-3 contraction kernels from the
+    committed rocprofv3 VALU-counter summary (64 lanes x (2 FMA + MUL + ADD) per wave
+    instruction, divided by the lanes); None if the summary is absent."""
+    path = os.path.join(ROOT, "profiles", "sc_c128_l3_cfg3_valu_counters.md")
+    out = {}
+    try:
+        for line in open(path):
+            if line.startswith("executed_flops_per_lane_"):
+                key, value = line.split(":", 1)
+                out[key[len("executed_flops_per_lane_"):]] = float(value)
+    except OSError:
+        return None
+    return out or None
 
 
 MACE_ATOMS, MACE_ZS, MACE_CPU_ATOMS = 2048, tuple(range(1, 11)), 128
@@ -551,7 +663,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--kernels-only", action="store_true")
-    ap.add_argument("--only", choices=("tp", "message", "sc", "mace", "graph"), default=None,
+    ap.add_argument("--only", choices=("tp", "tp0", "message", "sc", "mace", "graph"), default=None,
                     help="run one section and print its JSON (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -565,8 +677,9 @@ def main() -> int:
     if args.kernels_only:
         _kernels_only(op.plan, device)
         return 0
-    if args.only in ("message", "sc", "mace", "graph"):
-        fn = {"message": _bench_message, "sc": _bench_sc, "mace": _bench_mace, "graph": _bench_graph}[args.only]
+    if args.only in ("tp0", "message", "sc", "mace", "graph"):
+        fn = {"tp0": _bench_tp_cfg0, "message": _bench_message, "sc": _bench_sc, "mace": _bench_mace,
+              "graph": _bench_graph}[args.only]
         print(json.dumps({args.only: fn(device)}), flush=True)
         return 0
     elapsed, vjp_ms, fwd_ms = _time_gpu(args, op.plan, device)
@@ -579,9 +692,11 @@ def main() -> int:
     cpu = None if args.no_cpu else _cpu_baseline()
     others = {}
     if args.only is None:
-        others = {"message_cfg2": _bench_message(device), "sc_cfg3": _bench_sc(device),
+        others = {"tp_cfg0": _bench_tp_cfg0(device), "message_cfg2": _bench_message(device),
+                  "sc_cfg3": _bench_sc(device),
                   "mace_cfg4": _bench_mace(device), "radius_graph": _bench_graph(device)}
         if not args.no_cpu:
+            others["tp_cfg0"]["cpu_baseline"] = _cpu_tp_cfg0()
             others["message_cfg2"]["cpu_baseline"] = _cpu_message()
             others["sc_cfg3"]["cpu_baseline"] = _cpu_sc()
             others["mace_cfg4"]["cpu_baseline"] = _cpu_mace()

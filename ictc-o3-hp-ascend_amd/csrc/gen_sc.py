@@ -436,17 +436,12 @@ def weight_columns(lmax: int, target: int, corr: int) -> int:
 
 
 def flop_counts(lmax: int, target: int, corr: int) -> Dict[str, int]:
-    """Floating-point operations per (node, channel) of the emitted float forward and VJP,
-    counted on the emitted code: an fma counts 2, a multiply or an add 1."""
-    import re
-    text = emit(lmax, target, corr)
-    forward = text[text.index("void forward"):text.index("void vjp")]
-    if "  } else {" in forward:          # float instantiation: the straight-line branch only
-        forward = forward[:forward.index("  } else {")]
-    bodies = {"forward": forward, "vjp": text[text.index("void vjp"):text.index("void weight_features")]}
-    # an sfma whose accumulator is the literal 0 is a multiply (1 FLOP)
-    return {k: 2 * b.count("sfma(") - len(re.findall(r"sfma\([^()]*, 0\.0f\)", b)) + len(re.findall(r" [*+] ", b))
-            for k, b in bodies.items()}
+    """Useful floating-point operations per (node, channel) of the emitted float forward and
+    VJP (sc_flops.py: products with an exact zero or +-1 and sums with an exact zero are free;
+    an fma is its product plus its sum)."""
+    import sc_flops
+    D, NO, ktot = (lmax + 1) ** 2, (target + 1) ** 2, weight_columns(lmax, target, corr)
+    return sc_flops.useful_flops(emit(lmax, target, corr), D, NO, ktot)
 
 
 def configs():

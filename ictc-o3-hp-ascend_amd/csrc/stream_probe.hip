@@ -7,6 +7,11 @@
 // kernel gives the bandwidth an ideal streaming kernel reaches for that traffic on this
 // GPU, the practical ceiling beside the 8 TB/s datasheet peak.  Loads use the default or
 // the non-temporal cache policy (NT): callers take the better of the two.
+//
+// A second probe measures the fp32 vector (VALU) FMA rate this build can reach: every lane
+// runs 16 independent fma chains on registers (scalar v_fma/v_fmac: the library is compiled
+// without packed FP32, so no v_pk_fma_f32 can appear) and writes one float, so the work is
+// 32 FLOPs per lane per iteration and memory traffic is negligible.
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 
@@ -32,6 +37,20 @@ __global__ void __launch_bounds__(256) stream_mix_kernel(const f4* __restrict__ 
   }
 }
 
+__global__ void __launch_bounds__(256) valu_fma_kernel(float* __restrict__ out, int iters, float b, float c) {
+  float acc[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[i] = static_cast<float>(threadIdx.x + i);
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] = __builtin_fmaf(acc[i], b, c);
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) s += acc[i];
+  out[blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x] = s;
+}
+
 template <int R, int W, bool NT>
 int launch(const void* a, void* b, size_t units, int grid, hipStream_t stream) {
   hipLaunchKernelGGL((stream_mix_kernel<R, W, NT>), dim3(grid), dim3(256), 0, stream, static_cast<const f4*>(a),
@@ -53,4 +72,13 @@ extern "C" int ictc_probe_stream_mix(int reads, int writes, int nt_loads, const 
   if (reads == 2 && writes == 5)
     return nt_loads ? launch<2, 5, true>(a, b, units, grid, stream) : launch<2, 5, false>(a, b, units, grid, stream);
   return -1;
+}
+
+// fp32 FMA throughput: grid blocks of 256 lanes, each lane 16 chains x iters fmas
+// (32 * iters FLOPs per lane); out must hold grid * 256 floats.  Returns 0 or -1.
+extern "C" int ictc_probe_valu_fma(void* out, int iters, int grid, hipStream_t stream) {
+  if (out == nullptr || iters <= 0 || grid <= 0) return -1;
+  hipLaunchKernelGGL(valu_fma_kernel, dim3(grid), dim3(256), 0, stream, static_cast<float*>(out), iters,
+                     0.999f, 1e-3f);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
 }
