@@ -289,13 +289,14 @@ def _probe_lib():
         return None
     lib = ctypes.CDLL(path)
     lib.ictc_probe_valu_fma.restype = ctypes.c_int
-    lib.ictc_probe_valu_fma.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    lib.ictc_probe_valu_fma.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
     return lib
 
 
 def _valu_fma_tflops(device, grid: int = 16384, iters: int = 2048, reps: int = 5):
-    """fp32 FMA rate of a register-only kernel of scalar (non-packed) v_fma_f32 chains
-    (csrc/stream_probe.hip): the VALU ceiling this build's code can reach; None if the probe
+    """fp32 FMA rate of register-only kernels of scalar (non-packed) fma chains
+    (csrc/stream_probe.hip) in both instruction forms the compiler emits: v_fma_f32 with SGPR
+    operands (VOP3) and v_fmac_f32 with every operand in a VGPR (VOP2); None if the probe
     library is absent."""
     import ctypes
     lib = _probe_lib()
@@ -303,12 +304,14 @@ def _valu_fma_tflops(device, grid: int = 16384, iters: int = 2048, reps: int = 5
         return None
     out = torch.empty(grid * 256, device=device)
     stream = torch.cuda.current_stream(device)
-
-    def launch():
-        if lib.ictc_probe_valu_fma(out.data_ptr(), iters, grid, ctypes.c_void_p(stream.cuda_stream)) != 0:
-            raise RuntimeError("VALU probe launch failed")
-    ms = _event_ms(launch, device, reps=reps, warmup=2)
-    return 32.0 * iters * grid * 256 / (ms * 1e-3) / 1e12
+    rates = {}
+    for name, vgpr in (("v_fma_f32_sgpr_operands", 0), ("v_fmac_f32_vgpr_operands", 1)):
+        def launch():
+            if lib.ictc_probe_valu_fma(out.data_ptr(), iters, grid, vgpr, ctypes.c_void_p(stream.cuda_stream)) != 0:
+                raise RuntimeError("VALU probe launch failed")
+        ms = _event_ms(launch, device, reps=reps, warmup=2)
+        rates[name] = 32.0 * iters * grid * 256 / (ms * 1e-3) / 1e12
+    return rates
 
 
 TP0_C, TP0_L, TP0_P, TP0_ROWS = 64, 2, 11, 65536
@@ -489,7 +492,7 @@ def _bench_sc(device):
                "peak_tflops": VALU_PEAK_TFLOPS, "frac": tflops / VALU_PEAK_TFLOPS,
                "algorithmic_bytes": nbytes, "achieved_gbs": gbs, "hbm_frac": gbs / HBM_PEAK_GBS}
         if probe:
-            out["frac_of_measured_fma_rate"] = tflops / probe
+            out["frac_of_measured_fma_rate"] = tflops / max(probe.values())
         if executed and mode in executed:
             ex = executed[mode] * lanes / (ms * 1e-3) / 1e12
             out.update({"executed_flops_per_node": executed[mode] * SC_C, "executed_tflops": ex,

@@ -45,7 +45,10 @@ FLAGS = ["--offload-arch=" + ARCH, "-O3", "-std=c++20", "-fPIC", "-Wno-c99-desig
          "-I", INCLUDE, "-I", HERE]
 
 API_SOURCES = ["tp_api.hip", "harmonics_api.hip", "message_api.hip", "sc_api.hip", "graph_api.hip",
-               "elementwise_api.hip"]
+               "elementwise_api.hip", "blas_api.hip"]
+# rocBLAS (the channel-linear products): the same SONAME as the copy torch loads, which the
+# dynamic linker then binds to
+LINK_LIBS = ["-L/opt/rocm/lib", "-lrocblas"]
 HARM_LMAX = 6
 INSTANCE_KINDS = {
     "fwd": ("tp_kernels.hpp", "template int launch_forward<{a}, {b}, {c}>(const ictc_tp_desc&, "
@@ -164,7 +167,7 @@ def build(jobs: int | None = None, verbose: bool = True) -> str:
         objs = list(pool.map(_compile, units))
     os.makedirs(LIB_DIR, exist_ok=True)
     tmp = LIB + ".tmp"
-    res = subprocess.run([HIPCC, "--offload-arch=" + ARCH, "-shared", "-fPIC", *objs, "-o", tmp],
+    res = subprocess.run([HIPCC, "--offload-arch=" + ARCH, "-shared", "-fPIC", *objs, *LINK_LIBS, "-o", tmp],
                          capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")

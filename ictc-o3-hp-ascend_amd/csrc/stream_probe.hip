@@ -37,13 +37,19 @@ __global__ void __launch_bounds__(256) stream_mix_kernel(const f4* __restrict__ 
   }
 }
 
+// VGPR_B: acc += b * c with b, c per-lane register values (v_fmac_f32, the VOP2 form with the
+// accumulator as addend and every operand in a VGPR) rather than acc = acc * b + c with b, c
+// kernel arguments in SGPRs (v_fma_f32, VOP3).
+template <bool VGPR_B>
 __global__ void __launch_bounds__(256) valu_fma_kernel(float* __restrict__ out, int iters, float b, float c) {
   float acc[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) acc[i] = static_cast<float>(threadIdx.x + i);
+  const float bv = VGPR_B ? b + 1e-7f * static_cast<float>(threadIdx.x & 1) : b;
+  const float cv = VGPR_B ? c * static_cast<float>(1 + (threadIdx.x & 1)) : c;
   for (int it = 0; it < iters; ++it) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) acc[i] = __builtin_fmaf(acc[i], b, c);
+    for (int i = 0; i < 16; ++i) acc[i] = VGPR_B ? __builtin_fmaf(bv, cv, acc[i]) : __builtin_fmaf(acc[i], bv, cv);
   }
   float s = 0.f;
 #pragma unroll
@@ -75,10 +81,15 @@ extern "C" int ictc_probe_stream_mix(int reads, int writes, int nt_loads, const 
 }
 
 // fp32 FMA throughput: grid blocks of 256 lanes, each lane 16 chains x iters fmas
-// (32 * iters FLOPs per lane); out must hold grid * 256 floats.  Returns 0 or -1.
-extern "C" int ictc_probe_valu_fma(void* out, int iters, int grid, hipStream_t stream) {
+// (32 * iters FLOPs per lane); out must hold grid * 256 floats.  vgpr_operands != 0 keeps
+// every fma operand in a VGPR.  Returns 0 or -1.
+extern "C" int ictc_probe_valu_fma(void* out, int iters, int grid, int vgpr_operands, hipStream_t stream) {
   if (out == nullptr || iters <= 0 || grid <= 0) return -1;
-  hipLaunchKernelGGL(valu_fma_kernel, dim3(grid), dim3(256), 0, stream, static_cast<float*>(out), iters,
-                     0.999f, 1e-3f);
+  if (vgpr_operands)
+    hipLaunchKernelGGL(valu_fma_kernel<true>, dim3(grid), dim3(256), 0, stream, static_cast<float*>(out), iters,
+                       0.999f, 1e-3f);
+  else
+    hipLaunchKernelGGL(valu_fma_kernel<false>, dim3(grid), dim3(256), 0, stream, static_cast<float*>(out), iters,
+                       0.999f, 1e-3f);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }

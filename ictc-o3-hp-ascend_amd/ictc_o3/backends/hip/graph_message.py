@@ -311,9 +311,9 @@ def vjp(plan, graph, need, x, y, g, go, bonds=None):
     return tuple(o if n else None for o, n in zip(outs, need))
 
 
-def graph_message(plan: TensorProductPlan, features: torch.Tensor, harmonics: torch.Tensor,
-                  gates: torch.Tensor, src: torch.Tensor, dst: torch.Tensor, *,
-                  nodes_dst: Optional[int] = None, mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+def packed_graph_message(plan: TensorProductPlan, features: torch.Tensor, harmonics: torch.Tensor,
+                         gates: torch.Tensor, src: torch.Tensor, dst: torch.Tensor, *,
+                         nodes_dst: Optional[int] = None, mask: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Packed ir_mul message: features [N_src, C(L_in+1)^2], harmonics [E,(L_e+1)^2],
     gates [E, P*C] (path weights folded in), src/dst int64 [E] -> [N_dst, NOC*C]."""
     nodes_src = features.shape[0]

@@ -204,8 +204,8 @@ def vjp(plan, need, x, y, g, go):
     return tuple(o if n else None for o, n in zip(outs, need))
 
 
-def tensor_product(plan: TensorProductPlan, features: torch.Tensor, harmonics: torch.Tensor,
-                   gates: torch.Tensor) -> torch.Tensor:
+def packed_tensor_product(plan: TensorProductPlan, features: torch.Tensor, harmonics: torch.Tensor,
+                          gates: torch.Tensor) -> torch.Tensor:
     """Packed ir_mul TP: features [E, C(L_in+1)^2], harmonics [E,(L_e+1)^2],
     gates [E, P*C] (path weights already folded in) -> [E, NOC*C]."""
     if plan.is_full:
@@ -236,3 +236,108 @@ def packed_to_blocks(plan: TensorProductPlan, out: torch.Tensor) -> Dict[int, to
             rows, count * c, width)
         off += span
     return result
+
+
+# ----------------------------------------------------------------------------- reference hooks
+def owner_degrees(owner) -> Tuple[int, int]:
+    """(input lmax, edge lmax) the owner's paths need."""
+    return max(p[0] for p in owner.paths), max(p[1] for p in owner.paths)
+
+
+def pack_features(owner, features: Dict[int, torch.Tensor], rows: int) -> torch.Tensor:
+    """{l: [rows, C, 2l+1]} -> packed ir_mul [rows, C(L_in+1)^2]; degrees the dict leaves out are
+    zero (the reference skips their paths)."""
+    if not features:
+        raise ValueError("Feature blocks must not be empty")
+    c = owner.channels
+    for l, value in features.items():
+        if value.ndim != 3 or value.shape != (rows, c, 2 * l + 1):
+            raise ValueError("Feature blocks must have shape [N,C,2l+1]")
+    sample = next(iter(features.values()))
+    input_lmax = owner_degrees(owner)[0]
+    return blocks_to_packed({l: features[l] if l in features else sample.new_zeros(rows, c, 2 * l + 1)
+                             for l in range(input_lmax + 1)}, input_lmax)
+
+
+def pack_harmonics(owner, harmonics: Dict[int, torch.Tensor], rows: int, like: torch.Tensor) -> torch.Tensor:
+    """{l: [rows, 1, 2l+1]} -> [rows, (L_e+1)^2]; left-out degrees are zero."""
+    for l, value in harmonics.items():
+        if value.shape not in ((rows, 1, 2 * l + 1), (rows, 2 * l + 1)):
+            raise ValueError("Harmonic blocks must have shape [E,1,2l+1]")
+    edge_lmax = owner_degrees(owner)[1]
+    return torch.cat([harmonics[l].reshape(rows, 2 * l + 1) if l in harmonics else like.new_zeros(rows, 2 * l + 1)
+                      for l in range(edge_lmax + 1)], -1)
+
+
+def tensor_product(owner, features, harmonics, gates=None):
+    """The reference's TP hook (``backends/ascend/tensor_product.py:89-125``, called from the owner's
+    forward, ``ictd_irreps.py:2773-2775``): owner = EdgeWeightedPathPreservingTensorProduct,
+    features {l: [E,C,2l+1]}, harmonics {l: [E,1,2l+1]}, gates [E,P*C], [E,P,C] or None (the
+    owner's weight alone) -> {l: [E, count_l*C, 2l+1]} for every l <= owner.lmax."""
+    from .runtime import require_gpu_fp32
+    sample = next(iter(features.values()))
+    rows, channels = sample.shape[0], owner.channels
+    if gates is not None and gates.shape not in ((rows, owner.num_paths * channels),
+                                                 (rows, owner.num_paths, channels)):
+        raise ValueError("External gates must have shape [E,P*C] or [E,P,C]")
+    require_gpu_fp32(owner.weight, *features.values(), *harmonics.values(), *(() if gates is None else (gates,)))
+    x = pack_features(owner, features, rows)
+    y = pack_harmonics(owner, harmonics, rows, sample)
+    plan = owner.hip_plan(*owner_degrees(owner))
+    return packed_to_blocks(plan, packed_tensor_product(plan, x, y, owner.effective_gates(gates, rows)))
+
+
+def destination_nodes(owner, source_nodes: int) -> int:
+    """Owned destinations of a larger source halo (reference ``tensor_product.py:151-156``):
+    ``owner._ascend_destination_nodes`` (or ``_destination_nodes``), default all source nodes."""
+    nodes = getattr(owner, "_destination_nodes", getattr(owner, "_ascend_destination_nodes", source_nodes))
+    if not isinstance(nodes, int) or isinstance(nodes, bool) or not 0 <= nodes <= source_nodes:
+        raise ValueError("Destination node count must be between zero and the source node count")
+    return nodes
+
+
+def check_message_operands(owner, device, harmonics_rows, gates, src, dst, mask, edge_chunk_size):
+    """Shared argument checks of the message hooks (reference ``tensor_product.py:159-218``,
+    ``ascendc/graph.py:7-19``)."""
+    from .runtime import require_gpu_fp32
+    if edge_chunk_size is not None and (not isinstance(edge_chunk_size, int) or isinstance(edge_chunk_size, bool)
+                                        or edge_chunk_size < 1):
+        raise ValueError("Edge chunk size must be positive")
+    for value in (src, dst):
+        if value.ndim != 1 or value.dtype != torch.int64 or value.device != device:
+            raise ValueError("Graph indices must be int64 vectors on the GPU")
+    if dst.shape != src.shape:
+        raise ValueError("Source and destination index shapes must match")
+    edges = src.numel()
+    if any(rows != edges for rows in harmonics_rows):
+        raise ValueError("Harmonic row counts must match graph edges")
+    if gates is not None:
+        if gates.shape not in ((edges, owner.num_paths * owner.channels), (edges, owner.num_paths, owner.channels)):
+            raise ValueError("External gates must have shape [E,P*C] or [E,P,C]")
+        require_gpu_fp32(gates)
+    if mask is not None:
+        if mask.shape not in ((edges,), (edges, 1)) or mask.device != device:
+            raise ValueError("Expected an edge mask [E] or [E,1] on the feature device")
+        require_gpu_fp32(mask)
+    return edges
+
+
+def graph_message(owner, features, harmonics, gates, src, dst, mask=None, *, edge_chunk_size=16384):
+    """The reference's message hook (``backends/ascend/tensor_product.py:159-218``, called by the
+    interaction block at ``pure_cartesian_ictd_fix.py:1787-1800``):
+    node_out[n] = sum_{e: dst(e) = n} mask_e TP(features[src e], harmonics[e], gates[e]) as
+    {l: [N_dst, count_l*C, 2l+1]}.  One fused HIP kernel family (receiver CSR, no atomics, no
+    per-edge messages in HBM); ``edge_chunk_size`` is validated and otherwise unused."""
+    from .graph_message import packed_graph_message
+    from .runtime import require_gpu_fp32
+    sample = next(iter(features.values()))
+    nodes = sample.shape[0]
+    edges = check_message_operands(owner, sample.device, [v.shape[0] for v in harmonics.values()], gates,
+                                   src, dst, mask, edge_chunk_size)
+    require_gpu_fp32(owner.weight, *features.values(), *harmonics.values())
+    x = pack_features(owner, features, nodes)
+    y = pack_harmonics(owner, harmonics, edges, sample)
+    plan = owner.hip_plan(*owner_degrees(owner))
+    out = packed_graph_message(plan, x, y, owner.effective_gates(gates, edges), src, dst,
+                               nodes_dst=destination_nodes(owner, nodes), mask=mask)
+    return packed_to_blocks(plan, out)

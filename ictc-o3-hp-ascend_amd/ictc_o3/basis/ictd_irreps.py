@@ -315,18 +315,7 @@ class EdgeWeightedPathPreservingTensorProduct(nn.Module):
 
     def forward(self, x1: Dict[int, torch.Tensor], x2: Dict[int, torch.Tensor],
                 gates: Optional[torch.Tensor] = None) -> Dict[int, torch.Tensor]:
-        from ictc_o3.backends.hip import tensor_product as hip_tp
-        from ictc_o3.backends.hip.runtime import require_gpu_fp32
-        input_lmax = max(p[0] for p in self.paths)
-        edge_lmax = max(p[1] for p in self.paths)
-        sample = next(iter(x1.values()))
-        rows = sample.shape[0]
-        feats = [x1[l] if l in x1 else sample.new_zeros(rows, self.channels, 2 * l + 1)
-                 for l in range(input_lmax + 1)]
-        harms = [x2[l].reshape(rows, 2 * l + 1) if l in x2 else sample.new_zeros(rows, 2 * l + 1)
-                 for l in range(edge_lmax + 1)]
-        require_gpu_fp32(*feats, *harms, *(() if gates is None else (gates,)))
-        plan = self.hip_plan(input_lmax, edge_lmax)
-        packed = hip_tp.blocks_to_packed(dict(enumerate(feats)), input_lmax)
-        out = hip_tp.tensor_product(plan, packed, torch.cat(harms, -1), self.effective_gates(gates, rows))
-        return hip_tp.packed_to_blocks(plan, out)
+        """The reference's HP hook (ictd_irreps.py:2773-2775) taken unconditionally: the HIP
+        ``tensor_product(owner, x1, x2, gates)``."""
+        from ictc_o3.backends.hip.tensor_product import tensor_product
+        return tensor_product(self, x1, x2, gates)

@@ -9,6 +9,7 @@ from __future__ import annotations
 
 import torch
 
+from ictc_o3.backends.hip.linear import channel_linear, species_channel_linear
 from ictc_o3.backends.hip.runtime import require_gpu_fp32, strict_fp32
 
 
@@ -147,14 +148,14 @@ class EdgeTensorProduct(torch.nn.Module):
         return rows
 
     def forward(self, features, harmonics, gates):
-        from ictc_o3.backends.hip.tensor_product import tensor_product
+        from ictc_o3.backends.hip.tensor_product import packed_tensor_product
         rows = self._check(features, harmonics, gates)
         if not rows:
             zero = sum(v.sum() * 0 for v in (features, harmonics, self.tp.weight,
                                              *(() if gates is None else (gates,))))
             return features.new_empty(0, self.output_width) + zero
-        out = tensor_product(self.plan, self._to_ir_mul_features(features), harmonics,
-                             self.tp.effective_gates(gates, rows))
+        out = packed_tensor_product(self.plan, self._to_ir_mul_features(features), harmonics,
+                                    self.tp.effective_gates(gates, rows))
         return self._from_ir_mul_output(out)
 
 
@@ -180,35 +181,19 @@ class PackedGraphMessage(EdgeTensorProduct):
         return cls(op.tp, input_lmax=op.input_lmax, edge_lmax=op.edge_lmax,
                    layout=op.layout, edge_chunk_size=edge_chunk_size)
 
-    def _destination_nodes(self, source_nodes):
-        nodes = getattr(self.tp, "_destination_nodes",
-                        getattr(self.tp, "_ascend_destination_nodes", source_nodes))
-        if not isinstance(nodes, int) or isinstance(nodes, bool) or not 0 <= nodes <= source_nodes:
-            raise ValueError("Destination node count must be between zero and the source node count")
-        return nodes
-
     def _message(self, features, harmonics, gates, src, dst, mask):
-        from ictc_o3.backends.hip.graph_message import graph_message
-        for value in (src, dst):
-            if value.ndim != 1 or value.dtype != torch.int64 or value.device != features.device:
-                raise ValueError("Graph indices must be int64 vectors on the GPU")
-        if dst.shape != src.shape:
-            raise ValueError("Source and destination index shapes must match")
-        edges = src.numel()
-        require_gpu_fp32(features, harmonics, gates, self.tp.weight)
+        from ictc_o3.backends.hip.graph_message import packed_graph_message
+        from ictc_o3.backends.hip.tensor_product import check_message_operands, destination_nodes
+        edges = check_message_operands(self.tp, features.device, [harmonics.shape[0]], gates, src, dst, mask,
+                                       self.edge_chunk_size)
+        require_gpu_fp32(features, harmonics, self.tp.weight)
         if features.ndim != 2 or features.shape[1] != self.tp.channels * (self.input_lmax + 1) ** 2:
             raise ValueError("Packed features must have shape [E,C*(L_in+1)^2]")
         if harmonics.shape != (edges, (self.edge_lmax + 1) ** 2):
             raise ValueError("Harmonics must have shape [E,(L_edge+1)^2]")
-        if gates.shape not in ((edges, self.gate_width), (edges, self.tp.num_paths, self.tp.channels)):
-            raise ValueError("External gates must have shape [E,P*C] or [E,P,C]")
-        if mask is not None:
-            if mask.shape not in ((edges,), (edges, 1)):
-                raise ValueError("Edge mask must have shape [E] or [E,1]")
-            require_gpu_fp32(mask)
-        nodes = self._destination_nodes(features.shape[0])
-        return graph_message(self.plan, self._to_ir_mul_features(features), harmonics,
-                             self.tp.effective_gates(gates, edges), src, dst, nodes_dst=nodes, mask=mask)
+        nodes = destination_nodes(self.tp, features.shape[0])
+        return packed_graph_message(self.plan, self._to_ir_mul_features(features), harmonics,
+                                    self.tp.effective_gates(gates, edges), src, dst, nodes_dst=nodes, mask=mask)
 
     def forward(self, features, harmonics, gates, src, dst, mask=None):
         return self._from_ir_mul_output(self._message(features, harmonics, gates, src, dst, mask))
@@ -216,23 +201,13 @@ class PackedGraphMessage(EdgeTensorProduct):
 
 class GraphMessage(PackedGraphMessage):
     """Dictionary block interface for the same message map (reference ``operators.py:166-170``):
-    features {l: [N,C,2l+1]}, harmonics {l: [E,1,2l+1]} -> {l: [N_dst, count_l*C, 2l+1]}."""
+    features {l: [N,C,2l+1]}, harmonics {l: [E,1,2l+1]} -> {l: [N_dst, count_l*C, 2l+1]}, through
+    the ``graph_message`` hook as in the reference."""
 
     def forward(self, features, harmonics, gates, src, dst, mask=None):
-        from ictc_o3.backends.hip.tensor_product import blocks_to_packed, packed_to_blocks
-        sample = next(iter(features.values()))
-        rows = src.numel()
-        feats = {l: features[l] if l in features else sample.new_zeros(sample.shape[0], self.tp.channels, 2 * l + 1)
-                 for l in range(self.input_lmax + 1)}
-        harms = torch.cat([harmonics[l].reshape(rows, 2 * l + 1) if l in harmonics
-                           else sample.new_zeros(rows, 2 * l + 1) for l in range(self.edge_lmax + 1)], -1)
-        packed = blocks_to_packed(feats, self.input_lmax)
-        saved, self.layout = self.layout, "ir_mul"
-        try:
-            out = self._message(packed, harms, gates, src, dst, mask)
-        finally:
-            self.layout = saved
-        return packed_to_blocks(self.plan, out)
+        from ictc_o3.backends.hip.tensor_product import graph_message
+        return graph_message(self.tp, features, harmonics, gates, src, dst, mask,
+                             edge_chunk_size=self.edge_chunk_size)
 
 
 def direction_harmonics(directions, lmax, *, policy="auto"):
@@ -293,5 +268,5 @@ def normalized_silu(features, scale=1.):
 
 
 __all__ = ["EdgeTensorProduct", "PackedGraphMessage", "GraphMessage", "direction_harmonics",
-           "create_symmetric_contraction", "configure_symmetric_contraction", "normalized_silu",
-           "strict_fp32"]
+           "create_symmetric_contraction", "configure_symmetric_contraction",
+           "channel_linear", "species_channel_linear", "normalized_silu", "strict_fp32"]

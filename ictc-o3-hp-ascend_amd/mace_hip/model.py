@@ -40,7 +40,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from ictc_o3.backends.hip.graph_message import graph_message
+from ictc_o3.backends.hip.graph_message import packed_graph_message
 from ictc_o3.backends.hip.harmonics import direction_harmonics_packed
 from ictc_o3.basis.ictd_irreps import EdgeWeightedPathPreservingTensorProduct
 from ictc_o3.ops.symmetric_contraction import ICTDPureUSymmetricContractionSO3
@@ -202,7 +202,7 @@ class Interaction(nn.Module):
         x1 = self.linear_up.to_ir_mul(h)
         gates = self.tp.effective_gates(self.radial_mlp(edge_feats), edge_feats.shape[0])
         plan = self.tp.hip_plan(self.input_lmax, self.edge_lmax)
-        m = graph_message(plan, x1, harmonics, gates, src, dst, nodes_dst=n)
+        m = packed_graph_message(plan, x1, harmonics, gates, src, dst, nodes_dst=n)
         message = self.message_linear(m) / max(self.avg_num_neighbors, 1e-8)
         sc = self.self_connection(h[:, :self.channels], species)
         return message, sc

@@ -2,9 +2,11 @@
  * ictc_hip.h -- C ABI of the MI355X (gfx950) ictc_o3 equivariant operator library.
  *
  * libictc_hip.so exports plain extern "C" entry points taking device pointers,
- * sizes and a hipStream_t.  Nothing here allocates device memory: the caller owns
- * every input, output and workspace buffer.  Launches are asynchronous on the
- * given stream; every entry point is reentrant and keeps no mutable global state.
+ * sizes and a hipStream_t.  Nothing here allocates device memory (the caller owns
+ * every input, output and workspace buffer) except ictc_hip_sgemm, whose rocBLAS
+ * handle may allocate its own workspace.  Launches are asynchronous on the given
+ * stream; every entry point is reentrant and keeps no mutable global state other
+ * than ictc_hip_sgemm's per-thread rocBLAS handles.
  *
  * Data layout (all float32, row-major, channel-contiguous "ir_mul" packing):
  *   features   [rows, C*(L_in+1)^2]     per degree l: (2l+1) rows of C channels
@@ -374,6 +376,18 @@ int ictc_hip_radius_graph_fill_sorted(const ictc_cell_grid* grid, const double* 
  */
 int ictc_hip_silu_second(const float* x, const float* grad, const float* cotangent,
                          float* grad_grad, float* grad_x, int64_t n, hipStream_t stream);
+
+/*
+ * Row-major fp32 product C[m,n] = alpha * op(A) op(B) + beta * C on rocBLAS, for the dense
+ * channel linears around the operators.  op(A) is [m,k]: A is stored [m,k] (lda >= k) or,
+ * with trans_a != 0, [k,m] (lda >= m); likewise B with op(B) [k,n].  Each host thread uses
+ * one rocBLAS handle per device; the call is asynchronous on `stream`.  Replaces the fp32
+ * Cube GEMM binding of the reference (ictc_o3/ascendc/op_host/matmul_bindings.cpp:24-96,
+ * ascendc/linear.py:12-58) behind channel_linear (backends/ascend/linear.py:8-52).
+ */
+int ictc_hip_sgemm(int trans_a, int trans_b, int64_t m, int64_t n, int64_t k, float alpha,
+                   const float* a, int64_t lda, const float* b, int64_t ldb, float beta, float* c,
+                   int64_t ldc, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -1,10 +1,13 @@
-"""mace_hip.linear: the split-K matrix product equals a @ b, and its first and second
-derivatives (every derivative is the same Function) pass gradcheck / gradgradcheck.
-Small row blocks force the split path (several blocks plus a remainder) on the CPU."""
+"""ictc_o3.backends.hip.linear (the model's dense layers): the split-K matrix product equals
+a @ b, and its first and second derivatives (every derivative is the same Function) pass
+gradcheck / gradgradcheck.  Small row blocks force the split path (several blocks plus a
+remainder) on the CPU.  On the GPU the plain products run through ictc_hip_sgemm with the
+operands' storage order passed as transpose flags."""
 import pytest
 import torch
 
-from mace_hip import linear as L
+from ictc_o3.backends.hip import linear as L
+from mace_hip.linear import Linear
 
 
 @pytest.fixture
@@ -33,7 +36,7 @@ def test_split_path_taken_for_transposed_activations(small_blocks):
 
 
 def test_linear_module_keeps_parameter_contract():
-    lin = L.Linear(8, 5)
+    lin = Linear(8, 5)
     assert [n for n, _ in lin.named_parameters()] == ["weight"] and lin.weight.shape == (5, 8)
     x = torch.randn(7, 3, 8)
     assert torch.allclose(lin(x), x @ lin.weight.t(), atol=1e-6)
@@ -42,13 +45,13 @@ def test_linear_module_keeps_parameter_contract():
 @pytest.mark.gpu
 @pytest.mark.parametrize("k,n", [(64, 64), (64, 512), (64, 2944), (8, 64)])
 def test_tall_products_on_gpu(k, n):
-    """Edge-sized products ([E, K] @ [K, N], E above TALL_ROWS) take the rocBLAS route with a
-    column-major right operand; value, first and second derivatives (all through the same
-    Function) against float64, with the right operand both row-major and a transposed weight."""
+    """Edge-sized products ([E, K] @ [K, N]) on ictc_hip_sgemm; value, first and second
+    derivatives (all through the same Function, the weight gradient through the split-K
+    path) against float64, with the right operand both row-major and a transposed weight."""
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
     dev = torch.device("cuda", 0)
-    rows = L.TALL_ROWS + 1234
+    rows = 40000 + 1234
     g = torch.Generator().manual_seed(n + k)
     a64 = torch.randn(rows, k, generator=g, dtype=torch.float64)
     w64 = torch.randn(n, k, generator=g, dtype=torch.float64) / 8
@@ -70,3 +73,37 @@ def test_tall_products_on_gpu(k, n):
         for name, x, y in zip(("product", "input grad", "weight grad of input grad"), got, expect):
             err = (x.double().cpu() - y).abs().max() / y.abs().max()
             assert err < 1e-5, f"{name} (transposed={transposed}): relative error {err:.2e}"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_sgemm_storage_orders(ta, tb):
+    """ictc_hip_sgemm through every storage order of both operands, including row strides
+    larger than the row (slices of wider tensors), against float64."""
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    dev = torch.device("cuda", 0)
+    g = torch.Generator().manual_seed(ta * 2 + tb)
+    m, k, n = 37, 19, 23
+    a = torch.randn(m, k, generator=g, dtype=torch.float64)
+    b = torch.randn(k, n, generator=g, dtype=torch.float64)
+    wide_a = torch.randn(m + 5, k + 3, generator=g, dtype=torch.float64) if not ta else \
+        torch.randn(k + 3, m + 5, generator=g, dtype=torch.float64)
+    wide_b = torch.randn(k + 2, n + 4, generator=g, dtype=torch.float64) if not tb else \
+        torch.randn(n + 4, k + 2, generator=g, dtype=torch.float64)
+    if ta:
+        wide_a[:k, :m] = a.t()
+        av = wide_a.float().to(dev)[:k, :m].t()
+    else:
+        wide_a[:m, :k] = a
+        av = wide_a.float().to(dev)[:m, :k]
+    if tb:
+        wide_b[:n, :k] = b.t()
+        bv = wide_b.float().to(dev)[:n, :k].t()
+    else:
+        wide_b[:k, :n] = b
+        bv = wide_b.float().to(dev)[:k, :n]
+    assert L._storage(av)[1] == ta and L._storage(bv)[1] == tb
+    got = L._sgemm(av, bv).double().cpu()
+    err = (got - a @ b).abs().max() / (a @ b).abs().max()
+    assert err < 1e-6, f"relative error {err:.2e}"

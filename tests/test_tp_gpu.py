@@ -184,7 +184,7 @@ def test_owner_dict_interface(gpu):
 def test_full_size_properties(gpu):
     """At the benchmark size (C128/L3, 131,072 instances): trilinearity of the forward
     and the adjoint identity <F(x,Y,g), o> = <x, Gx> = <g, Gg> = <Y, GY>."""
-    from ictc_o3.backends.hip.tensor_product import tensor_product, vjp
+    from ictc_o3.backends.hip.tensor_product import packed_tensor_product as tensor_product, vjp
     op = _op(128, 3, 3, 3, "ir_mul", gpu)
     plan = op.plan
     rows = 131072
