@@ -325,9 +325,9 @@ def packed_graph_message(plan: TensorProductPlan, features: torch.Tensor, harmon
     if not plan.is_full:
         slots = torch.tensor(plan.slot_of_path, device=gates.device)
         gates = gates.new_zeros(rows, len(plan.full_paths), c).index_copy(
-            1, slots, gates.reshape(rows, plan.num_paths, c)).reshape(rows, -1)
+            1, slots, gates.reshape(rows, plan.num_paths, c)).reshape(rows, len(plan.full_paths) * c)
     out = _Forward.apply(plan, graph, features.contiguous(), harmonics.contiguous(), gates.contiguous())
     if not plan.is_full:
         keep = torch.tensor(plan.output_rows, device=gates.device)
-        out = out.reshape(nodes_dst, -1, c).index_select(1, keep).reshape(nodes_dst, -1)
+        out = out.reshape(nodes_dst, -1, c).index_select(1, keep).reshape(nodes_dst, len(plan.output_rows) * c)
     return out

@@ -10,9 +10,11 @@ Routing of ``mm`` (measured on MI355X at the MACE cfg-4 shapes, E = 105,634 edge
 
 * plain products call rocBLAS explicitly through ``ictc_hip_sgemm`` with the operands' own
   storage order passed as transpose flags (no copies, no process-wide library preference);
-  for an edge-sized left operand against a weight (``x @ W^T``) that is rocBLAS with a
-  column-major right operand, 0.485 vs 0.571 ms for ``[E,64]@[64,2944]`` on hipBLASLt;
-  a short reduction (K < 16, ``[E,8]@[8,64]``) keeps a row-major right operand (25 vs 35 us);
+  an edge-sized left operand against a weight (``x @ W^T``, and ``g @ W`` in the backward, where
+  the weight-sized right operand is copied column-major) runs with a column-major right operand:
+  0.485 vs 0.571 ms for ``[E,64]@[64,2944]`` on hipBLASLt, 0.372 vs 0.39-0.41 ms for
+  ``[E,2944]@[2944,64]``; a short reduction (K < 16, ``[E,8]@[8,64]``) keeps a row-major right
+  operand (25 vs 35 us);
 * a weight gradient ``g^T x`` reduces over ~10^5 rows into a small output, which one GEMM
   covers with a handful of output tiles (0.3 ms for 0.9 GFLOP); it is split into row blocks
   multiplied as one batched GEMM (torch.bmm on its default library) and summed: 2,048-row
@@ -34,6 +36,8 @@ SPLIT_ROWS_LARGE = 8192
 SPLIT_LARGE_OUTPUT = 1 << 17
 SPLIT_SINGLE_GEMM_OUTPUT = 4096
 ROW_MAJOR_RIGHT_BELOW_K = 16
+TALL_ROWS = 32768          # edge-sized left operand ...
+TALL_MAX_RIGHT = 1 << 22   # ... against a weight-sized right operand: column-major right operand
 
 
 def _storage(t: torch.Tensor):
@@ -70,7 +74,12 @@ def _sgemm(a: torch.Tensor, b: torch.Tensor, *, row_major_b: bool = False) -> to
 def _plain(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     if not a.is_cuda:
         return a @ b
-    return _sgemm(a, b, row_major_b=b.shape[0] < ROW_MAJOR_RIGHT_BELOW_K)
+    m, k = a.shape
+    if k < ROW_MAJOR_RIGHT_BELOW_K:
+        return _sgemm(a, b, row_major_b=True)
+    if m >= TALL_ROWS and k * b.shape[1] <= TALL_MAX_RIGHT and b.stride(0) != 1:
+        b = b.t().contiguous().t()             # weight-sized copy: column-major right operand
+    return _sgemm(a, b)
 
 
 def _product(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:

@@ -64,7 +64,8 @@ def _species_sum(plan: ContractionPlan, species, phi):
     species one-hot matrix (a few species rows: atomic adds into them would all contend)."""
     n = phi.shape[0]
     onehot = torch.nn.functional.one_hot(species, plan.num_elements).to(torch.float32)
-    return torch.mm(onehot.t(), phi.reshape(n, -1)).reshape(plan.num_elements, plan.ktot, plan.channels)
+    return torch.mm(onehot.t(), phi.reshape(n, plan.ktot * plan.channels)).reshape(
+        plan.num_elements, plan.ktot, plan.channels)
 
 
 def _weight_grad(plan: ContractionPlan, x, species, go):

@@ -215,15 +215,16 @@ def packed_tensor_product(plan: TensorProductPlan, features: torch.Tensor, harmo
     full_gates = gates.new_zeros(rows, len(plan.full_paths), c).index_copy(
         1, slots, gates.reshape(rows, plan.num_paths, c))
     out = _Forward.apply(plan, features.contiguous(), harmonics.contiguous(),
-                         full_gates.reshape(rows, -1))
+                         full_gates.reshape(rows, len(plan.full_paths) * c))
     keep = torch.tensor(plan.output_rows, device=gates.device)
-    return out.reshape(rows, -1, c).index_select(1, keep).reshape(rows, -1)
+    return out.reshape(rows, -1, c).index_select(1, keep).reshape(rows, len(plan.output_rows) * c)
 
 
 def blocks_to_packed(blocks: Dict[int, torch.Tensor], lmax: int) -> torch.Tensor:
     """{l: [E,C,2l+1]} -> ir_mul packed [E, C(lmax+1)^2]."""
     rows = next(iter(blocks.values())).shape[0]
-    return torch.cat([blocks[l].transpose(1, 2).reshape(rows, -1) for l in range(lmax + 1)], -1)
+    return torch.cat([blocks[l].transpose(1, 2).reshape(rows, blocks[l].shape[1] * (2 * l + 1))
+                      for l in range(lmax + 1)], -1)
 
 
 def packed_to_blocks(plan: TensorProductPlan, out: torch.Tensor) -> Dict[int, torch.Tensor]:

@@ -311,7 +311,7 @@ class EdgeWeightedPathPreservingTensorProduct(nn.Module):
             if bool(torch.all(w == 1)):
                 self._unit_weight_key = key
                 return gates
-        return (gates.reshape(rows, self.num_paths, self.channels) * w[None]).reshape(rows, -1)
+        return (gates.reshape(rows, self.num_paths, self.channels) * w[None]).reshape(rows, self.num_paths * self.channels)
 
     def forward(self, x1: Dict[int, torch.Tensor], x2: Dict[int, torch.Tensor],
                 gates: Optional[torch.Tensor] = None) -> Dict[int, torch.Tensor]:

@@ -58,7 +58,7 @@ def test_tensor_product_hook(gpu, gate_form):
     y = _harm(rows, 2, gen)
     g = torch.randn(rows, ref.num_paths, c, generator=gen, dtype=torch.float64) / math.sqrt(ref.num_paths)
     gates = {"flat": g.reshape(rows, -1), "path_major": g, "none": None}[gate_form]
-    x_full = dict(x, **{1: torch.zeros(rows, c, 3, dtype=torch.float64)})
+    x_full = {**x, 1: torch.zeros(rows, c, 3, dtype=torch.float64)}
     expect = ref.forward_blocks(x_full, y, torch.ones_like(g) if gates is None else gates)
     got = tensor_product(owner, {l: v.float().to(gpu) for l, v in x.items()},
                          {l: v.float().to(gpu) for l, v in y.items()},

@@ -42,3 +42,9 @@ def test_write_through_data_after_invalidation():
     assert torch.equal(tp.effective_gates(gates, 3), _expected(tp, gates))
     tp.weight.data = torch.ones_like(tp.weight) * 0.5        # new storage: detected by address
     assert torch.equal(tp.effective_gates(gates, 3), _expected(tp, gates))
+
+
+def test_live_weight_fold_of_an_empty_edge_set():
+    tp = _owner()
+    tp.weight.requires_grad_(True)
+    assert tp.effective_gates(torch.randn(0, tp.num_paths * tp.channels), 0).shape == (0, tp.num_paths * tp.channels)
