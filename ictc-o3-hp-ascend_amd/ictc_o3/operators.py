@@ -224,10 +224,13 @@ def direction_harmonics(directions, lmax, *, policy="auto"):
 
 
 def configure_symmetric_contraction(module, *, policy="auto", training=False):
-    """Select the HIP contraction for a module (reference ``operators.py:189-201``)."""
-    from ictc_o3.ops.symmetric_contraction import ICTDPureUSymmetricContractionSO3
-    if not isinstance(module, ICTDPureUSymmetricContractionSO3):
-        raise TypeError("Expected an ICTC symmetric contraction")
+    """Select the HIP contraction for a module (reference ``operators.py:189-201``): the bridge-U
+    module the factory returns, or the pure-ICTC variant.  Checks the compiled configuration and,
+    for the bridge-U module, that its U buffers pass the reconstruction gate."""
+    from ictc_o3.ops.symmetric_contraction import (ICTDBridgeUSymmetricContractionSO3,
+                                                   ICTDPureUSymmetricContractionSO3)
+    if not isinstance(module, (ICTDBridgeUSymmetricContractionSO3, ICTDPureUSymmetricContractionSO3)):
+        raise TypeError("Expected an ICTC bridge-U symmetric contraction")
     if policy not in ("auto", "generated", "reference"):
         raise ValueError("policy must be auto, generated or reference")
     if policy == "reference":
@@ -237,13 +240,16 @@ def configure_symmetric_contraction(module, *, policy="auto", training=False):
         raise ValueError("symmetric contraction supports correlation 1, 2 and 3")
     strict_fp32()
     module.plan  # compiled configuration check
+    if isinstance(module, ICTDBridgeUSymmetricContractionSO3):
+        module.weight_table(next(module.parameters()))   # reconstruction gate
+    module._ascend_hp = True
     return {"backend": "hip", "selected": "generated"}
 
 
 def create_symmetric_contraction(*, num_elements, lmax, target_lmax=None, channels=64, correlation=3,
                                  device="cuda", policy="generated", training=False):
-    """Factory (reference ``operators.py:204-218``).  U tensors are the ICTC coupling
-    chains of the reference's e3nn-free generator (``ictd_irreps.py:1387-1517``)."""
+    """Factory (reference ``operators.py:204-218``): the bridge-U contraction (U tensors of the
+    e3nn generalized coupling folded into the ICTC basis) on the HIP kernels."""
     for value, name in ((num_elements, "num_elements"), (channels, "channels"), (correlation, "correlation")):
         _positive_integer(value, name)
     if correlation not in (1, 2, 3):
@@ -252,10 +258,10 @@ def create_symmetric_contraction(*, num_elements, lmax, target_lmax=None, channe
     target_lmax = lmax if target_lmax is None else target_lmax
     _degree(target_lmax, "target_lmax")
     device = _require_gpu_device(device)
-    from ictc_o3.ops.symmetric_contraction import ICTDPureUSymmetricContractionSO3
-    module = ICTDPureUSymmetricContractionSO3(num_elements=num_elements, channels=channels, lmax=lmax,
-                                              target_lmax=target_lmax, correlation=correlation
-                                              ).to(device=device, dtype=torch.float32)
+    from ictc_o3.ops.symmetric_contraction import ICTDBridgeUSymmetricContractionSO3
+    module = ICTDBridgeUSymmetricContractionSO3(num_elements=num_elements, channels=channels, lmax=lmax,
+                                                target_lmax=target_lmax, correlation=correlation
+                                                ).to(device=device, dtype=torch.float32)
     configure_symmetric_contraction(module, policy=policy, training=training)
     return module
 

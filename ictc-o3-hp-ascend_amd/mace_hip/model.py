@@ -43,7 +43,7 @@ import torch.nn.functional as F
 from ictc_o3.backends.hip.graph_message import packed_graph_message
 from ictc_o3.backends.hip.harmonics import direction_harmonics_packed
 from ictc_o3.basis.ictd_irreps import EdgeWeightedPathPreservingTensorProduct
-from ictc_o3.ops.symmetric_contraction import ICTDPureUSymmetricContractionSO3
+from ictc_o3.ops.symmetric_contraction import ICTDBridgeUSymmetricContractionSO3
 
 from .activation import silu
 from .linear import Linear, linear
@@ -212,7 +212,8 @@ class Product(nn.Module):
     def __init__(self, *, channels: int, lmax: int, target_lmax: int, correlation: int, num_elements: int):
         super().__init__()
         self.channels, self.target_lmax = channels, target_lmax
-        self.symmetric_contractions = ICTDPureUSymmetricContractionSO3(
+        # ICTDBridgeUProductBasisBlockSO3 (:1145-1195): the bridge-U contraction the reference ships
+        self.symmetric_contractions = ICTDBridgeUSymmetricContractionSO3(
             num_elements=num_elements, channels=channels, lmax=lmax, target_lmax=target_lmax,
             correlation=correlation)
         self.linear = IrrepsLinear(channels, target_lmax)

@@ -5,7 +5,7 @@ edge geometry and masks (:2914-2937), ICTC direction harmonics (``ictd_irreps.py
 Bessel x polynomial-cutoff radial features (``radial_basis.py:11-92``), the interaction
 block (:1762-2055: linear_up, radial MLP ``fc`` :1545-1553, gather -> TP -> mask ->
 index_add message, path-preserving message linear / avg_num_neighbors, element-conditioned
-self connection), the product block (:1145-1195 with the pure-ICTC contraction, o3.Linear,
+self connection), the product block (:1145-1195 with the module's bridge-U contraction, o3.Linear,
 ``_add_product_self_connection`` :94-118) and the readouts (:1434-1449,
 ``pure_cartesian_ictd_layers.py:46-70``); energy and forces as ``hp/runtime.py:84-119``.
 
@@ -79,12 +79,16 @@ class MaceOracle:
             self.scs.append(SymmetricContractionOracle(num_elements, channels, lmax, target, correlation, seed=0))
 
     def _sc_weights(self, t, target):
+        """Weights and U buffers of product t's bridge-U contraction, read by name; the oracle
+        contracts with the module's own U (``ops/symmetric_contraction.py:92-206``)."""
         w = {}
         for l in range(target + 1):
-            pre = f"products.{t}.symmetric_contractions.contractions.{l}"
+            pre = f"products.{t}.symmetric_contractions.symmetric_contractions.contractions.{l}"
             w[(l, self.corr)] = self.p[f"{pre}.weights_max"]
             for i, nu in enumerate(range(self.corr - 1, 0, -1)):
                 w[(l, nu)] = self.p[f"{pre}.weights.{i}"]
+            for nu in range(1, self.corr + 1):
+                self.scs[t].u[(l, nu)] = self.p[f"{pre}.U_matrix_{nu}"].to(torch.float64)
         return w
 
     def atomic_energies(self, pos, species, src, dst, shifts, cell, batch):

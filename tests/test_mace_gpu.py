@@ -38,7 +38,8 @@ def _setup(gpu, *, channels=32, atoms=48, density=0.05, cutoff=4.0, seed=3):
     graph = dict(positions=st.positions.to(gpu), atomic_numbers=z.to(gpu),
                  batch=torch.zeros(atoms, dtype=torch.int64, device=gpu), edge_src=src.to(gpu),
                  edge_dst=dst.to(gpu), edge_shifts=shifts.to(gpu), cell=st.cell[None].to(gpu))
-    oracle = MaceOracle({k: v.detach().double().cpu() for k, v in model.named_parameters()},
+    state = [*model.named_parameters(), *model.named_buffers()]      # buffers: the contractions' U
+    oracle = MaceOracle({k: v.detach().double().cpu() for k, v in state},
                         channels=channels, lmax=3, num_interactions=2, correlation=3, num_elements=len(ZS),
                         cutoff=cutoff, avg_num_neighbors=12.0)
     cpu = dict(pos=st.positions.double(), species=st.species, src=src, dst=dst, shifts=shifts.double(),

@@ -92,7 +92,7 @@ def _oracle(channels=8, seed=0):
         for name, p in model.named_parameters():
             if "linear_up" in name or "self_connection" in name:
                 p.add_(torch.randn_like(p) * 0.2)
-    params = {k: v.detach().double() for k, v in model.named_parameters()}
+    params = {k: v.detach().double() for k, v in [*model.named_parameters(), *model.named_buffers()]}
     return MaceOracle(params, channels=channels, lmax=2, num_interactions=2, correlation=3, num_elements=3,
                       cutoff=3.5, avg_num_neighbors=8.0)
 

@@ -17,9 +17,12 @@ pytestmark = pytest.mark.gpu
 
 
 def _module(ref, device):
-    from ictc_o3 import create_symmetric_contraction
-    mod = create_symmetric_contraction(num_elements=ref.S, lmax=ref.lmax, target_lmax=ref.target_lmax,
-                                       channels=ref.C, correlation=ref.correlation, device=device)
+    """The pure-ICTC module: its weights address the coupling chains the oracle's U holds."""
+    from ictc_o3 import configure_symmetric_contraction
+    from ictc_o3.ops.symmetric_contraction import ICTDPureUSymmetricContractionSO3
+    mod = ICTDPureUSymmetricContractionSO3(num_elements=ref.S, lmax=ref.lmax, target_lmax=ref.target_lmax,
+                                           channels=ref.C, correlation=ref.correlation).to(device)
+    configure_symmetric_contraction(mod)
     with torch.no_grad():
         for l, con in enumerate(mod.contractions):
             con.weights_max.copy_(ref.weights[(l, ref.correlation)].float())
