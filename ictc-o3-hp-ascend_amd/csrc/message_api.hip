@@ -1,6 +1,8 @@
 // extern "C" entry points of the graph-message family; per-degree instantiations of the
 // bond, forward and edge-adjoint kernels are compiled in generated/msg_inst_*.hip, the
 // source-node segmented sum (which depends on the input degree only) here.
+#include <mutex>
+
 #include "message_kernels.hpp"
 
 namespace ictc {
@@ -108,6 +110,58 @@ inline int msg_common(const ictc_tp_desc* d, int64_t nodes_src, int64_t nodes_ds
 
 }  // namespace ictc
 
+// Staging for ictc_hip_message_edge_grad_static: the per-chunk harmonics partials
+// [edges, chunks, NY] of wide channel counts.  One array per device, held until the process
+// ends.  Host code never passes this name to a kernel or a copy (on the host it is only a
+// stand-in for the device symbol): its device address is fetched once per device with
+// hipGetSymbolAddress, with that device current, and only that address is used.
+static __device__ __align__(256) float scratch[ICTC_MSG_STATIC_SCRATCH_FLOATS];
+
+namespace ictc {
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_lock;
+float* g_scratch_address[kMaxDevices] = {};
+
+// Device address of `scratch` on the device that owns `stream` (the current device: a stream
+// of another device is rejected).
+int static_scratch(hipStream_t stream, float** address) {
+  int device = -1;
+  if (hipGetDevice(&device) != hipSuccess) return ICTC_ERR_LAUNCH;
+  if (device < 0 || device >= kMaxDevices) return ICTC_ERR_UNSUPPORTED;
+  if (stream != nullptr) {
+    hipDevice_t owner = -1;
+    if (hipStreamGetDevice(stream, &owner) != hipSuccess) return ICTC_ERR_LAUNCH;
+    if (owner != device) return ICTC_ERR_INVALID_ARGUMENT;
+  }
+  std::lock_guard<std::mutex> guard(g_scratch_lock);
+  if (g_scratch_address[device] == nullptr) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) return ICTC_ERR_LAUNCH;
+    g_scratch_address[device] = static_cast<float*>(p);
+  }
+  *address = g_scratch_address[device];
+  return ICTC_OK;
+}
+
+// out[e, j] = sum_q partial[e, q, j] (q ascending), one thread per (e, j).
+__global__ void __launch_bounds__(256)
+chunk_sum_kernel(const float* __restrict__ partial, float* __restrict__ out, int64_t total, int chunks,
+                 int width) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int64_t e = i / width;
+  const int64_t j = i - e * width;
+  const float* p = partial + e * chunks * width + j;
+  float s = p[0];
+  for (int q = 1; q < chunks; ++q) s += p[static_cast<int64_t>(q) * width];
+  out[i] = s;
+}
+
+}  // namespace
+}  // namespace ictc
+
 extern "C" {
 
 int ictc_hip_message_chunks(int channels) { return channels < 1 ? -1 : (channels + 63) / 64; }
@@ -159,6 +213,35 @@ int ictc_hip_message_edge_grad(const ictc_tp_desc* desc, const float* node_featu
   if (fn == nullptr) return ICTC_ERR_UNSUPPORTED;
   return fn(*desc, node_features, bonds, gates, grad_out, src, dst_rowptr, dst_perm, grad_harmonics_partial,
             grad_gates, edge_grad_features, nodes_src, nodes_dst, stream);
+}
+
+int ictc_hip_message_edge_grad_static(const ictc_tp_desc* desc, const float* node_features, const float* bonds,
+                                      const float* gates, const float* grad_out, const int64_t* src,
+                                      const int64_t* dst_rowptr, const int64_t* dst_perm, float* grad_harmonics,
+                                      float* grad_gates, float* edge_grad_features, int64_t nodes_src,
+                                      int64_t nodes_dst, int64_t edges, hipStream_t stream) {
+  const int st = ictc::msg_common(desc, nodes_src, nodes_dst, edges);
+  if (st != ICTC_OK) return st;
+  if (edges == 0 || nodes_dst == 0 || (!grad_harmonics && !grad_gates && !edge_grad_features)) return ICTC_OK;
+  if (!bonds || !gates || !grad_out || !src || !dst_rowptr) return ICTC_ERR_INVALID_ARGUMENT;
+  if ((grad_harmonics || grad_gates) && !node_features) return ICTC_ERR_INVALID_ARGUMENT;
+  const ictc::MsgEdge fn = ictc::kMsgEdge[ictc::msg_index(desc)];
+  if (fn == nullptr) return ICTC_ERR_UNSUPPORTED;
+  const int chunks = ictc_hip_message_chunks(desc->channels);
+  const int ny = (desc->edge_lmax + 1) * (desc->edge_lmax + 1);
+  float* partial = grad_harmonics;   // one chunk: the kernel writes the sums itself
+  if (grad_harmonics != nullptr && chunks > 1) {
+    if (edges > ICTC_MSG_STATIC_SCRATCH_FLOATS / (static_cast<int64_t>(chunks) * ny)) return ICTC_ERR_CAPACITY;
+    const int sst = ictc::static_scratch(stream, &partial);
+    if (sst != ICTC_OK) return sst;
+  }
+  const int r = fn(*desc, node_features, bonds, gates, grad_out, src, dst_rowptr, dst_perm, partial, grad_gates,
+                   edge_grad_features, nodes_src, nodes_dst, stream);
+  if (r != ICTC_OK || partial == grad_harmonics) return r;
+  const int64_t total = edges * ny;
+  hipLaunchKernelGGL(ictc::chunk_sum_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0,
+                     stream, partial, grad_harmonics, total, chunks, ny);
+  return hipGetLastError() == hipSuccess ? ICTC_OK : ICTC_ERR_LAUNCH;
 }
 
 int ictc_hip_message_forward_tangent(const ictc_tp_desc* desc, const float* node_features, const float* bonds,

@@ -58,11 +58,12 @@ const char* ictc_hip_status_string(int status) {
     case ICTC_ERR_UNSUPPORTED: return "unsupported degree combination";
     case ICTC_ERR_LAUNCH: return "kernel launch failed";
     case ICTC_ERR_INDEX: return "index out of range";
+    case ICTC_ERR_CAPACITY: return "input exceeds the static scratch capacity";
     default: return "unknown status";
   }
 }
 
-int ictc_hip_abi_version(void) { return 7; }
+int ictc_hip_abi_version(void) { return 8; }
 
 int ictc_hip_tp_slot_count(int input_lmax, int edge_lmax, int output_lmax) {
   if (input_lmax < 0 || edge_lmax < 0 || output_lmax < 0 || input_lmax > 3 || edge_lmax > 3 ||

@@ -15,7 +15,7 @@ import torch  # noqa: F401  (must precede CDLL, see module docstring)
 
 MAX_PATHS = 64
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libictc_hip.so")
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 
 class TpDesc(ctypes.Structure):
@@ -72,6 +72,8 @@ _SIGNATURES = {
                                                 _I64, _I64, _I64, _P]),
     "ictc_hip_message_edge_grad": (ctypes.c_int, [ctypes.POINTER(TpDesc), _P, _P, _P, _P, _P, _P, _P,
                                                   _P, _P, _P, _I64, _I64, _I64, _P]),
+    "ictc_hip_message_edge_grad_static": (ctypes.c_int, [ctypes.POINTER(TpDesc), _P, _P, _P, _P, _P, _P, _P,
+                                                         _P, _P, _P, _I64, _I64, _I64, _P]),
     "ictc_hip_message_node_grad": (ctypes.c_int, [ctypes.POINTER(TpDesc), _P, _P, _P, _P, _I64, _I64, _P]),
     "ictc_hip_message_forward_tangent": (ctypes.c_int, [ctypes.POINTER(TpDesc)] + [_P] * 10 + [_I64, _I64, _I64,
                                                                                           _P]),

@@ -36,7 +36,8 @@ typedef enum ictc_status {
     ICTC_ERR_INVALID_ARGUMENT = 1,   /* null pointer, negative size, bad descriptor */
     ICTC_ERR_UNSUPPORTED = 2,        /* degree combination not compiled in */
     ICTC_ERR_LAUNCH = 3,             /* hipLaunchKernel / hipGetLastError failed */
-    ICTC_ERR_INDEX = 4               /* graph or species index out of range (checked kernels) */
+    ICTC_ERR_INDEX = 4,              /* graph or species index out of range (checked kernels) */
+    ICTC_ERR_CAPACITY = 5            /* input exceeds a static scratch array (nothing launched) */
 } ictc_status;
 
 /*
@@ -167,6 +168,29 @@ int ictc_hip_message_edge_grad(const ictc_tp_desc* desc, const float* node_featu
                                const int64_t* dst_perm, float* grad_harmonics_partial,
                                float* grad_gates, float* edge_grad_features, int64_t nodes_src,
                                int64_t nodes_dst, int64_t edges, hipStream_t stream);
+
+/*
+ * No counterpart in the reference: for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * ictc_hip_message_edge_grad with the harmonics gradient already summed over the channel
+ * chunks: grad_harmonics [edges, (L_e+1)^2] = sum_q grad_harmonics_partial[e, q, :], so no
+ * partial buffer is needed; grad_gates and edge_grad_features are as above (bit-identical).
+ * With more than one 64-channel chunk the partials are staged in a library-owned device array
+ * of ICTC_MSG_STATIC_SCRATCH_FLOATS floats (16 MiB on each GPU the library runs on, held until
+ * the process ends); edges * chunks * (L_e+1)^2 above that size returns ICTC_ERR_CAPACITY
+ * before any launch.  Every row the call reads from the array it first writes (a receiver CSR
+ * that covers every edge once, as for the entry point above).  The stream must belong to the
+ * current device.  Allocates nothing.  Calls that overlap on one GPU (concurrent streams or
+ * host threads) share the array and race: serialise them.
+ */
+#define ICTC_MSG_STATIC_SCRATCH_FLOATS 4194304
+int ictc_hip_message_edge_grad_static(const ictc_tp_desc* desc, const float* node_features,
+                                      const float* bonds, const float* gates, const float* grad_out,
+                                      const int64_t* src, const int64_t* dst_rowptr,
+                                      const int64_t* dst_perm, float* grad_harmonics,
+                                      float* grad_gates, float* edge_grad_features,
+                                      int64_t nodes_src, int64_t nodes_dst, int64_t edges,
+                                      hipStream_t stream);
 
 /*
  * Mixed second derivatives of the message, as directional derivatives (JVPs) in the
