@@ -5,7 +5,8 @@
 // [k, n]; trans_a != 0 means A is stored as [k, m] (lda >= m), otherwise as [m, k]
 // (lda >= k); likewise B.  rocBLAS is column-major, so the row-major product is issued as the
 // column-major C^T = op(B)^T op(A)^T.  Each host thread keeps one rocBLAS handle per device
-// (a handle must not be used by two threads at once); the stream is set on every call.
+// (a handle must not be used by two threads at once); the stream is set on every call, and
+// atomics are disallowed on every handle so repeated products are bit-identical.
 #include <hip/hip_runtime.h>
 #include <rocblas/rocblas.h>
 
@@ -23,6 +24,11 @@ rocblas_handle handle_for_current_device() {
   if (it != handles.end()) return it->second;
   rocblas_handle h = nullptr;
   if (rocblas_create_handle(&h) != rocblas_status_success) return nullptr;
+  // no kernels that accumulate through atomics: a product's result is the same on every run
+  if (rocblas_set_atomics_mode(h, rocblas_atomics_not_allowed) != rocblas_status_success) {
+    rocblas_destroy_handle(h);
+    return nullptr;
+  }
   handles.emplace(device, h);
   return h;
 }

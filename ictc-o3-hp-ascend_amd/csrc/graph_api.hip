@@ -69,4 +69,21 @@ int ictc_hip_radius_graph_fill_sorted(const ictc_cell_grid* grid, const double* 
   return hipGetLastError() == hipSuccess ? ICTC_OK : ICTC_ERR_LAUNCH;
 }
 
+int ictc_hip_edge_vector_grad(int dtype, const void* grad_vec, const int64_t* dst_rowptr, const int64_t* dst_perm,
+                              const int64_t* src_rowptr, const int64_t* src_perm, void* grad_pos, int64_t nodes,
+                              hipStream_t stream) {
+  if (nodes < 0 || (dtype != 0 && dtype != 1)) return ICTC_ERR_INVALID_ARGUMENT;
+  if (nodes == 0) return ICTC_OK;
+  if (!grad_pos || !dst_rowptr || !src_rowptr || !grad_vec) return ICTC_ERR_INVALID_ARGUMENT;
+  if (dtype == 0)
+    hipLaunchKernelGGL(ictc::edge_vector_grad_kernel<float>, ictc::wave_blocks(nodes),
+                       dim3(ictc::kGraphWaves * ictc::kWave), 0, stream, static_cast<const float*>(grad_vec),
+                       dst_rowptr, dst_perm, src_rowptr, src_perm, static_cast<float*>(grad_pos), nodes);
+  else
+    hipLaunchKernelGGL(ictc::edge_vector_grad_kernel<double>, ictc::wave_blocks(nodes),
+                       dim3(ictc::kGraphWaves * ictc::kWave), 0, stream, static_cast<const double*>(grad_vec),
+                       dst_rowptr, dst_perm, src_rowptr, src_perm, static_cast<double*>(grad_pos), nodes);
+  return hipGetLastError() == hipSuccess ? ICTC_OK : ICTC_ERR_LAUNCH;
+}
+
 }  // extern "C"

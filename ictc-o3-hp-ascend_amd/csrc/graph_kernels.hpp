@@ -204,4 +204,48 @@ radius_fill_kernel(const double* __restrict__ wpos, const int32_t* __restrict__ 
   }
 }
 
+// ----------------------------------------------------------------------------- edge vectors
+// Adjoint of the edge vectors vec[e] = pos[dst(e)] - pos[src(e)] (+ constant shift):
+//   grad_pos[n] = sum_{e: dst(e) = n} grad_vec[e] - sum_{e: src(e) = n} grad_vec[e],
+// one wave per node over its receiver-CSR and source-CSR rows; lane l takes the slots
+// l, l + 64, ... of each row and the lanes' partials meet in a fixed butterfly, so the result
+// does not depend on scheduling (no atomics).
+template <typename T>
+__device__ __forceinline__ T wave_sum_t(T v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+template <typename T>
+__global__ void __launch_bounds__(kGraphWaves * kWave)
+edge_vector_grad_kernel(const T* __restrict__ grad_vec, const int64_t* __restrict__ rowptr_dst,
+                        const int64_t* __restrict__ perm_dst, const int64_t* __restrict__ rowptr_src,
+                        const int64_t* __restrict__ perm_src, T* __restrict__ grad_pos, int64_t nodes) {
+  const int64_t n = static_cast<int64_t>(blockIdx.x) * kGraphWaves + threadIdx.x / kWave;
+  if (n >= nodes) return;
+  const int lane = threadIdx.x & (kWave - 1);
+  T a0 = 0, a1 = 0, a2 = 0;
+  for (int64_t s = rowptr_dst[n] + lane; s < rowptr_dst[n + 1]; s += kWave) {
+    const int64_t e = perm_dst ? perm_dst[s] : s;
+    a0 += grad_vec[3 * e];
+    a1 += grad_vec[3 * e + 1];
+    a2 += grad_vec[3 * e + 2];
+  }
+  for (int64_t s = rowptr_src[n] + lane; s < rowptr_src[n + 1]; s += kWave) {
+    const int64_t e = perm_src ? perm_src[s] : s;
+    a0 -= grad_vec[3 * e];
+    a1 -= grad_vec[3 * e + 1];
+    a2 -= grad_vec[3 * e + 2];
+  }
+  a0 = wave_sum_t(a0);
+  a1 = wave_sum_t(a1);
+  a2 = wave_sum_t(a2);
+  if (lane == 0) {
+    grad_pos[3 * n] = a0;
+    grad_pos[3 * n + 1] = a1;
+    grad_pos[3 * n + 2] = a2;
+  }
+}
+
 }  // namespace ictc

@@ -15,7 +15,7 @@ import torch  # noqa: F401  (must precede CDLL, see module docstring)
 
 MAX_PATHS = 64
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libictc_hip.so")
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 
 class TpDesc(ctypes.Structure):
@@ -79,6 +79,7 @@ _SIGNATURES = {
                                                                                           _P]),
     "ictc_hip_message_edge_grad_tangent": (ctypes.c_int, [ctypes.POINTER(TpDesc)] + [_P] * 13 + [_I64, _I64,
                                                                                             _I64, _P]),
+    "ictc_hip_edge_vector_grad": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _P, _P, _P, _I64, _P]),
     "ictc_hip_silu_second": (ctypes.c_int, [_P, _P, _P, _P, _P, _I64, _P]),
     "ictc_hip_sgemm": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, _I64, _I64, _I64, ctypes.c_float, _P, _I64, _P,
                                       _I64, ctypes.c_float, _P, _I64, _P]),

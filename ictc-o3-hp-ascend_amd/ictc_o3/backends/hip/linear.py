@@ -162,7 +162,9 @@ def species_channel_linear(features, weight, species, bias=None):
     index = species.to(torch.int64).view(n, 1, 1, 1).expand(n, m, 1, o)
     picked = every.gather(2, index).squeeze(2)                      # [N, M, O]
     if bias is not None:
-        picked = picked + bias.index_select(0, species.to(torch.int64)).unsqueeze(1)
+        # one_hot(species) @ bias: the bias gradient is a GEMM (fixed order), not an atomic index_add
+        hot = (species.to(torch.int64).view(n, 1) == torch.arange(s, device=species.device)).to(torch.float32)
+        picked = picked + mm(hot, bias).unsqueeze(1)
     return picked.transpose(1, 2)
 
 

@@ -25,11 +25,12 @@ Layouts.  Node features between blocks are the reference's flat mul_ir layout
 kernels read directly.  ``linear_up`` writes the channel-contiguous ir_mul layout the
 message kernels read (the transpose is folded into its GEMM), and ``message_linear``
 reads the message kernel's packed ir_mul output and writes mul_ir (again folded).
-The product's symmetric contraction uses the pure-ICTC coupling basis
-(``ICTDPureUProductBasisBlockSO3``, the reference's ``ictd-pure-u`` backend, :1397-1431)
-because the bridge basis needs e3nn; the surrounding ``o3.Linear`` is restated as a
-per-degree C x C map with weights ~ N(0, 1) scaled by 1/sqrt(C) (e3nn's element
-normalisation for one path).
+The product's symmetric contraction is the bridge-U module (``ICTDBridgeUProductBasisBlockSO3``,
+the reference's default ``ictd-bridge-u`` backend, :1145-1195); the surrounding ``o3.Linear`` is
+restated as a per-degree C x C map with weights ~ N(0, 1) scaled by 1/sqrt(C) (e3nn's element
+normalisation for one path).  Every sum over atoms or edges has a fixed order (HIP kernels over
+CSR rows, GEMMs against indicator rows), so energies, forces and training gradients are
+bit-identical from run to run.
 """
 from __future__ import annotations
 
@@ -46,6 +47,7 @@ from ictc_o3.basis.ictd_irreps import EdgeWeightedPathPreservingTensorProduct
 from ictc_o3.ops.symmetric_contraction import ICTDBridgeUSymmetricContractionSO3
 
 from .activation import silu
+from .geometry import edge_vectors, one_hot_rows
 from .linear import Linear, linear
 from .radial import bessel_embedding
 
@@ -269,8 +271,8 @@ class MaceICTC(nn.Module):
         # index_select rather than advanced indexing (cheaper to issue; same gather)
         edge_cell = cell.index_select(0, batch.index_select(0, edge_src)).to(pos.dtype)
         shift_vecs = (edge_shifts.to(pos.dtype).unsqueeze(-1) * edge_cell).sum(1)
-        # index_select: its backward is a direct index_add (advanced indexing would scatter through a sort)
-        vec = pos.index_select(0, edge_dst) - pos.index_select(0, edge_src) + shift_vecs
+        # pos[dst] - pos[src] with a fixed-order (atomic-free) adjoint: forces are reproducible
+        vec = edge_vectors(pos, edge_src, edge_dst) + shift_vecs
         length = vec.norm(dim=1)
         directions = vec / length.clamp(min=1e-8).unsqueeze(-1)
         mask = (length <= self.cutoff).to(pos.dtype)
@@ -278,7 +280,9 @@ class MaceICTC(nn.Module):
         edge_feats = bessel_embedding(length, r_max=self.cutoff, num_basis=self.num_basis, cutoff_p=self.cutoff_p)
         if species is None:
             species = self.species_index(atomic_numbers)
-        h = self.node_embedding.weight.t().index_select(0, species)
+        # the embedding as the product one_hot(species) @ W^T (the reference's node_embedding on
+        # one-hot attributes): its weight gradient is a GEMM, not an atomic index_add
+        h = linear(one_hot_rows(species, self.num_elements), self.node_embedding.weight)
         energy = None
         for t, (interaction, product) in enumerate(zip(self.interactions, self.products)):
             message, sc = interaction(h, harmonics, edge_feats, edge_src, edge_dst, mask, species)

@@ -20,6 +20,8 @@ import torch
 from ictc_o3.backends.hip.graph_message import pin_graphs
 from ictc_o3.backends.hip.runtime import require_gpu_fp32
 
+from .geometry import one_hot_rows
+from .linear import mm
 from .model import MaceICTC
 
 
@@ -60,7 +62,8 @@ def energy_and_forces(model, positions, atomic_numbers, batch, edge_src, edge_ds
     with torch.enable_grad():
         pos = positions if positions.requires_grad else positions.detach().requires_grad_(True)
         atomic = model(pos, atomic_numbers, batch, edge_src, edge_dst, edge_shifts, cell, species=species)
-        energy = atomic.new_zeros(cell.shape[0]).index_add(0, batch, atomic)
+        # per-structure sums as one_hot(batch)^T @ atomic: a fixed summation order
+        energy = mm(one_hot_rows(batch, cell.shape[0]).t(), atomic.unsqueeze(1)).squeeze(1)
         # keep the coordinate dependency for zero-edge graphs (a 3-element sum: no multi-block
         # reduction, so the step stays capturable into a HIP graph)
         force = -torch.autograd.grad(energy.sum() + pos[:1].sum() * 0.0, pos, create_graph=training,

@@ -389,6 +389,22 @@ int ictc_hip_radius_graph_fill_sorted(const ictc_cell_grid* grid, const double* 
                                       double* shifts, hipStream_t stream);
 
 /*
+ * Adjoint of the edge vectors vec[e] = pos[dst(e)] - pos[src(e)] + shift[e] (the edge geometry
+ * of reference mace_ictc/models/pure_cartesian_ictd_fix.py:2930-2933, whose autograd scatters
+ * through index_add):
+ *   grad_pos[n] = sum_{e: dst(e)=n} grad_vec[e] - sum_{e: src(e)=n} grad_vec[e]
+ * over the receiver CSR (dst_rowptr [nodes+1], dst_perm [edges] or null when sorted) and the
+ * source CSR (src_rowptr, src_perm) of one edge list with nodes_src = nodes_dst = nodes.
+ * grad_vec [edges,3], grad_pos [nodes,3] (fully overwritten); dtype 0 = float32, 1 = float64.
+ * A fixed summation order (one wave per node, fixed lane assignment and butterfly): the
+ * result is bit-identical from run to run.
+ */
+int ictc_hip_edge_vector_grad(int dtype, const void* grad_vec, const int64_t* dst_rowptr,
+                              const int64_t* dst_perm, const int64_t* src_rowptr,
+                              const int64_t* src_perm, void* grad_pos, int64_t nodes,
+                              hipStream_t stream);
+
+/*
  * SiLU derivative forms of force training's double backward through the radial MLP: for the
  * first-order backward y = grad * silu'(x) and a cotangent of y, one elementwise pass over n
  * floats writes

@@ -1,7 +1,8 @@
 """MACE-style energy + force model on the HIP operators against the float64 oracle
 restatement (oracle/mace.py) on the same parameters and graph.
 
-* energies (rel 1e-5) and forces (rel 1e-4) on a small periodic structure;
+* energies (rel 1e-5) and forces (rel 1e-4) on a small periodic structure, at C = 32 and at
+  cfg 4's C = 128;
 * force-loss training gradients of every trainable parameter (rel 1e-4): the loss
   depends on the forces, so this exercises the mixed second derivatives of the graph
   message, the symmetric contraction and the direction harmonics end to end;
@@ -47,9 +48,10 @@ def _setup(gpu, *, channels=32, atoms=48, density=0.05, cutoff=4.0, seed=3):
     return model, graph, oracle, cpu
 
 
-def test_energy_and_forces_match_oracle(gpu):
+@pytest.mark.parametrize("channels", [32, 128])
+def test_energy_and_forces_match_oracle(gpu, channels):
     from mace_hip import energy_and_forces
-    model, graph, oracle, cpu = _setup(gpu)
+    model, graph, oracle, cpu = _setup(gpu, channels=channels)
     assert graph["edge_src"].numel() > 300
     got = energy_and_forces(model, **graph)
     e, f, atomic = oracle.energy_and_forces(**cpu)
@@ -58,9 +60,10 @@ def test_energy_and_forces_match_oracle(gpu):
     assert_rel(got["forces"], f, rtol=RTOL_FORCE, what="forces")
 
 
-def test_force_loss_gradients_match_oracle(gpu):
+@pytest.mark.parametrize("channels", [32, 128])
+def test_force_loss_gradients_match_oracle(gpu, channels):
     from mace_hip import energy_and_forces, force_loss
-    model, graph, oracle, cpu = _setup(gpu, seed=5)
+    model, graph, oracle, cpu = _setup(gpu, channels=channels, seed=5)
     atoms = graph["positions"].shape[0]
     pred = energy_and_forces(model, **graph, training=True)
     loss = force_loss(pred, atoms)

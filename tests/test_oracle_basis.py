@@ -7,6 +7,11 @@ Pins (each chosen so a plausible mistake fails one of them):
   parity-forbidden paths, l1=0 couplings are scaled identities
   (reference ictd_irreps.py:2550-2568), and agreement up to sign with the
   independent null-space intertwiner (ictd_irreps.py:1304-1374);
+* CG sign and size in closed form: contracting a path's coupling with the harmonics of one
+  direction gives sum_ij C[i,j,k] Y_l1(n)_i Y_l2(n)_j = c Y_l3(n)_k with
+  c = +sqrt((2l1+1)(2l2+1)) |(l1 l2 l3; 0 0 0)| (the Gaunt coefficient of component-normalised
+  harmonics; the product of Legendre polynomials has non-negative Legendre coefficients, so a
+  coupling built from polynomial products is positive), for every natural-parity path;
 * Y: Y_0 = 1, Y_1 = sqrt(3) * (z, y, x) (closed form of the l=1 basis),
   unit mean square per component on the sphere, rotation covariance;
 * the product's host constants (CG, harmonics tables, path plans) equal the
@@ -90,6 +95,40 @@ def test_cg_matches_nullspace_intertwiner_up_to_sign(l1, l2, l3):
     c = c / c.norm()
     sign = torch.sign((c * f).sum())
     assert (c - sign * f).abs().max() < 1e-9
+
+
+def _wigner_3j_000(l1, l2, l3):
+    """(l1 l2 l3; 0 0 0) in closed form (Racah): zero for odd l1 + l2 + l3."""
+    big = l1 + l2 + l3
+    if big % 2:
+        return 0.0
+    g, f = big // 2, math.factorial
+    return ((-1) ** g * math.sqrt(f(big - 2 * l1) * f(big - 2 * l2) * f(big - 2 * l3) / f(big + 1))
+            * f(g) / (f(g - l1) * f(g - l2) * f(g - l3)))
+
+
+@pytest.mark.parametrize("source", ["oracle", "product"])
+def test_cg_sign_and_size_closed_form(source):
+    from ictc_o3.basis import ictd_irreps as P
+    g = torch.Generator().manual_seed(11)
+    n = torch.nn.functional.normalize(torch.randn(64, 3, generator=g, dtype=torch.float64), dim=-1)
+    ys = B.direction_harmonics_all(n, 6)
+    checked = 0
+    for l1 in range(4):
+        for l2 in range(4):
+            for l3 in range(abs(l1 - l2), l1 + l2 + 1):
+                if (l1 + l2 + l3) % 2:
+                    continue
+                raw = (B.cg_tensor(l1, l2, l3) if source == "oracle"
+                       else torch.from_numpy(P.coupling_tensor(l1, l2, l3)))
+                c = B.cg_component_normalised(raw, l3)
+                f = torch.einsum("ijk,ni,nj->nk", c, ys[l1], ys[l2])
+                want = math.sqrt((2 * l1 + 1) * (2 * l2 + 1)) * abs(_wigner_3j_000(l1, l2, l3))
+                assert want > 0
+                assert (f - want * ys[l3]).abs().max() < 1e-12 * max(1.0, float(ys[l3].abs().max())) * 50, \
+                    (l1, l2, l3)
+                checked += 1
+    assert checked == 30
 
 
 def test_harmonics_closed_forms_and_normalisation():
