@@ -192,6 +192,17 @@ def _kernels_only(plan, device) -> None:
     print("kernels-only pass done", flush=True)
 
 
+def _profile_value(name: str, key: str):
+    """A `key: value` line of a committed profiles/ summary (None if absent)."""
+    try:
+        for line in open(os.path.join(ROOT, "profiles", name)):
+            if line.startswith(key + ":"):
+                return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def _measured_traffic():
     """HBM bytes per VJP launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary
     (calibrated against a 1 GiB copy); None if the summary is absent."""
@@ -341,12 +352,14 @@ def _bench_tp_cfg0(device):
     y = direction_harmonics_packed(n.to(device), TP0_L).contiguous()
     ms = _event_ms(lambda: _forward_raw(op.plan, x, y, g), device, reps=20)
     gbs = BYTES_TP0 * TP0_ROWS / (ms * 1e-3) / 1e9
+    traffic = _profile_value("tp_c64_l2_cfg0_kernel_trace_and_traffic.md", "traffic_bytes_per_launch")
     return {"workload": "cfg0 channelwise TP forward C64/lmax2 (11 paths), 65,536 instances, ir_mul",
             "kernel": "tp_forward_kernel<2,2,2,1>", "mean_launch_ms": ms,
             "instances_per_s": TP0_ROWS / (ms * 1e-3), "vs_published_11.57M": TP0_ROWS / (ms * 1e-3) / 11.57e6,
             "roofline": {"bound": "hbm", "algorithmic_bytes_per_instance": BYTES_TP0,
                          "algorithmic_bytes_per_launch": BYTES_TP0 * TP0_ROWS, "achieved": gbs,
-                         "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS}}
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS,
+                         "traffic": traffic, "traffic_unit": "bytes/launch"}}
 
 
 def _cpu_tp_cfg0(budget_s: float = 10.0, rows: int = 8192):
@@ -553,6 +566,11 @@ def _bench_mace(device):
     train_ms = _median_call_ms(lambda: training_step(model, opt, graph, species=species), device)
     model.eval().requires_grad_(False)
     infer_ms = _median_call_ms(lambda: energy_and_forces(model, **graph, species=species), device)
+    infer_peak = _peak_bytes(lambda: energy_and_forces(model, **graph, species=species), device)
+    model.set_message_streaming(16384)         # radial streaming: no [E, P*C] gate tensor
+    stream_ms = _median_call_ms(lambda: energy_and_forces(model, **graph, species=species), device)
+    stream_peak = _peak_bytes(lambda: energy_and_forces(model, **graph, species=species), device)
+    model.set_message_streaming(None)
     captured = CapturedEnergyAndForces(model, **graph, species=species)
     infer_graph_ms = _median_call_ms(lambda: captured(graph["positions"]), device)
     del captured
@@ -571,7 +589,22 @@ def _bench_mace(device):
             "inference": leg(infer_ms, 11.0e3, "eager"),
             "training": leg(train_ms, 3.81e3, "eager"),
             "inference_hip_graph": leg(infer_graph_ms, 11.0e3, "HIP graph replay"),
-            "training_hip_graph": leg(train_graph_ms, 3.81e3, "HIP graph replay")}
+            "training_hip_graph": leg(train_graph_ms, 3.81e3, "HIP graph replay"),
+            "inference_radial_streaming": {
+                **leg(stream_ms, 11.0e3, "eager, radial streaming over 16,384-edge receiver ranges"),
+                "peak_bytes": stream_peak, "peak_bytes_whole_gates": infer_peak,
+                "gate_tensor_bytes": graph["edge_src"].numel() * 23 * 128 * 4}}
+
+
+def _peak_bytes(fn, device) -> int:
+    """Device memory a call allocates at its peak beyond what was allocated before it."""
+    fn()
+    torch.cuda.synchronize(device)
+    torch.cuda.reset_peak_memory_stats(device)
+    base = torch.cuda.memory_allocated(device)
+    fn()
+    torch.cuda.synchronize(device)
+    return int(torch.cuda.max_memory_allocated(device) - base)
 
 
 def _bench_graph(device):

@@ -43,6 +43,7 @@ import torch.nn.functional as F
 
 from ictc_o3.backends.hip.graph_message import packed_graph_message
 from ictc_o3.backends.hip.harmonics import direction_harmonics_packed
+from ictc_o3.backends.hip.radial_message import fold_projection, packed_radial_graph_message
 from ictc_o3.basis.ictd_irreps import EdgeWeightedPathPreservingTensorProduct
 from ictc_o3.ops.symmetric_contraction import ICTDBridgeUSymmetricContractionSO3
 
@@ -184,16 +185,25 @@ class Interaction(nn.Module):
                                 NormalizedSiLU(), _mace_linear(64, 64), NormalizedSiLU(),
                                 _mace_linear(64, self.tp.num_paths * channels))
         self.message_linear = MessageLinear(self.tp.path_counts_by_l, channels, edge_lmax)
+        # None: the gates are one [E, P*C] tensor; an int: radial streaming over receiver ranges of
+        # at most that many edges (the reference's _ascend_edge_chunk_size)
+        self.edge_chunk_size: Optional[int] = None
         self.self_connection = SpeciesLinear(num_elements, channels)
 
-    def radial_mlp(self, edge_feats):
-        """self.fc on the edge features with each normalised SiLU's constant folded into the next
-        layer's (64 x 64 or 64 x P*C) weight instead of scaling the [E, 64] activations."""
+    def radial_hidden(self, edge_feats):
+        """self.fc up to its last Linear: (the last layer's input [E, 64], its weight [P*C, 64]),
+        each normalised SiLU's constant folded into the next layer's weight instead of scaling
+        the [E, 64] activations."""
         layers = [m for m in self.fc if isinstance(m, nn.Linear)]
         h = layers[0](edge_feats)
-        for lin in layers[1:]:
+        for lin in layers[1:-1]:
             h = linear(silu(h), lin.weight * SILU_SCALE)
-        return h
+        return silu(h), layers[-1].weight * SILU_SCALE
+
+    def radial_mlp(self, edge_feats):
+        """self.fc on the edge features: the gates [E, P*C]."""
+        hidden, weight = self.radial_hidden(edge_feats)
+        return linear(hidden, weight)
 
     def forward(self, h, harmonics, edge_feats, src, dst, mask, species):
         """mask: the reference multiplies the gates by (r <= r_max) (:1801-1808).  The radial
@@ -202,9 +212,17 @@ class Interaction(nn.Module):
         is skipped (mask is accepted for the signature)."""
         n = h.shape[0]
         x1 = self.linear_up.to_ir_mul(h)
-        gates = self.tp.effective_gates(self.radial_mlp(edge_feats), edge_feats.shape[0])
         plan = self.tp.hip_plan(self.input_lmax, self.edge_lmax)
-        m = packed_graph_message(plan, x1, harmonics, gates, src, dst, nodes_dst=n)
+        if self.edge_chunk_size is None:
+            gates = self.tp.effective_gates(self.radial_mlp(edge_feats), edge_feats.shape[0])
+            m = packed_graph_message(plan, x1, harmonics, gates, src, dst, nodes_dst=n)
+        else:
+            # the radial MLP's last layer produced one receiver range at a time inside the message
+            # (reference capacity mode, capacity_message.py:109-179): no [E, P*C] gate tensor
+            hidden, weight = self.radial_hidden(edge_feats)
+            weight, _ = fold_projection(self.tp, plan, weight, None)
+            m = packed_radial_graph_message(plan, x1, harmonics, hidden, weight, None, src, dst, nodes_dst=n,
+                                            edge_chunk_size=self.edge_chunk_size)
         message = self.message_linear(m) / max(self.avg_num_neighbors, 1e-8)
         sc = self.self_connection(h[:, :self.channels], species)
         return message, sc
@@ -255,6 +273,14 @@ class MaceICTC(nn.Module):
         self.layer_readouts = nn.ModuleList([_mace_linear(self.channels, 1) for _ in range(num_interactions - 1)])
         self.last_readout = nn.Sequential(_mace_linear(self.channels, readout_hidden), NormalizedSiLU(),
                                           _mace_linear(readout_hidden, 1))
+
+    def set_message_streaming(self, edge_chunk_size: Optional[int]) -> None:
+        """Radial streaming in every interaction (receiver ranges of at most ``edge_chunk_size``
+        edges), or None for whole gate tensors."""
+        if edge_chunk_size is not None and (not isinstance(edge_chunk_size, int) or edge_chunk_size < 1):
+            raise ValueError("Edge chunk size must be a positive integer or None")
+        for interaction in self.interactions:
+            interaction.edge_chunk_size = edge_chunk_size
 
     def species_index(self, atomic_numbers: torch.Tensor) -> torch.Tensor:
         a = atomic_numbers.long()
