@@ -596,6 +596,48 @@ def _bench_mace(device):
                 "gate_tensor_bytes": graph["edge_src"].numel() * 23 * 128 * 4}}
 
 
+LIN_COUNTS, LIN_C, MFMA_F32_PEAK_TFLOPS = (4, 6, 7, 6), 128, 157.3   # fp32 MFMA, dense (published)
+
+
+def _bench_linear(device):
+    """The second interaction's message linear of the cfg-4 MACE step (per degree 4 / 6 / 7 / 6
+    path blocks of C = 128 channels into 128, 2,048 atoms, alpha = 1/avg_num_neighbors) on the
+    fp32-MFMA kernel, forward and input adjoint, beside the dense-GEMM route it replaced
+    (per-degree rearranged copies, rocBLAS products, concatenation)."""
+    from ictc_o3.backends.hip.degree_linear import DegreeLinearPlan, _forward_raw, _input_grad_raw
+    from ictc_o3.backends.hip.linear import mm
+    n, c, alpha = MACE_ATOMS, LIN_C, 1.0 / 50.0
+    plan = DegreeLinearPlan(LIN_COUNTS, c, c)
+    gen = torch.Generator().manual_seed(0)
+    x = torch.randn(n, plan.in_width, generator=gen).to(device)
+    gy = torch.randn(n, plan.out_width, generator=gen).to(device)
+    ws = [(torch.randn(c, k * c, generator=gen) / math.sqrt(k * c)).to(device) for k in LIN_COUNTS]
+
+    def dense_forward():
+        return torch.cat([mm(plan.x_rows(x, l), ws[l].t()).reshape(n, 2 * l + 1, c).transpose(1, 2)
+                          .reshape(n, -1) for l in range(len(LIN_COUNTS))], 1) * alpha
+
+    def dense_input_grad():
+        return torch.cat([mm(plan.y_rows(gy, l), ws[l]).reshape(n, 2 * l + 1, k, c).transpose(1, 2)
+                          .reshape(n, -1) for l, k in enumerate(LIN_COUNTS)], 1) * alpha
+    fwd_ms = _event_ms(lambda: _forward_raw(plan, x, ws, alpha), device, reps=50)
+    grad_ms = _event_ms(lambda: _input_grad_raw(plan, gy, ws, alpha), device, reps=50)
+    dense = (_event_ms(dense_forward, device, reps=20), _event_ms(dense_input_grad, device, reps=20))
+    flops = 2 * n * c * sum((2 * l + 1) * k * c for l, k in enumerate(LIN_COUNTS))
+    nbytes = 4 * (n * (plan.in_width + plan.out_width) + sum(w.numel() for w in ws))
+
+    def leg(ms, dense_ms, kernel):
+        tf = flops / (ms * 1e-3) / 1e12
+        return {"kernel": kernel, "mean_launch_ms": ms, "dense_gemm_route_ms": dense_ms,
+                "roofline": {"bound": "mfma", "achieved": tf, "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                             "frac": tf / MFMA_F32_PEAK_TFLOPS, "flops_per_launch": flops},
+                "algorithmic_bytes": nbytes, "hbm_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+    return {"workload": "cfg4 MACE message linear (interaction 2): per-degree path blocks 4/6/7/6 x C128 -> C128, "
+                        "2,048 atoms, fp32",
+            "forward": leg(fwd_ms, dense[0], "degree_linear_kernel<true, true>"),
+            "input_grad": leg(grad_ms, dense[1], "degree_linear_kernel<false, true>")}
+
+
 def _peak_bytes(fn, device) -> int:
     """Device memory a call allocates at its peak beyond what was allocated before it."""
     fn()
@@ -699,7 +741,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--kernels-only", action="store_true")
-    ap.add_argument("--only", choices=("tp", "tp0", "message", "sc", "mace", "graph"), default=None,
+    ap.add_argument("--only", choices=("tp", "tp0", "message", "sc", "mace", "graph", "linear"), default=None,
                     help="run one section and print its JSON (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -713,9 +755,9 @@ def main() -> int:
     if args.kernels_only:
         _kernels_only(op.plan, device)
         return 0
-    if args.only in ("tp0", "message", "sc", "mace", "graph"):
+    if args.only in ("tp0", "message", "sc", "mace", "graph", "linear"):
         fn = {"tp0": _bench_tp_cfg0, "message": _bench_message, "sc": _bench_sc, "mace": _bench_mace,
-              "graph": _bench_graph}[args.only]
+              "graph": _bench_graph, "linear": _bench_linear}[args.only]
         print(json.dumps({args.only: fn(device)}), flush=True)
         return 0
     elapsed, vjp_ms, fwd_ms = _time_gpu(args, op.plan, device)
@@ -730,7 +772,8 @@ def main() -> int:
     if args.only is None:
         others = {"tp_cfg0": _bench_tp_cfg0(device), "message_cfg2": _bench_message(device),
                   "sc_cfg3": _bench_sc(device),
-                  "mace_cfg4": _bench_mace(device), "radius_graph": _bench_graph(device)}
+                  "mace_cfg4": _bench_mace(device), "message_linear_cfg4": _bench_linear(device),
+                  "radius_graph": _bench_graph(device)}
         if not args.no_cpu:
             others["tp_cfg0"]["cpu_baseline"] = _cpu_tp_cfg0()
             others["message_cfg2"]["cpu_baseline"] = _cpu_message()

@@ -16,7 +16,7 @@ Every HIP TU is compiled with ``-Xclang -target-feature -Xclang -packed-fp32-ops
 ``ICTC_HIP_COMBOS`` (e.g. ``"333,222,033"``) restricts the degree combinations for
 quick development builds; entries left out report ICTC_ERR_UNSUPPORTED at run time.
 
-Usage: python build.py [-j JOBS]
+Usage: python build.py [-j JOBS] [--incremental]
 """
 from __future__ import annotations
 
@@ -45,7 +45,7 @@ FLAGS = ["--offload-arch=" + ARCH, "-O3", "-std=c++20", "-fPIC", "-Wno-c99-desig
          "-I", INCLUDE, "-I", HERE]
 
 API_SOURCES = ["tp_api.hip", "harmonics_api.hip", "message_api.hip", "sc_api.hip", "graph_api.hip",
-               "elementwise_api.hip", "blas_api.hip"]
+               "elementwise_api.hip", "blas_api.hip", "linear_api.hip"]
 # rocBLAS (the channel-linear products): the same SONAME as the copy torch loads, which the
 # dynamic linker then binds to
 LINK_LIBS = ["-L/opt/rocm/lib", "-lrocblas"]
@@ -148,9 +148,35 @@ def _generate(combos) -> list:
     return [p for _, p in units]
 
 
-def _compile(src: str) -> str:
+_INCLUDE_RE = None
+
+
+def _newest_dependency(src: str, seen=None) -> float:
+    """Latest modification time of src and of every file it includes with quotes
+    (searched next to it, in this directory, generated/ and include/)."""
+    import re
+    global _INCLUDE_RE
+    if _INCLUDE_RE is None:
+        _INCLUDE_RE = re.compile(r'^\s*#\s*include\s+"([^"]+)"', re.M)
+    seen = set() if seen is None else seen
+    if src in seen:
+        return 0.0
+    seen.add(src)
+    newest = os.path.getmtime(src)
+    for name in _INCLUDE_RE.findall(open(src).read()):
+        for base in (os.path.dirname(src), HERE, GEN, INCLUDE):
+            path = os.path.join(base, name)
+            if os.path.isfile(path):
+                newest = max(newest, _newest_dependency(path, seen))
+                break
+    return newest
+
+
+def _compile(src: str, incremental: bool = False) -> str:
     os.makedirs(OBJ, exist_ok=True)
     obj = os.path.join(OBJ, os.path.splitext(os.path.basename(src))[0] + ".o")
+    if incremental and os.path.exists(obj) and os.path.getmtime(obj) >= _newest_dependency(src):
+        return obj
     cmd = [HIPCC, *FLAGS, "-c", src, "-o", obj]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
@@ -158,13 +184,15 @@ def _compile(src: str) -> str:
     return obj
 
 
-def build(jobs: int | None = None, verbose: bool = True) -> str:
+def build(jobs: int | None = None, verbose: bool = True, incremental: bool = False) -> str:
+    """Compile every unit (incremental: only units whose object is older than the unit or
+    anything it includes) and link the library."""
     t0 = time.time()
     combos = _combos()
     units = [os.path.join(HERE, s) for s in API_SOURCES] + _generate(combos)
     jobs = jobs or max(1, min(len(units), os.cpu_count() or 1))
     with cf.ThreadPoolExecutor(max_workers=jobs) as pool:
-        objs = list(pool.map(_compile, units))
+        objs = list(pool.map(lambda u: _compile(u, incremental), units))
     os.makedirs(LIB_DIR, exist_ok=True)
     tmp = LIB + ".tmp"
     res = subprocess.run([HIPCC, "--offload-arch=" + ARCH, "-shared", "-fPIC", *objs, *LINK_LIBS, "-o", tmp],
@@ -186,4 +214,7 @@ def build(jobs: int | None = None, verbose: bool = True) -> str:
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("-j", "--jobs", type=int, default=None)
-    build(ap.parse_args().jobs)
+    ap.add_argument("--incremental", action="store_true",
+                    help="recompile only units whose sources or included headers changed")
+    args = ap.parse_args()
+    build(args.jobs, incremental=args.incremental)

@@ -1,0 +1,238 @@
+// Per-degree channel linear on fp32 MFMA (gfx950): the path-preserving message linear of the
+// MACE interaction (reference mace_ictc/models/pure_cartesian_ictd_fix.py:629-661,
+// PathPreservingLinearSO3; native route ictc_o3/ascendc/linear.py:12-136), applied straight to
+// the message kernel's packed output and writing the mul_ir node layout.
+//
+// Per degree l (d = 2l + 1, K_l = counts[l] * C):
+//   x  row n, degree block l:  [counts[l]][d][C]          (ir_mul, the message output)
+//   y  row n, degree block l:  [O][d]                     (mul_ir, offset O * l^2)
+//   forward:     y[n, o, m]            = alpha * sum_{k, c} W_l[o, k C + c] x[n, k, m, c]
+//   input grad:  gx[n, k, m, c]        = alpha * sum_o gy[n, o, m] W_l[o, k C + c]
+// i.e. for the rows rho = n d + m, Y = alpha X W^T and gX = alpha gY W, one GEMM per degree with
+// the layout changes folded into the tile loads and stores (no transposed copies, no
+// concatenation, the 1/avg_num_neighbors scale as alpha).
+//
+// Tiling: a 256-thread block computes a 64-row x 64-column output tile of one degree (grid.z);
+// K is walked in chunks of 32 staged through LDS with coalesced loads, then each wave runs
+// v_mfma_f32_16x16x4_f32 over its 16 rows and the tile's 4 column tiles (operand layout of that
+// instruction: lane l supplies A[l % 16][k0 + l / 16] and B[k0 + l / 16][l % 16] and receives
+// D[4 (l / 16) + v][l % 16], v = 0..3).  Every sum runs in a fixed order.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "ictc_hip.h"
+
+namespace ictc {
+namespace {
+
+constexpr int kTile = 64;   // rows and columns per block
+constexpr int kKc = 32;     // K per LDS chunk
+constexpr int kPad = kKc + 1;
+
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+struct DegreeGeometry {
+  int64_t rows;       // N d
+  int d;              // 2l + 1
+  int k;              // counts[l] * C
+  int64_t xoff;       // first float of the degree block in an x row
+  int64_t yoff;       // first float of the degree block in a y row
+  const float* w;     // [O, k]
+};
+
+struct LinearArgs {
+  DegreeGeometry g[ICTC_LINEAR_MAX_DEGREES];
+  int64_t xwidth, ywidth;
+  int channels, out_channels;
+  float alpha;
+};
+
+// FWD: A = x rows (K = x columns), B^T = W rows, D -> y.  !FWD: A = gy rows (K = O), B = W,
+// D -> gx columns.  VEC (channels a multiple of 32): each 32-wide K chunk of an x row lies in one
+// path block, so rows and weight rows are staged with float4 loads and the row geometry is
+// computed once per thread; otherwise element by element.
+template <bool FWD, bool VEC>
+__global__ void __launch_bounds__(256)
+degree_linear_kernel(const float* __restrict__ in, float* __restrict__ out, const LinearArgs a) {
+  const DegreeGeometry& g = a.g[blockIdx.z];
+  const int ncols = FWD ? a.out_channels : g.k;   // output columns
+  const int kdim = FWD ? g.k : a.out_channels;    // reduction length
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kTile;
+  const int c0 = blockIdx.y * kTile;
+  // uniform per block; a degree without path blocks (kdim 0) writes its zero forward rows
+  if (r0 >= g.rows || c0 >= ncols) return;
+  __shared__ float sA[kTile][kPad];   // [row][k]
+  __shared__ float sB[kTile][kPad];   // [column][k]
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int C = a.channels;
+  // A staging: thread t loads 8 consecutive k of tile row t / 4
+  const int ar = tid >> 2, akq = (tid & 3) * 8;
+  const int64_t arho = r0 + ar;
+  const bool arow = arho < g.rows;
+  const int64_t an = arow ? arho / g.d : 0;
+  const int am = arow ? static_cast<int>(arho - an * g.d) : 0;
+  const float* __restrict__ abase = FWD ? in + an * a.xwidth + g.xoff + static_cast<int64_t>(am) * C
+                                        : in + an * a.ywidth + g.yoff + am;
+  f32x4_t acc[4] = {};
+  for (int k0 = 0; k0 < kdim; k0 += kKc) {
+    if (FWD && VEC) {
+      const int blk = k0 / C, c = k0 - blk * C + akq;
+      f32x4_t v0 = {}, v1 = {};
+      if (arow && k0 + akq < kdim) {
+        const float* p = abase + static_cast<int64_t>(blk) * g.d * C + c;
+        v0 = *reinterpret_cast<const f32x4_t*>(p);
+        v1 = *reinterpret_cast<const f32x4_t*>(p + 4);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        sA[ar][akq + u] = v0[u];
+        sA[ar][akq + 4 + u] = v1[u];
+      }
+      const int col = c0 + ar;   // weight row col, 8 consecutive k
+      f32x4_t w0 = {}, w1 = {};
+      if (col < ncols && k0 + akq < kdim) {
+        const float* p = g.w + static_cast<int64_t>(col) * g.k + k0 + akq;
+        w0 = *reinterpret_cast<const f32x4_t*>(p);
+        w1 = *reinterpret_cast<const f32x4_t*>(p + 4);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        sB[ar][akq + u] = w0[u];
+        sB[ar][akq + 4 + u] = w1[u];
+      }
+    } else if (FWD) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int kk = k0 + akq + u;
+        float v = 0.f;
+        if (arow && kk < kdim) {
+          const int blk = kk / C, c = kk - blk * C;
+          v = abase[static_cast<int64_t>(blk) * g.d * C + c];
+        }
+        sA[ar][akq + u] = v;
+        const int col = c0 + ar;
+        sB[ar][akq + u] = (col < ncols && kk < kdim) ? g.w[static_cast<int64_t>(col) * g.k + kk] : 0.f;
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {   // gy row: stride d over the output channels
+        const int kk = k0 + akq + u;
+        sA[ar][akq + u] = (arow && kk < kdim) ? abase[static_cast<int64_t>(kk) * g.d] : 0.f;
+      }
+      // weight rows kk (= output channel), 8 consecutive columns per thread
+      const int wk = tid >> 3, wc = (tid & 7) * 8;
+      const int kk = k0 + wk;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int col = c0 + wc + u;
+        sB[wc + u][wk] = (kk < kdim && col < ncols) ? g.w[static_cast<int64_t>(kk) * g.k + col] : 0.f;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < kKc / 4; ++ks) {
+      const float av = sA[wave * 16 + (lane & 15)][ks * 4 + (lane >> 4)];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const float bv = sB[t * 16 + (lane & 15)][ks * 4 + (lane >> 4)];
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[t], 0, 0, 0);
+      }
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int64_t rho = r0 + wave * 16 + 4 * (lane >> 4) + v;
+    if (rho >= g.rows) continue;
+    const int64_t n = rho / g.d;
+    const int m = static_cast<int>(rho - n * g.d);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int col = c0 + t * 16 + (lane & 15);
+      if (col >= ncols) continue;
+      const float val = a.alpha * acc[t][v];
+      if (FWD) {
+        out[n * a.ywidth + g.yoff + static_cast<int64_t>(col) * g.d + m] = val;
+      } else {
+        const int blk = col / C, c = col - blk * C;
+        out[n * a.xwidth + g.xoff + (static_cast<int64_t>(blk) * g.d + m) * C + c] = val;
+      }
+    }
+  }
+}
+
+int prepare(const ictc_degree_linear_desc* desc, const float* const* weights, float alpha, int64_t nodes,
+            LinearArgs* a, int* live_degrees, int64_t* max_rows, int* max_cols, bool fwd) {
+  if (desc == nullptr || weights == nullptr || nodes < 0) return ICTC_ERR_INVALID_ARGUMENT;
+  if (desc->lmax < 0 || desc->lmax >= ICTC_LINEAR_MAX_DEGREES || desc->channels < 1 || desc->out_channels < 1)
+    return ICTC_ERR_INVALID_ARGUMENT;
+  int64_t xw = 0;
+  for (int l = 0; l <= desc->lmax; ++l) {
+    if (desc->counts[l] < 0) return ICTC_ERR_INVALID_ARGUMENT;
+    xw += static_cast<int64_t>(desc->counts[l]) * (2 * l + 1) * desc->channels;
+  }
+  a->xwidth = xw;
+  a->ywidth = static_cast<int64_t>(desc->out_channels) * (desc->lmax + 1) * (desc->lmax + 1);
+  a->channels = desc->channels;
+  a->out_channels = desc->out_channels;
+  a->alpha = alpha;
+  *live_degrees = desc->lmax + 1;
+  *max_rows = 0;
+  *max_cols = 0;
+  int64_t xoff = 0;
+  for (int l = 0; l <= desc->lmax; ++l) {
+    DegreeGeometry& g = a->g[l];
+    g.d = 2 * l + 1;
+    g.rows = nodes * g.d;
+    g.k = desc->counts[l] * desc->channels;
+    g.xoff = xoff;
+    g.yoff = static_cast<int64_t>(desc->out_channels) * l * l;
+    g.w = weights[l];
+    if (g.k > 0 && g.w == nullptr) return ICTC_ERR_INVALID_ARGUMENT;
+    xoff += static_cast<int64_t>(g.k) * g.d;
+    if (g.rows > *max_rows) *max_rows = g.rows;
+    const int cols = fwd ? desc->out_channels : g.k;
+    if (cols > *max_cols) *max_cols = cols;
+  }
+  return ICTC_OK;
+}
+
+template <bool FWD>
+int launch(const ictc_degree_linear_desc* desc, const float* in, const float* const* weights, float alpha,
+           float* out, int64_t nodes, hipStream_t stream) {
+  LinearArgs a{};
+  int degrees = 0, max_cols = 0;
+  int64_t max_rows = 0;
+  const int st = prepare(desc, weights, alpha, nodes, &a, &degrees, &max_rows, &max_cols, FWD);
+  if (st != ICTC_OK) return st;
+  if (nodes == 0) return ICTC_OK;
+  if (in == nullptr || out == nullptr) return ICTC_ERR_INVALID_ARGUMENT;
+  const int64_t row_tiles = (max_rows + kTile - 1) / kTile;
+  if (row_tiles > 0x7fffffff) return ICTC_ERR_UNSUPPORTED;
+  const dim3 grid(static_cast<unsigned>(row_tiles), static_cast<unsigned>((max_cols + kTile - 1) / kTile),
+                  static_cast<unsigned>(degrees));
+  if (desc->channels % 32 == 0)
+    hipLaunchKernelGGL((degree_linear_kernel<FWD, true>), grid, dim3(256), 0, stream, in, out, a);
+  else
+    hipLaunchKernelGGL((degree_linear_kernel<FWD, false>), grid, dim3(256), 0, stream, in, out, a);
+  return hipGetLastError() == hipSuccess ? ICTC_OK : ICTC_ERR_LAUNCH;
+}
+
+}  // namespace
+}  // namespace ictc
+
+extern "C" {
+
+int ictc_hip_degree_linear_forward(const ictc_degree_linear_desc* desc, const float* x, const float* const* weights,
+                                   float alpha, float* y, int64_t nodes, hipStream_t stream) {
+  return ictc::launch<true>(desc, x, weights, alpha, y, nodes, stream);
+}
+
+int ictc_hip_degree_linear_input_grad(const ictc_degree_linear_desc* desc, const float* grad_y,
+                                      const float* const* weights, float alpha, float* grad_x, int64_t nodes,
+                                      hipStream_t stream) {
+  return ictc::launch<false>(desc, grad_y, weights, alpha, grad_x, nodes, stream);
+}
+
+}  // extern "C"

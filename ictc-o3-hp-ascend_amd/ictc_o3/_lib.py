@@ -15,7 +15,7 @@ import torch  # noqa: F401  (must precede CDLL, see module docstring)
 
 MAX_PATHS = 64
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libictc_hip.so")
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 
 class TpDesc(ctypes.Structure):
@@ -30,6 +30,16 @@ class TpDesc(ctypes.Structure):
         ("gate_index", ctypes.c_int32 * MAX_PATHS),
         ("out_offset", ctypes.c_int32 * MAX_PATHS),
         ("scale", ctypes.c_float * MAX_PATHS),
+    ]
+
+
+class DegreeLinearDesc(ctypes.Structure):
+    """Mirror of ``ictc_degree_linear_desc``."""
+    _fields_ = [
+        ("lmax", ctypes.c_int32),
+        ("channels", ctypes.c_int32),
+        ("out_channels", ctypes.c_int32),
+        ("counts", ctypes.c_int32 * 8),
     ]
 
 
@@ -80,6 +90,10 @@ _SIGNATURES = {
     "ictc_hip_message_edge_grad_tangent": (ctypes.c_int, [ctypes.POINTER(TpDesc)] + [_P] * 13 + [_I64, _I64,
                                                                                             _I64, _P]),
     "ictc_hip_edge_vector_grad": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _P, _P, _P, _I64, _P]),
+    "ictc_hip_degree_linear_forward": (ctypes.c_int, [ctypes.POINTER(DegreeLinearDesc), _P, _P, ctypes.c_float, _P,
+                                                      _I64, _P]),
+    "ictc_hip_degree_linear_input_grad": (ctypes.c_int, [ctypes.POINTER(DegreeLinearDesc), _P, _P, ctypes.c_float,
+                                                         _P, _I64, _P]),
     "ictc_hip_silu_second": (ctypes.c_int, [_P, _P, _P, _P, _P, _I64, _P]),
     "ictc_hip_sgemm": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, _I64, _I64, _I64, ctypes.c_float, _P, _I64, _P,
                                       _I64, ctypes.c_float, _P, _I64, _P]),

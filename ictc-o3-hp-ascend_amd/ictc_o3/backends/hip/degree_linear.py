@@ -1,0 +1,141 @@
+"""Per-degree channel linear on the fp32-MFMA kernels of ``csrc/linear_api.hip``: the
+path-preserving message linear of the MACE interaction (reference
+``mace_ictc/models/pure_cartesian_ictd_fix.py:629-661``), read straight from the message
+kernels' packed ir_mul output and written in the mul_ir node layout.
+
+    y[n, l-block][o, m] = alpha * sum_{k, c} W_l[o, k C + c] * x[n, l-block][k, m, c]
+
+x rows hold, per degree l, ``counts[l]`` path blocks of [2l+1][C]; y rows hold, per degree,
+[O][2l+1]; ``weights[l]`` is [O, counts[l] C].  The map is bilinear in (x, W): its input
+adjoint is the second kernel (``ictc_hip_degree_linear_input_grad``), whose own adjoints are
+the forward kernel again, and every weight adjoint is the dense product
+alpha * gY_l^T X_l on the rearranged blocks (``linear.mm``), so derivatives of any order stay
+on these routes.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import List, Sequence
+
+import torch
+
+from ... import _lib
+from ...autograd.adjoint_requirements import required_gradients
+from .linear import mm
+
+
+class DegreeLinearPlan:
+    def __init__(self, counts: Sequence[int], channels: int, out_channels: int):
+        self.counts = [int(c) for c in counts]
+        self.lmax = len(self.counts) - 1
+        if not 0 <= self.lmax < 8:
+            raise ValueError("degree linear supports degrees 0..7")
+        self.channels, self.out_channels = int(channels), int(out_channels)
+        self.desc = _lib.DegreeLinearDesc()
+        self.desc.lmax, self.desc.channels, self.desc.out_channels = self.lmax, self.channels, self.out_channels
+        for l, c in enumerate(self.counts):
+            self.desc.counts[l] = c
+        self.in_width = sum(c * (2 * l + 1) * self.channels for l, c in enumerate(self.counts))
+        self.out_width = self.out_channels * (self.lmax + 1) ** 2
+
+    def x_rows(self, x: torch.Tensor, l: int) -> torch.Tensor:
+        """Packed x -> the degree-l rows [N (2l+1), counts[l] C] (column k C + c)."""
+        d, k, c = 2 * l + 1, self.counts[l], self.channels
+        off = sum(self.counts[j] * (2 * j + 1) * c for j in range(l))
+        blk = x[:, off:off + k * d * c].reshape(x.shape[0], k, d, c)
+        return blk.transpose(1, 2).reshape(x.shape[0] * d, k * c)
+
+    def y_rows(self, y: torch.Tensor, l: int) -> torch.Tensor:
+        """mul_ir y -> the degree-l rows [N (2l+1), O]."""
+        d, o = 2 * l + 1, self.out_channels
+        blk = y[:, o * l * l:o * (l + 1) ** 2].reshape(y.shape[0], o, d)
+        return blk.transpose(1, 2).reshape(y.shape[0] * d, o)
+
+
+def _pointers(weights: List[torch.Tensor]):
+    arr = (ctypes.c_void_p * len(weights))()
+    for i, w in enumerate(weights):
+        arr[i] = w.data_ptr() if w.numel() else None
+    return arr
+
+
+def _forward_raw(plan: DegreeLinearPlan, x, weights, alpha):
+    y = torch.empty(x.shape[0], plan.out_width, device=x.device, dtype=torch.float32)
+    _lib.check(_lib.lib().ictc_hip_degree_linear_forward(
+        ctypes.byref(plan.desc), x.data_ptr() if x.numel() else None, _pointers(weights), float(alpha),
+        y.data_ptr() if y.numel() else None, x.shape[0], _lib.stream_of(x.device)), "ictc_hip_degree_linear_forward")
+    return y
+
+
+def _input_grad_raw(plan: DegreeLinearPlan, gy, weights, alpha):
+    gx = torch.empty(gy.shape[0], plan.in_width, device=gy.device, dtype=torch.float32)
+    _lib.check(_lib.lib().ictc_hip_degree_linear_input_grad(
+        ctypes.byref(plan.desc), gy.data_ptr() if gy.numel() else None, _pointers(weights), float(alpha),
+        gx.data_ptr() if gx.numel() else None, gy.shape[0], _lib.stream_of(gy.device)),
+        "ictc_hip_degree_linear_input_grad")
+    return gx
+
+
+def _weight_grads(plan: DegreeLinearPlan, gy, x, alpha, need):
+    """alpha * gY_l^T X_l per degree (dense products on rearranged rows; differentiable)."""
+    out = []
+    for l, n in enumerate(need):
+        if not n or plan.counts[l] == 0:
+            out.append(None)
+            continue
+        out.append(mm(plan.y_rows(gy, l).t(), plan.x_rows(x, l)) * alpha)
+    return out
+
+
+class _Forward(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, plan, alpha, x, *weights):
+        ctx.plan, ctx.alpha = plan, alpha
+        ctx.save_for_backward(x, *weights)
+        return _forward_raw(plan, x, list(weights), alpha)
+
+    @staticmethod
+    def backward(ctx, gy):
+        x, *weights = ctx.saved_tensors
+        need = required_gradients((x, *weights), ctx.needs_input_grad[2:])
+        if gy is None or not any(need):
+            return (None, None, None) + (None,) * len(weights)
+        gy = gy.contiguous()
+        gx = _InputGrad.apply(ctx.plan, ctx.alpha, gy, *weights) if need[0] else None
+        return (None, None, gx, *_weight_grads(ctx.plan, gy, x, ctx.alpha, need[1:]))
+
+
+class _InputGrad(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, plan, alpha, gy, *weights):
+        ctx.plan, ctx.alpha = plan, alpha
+        ctx.save_for_backward(gy, *weights)
+        return _input_grad_raw(plan, gy, list(weights), alpha)
+
+    @staticmethod
+    def backward(ctx, z):
+        gy, *weights = ctx.saved_tensors
+        need = required_gradients((gy, *weights), ctx.needs_input_grad[2:])
+        if z is None or not any(need):
+            return (None, None, None) + (None,) * len(weights)
+        z = z.contiguous()
+        ggy = _Forward.apply(ctx.plan, ctx.alpha, z, *weights) if need[0] else None
+        return (None, None, ggy, *_weight_grads(ctx.plan, gy, z, ctx.alpha, need[1:]))
+
+
+def degree_linear(x: torch.Tensor, weights: Sequence[torch.Tensor], plan: DegreeLinearPlan,
+                  alpha: float = 1.0) -> torch.Tensor:
+    """x [N, plan.in_width] (packed per-degree path blocks [count][2l+1][C]), weights[l]
+    [O, counts[l] C] -> alpha * per-degree linear [N, O (L+1)^2] (mul_ir)."""
+    if x.ndim != 2 or x.shape[1] != plan.in_width:
+        raise ValueError("features must have shape [N, sum_l counts[l] (2l+1) C]")
+    if len(weights) != plan.lmax + 1:
+        raise ValueError("one weight per degree is required")
+    for l, w in enumerate(weights):
+        if w.shape != (plan.out_channels, plan.counts[l] * plan.channels):
+            raise ValueError(f"weight of degree {l} must have shape [O, counts[l] C]")
+        if w.dtype != torch.float32 or w.device != x.device:
+            raise ValueError("weights must be float32 on the features' device")
+    if x.dtype != torch.float32 or not x.is_cuda:
+        raise ValueError("features must be float32 on a ROCm GPU")
+    return _Forward.apply(plan, float(alpha), x.contiguous(), *[w.contiguous() for w in weights])

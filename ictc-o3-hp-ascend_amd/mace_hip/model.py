@@ -41,6 +41,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from ictc_o3.backends.hip.degree_linear import DegreeLinearPlan, degree_linear
 from ictc_o3.backends.hip.graph_message import packed_graph_message
 from ictc_o3.backends.hip.harmonics import direction_harmonics_packed
 from ictc_o3.backends.hip.radial_message import fold_projection, packed_radial_graph_message
@@ -107,12 +108,15 @@ class ChannelLinear(nn.Module):
 
 class MessageLinear(nn.Module):
     """PathPreservingLinearSO3 (pure_cartesian_ictd_fix.py:629-661) reading the packed ir_mul
-    message (per degree: [count_l paths][2l+1][C]) and writing mul_ir [N, C(L+1)^2]."""
+    message (per degree: [count_l paths][2l+1][C]) and writing mul_ir [N, C(L+1)^2]: one
+    fp32-MFMA launch over every degree (degree_linear), the layout changes folded into its tile
+    loads and stores and the 1/avg_num_neighbors scale passed as its alpha."""
 
     def __init__(self, counts: Dict[int, int], channels: int, lmax: int):
         super().__init__()
         self.channels, self.lmax = channels, lmax
         self.counts = [int(counts.get(l, 0)) for l in range(lmax + 1)]
+        self.plan = DegreeLinearPlan(self.counts, channels, channels)
         self.weights = nn.ParameterList()
         for l in range(lmax + 1):
             fan_in = channels * self.counts[l]
@@ -121,20 +125,10 @@ class MessageLinear(nn.Module):
                 nn.init.normal_(w, mean=0.0, std=1.0 / math.sqrt(fan_in))
             self.weights.append(nn.Parameter(w))
 
-    def forward(self, m: torch.Tensor) -> torch.Tensor:
-        n, c, out = m.shape[0], self.channels, []
-        # one split (its backward concatenates the block gradients) rather than a slice per degree
-        # (each slice's backward zero-fills a full [N, NOC*C] gradient and the engine adds them)
-        sizes = [self.counts[l] * (2 * l + 1) * c for l in range(self.lmax + 1)]
-        blocks = m.split([*sizes, m.shape[1] - sum(sizes)], dim=-1)
-        for l in range(self.lmax + 1):
-            k, d = self.counts[l], 2 * l + 1
-            if k == 0:
-                out.append(m.new_zeros(n, c * d))
-                continue
-            blk = blocks[l].reshape(n, k, d, c).transpose(1, 2).reshape(n * d, k * c)
-            out.append(linear(blk, self.weights[l]).reshape(n, d, c).transpose(1, 2).reshape(n, c * d))
-        return torch.cat(out, dim=-1)
+    def forward(self, m: torch.Tensor, alpha: float = 1.0) -> torch.Tensor:
+        if m.shape[1] != self.plan.in_width:
+            raise ValueError(f"message width {m.shape[1]} differs from the linear's {self.plan.in_width}")
+        return degree_linear(m, list(self.weights), self.plan, alpha)
 
 
 class SpeciesLinear(nn.Module):
@@ -223,7 +217,7 @@ class Interaction(nn.Module):
             weight, _ = fold_projection(self.tp, plan, weight, None)
             m = packed_radial_graph_message(plan, x1, harmonics, hidden, weight, None, src, dst, nodes_dst=n,
                                             edge_chunk_size=self.edge_chunk_size)
-        message = self.message_linear(m) / max(self.avg_num_neighbors, 1e-8)
+        message = self.message_linear(m, 1.0 / max(self.avg_num_neighbors, 1e-8))
         sc = self.self_connection(h[:, :self.channels], species)
         return message, sc
 

@@ -418,6 +418,38 @@ int ictc_hip_silu_second(const float* x, const float* grad, const float* cotange
                          float* grad_grad, float* grad_x, int64_t n, hipStream_t stream);
 
 /*
+ * Per-degree channel linear on fp32 MFMA (v_mfma_f32_16x16x4_f32), for the path-preserving
+ * message linear of the MACE interaction (reference
+ * mace_ictc/models/pure_cartesian_ictd_fix.py:629-661; native route ictc_o3/ascendc/linear.py:
+ * 12-136), reading the message kernels' packed output directly.  For degree l (d = 2l + 1):
+ *   x [nodes, sum_l counts[l] d C]: per node and degree, counts[l] path blocks of [d][C]
+ *                                    (ir_mul; the ictc_hip_message_forward output layout);
+ *   y [nodes, O (lmax+1)^2]:         per node and degree, [O][d] at offset O l^2 (mul_ir);
+ *   weights[l] [O, counts[l] C]:     row-major, column k C + c = (path block k, channel c)
+ *                                    (weights is a host array of lmax + 1 device pointers).
+ *   forward:    y[n, o, m]     = alpha sum_{k,c} weights[l][o, k C + c] x[n, k, m, c]
+ *   input_grad: grad_x[n,k,m,c] = alpha sum_o grad_y[n, o, m] weights[l][o, k C + c]
+ * (the adjoint of the forward in x; the weight gradient is the caller's dense product).  y and
+ * grad_x are fully overwritten; a degree with counts[l] = 0 gets zero y rows.  Fixed
+ * summation order (bit-identical run to run).
+ */
+#define ICTC_LINEAR_MAX_DEGREES 8
+typedef struct ictc_degree_linear_desc {
+    int32_t lmax;                               /* degrees 0..lmax, lmax < 8 */
+    int32_t channels;                           /* C, channels of an input path block */
+    int32_t out_channels;                       /* O */
+    int32_t counts[ICTC_LINEAR_MAX_DEGREES];    /* path blocks per degree */
+} ictc_degree_linear_desc;
+
+int ictc_hip_degree_linear_forward(const ictc_degree_linear_desc* desc, const float* x,
+                                   const float* const* weights, float alpha, float* y,
+                                   int64_t nodes, hipStream_t stream);
+
+int ictc_hip_degree_linear_input_grad(const ictc_degree_linear_desc* desc, const float* grad_y,
+                                      const float* const* weights, float alpha, float* grad_x,
+                                      int64_t nodes, hipStream_t stream);
+
+/*
  * Row-major fp32 product C[m,n] = alpha * op(A) op(B) + beta * C on rocBLAS, for the dense
  * channel linears around the operators.  op(A) is [m,k]: A is stored [m,k] (lda >= k) or,
  * with trans_a != 0, [k,m] (lda >= m); likewise B with op(B) [k,n].  Each host thread uses
