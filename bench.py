@@ -634,8 +634,8 @@ def _bench_linear(device):
                 "algorithmic_bytes": nbytes, "hbm_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
     return {"workload": "cfg4 MACE message linear (interaction 2): per-degree path blocks 4/6/7/6 x C128 -> C128, "
                         "2,048 atoms, fp32",
-            "forward": leg(fwd_ms, dense[0], "degree_linear_kernel<true, true>"),
-            "input_grad": leg(grad_ms, dense[1], "degree_linear_kernel<false, true>")}
+            "forward": leg(fwd_ms, dense[0], "degree_linear_kernel<true, true, 2>"),
+            "input_grad": leg(grad_ms, dense[1], "degree_linear_kernel<false, true, 1>")}
 
 
 def _peak_bytes(fn, device) -> int:
@@ -664,8 +664,9 @@ def _bench_graph(device):
     return out
 
 
-def _cpu_time(fn, budget_s: float):
-    fn()
+def _cpu_time(fn, budget_s: float, warmup: bool = True):
+    if warmup:
+        fn()
     done, t0 = 0, time.perf_counter()
     while time.perf_counter() - t0 < budget_s or done == 0:
         fn()
@@ -714,8 +715,10 @@ def _cpu_sc(budget_s: float = 8.0):
             "sample": f"oracle contraction recursion + autograd VJP (fp32), 256 nodes x {done} calls in {dt:.1f}s"}
 
 
-def _cpu_mace(budget_s: float = 10.0):
-    """Float32 oracle model E + F on a smaller cell (same density and cutoff as cfg 4)."""
+def _cpu_mace(budget_s: float = 10.0, training: bool = False):
+    """Float32 oracle model on a smaller cell (same density and cutoff as cfg 4): E + F
+    (inference), or the force-loss training step (E + F with create_graph, loss
+    mean((E/N)^2) + mean(F^2), backward to every parameter, AdamW)."""
     sys.path.insert(0, ROOT)
     from oracle.mace import MaceOracle
     from mace_hip.model import MaceICTC
@@ -723,15 +726,32 @@ def _cpu_mace(budget_s: float = 10.0):
     torch.set_num_threads(threads)
     torch.manual_seed(0)
     model = MaceICTC(channels=128, lmax=3, num_interactions=2, correlation=3, atomic_numbers=MACE_ZS, cutoff=5.0)
-    oracle = MaceOracle({k: v.detach() for k, v in model.named_parameters()}, channels=128, lmax=3,
-                        num_interactions=2, correlation=3, num_elements=10, cutoff=5.0, avg_num_neighbors=50.0)
+    params = {k: v.detach().clone().requires_grad_(training) for k, v in model.named_parameters()}
+    oracle = MaceOracle({**dict(model.named_buffers()), **params}, channels=128, lmax=3, num_interactions=2, correlation=3, num_elements=10,
+                        cutoff=5.0, avg_num_neighbors=50.0)
     st, g = _mace_graph("cpu", atoms=MACE_CPU_ATOMS)
     args = dict(pos=g["positions"], species=st.species, src=g["edge_src"], dst=g["edge_dst"],
                 shifts=g["edge_shifts"], cell=g["cell"], batch=g["batch"])
-    done, dt = _cpu_time(lambda: oracle.energy_and_forces(**args), budget_s)
-    return {"value": MACE_CPU_ATOMS * done / dt, "unit": "atom-steps/s (E+F inference)", "cores": threads, "cpu_model": _cpu_model(), "kind": "port",
-            "sample": f"oracle MACE restatement fp32 E+F, {MACE_CPU_ATOMS} atoms ({g['edge_src'].numel()} edges) x {done} "
-                      f"calls in {dt:.1f}s"}
+    if training:
+        opt = torch.optim.AdamW(list(params.values()), lr=1e-3)
+
+        def step():
+            energy, forces, _ = oracle.energy_and_forces(**args, create_graph=True)
+            loss = (energy / MACE_CPU_ATOMS).square().mean() + forces.square().mean()
+            loss.backward()
+            opt.step()
+            opt.zero_grad(set_to_none=True)
+        what, unit = "force-loss training step", "atom-steps/s (force-loss training)"
+    else:
+        def step():
+            oracle.energy_and_forces(**args)
+        what, unit = "E+F", "atom-steps/s (E+F inference)"
+    # a training step takes seconds on the host: it is timed without a warmup call
+    done, dt = _cpu_time(step, budget_s, warmup=not training)
+    return {"value": MACE_CPU_ATOMS * done / dt, "unit": unit, "cores": threads, "cpu_model": _cpu_model(),
+            "kind": "port",
+            "sample": f"oracle MACE restatement fp32 {what}, {MACE_CPU_ATOMS} atoms ({g['edge_src'].numel()} edges) "
+                      f"x {done} calls in {dt:.1f}s"}
 
 
 def main() -> int:
@@ -779,6 +799,7 @@ def main() -> int:
             others["message_cfg2"]["cpu_baseline"] = _cpu_message()
             others["sc_cfg3"]["cpu_baseline"] = _cpu_sc()
             others["mace_cfg4"]["cpu_baseline"] = _cpu_mace()
+            others["mace_cfg4"]["cpu_baseline_training"] = _cpu_mace(training=True)
     line = {
         "metric": "TP instances/s fwd+VJP C128/lmax3; MACE E+F atom-steps/s; % HBM peak",
         "value": value, "unit": "instances/s", "n_gpus": 1, "steps": args.steps,

@@ -13,10 +13,13 @@
 // concatenation, the 1/avg_num_neighbors scale as alpha).
 //
 // Tiling: a 256-thread block computes a 64-row x 64-column output tile of one degree (grid.z);
-// K is walked in chunks of 32 staged through LDS with coalesced loads, then each wave runs
-// v_mfma_f32_16x16x4_f32 over its 16 rows and the tile's 4 column tiles (operand layout of that
-// instruction: lane l supplies A[l % 16][k0 + l / 16] and B[k0 + l / 16][l % 16] and receives
-// D[4 (l / 16) + v][l % 16], v = 0..3).  Every sum runs in a fixed order.
+// K is walked in chunks of 32 staged through LDS, then each wave runs v_mfma_f32_16x16x4_f32 over
+// its 16 rows and the tile's 4 column tiles.  Operand layout of that instruction: lane l supplies
+// A[l % 16][k_l] and B[k_l][l % 16] and receives D[4 (l / 16) + v][l % 16], v = 0..3, where k_l is
+// the instruction's k index l / 16.  Which actual k a lane feeds is free as long as A and B agree:
+// here four consecutive MFMAs j = 0..3 cover a 16-wide k group with k = 4 (l / 16) + j, so each
+// lane reads its four A (and B) values of a group with one 16-byte LDS read.  Every sum runs in a
+// fixed order (bit-identical run to run).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -27,7 +30,7 @@ namespace {
 
 constexpr int kTile = 64;   // rows and columns per block
 constexpr int kKc = 32;     // K per LDS chunk
-constexpr int kPad = kKc + 1;
+constexpr int kPitch = kKc + 4;   // LDS row pitch in floats (16-byte aligned rows)
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
@@ -49,10 +52,14 @@ struct LinearArgs {
 
 // FWD: A = x rows (K = x columns), B^T = W rows, D -> y.  !FWD: A = gy rows (K = O), B = W,
 // D -> gx columns.  VEC (channels a multiple of 32): each 32-wide K chunk of an x row lies in one
-// path block, so rows and weight rows are staged with float4 loads and the row geometry is
-// computed once per thread; otherwise element by element.
-template <bool FWD, bool VEC>
-__global__ void __launch_bounds__(256)
+// path block and weight rows are float4-aligned, so operands are fetched into registers one chunk
+// ahead (their loads in flight while the MFMAs of the current chunk run); with two LDS buffers
+// (NBUF 2) the next chunk is staged into the other buffer right after those MFMAs (one barrier per
+// chunk), with one (NBUF 1, half the LDS and so twice the resident blocks) after a second barrier.
+// The forward's long K (counts C) takes two buffers, the input adjoint's short K (O) one.
+// Without VEC, element by element, one chunk at a time.
+template <bool FWD, bool VEC, int NBUF>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NBUF == 1 ? 8 : 4)))
 degree_linear_kernel(const float* __restrict__ in, float* __restrict__ out, const LinearArgs a) {
   const DegreeGeometry& g = a.g[blockIdx.z];
   const int ncols = FWD ? a.out_channels : g.k;   // output columns
@@ -61,12 +68,12 @@ degree_linear_kernel(const float* __restrict__ in, float* __restrict__ out, cons
   const int c0 = blockIdx.y * kTile;
   // uniform per block; a degree without path blocks (kdim 0) writes its zero forward rows
   if (r0 >= g.rows || c0 >= ncols) return;
-  __shared__ float sA[kTile][kPad];   // [row][k]
-  __shared__ float sB[kTile][kPad];   // [column][k]
+  __shared__ __align__(16) float sA[NBUF][kTile][kPitch];   // [buffer][row][k]
+  __shared__ __align__(16) float sB[NBUF][kTile][kPitch];   // [buffer][column][k]
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int C = a.channels;
-  // A staging: thread t loads 8 consecutive k of tile row t / 4
+  // A staging: thread t holds 8 consecutive k of tile row t / 4
   const int ar = tid >> 2, akq = (tid & 3) * 8;
   const int64_t arho = r0 + ar;
   const bool arow = arho < g.rows;
@@ -74,72 +81,148 @@ degree_linear_kernel(const float* __restrict__ in, float* __restrict__ out, cons
   const int am = arow ? static_cast<int>(arho - an * g.d) : 0;
   const float* __restrict__ abase = FWD ? in + an * a.xwidth + g.xoff + static_cast<int64_t>(am) * C
                                         : in + an * a.ywidth + g.yoff + am;
+  // !FWD B staging: thread t holds weight row k0 + t / 8, columns c0 + 8 (t % 8) .. + 7 (two
+  // float4 loads), stored transposed element by element.  The k index of B column col is
+  // XOR-swizzled by bsw(col) (a multiple of 8 below 32, so every aligned 4-group of k stays
+  // contiguous and in its row): the transposed stores of a wave then meet at most two lanes per
+  // bank, and with the 36-float pitch the 16-byte MFMA operand reads stay conflict-free.
+  const int wk = tid >> 3, wc = (tid & 7) * 8;
+  auto bsw = [](int col) { return FWD ? 0 : ((col >> 3) & 3) * 8; };
   f32x4_t acc[4] = {};
-  for (int k0 = 0; k0 < kdim; k0 += kKc) {
-    if (FWD && VEC) {
-      const int blk = k0 / C, c = k0 - blk * C + akq;
-      f32x4_t v0 = {}, v1 = {};
-      if (arow && k0 + akq < kdim) {
-        const float* p = abase + static_cast<int64_t>(blk) * g.d * C + c;
-        v0 = *reinterpret_cast<const f32x4_t*>(p);
-        v1 = *reinterpret_cast<const f32x4_t*>(p + 4);
-      }
+  const int fr = lane & 15, fq = (lane >> 4) * 4;
+  auto mfma_chunk = [&](int buf) {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        sA[ar][akq + u] = v0[u];
-        sA[ar][akq + 4 + u] = v1[u];
-      }
-      const int col = c0 + ar;   // weight row col, 8 consecutive k
-      f32x4_t w0 = {}, w1 = {};
-      if (col < ncols && k0 + akq < kdim) {
-        const float* p = g.w + static_cast<int64_t>(col) * g.k + k0 + akq;
-        w0 = *reinterpret_cast<const f32x4_t*>(p);
-        w1 = *reinterpret_cast<const f32x4_t*>(p + 4);
-      }
+    for (int kg = 0; kg < kKc; kg += 16) {
+      const f32x4_t av = *reinterpret_cast<const f32x4_t*>(&sA[buf][wave * 16 + fr][kg + fq]);
+      if constexpr (NBUF == 1) {
+        // one B operand live at a time (the register budget of 8 waves per SIMD); the
+        // accumulation chains of the other resident waves fill the MFMA pipe
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        sB[ar][akq + u] = w0[u];
-        sB[ar][akq + 4 + u] = w1[u];
-      }
-    } else if (FWD) {
+        for (int t = 0; t < 4; ++t) {
+          const f32x4_t bv = *reinterpret_cast<const f32x4_t*>(&sB[buf][t * 16 + fr][(kg + fq) ^ bsw(t * 16 + fr)]);
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int kk = k0 + akq + u;
-        float v = 0.f;
-        if (arow && kk < kdim) {
-          const int blk = kk / C, c = kk - blk * C;
-          v = abase[static_cast<int64_t>(blk) * g.d * C + c];
+          for (int j = 0; j < 4; ++j) acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j], bv[j], acc[t], 0, 0, 0);
         }
-        sA[ar][akq + u] = v;
-        const int col = c0 + ar;
-        sB[ar][akq + u] = (col < ncols && kk < kdim) ? g.w[static_cast<int64_t>(col) * g.k + kk] : 0.f;
+      } else {
+        f32x4_t bv[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          bv[t] = *reinterpret_cast<const f32x4_t*>(&sB[buf][t * 16 + fr][(kg + fq) ^ bsw(t * 16 + fr)]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+          for (int t = 0; t < 4; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j], bv[t][j], acc[t], 0, 0, 0);
+        }
+      }
+    }
+  };
+  if constexpr (VEC) {
+    // registers of one chunk: A (8 floats of the thread's row), B (8 floats)
+    f32x4_t ra0, ra1, rb0, rb1;
+    auto fetch = [&](int k0) {
+      const bool kin = k0 + akq < kdim;
+      ra0 = f32x4_t{};
+      ra1 = f32x4_t{};
+      rb0 = f32x4_t{};
+      rb1 = f32x4_t{};
+      if constexpr (FWD) {
+        const int blk = k0 / C, c = k0 - blk * C + akq;
+        if (arow && kin) {
+          const float* p = abase + static_cast<int64_t>(blk) * g.d * C + c;
+          ra0 = *reinterpret_cast<const f32x4_t*>(p);
+          ra1 = *reinterpret_cast<const f32x4_t*>(p + 4);
+        }
+        const int col = c0 + ar;   // weight row col, 8 consecutive k
+        if (col < ncols && kin) {
+          const float* p = g.w + static_cast<int64_t>(col) * g.k + k0 + akq;
+          rb0 = *reinterpret_cast<const f32x4_t*>(p);
+          rb1 = *reinterpret_cast<const f32x4_t*>(p + 4);
+        }
+      } else {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {   // gy row: stride d over the output channels
+          if (arow && k0 + akq + u < kdim) ra0[u] = abase[static_cast<int64_t>(k0 + akq + u) * g.d];
+          if (arow && k0 + akq + 4 + u < kdim) ra1[u] = abase[static_cast<int64_t>(k0 + akq + 4 + u) * g.d];
+        }
+        const int kk = k0 + wk;
+        if (kk < kdim && c0 + wc < ncols) {   // ncols (counts C) is a multiple of 32
+          const float* p = g.w + static_cast<int64_t>(kk) * g.k + c0 + wc;
+          rb0 = *reinterpret_cast<const f32x4_t*>(p);
+          rb1 = *reinterpret_cast<const f32x4_t*>(p + 4);
+        }
+      }
+    };
+    auto stage = [&](int buf) {
+      *reinterpret_cast<f32x4_t*>(&sA[buf][ar][akq]) = ra0;
+      *reinterpret_cast<f32x4_t*>(&sA[buf][ar][akq + 4]) = ra1;
+      if constexpr (FWD) {
+        *reinterpret_cast<f32x4_t*>(&sB[buf][ar][akq]) = rb0;
+        *reinterpret_cast<f32x4_t*>(&sB[buf][ar][akq + 4]) = rb1;
+      } else {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          sB[buf][wc + u][wk ^ bsw(wc + u)] = rb0[u];
+          sB[buf][wc + 4 + u][wk ^ bsw(wc + 4 + u)] = rb1[u];
+        }
+      }
+    };
+    fetch(0);
+    if constexpr (NBUF == 2) {
+      // buffer c & 1 holds chunk c; chunk c + 1 is fetched before and staged after chunk c's
+      // MFMAs, into the buffer every wave finished reading at the previous barrier
+      stage(0);
+      __syncthreads();
+      int buf = 0;
+      for (int k0 = 0; k0 < kdim; k0 += kKc) {
+        const bool more = k0 + kKc < kdim;
+        if (more) fetch(k0 + kKc);
+        mfma_chunk(buf);
+        if (more) stage(buf ^ 1);
+        __syncthreads();
+        buf ^= 1;
       }
     } else {
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {   // gy row: stride d over the output channels
-        const int kk = k0 + akq + u;
-        sA[ar][akq + u] = (arow && kk < kdim) ? abase[static_cast<int64_t>(kk) * g.d] : 0.f;
-      }
-      // weight rows kk (= output channel), 8 consecutive columns per thread
-      const int wk = tid >> 3, wc = (tid & 7) * 8;
-      const int kk = k0 + wk;
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int col = c0 + wc + u;
-        sB[wc + u][wk] = (kk < kdim && col < ncols) ? g.w[static_cast<int64_t>(kk) * g.k + col] : 0.f;
+      for (int k0 = 0; k0 < kdim; k0 += kKc) {
+        stage(0);
+        __syncthreads();
+        if (k0 + kKc < kdim) fetch(k0 + kKc);
+        mfma_chunk(0);
+        __syncthreads();
       }
     }
-    __syncthreads();
+  } else {
+    for (int k0 = 0; k0 < kdim; k0 += kKc) {
+      if constexpr (FWD) {
 #pragma unroll
-    for (int ks = 0; ks < kKc / 4; ++ks) {
-      const float av = sA[wave * 16 + (lane & 15)][ks * 4 + (lane >> 4)];
+        for (int u = 0; u < 8; ++u) {
+          const int kk = k0 + akq + u;
+          float v = 0.f;
+          if (arow && kk < kdim) {
+            const int blk = kk / C, c = kk - blk * C;
+            v = abase[static_cast<int64_t>(blk) * g.d * C + c];
+          }
+          sA[0][ar][akq + u] = v;
+          const int col = c0 + ar;
+          sB[0][ar][akq + u] = (col < ncols && kk < kdim) ? g.w[static_cast<int64_t>(col) * g.k + kk] : 0.f;
+        }
+      } else {
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const float bv = sB[t * 16 + (lane & 15)][ks * 4 + (lane >> 4)];
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[t], 0, 0, 0);
+        for (int u = 0; u < 8; ++u) {
+          const int kk = k0 + akq + u;
+          sA[0][ar][akq + u] = (arow && kk < kdim) ? abase[static_cast<int64_t>(kk) * g.d] : 0.f;
+        }
+        const int kk = k0 + wk;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int col = c0 + wc + u;
+          sB[0][wc + u][wk ^ bsw(wc + u)] =
+              (kk < kdim && col < ncols) ? g.w[static_cast<int64_t>(kk) * g.k + col] : 0.f;
+        }
       }
+      __syncthreads();
+      mfma_chunk(0);
+      __syncthreads();
     }
-    __syncthreads();
   }
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
@@ -213,9 +296,9 @@ int launch(const ictc_degree_linear_desc* desc, const float* in, const float* co
   const dim3 grid(static_cast<unsigned>(row_tiles), static_cast<unsigned>((max_cols + kTile - 1) / kTile),
                   static_cast<unsigned>(degrees));
   if (desc->channels % 32 == 0)
-    hipLaunchKernelGGL((degree_linear_kernel<FWD, true>), grid, dim3(256), 0, stream, in, out, a);
+    hipLaunchKernelGGL((degree_linear_kernel<FWD, true, FWD ? 2 : 1>), grid, dim3(256), 0, stream, in, out, a);
   else
-    hipLaunchKernelGGL((degree_linear_kernel<FWD, false>), grid, dim3(256), 0, stream, in, out, a);
+    hipLaunchKernelGGL((degree_linear_kernel<FWD, false, 1>), grid, dim3(256), 0, stream, in, out, a);
   return hipGetLastError() == hipSuccess ? ICTC_OK : ICTC_ERR_LAUNCH;
 }
 
