@@ -22,6 +22,9 @@
 //     dout[n] in LDS once and its waves split the node's edges; per edge dg, dY partials
 //     per chunk, or the edge's contribution to the source-feature adjoint
 //     dxe[e] = sum_p g_p M_p^T dout[dst(e)] (so dout is never gathered per edge);
+//   * msg_forward_degree_kernel / msg_edge_grad_degree_kernel: the forward and the first-order
+//     VJP (dg, dY and dxe in one pass) for degree sets with a bond buffer, one launch per input
+//     degree with two channel chunks per lane;
 //   * msg_node_grad_kernel (source CSR): dx[s] = sum over the out-edges of s of dxe[e],
 //     a streaming segmented sum.
 // Node-feature gathers go through buffer descriptors spanning the whole node tensor,
@@ -958,21 +961,237 @@ int launch_msg_forward_tangent(const ictc_tp_desc& d, const float* x, const floa
   }
 }
 
+// ----------------------------------------------------------------------------- VJP by degree
+// First-order VJP for degree sets with a bond buffer (lmax 3), in one pass per input degree l1
+// (the groups of msg_forward_degree_kernel: each owns the x rows of degree l1, its paths' gates,
+// bond entries and dout rows, and so its dg columns and dxe rows).  Per edge and path, with
+// w_I = sum_K M[K][I] dout_K (one LDS bond broadcast per (K, I), shared by the lane's CPL channels):
+//   dg_p   = sum_I x_I w_I                        (= sum_K dout_K sum_I x_I M[K][I])
+//   dxe_I += g_p w_I
+//   dY_j  += s_p sum_{I,K} C_p[I, j, K] (sum over the lane's channels of x_I g_p dout_K)
+// so the gates and bond rows are read once for all three outputs (the one-degree kernels read
+// them once in the dg/dY pass and again in the dxe pass).  dY partials: group launches run in
+// order on one stream; the first writes a block's channel sum into the slot of its first chunk
+// (and zero into its second), later groups add to it (a fixed order).
+template <int LIN, int LE, int LOUT, int L1, int CPL>
+__global__ void __launch_bounds__(kMsgBlock)
+msg_edge_grad_degree_kernel(const float* __restrict__ x, const float* __restrict__ bonds,
+                            const float* __restrict__ g, const float* __restrict__ go,
+                            const int64_t* __restrict__ src, const int64_t* __restrict__ rowptr,
+                            const int64_t* __restrict__ perm, float* __restrict__ dyp, float* __restrict__ dg,
+                            float* __restrict__ dxe, const ictc_tp_desc d, int64_t nodes_src, int nblk,
+                            int nchunks, int first) {
+  using PS = Paths<LIN, LE, LOUT>;
+  constexpr DegreeGroup GT = DegreeGroupOf<LIN, LE, LOUT, L1>::tab;
+  constexpr int NX = PS::NX, NY = PS::NY, NP = PS::N, NOCF = PS::NOC, NBF = PS::NB;
+  constexpr int NPG = GT.np, NOC = GT.noc, NBG = GT.nb, NI = GT.nx;
+  constexpr int NV = (NBG + kWave - 1) / kWave;
+  static_assert(NPG > 0, "an input degree without paths has no launch");
+  __shared__ float sB[kMsgWaves][NV * kWave];
+  __shared__ float sO[NOC][CPL * kWave];   // the group's dout rows of the node, for the block's chunks
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const uint32_t item = xcd_block(blockIdx.x, gridDim.x);   // receivers contiguous per XCD
+  const int64_t node = static_cast<int64_t>(item) / nblk;
+  const int chunk0 = static_cast<int>(item - node * nblk) * CPL;
+  const int C = d.channels;
+  const uint32_t row = static_cast<uint32_t>(C) * 4u;
+  bool live[CPL];
+  uint32_t vc[CPL];   // lanes past C read channel 0, zero it and store nothing
+#pragma unroll
+  for (int h = 0; h < CPL; ++h) {
+    const int c = (chunk0 + h) * kWave + lane;
+    live[h] = c < C;
+    vc[h] = static_cast<uint32_t>(live[h] ? c : 0) * 4u;
+  }
+  {
+    const rsrc_t ron = make_rsrc(go + node * NOCF * C, NOCF * row);
+    for (int r = wave; r < NOC; r += kMsgWaves) {
+      const uint32_t soff = static_cast<uint32_t>(kDegreeGroup<LIN, LE, LOUT, L1>.rowmap[r]) * row;
+#pragma unroll
+      for (int h = 0; h < CPL; ++h) {
+        const float v = buf_load_vs<kNonTemporal>(ron, vc[h], soff);
+        sO[r][h * kWave + lane] = live[h] ? v : 0.f;
+      }
+    }
+  }
+  __syncthreads();
+  const uint32_t xbytes = static_cast<uint32_t>(nodes_src * NX * row);
+  const rsrc_t rx = make_rsrc(dg != nullptr || dyp != nullptr ? x : nullptr, xbytes);   // range-checked gathers
+  uint32_t boff[NV];   // byte offsets of the lane's bond entries in a bond row
+#pragma unroll
+  for (int r = 0; r < NV; ++r) {
+    const int idx = lane + r * kWave;
+    boff[r] = static_cast<uint32_t>(idx < NBG ? kDegreeGroup<LIN, LE, LOUT, L1>.bidx[idx] : 0) * 4u;
+  }
+  const int64_t s0 = rowptr[node], s1 = rowptr[node + 1];
+#pragma clang loop unroll(disable)
+  for (int64_t slot = s0 + wave; slot < s1; slot += kMsgWaves) {
+    const int64_t e = perm ? perm[slot] : slot;
+    float bv[NV], xr[CPL][NI], gv[CPL][NPG];
+    {
+      const rsrc_t rb = make_rsrc(bonds + e * NBF, NBF * 4u);
+#pragma unroll
+      for (int r = 0; r < NV; ++r) bv[r] = buf_load<1>(rb, boff[r]).v[0];
+    }
+    const uint32_t xoff = static_cast<uint32_t>(src[e]) * NX * row;
+#pragma unroll
+    for (int h = 0; h < CPL; ++h)
+#pragma unroll
+      for (int m = 0; m < NI; ++m) {
+        const float v = buf_load_vs(rx, xoff + vc[h], (L1 * L1 + m) * row);
+        xr[h][m] = live[h] ? v : 0.f;
+      }
+    const rsrc_t rg = make_rsrc(g + e * NP * C, NP * row);
+#pragma unroll
+    for (int h = 0; h < CPL; ++h)
+#pragma unroll
+      for (int k = 0; k < NPG; ++k) gv[h][k] = buf_load_vs<kNonTemporal>(rg, vc[h], GT.path[k] * row);
+#pragma unroll
+    for (int r = 0; r < NV; ++r) sB[wave][lane + r * kWave] = bv[r];
+    wave_lds_sync();
+    const rsrc_t rdg = make_rsrc(dg ? dg + e * NP * C : nullptr, NP * row);
+    float dyl[NY], dxl[CPL][NI];
+#pragma unroll
+    for (int j = 0; j < NY; ++j) dyl[j] = 0.f;
+#pragma unroll
+    for (int h = 0; h < CPL; ++h)
+#pragma unroll
+      for (int m = 0; m < NI; ++m) dxl[h][m] = 0.f;
+    static_for<0, NPG>([&](auto Q) {
+      constexpr int k = Q;
+      constexpr int p = GT.path[k];
+      constexpr int l2 = PS::tab.l2[p], l3 = PS::tab.l3[p];
+      constexpr int ni = NI, nj = 2 * l2 + 1, no = 2 * l3 + 1;
+      constexpr int bo = GT.bond[k], oo = GT.out[k];
+      using CG = CGTab<L1, l2, l3>;
+      const float* bp = opaque_lds_row(&sB[wave][bo]);
+      __builtin_amdgcn_sched_barrier(0);
+      float w[CPL][ni];
+#pragma unroll
+      for (int h = 0; h < CPL; ++h)
+#pragma unroll
+        for (int i = 0; i < ni; ++i) w[h][i] = 0.f;
+      static_for<0, no>([&](auto K) {
+        float ov[CPL];
+#pragma unroll
+        for (int h = 0; h < CPL; ++h) ov[h] = sO[oo + K][h * kWave + lane];
+        static_for<0, ni>([&](auto I) {
+          const float b = bp[K * ni + I];
+#pragma unroll
+          for (int h = 0; h < CPL; ++h) w[h][I] = fmaf(b, ov[h], w[h][I]);
+        });
+      });
+#pragma unroll
+      for (int h = 0; h < CPL; ++h) {
+        float dgv = 0.f;
+#pragma unroll
+        for (int i = 0; i < ni; ++i) {
+          dgv = fmaf(xr[h][i], w[h][i], dgv);
+          dxl[h][i] = fmaf(gv[h][k], w[h][i], dxl[h][i]);
+        }
+        buf_store_lane(rdg, live[h], vc[h] + p * row, dgv);   // null dg: empty descriptor
+      }
+      if (dyp != nullptr) {
+        float part[nj];
+#pragma unroll
+        for (int j = 0; j < nj; ++j) part[j] = 0.f;
+        static_for<0, ni>([&](auto I) {
+          float xg[CPL];
+#pragma unroll
+          for (int h = 0; h < CPL; ++h) xg[h] = xr[h][I] * gv[h][k];
+          static_for<0, no>([&](auto K) {
+            float tt = xg[0] * sO[oo + K][lane];
+#pragma unroll
+            for (int h = 1; h < CPL; ++h) tt = fmaf(xg[h], sO[oo + K][h * kWave + lane], tt);
+            static_for<0, nj>([&](auto J) {
+              constexpr float cg = CG::v[(I * nj + J) * no + K];
+              if constexpr (cg != 0.0f) part[J] = fmaf(cg, tt, part[J]);
+            });
+          });
+        });
+        const float sc = d.scale[p];
+#pragma unroll
+        for (int j = 0; j < nj; ++j) dyl[l2 * l2 + j] = fmaf(sc, part[j], dyl[l2 * l2 + j]);
+      }
+    });
+    if (dxe != nullptr) {
+      const rsrc_t rde = make_rsrc(dxe + e * NX * C, NX * row);
+#pragma unroll
+      for (int h = 0; h < CPL; ++h)
+#pragma unroll
+        for (int m = 0; m < NI; ++m) buf_store_lane(rde, live[h], vc[h] + (L1 * L1 + m) * row, dxl[h][m]);
+    }
+    if (dyp != nullptr) {   // channel sums of the NY partials, one transposing butterfly
+      using WS = WaveSums<NY>;
+      const float tot = WS::reduce(dyl, lane);
+      const int j = WS::index(lane);
+      if (WS::owner(lane) && j < NY) {
+        float* q = dyp + (e * nchunks + chunk0) * NY + j;
+        if (first) {
+          q[0] = tot;
+#pragma unroll
+          for (int h = 1; h < CPL; ++h)
+            if (chunk0 + h < nchunks) q[h * NY] = 0.f;
+        } else {
+          q[0] += tot;
+        }
+      }
+    }
+  }
+}
+
+// One launch per input degree that has paths (dY partials accumulated across them in launch
+// order); two chunks per lane when the channels span two.
+template <int LIN, int LE, int LOUT>
+int launch_msg_edge_grad_degrees(const ictc_tp_desc& d, const float* x, const float* bonds, const float* g,
+                                 const float* go, const int64_t* src, const int64_t* rowptr, const int64_t* perm,
+                                 float* dyp, float* dg, float* dxe, int64_t nodes_src, int64_t nodes_dst,
+                                 hipStream_t stream) {
+  const int nchunks = (d.channels + kWave - 1) / kWave;
+  const bool two = nchunks >= 2;
+  const int nblk = two ? (nchunks + 1) / 2 : nchunks;
+  const dim3 grid(static_cast<unsigned>(nodes_dst * nblk));
+  int first = 1;
+  auto one = [&](auto deg) {
+    constexpr int L1 = decltype(deg)::value;
+    if constexpr (DegreeGroupOf<LIN, LE, LOUT, L1>::tab.np > 0) {
+      if (two)
+        hipLaunchKernelGGL((msg_edge_grad_degree_kernel<LIN, LE, LOUT, L1, 2>), grid, dim3(kMsgBlock), 0, stream,
+                           x, bonds, g, go, src, rowptr, perm, dyp, dg, dxe, d, nodes_src, nblk, nchunks, first);
+      else
+        hipLaunchKernelGGL((msg_edge_grad_degree_kernel<LIN, LE, LOUT, L1, 1>), grid, dim3(kMsgBlock), 0, stream,
+                           x, bonds, g, go, src, rowptr, perm, dyp, dg, dxe, d, nodes_src, nblk, nchunks, first);
+      first = 0;
+    }
+  };
+  one(Int<0>{});
+  if constexpr (LIN >= 1) one(Int<1>{});
+  if constexpr (LIN >= 2) one(Int<2>{});
+  if constexpr (LIN >= 3) one(Int<3>{});
+  return msg_launch_status();
+}
+
 template <int LIN, int LE, int LOUT>
 int launch_msg_edge_grad(const ictc_tp_desc& d, const float* x, const float* bonds, const float* g,
                          const float* go, const int64_t* src, const int64_t* rowptr, const int64_t* perm,
                          float* dyp, float* dg, float* dxe, int64_t nodes_src, int64_t nodes_dst,
                          hipStream_t stream) {
-  const int nchunks = (d.channels + kWave - 1) / kWave;
-  const dim3 grid(static_cast<unsigned>(nodes_dst * nchunks));   // one block per (node, chunk)
-  if (dyp != nullptr || dg != nullptr)
-    hipLaunchKernelGGL((msg_edge_grad_kernel<LIN, LE, LOUT, true>), grid, dim3(kMsgBlock), 0, stream, x, bonds, g,
-                       MsgTangent{}, go, src, rowptr, perm, dyp, dg, nullptr, d, nodes_src, nodes_dst, nchunks);
-  if (dxe != nullptr)
-    hipLaunchKernelGGL((msg_edge_grad_kernel<LIN, LE, LOUT, false>), grid, dim3(kMsgBlock), 0, stream, nullptr, bonds,
-                       g, MsgTangent{}, go, src, rowptr, perm, nullptr, nullptr, dxe, d, nodes_src, nodes_dst,
-                       nchunks);
-  return msg_launch_status();
+  if constexpr (!BondInline<LIN, LE, LOUT>::value && Paths<LIN, LE, LOUT>::NB > 0) {
+    return launch_msg_edge_grad_degrees<LIN, LE, LOUT>(d, x, bonds, g, go, src, rowptr, perm, dyp, dg, dxe,
+                                                      nodes_src, nodes_dst, stream);
+  } else {
+    const int nchunks = (d.channels + kWave - 1) / kWave;
+    const dim3 grid(static_cast<unsigned>(nodes_dst * nchunks));   // one block per (node, chunk)
+    if (dyp != nullptr || dg != nullptr)
+      hipLaunchKernelGGL((msg_edge_grad_kernel<LIN, LE, LOUT, true>), grid, dim3(kMsgBlock), 0, stream, x, bonds,
+                         g, MsgTangent{}, go, src, rowptr, perm, dyp, dg, nullptr, d, nodes_src, nodes_dst, nchunks);
+    if (dxe != nullptr)
+      hipLaunchKernelGGL((msg_edge_grad_kernel<LIN, LE, LOUT, false>), grid, dim3(kMsgBlock), 0, stream, nullptr,
+                         bonds, g, MsgTangent{}, go, src, rowptr, perm, nullptr, nullptr, dxe, d, nodes_src,
+                         nodes_dst, nchunks);
+    return msg_launch_status();
+  }
 }
 
 template <int LIN, int LE, int LOUT>

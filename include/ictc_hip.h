@@ -152,9 +152,12 @@ int ictc_hip_message_chunks(int channels);
 /*
  * Message VJP, per-edge part (receiver CSR, grad_out[n] read once per node): for every edge
  *   grad_gates[e]               = d<grad_out, node_out>/d gates[e]            [edges, P*C]
- *   grad_harmonics_partial[e,q] = the harmonics gradient of edge e summed over the
- *                                 channels of chunk q                 [edges, chunks, NY]
- *                                 (the caller sums the chunk axis)
+ *   grad_harmonics_partial[e,q] = partial sums over the channels of the harmonics
+ *                                 gradient of edge e              [edges, chunks, NY];
+ *                                 their sum over q (which the caller forms) is the
+ *                                 gradient.  Which channels a slot holds depends on
+ *                                 the kernel schedule (a slot may hold two chunks'
+ *                                 sum, its neighbour zero); it is fixed per degree set.
  *   edge_grad_features[e]       = sum_p gates[e,p] M_p[e]^T grad_out[dst(e)], the edge's
  *                                 contribution to the source-feature gradient
  *                                 [edges, C*(L_in+1)^2] (features layout)
