@@ -962,21 +962,25 @@ int launch_msg_forward_tangent(const ictc_tp_desc& d, const float* x, const floa
 }
 
 // ----------------------------------------------------------------------------- VJP by degree
-// First-order VJP for degree sets with a bond buffer (lmax 3), in one pass per input degree l1
-// (the groups of msg_forward_degree_kernel: each owns the x rows of degree l1, its paths' gates,
-// bond entries and dout rows, and so its dg columns and dxe rows).  Per edge and path, with
+// VJP for degree sets with a bond buffer (lmax 3), in one pass per input degree l1 (the groups of
+// msg_forward_degree_kernel: each owns the x rows of degree l1, its paths' gates, bond entries
+// and dout rows, and so its dg columns and dxe rows).  Per edge and path, with
 // w_I = sum_K M[K][I] dout_K (one LDS bond broadcast per (K, I), shared by the lane's CPL channels):
 //   dg_p   = sum_I x_I w_I                        (= sum_K dout_K sum_I x_I M[K][I])
 //   dxe_I += g_p w_I
 //   dY_j  += s_p sum_{I,K} C_p[I, j, K] (sum over the lane's channels of x_I g_p dout_K)
 // so the gates and bond rows are read once for all three outputs (the one-degree kernels read
-// them once in the dg/dY pass and again in the dxe pass).  dY partials: group launches run in
-// order on one stream; the first writes a block's channel sum into the slot of its first chunk
-// (and zero into its second), later groups add to it (a fixed order).
-template <int LIN, int LE, int LOUT, int L1, int CPL>
+// them once in the dg/dY pass and again in the dxe pass).  JVP = true gives the directional
+// derivative of all three in direction t = (tx, tM, tg) with dout fixed (the mixed second
+// derivatives; tw_I = sum_K tM[K][I] dout_K):
+//   dg_p = sum_I (tx_I w_I + x_I tw_I),  dxe_I += g_p tw_I + tg_p w_I,  x_I g_p -> tx_I g_p + x_I tg_p in dY.
+// dY partials: group launches run in order on one stream; the first writes a block's channel sum
+// into the slot of its first chunk (and zero into its second), later groups add to it (a fixed
+// order).
+template <int LIN, int LE, int LOUT, int L1, int CPL, bool JVP>
 __global__ void __launch_bounds__(kMsgBlock)
 msg_edge_grad_degree_kernel(const float* __restrict__ x, const float* __restrict__ bonds,
-                            const float* __restrict__ g, const float* __restrict__ go,
+                            const float* __restrict__ g, const MsgTangent t, const float* __restrict__ go,
                             const int64_t* __restrict__ src, const int64_t* __restrict__ rowptr,
                             const int64_t* __restrict__ perm, float* __restrict__ dyp, float* __restrict__ dg,
                             float* __restrict__ dxe, const ictc_tp_desc d, int64_t nodes_src, int nblk,
@@ -986,8 +990,9 @@ msg_edge_grad_degree_kernel(const float* __restrict__ x, const float* __restrict
   constexpr int NX = PS::NX, NY = PS::NY, NP = PS::N, NOCF = PS::NOC, NBF = PS::NB;
   constexpr int NPG = GT.np, NOC = GT.noc, NBG = GT.nb, NI = GT.nx;
   constexpr int NV = (NBG + kWave - 1) / kWave;
+  constexpr int NT = JVP ? 2 : 1;   // input sets per edge: primal (+ direction)
   static_assert(NPG > 0, "an input degree without paths has no launch");
-  __shared__ float sB[kMsgWaves][NV * kWave];
+  __shared__ float sB[kMsgWaves][NT][NV * kWave];
   __shared__ float sO[NOC][CPL * kWave];   // the group's dout rows of the node, for the block's chunks
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -1017,7 +1022,10 @@ msg_edge_grad_degree_kernel(const float* __restrict__ x, const float* __restrict
   }
   __syncthreads();
   const uint32_t xbytes = static_cast<uint32_t>(nodes_src * NX * row);
-  const rsrc_t rx = make_rsrc(dg != nullptr || dyp != nullptr ? x : nullptr, xbytes);   // range-checked gathers
+  const bool xdep = JVP || dg != nullptr || dyp != nullptr;   // the plain dxe needs no x
+  const rsrc_t rx[2] = {make_rsrc(xdep ? x : nullptr, xbytes), make_rsrc(JVP ? t.x : nullptr, xbytes)};
+  const float* gs[2] = {g, t.g};
+  const float* bsrc[2] = {bonds, t.bonds};
   uint32_t boff[NV];   // byte offsets of the lane's bond entries in a bond row
 #pragma unroll
   for (int r = 0; r < NV; ++r) {
@@ -1028,27 +1036,35 @@ msg_edge_grad_degree_kernel(const float* __restrict__ x, const float* __restrict
 #pragma clang loop unroll(disable)
   for (int64_t slot = s0 + wave; slot < s1; slot += kMsgWaves) {
     const int64_t e = perm ? perm[slot] : slot;
-    float bv[NV], xr[CPL][NI], gv[CPL][NPG];
-    {
-      const rsrc_t rb = make_rsrc(bonds + e * NBF, NBF * 4u);
+    float bv[NT][NV], xr[NT][CPL][NI], gv[NT][CPL][NPG];
 #pragma unroll
-      for (int r = 0; r < NV; ++r) bv[r] = buf_load<1>(rb, boff[r]).v[0];
+    for (int q = 0; q < NT; ++q) {   // bond entries first (staged into LDS below)
+      const rsrc_t rb = make_rsrc(bsrc[q] + e * NBF, NBF * 4u);
+#pragma unroll
+      for (int r = 0; r < NV; ++r) bv[q][r] = buf_load<1>(rb, boff[r]).v[0];
     }
     const uint32_t xoff = static_cast<uint32_t>(src[e]) * NX * row;
 #pragma unroll
-    for (int h = 0; h < CPL; ++h)
+    for (int q = 0; q < NT; ++q)
 #pragma unroll
-      for (int m = 0; m < NI; ++m) {
-        const float v = buf_load_vs(rx, xoff + vc[h], (L1 * L1 + m) * row);
-        xr[h][m] = live[h] ? v : 0.f;
-      }
-    const rsrc_t rg = make_rsrc(g + e * NP * C, NP * row);
+      for (int h = 0; h < CPL; ++h)
 #pragma unroll
-    for (int h = 0; h < CPL; ++h)
+        for (int m = 0; m < NI; ++m) {
+          const float v = buf_load_vs(rx[q], xoff + vc[h], (L1 * L1 + m) * row);
+          xr[q][h][m] = live[h] ? v : 0.f;
+        }
 #pragma unroll
-      for (int k = 0; k < NPG; ++k) gv[h][k] = buf_load_vs<kNonTemporal>(rg, vc[h], GT.path[k] * row);
+    for (int q = 0; q < NT; ++q) {
+      const rsrc_t rg = make_rsrc(gs[q] + e * NP * C, NP * row);
 #pragma unroll
-    for (int r = 0; r < NV; ++r) sB[wave][lane + r * kWave] = bv[r];
+      for (int h = 0; h < CPL; ++h)
+#pragma unroll
+        for (int k = 0; k < NPG; ++k) gv[q][h][k] = buf_load_vs<kNonTemporal>(rg, vc[h], GT.path[k] * row);
+    }
+#pragma unroll
+    for (int q = 0; q < NT; ++q)
+#pragma unroll
+      for (int r = 0; r < NV; ++r) sB[wave][q][lane + r * kWave] = bv[q][r];
     wave_lds_sync();
     const rsrc_t rdg = make_rsrc(dg ? dg + e * NP * C : nullptr, NP * row);
     float dyl[NY], dxl[CPL][NI];
@@ -1065,21 +1081,26 @@ msg_edge_grad_degree_kernel(const float* __restrict__ x, const float* __restrict
       constexpr int ni = NI, nj = 2 * l2 + 1, no = 2 * l3 + 1;
       constexpr int bo = GT.bond[k], oo = GT.out[k];
       using CG = CGTab<L1, l2, l3>;
-      const float* bp = opaque_lds_row(&sB[wave][bo]);
+      const float* bp = opaque_lds_row(&sB[wave][0][bo]);
+      const float* tp = JVP ? opaque_lds_row(&sB[wave][NT - 1][bo]) : bp;
       __builtin_amdgcn_sched_barrier(0);
-      float w[CPL][ni];
+      float w[CPL][ni], tw[CPL][ni];
 #pragma unroll
       for (int h = 0; h < CPL; ++h)
 #pragma unroll
-        for (int i = 0; i < ni; ++i) w[h][i] = 0.f;
+        for (int i = 0; i < ni; ++i) w[h][i] = tw[h][i] = 0.f;
       static_for<0, no>([&](auto K) {
         float ov[CPL];
 #pragma unroll
         for (int h = 0; h < CPL; ++h) ov[h] = sO[oo + K][h * kWave + lane];
         static_for<0, ni>([&](auto I) {
           const float b = bp[K * ni + I];
+          const float tb = JVP ? tp[K * ni + I] : 0.f;
 #pragma unroll
-          for (int h = 0; h < CPL; ++h) w[h][I] = fmaf(b, ov[h], w[h][I]);
+          for (int h = 0; h < CPL; ++h) {
+            w[h][I] = fmaf(b, ov[h], w[h][I]);
+            if constexpr (JVP) tw[h][I] = fmaf(tb, ov[h], tw[h][I]);
+          }
         });
       });
 #pragma unroll
@@ -1087,8 +1108,15 @@ msg_edge_grad_degree_kernel(const float* __restrict__ x, const float* __restrict
         float dgv = 0.f;
 #pragma unroll
         for (int i = 0; i < ni; ++i) {
-          dgv = fmaf(xr[h][i], w[h][i], dgv);
-          dxl[h][i] = fmaf(gv[h][k], w[h][i], dxl[h][i]);
+          if constexpr (JVP) {
+            dgv = fmaf(xr[1][h][i], w[h][i], dgv);
+            dgv = fmaf(xr[0][h][i], tw[h][i], dgv);
+            dxl[h][i] = fmaf(gv[0][h][k], tw[h][i], dxl[h][i]);
+            dxl[h][i] = fmaf(gv[1][h][k], w[h][i], dxl[h][i]);
+          } else {
+            dgv = fmaf(xr[0][h][i], w[h][i], dgv);
+            dxl[h][i] = fmaf(gv[0][h][k], w[h][i], dxl[h][i]);
+          }
         }
         buf_store_lane(rdg, live[h], vc[h] + p * row, dgv);   // null dg: empty descriptor
       }
@@ -1099,7 +1127,8 @@ msg_edge_grad_degree_kernel(const float* __restrict__ x, const float* __restrict
         static_for<0, ni>([&](auto I) {
           float xg[CPL];
 #pragma unroll
-          for (int h = 0; h < CPL; ++h) xg[h] = xr[h][I] * gv[h][k];
+          for (int h = 0; h < CPL; ++h)
+            xg[h] = JVP ? fmaf(xr[1][h][I], gv[0][h][k], xr[0][h][I] * gv[1][h][k]) : xr[0][h][I] * gv[0][h][k];
           static_for<0, no>([&](auto K) {
             float tt = xg[0] * sO[oo + K][lane];
 #pragma unroll
@@ -1142,26 +1171,33 @@ msg_edge_grad_degree_kernel(const float* __restrict__ x, const float* __restrict
 }
 
 // One launch per input degree that has paths (dY partials accumulated across them in launch
-// order); two chunks per lane when the channels span two.
-template <int LIN, int LE, int LOUT>
+// order); two chunks per lane when the channels span two, except for the tangent passes of the
+// groups with more than 96 bond entries (l1 = 2, 3 at lmax 3), whose doubled inputs need 256
+// VGPRs at two chunks (one wave per SIMD): one chunk per lane there, 156-165 VGPRs (measured
+// at C = 128: 741 / 893 us at two chunks, 517 / 609 us at one).
+template <int LIN, int LE, int LOUT, bool JVP>
 int launch_msg_edge_grad_degrees(const ictc_tp_desc& d, const float* x, const float* bonds, const float* g,
-                                 const float* go, const int64_t* src, const int64_t* rowptr, const int64_t* perm,
-                                 float* dyp, float* dg, float* dxe, int64_t nodes_src, int64_t nodes_dst,
-                                 hipStream_t stream) {
+                                 const MsgTangent& t, const float* go, const int64_t* src, const int64_t* rowptr,
+                                 const int64_t* perm, float* dyp, float* dg, float* dxe, int64_t nodes_src,
+                                 int64_t nodes_dst, hipStream_t stream) {
   const int nchunks = (d.channels + kWave - 1) / kWave;
-  const bool two = nchunks >= 2;
-  const int nblk = two ? (nchunks + 1) / 2 : nchunks;
-  const dim3 grid(static_cast<unsigned>(nodes_dst * nblk));
   int first = 1;
   auto one = [&](auto deg) {
     constexpr int L1 = decltype(deg)::value;
-    if constexpr (DegreeGroupOf<LIN, LE, LOUT, L1>::tab.np > 0) {
+    constexpr DegreeGroup GT = DegreeGroupOf<LIN, LE, LOUT, L1>::tab;
+    if constexpr (GT.np > 0) {
+      constexpr bool kOneChunk = JVP && GT.nb > 96;
+      const bool two = !kOneChunk && nchunks >= 2;
+      const int nblk = two ? (nchunks + 1) / 2 : nchunks;
+      const dim3 grid(static_cast<unsigned>(nodes_dst * nblk));
       if (two)
-        hipLaunchKernelGGL((msg_edge_grad_degree_kernel<LIN, LE, LOUT, L1, 2>), grid, dim3(kMsgBlock), 0, stream,
-                           x, bonds, g, go, src, rowptr, perm, dyp, dg, dxe, d, nodes_src, nblk, nchunks, first);
+        hipLaunchKernelGGL((msg_edge_grad_degree_kernel<LIN, LE, LOUT, L1, 2, JVP>), grid, dim3(kMsgBlock), 0,
+                           stream, x, bonds, g, t, go, src, rowptr, perm, dyp, dg, dxe, d, nodes_src, nblk, nchunks,
+                           first);
       else
-        hipLaunchKernelGGL((msg_edge_grad_degree_kernel<LIN, LE, LOUT, L1, 1>), grid, dim3(kMsgBlock), 0, stream,
-                           x, bonds, g, go, src, rowptr, perm, dyp, dg, dxe, d, nodes_src, nblk, nchunks, first);
+        hipLaunchKernelGGL((msg_edge_grad_degree_kernel<LIN, LE, LOUT, L1, 1, JVP>), grid, dim3(kMsgBlock), 0,
+                           stream, x, bonds, g, t, go, src, rowptr, perm, dyp, dg, dxe, d, nodes_src, nblk, nchunks,
+                           first);
       first = 0;
     }
   };
@@ -1178,8 +1214,8 @@ int launch_msg_edge_grad(const ictc_tp_desc& d, const float* x, const float* bon
                          float* dyp, float* dg, float* dxe, int64_t nodes_src, int64_t nodes_dst,
                          hipStream_t stream) {
   if constexpr (!BondInline<LIN, LE, LOUT>::value && Paths<LIN, LE, LOUT>::NB > 0) {
-    return launch_msg_edge_grad_degrees<LIN, LE, LOUT>(d, x, bonds, g, go, src, rowptr, perm, dyp, dg, dxe,
-                                                      nodes_src, nodes_dst, stream);
+    return launch_msg_edge_grad_degrees<LIN, LE, LOUT, false>(d, x, bonds, g, MsgTangent{}, go, src, rowptr, perm,
+                                                             dyp, dg, dxe, nodes_src, nodes_dst, stream);
   } else {
     const int nchunks = (d.channels + kWave - 1) / kWave;
     const dim3 grid(static_cast<unsigned>(nodes_dst * nchunks));   // one block per (node, chunk)
@@ -1199,20 +1235,25 @@ int launch_msg_edge_grad_tangent(const ictc_tp_desc& d, const float* x, const fl
                                  const MsgTangent& t, const float* go, const int64_t* src, const int64_t* rowptr,
                                  const int64_t* perm, float* dyp, float* dg, float* dxe, int64_t nodes_src,
                                  int64_t nodes_dst, hipStream_t stream) {
-  const int nchunks = (d.channels + kWave - 1) / kWave;
-  const dim3 grid(static_cast<unsigned>(nodes_dst * nchunks));
-  if (dyp != nullptr || dg != nullptr)
-    hipLaunchKernelGGL((msg_edge_grad_kernel<LIN, LE, LOUT, true, true>), grid, dim3(kMsgBlock), 0, stream, x,
-                       bonds, g, t, go, src, rowptr, perm, dyp, dg, nullptr, d, nodes_src, nodes_dst, nchunks);
-  if (dxe != nullptr) {
-    hipLaunchKernelGGL((msg_edge_grad_kernel<LIN, LE, LOUT, false>), grid, dim3(kMsgBlock), 0, stream, nullptr,
-                       t.bonds, g, MsgTangent{}, go, src, rowptr, perm, nullptr, nullptr, dxe, d, nodes_src,
-                       nodes_dst, nchunks);
-    hipLaunchKernelGGL((msg_edge_grad_kernel<LIN, LE, LOUT, false, false, true>), grid, dim3(kMsgBlock), 0, stream,
-                       nullptr, bonds, t.g, MsgTangent{}, go, src, rowptr, perm, nullptr, nullptr, dxe, d, nodes_src,
-                       nodes_dst, nchunks);
+  if constexpr (!BondInline<LIN, LE, LOUT>::value && Paths<LIN, LE, LOUT>::NB > 0) {
+    return launch_msg_edge_grad_degrees<LIN, LE, LOUT, true>(d, x, bonds, g, t, go, src, rowptr, perm, dyp, dg, dxe,
+                                                            nodes_src, nodes_dst, stream);
+  } else {
+    const int nchunks = (d.channels + kWave - 1) / kWave;
+    const dim3 grid(static_cast<unsigned>(nodes_dst * nchunks));
+    if (dyp != nullptr || dg != nullptr)
+      hipLaunchKernelGGL((msg_edge_grad_kernel<LIN, LE, LOUT, true, true>), grid, dim3(kMsgBlock), 0, stream, x,
+                         bonds, g, t, go, src, rowptr, perm, dyp, dg, nullptr, d, nodes_src, nodes_dst, nchunks);
+    if (dxe != nullptr) {
+      hipLaunchKernelGGL((msg_edge_grad_kernel<LIN, LE, LOUT, false>), grid, dim3(kMsgBlock), 0, stream, nullptr,
+                         t.bonds, g, MsgTangent{}, go, src, rowptr, perm, nullptr, nullptr, dxe, d, nodes_src,
+                         nodes_dst, nchunks);
+      hipLaunchKernelGGL((msg_edge_grad_kernel<LIN, LE, LOUT, false, false, true>), grid, dim3(kMsgBlock), 0,
+                         stream, nullptr, bonds, t.g, MsgTangent{}, go, src, rowptr, perm, nullptr, nullptr, dxe, d,
+                         nodes_src, nodes_dst, nchunks);
+    }
+    return msg_launch_status();
   }
-  return msg_launch_status();
 }
 
 template <int LIN>
