@@ -18,13 +18,13 @@
 //     requested together (one round trip), the bond row is staged in the wave's LDS row,
 //     and the kernel is kept small enough in registers that several waves per SIMD hide
 //     the latency;
-//   * msg_edge_grad_kernel (receiver CSR): one block per (node, 64-channel chunk) stages
-//     dout[n] in LDS once and its waves split the node's edges; per edge dg, dY partials
-//     per chunk, or the edge's contribution to the source-feature adjoint
-//     dxe[e] = sum_p g_p M_p^T dout[dst(e)] (so dout is never gathered per edge);
-//   * msg_forward_degree_kernel / msg_edge_grad_degree_kernel: the forward and the first-order
-//     VJP (dg, dY and dxe in one pass) for degree sets with a bond buffer, one launch per input
-//     degree with two channel chunks per lane;
+//   * msg_forward_degree_kernel (degree sets with a bond buffer): the forward and its tangent,
+//     one launch per input degree with two channel chunks per lane;
+//   * msg_edge_grad_degree_kernel (receiver CSR, every degree set): one block per (node, channel
+//     chunks) stages the node's dout rows in LDS once and its waves split the node's edges;
+//     per edge dg, dY partials and the edge's contribution to the source-feature adjoint
+//     dxe[e] = sum_p g_p M_p^T dout[dst(e)] (so dout is never gathered per edge), in one pass
+//     per input degree (first order or tangent);
 //   * msg_node_grad_kernel (source CSR): dx[s] = sum over the out-edges of s of dxe[e],
 //     a streaming segmented sum.
 // Node-feature gathers go through buffer descriptors spanning the whole node tensor,
@@ -654,214 +654,6 @@ int launch_msg_forward_degrees(const ictc_tp_desc& d, const float* x, const floa
   return msg_launch_status();
 }
 
-// ----------------------------------------------------------------------------- VJP: per edge
-// Optional outputs (null = skip): dyp[e*nchunks + chunk][NY] dY partials, dg[e] raw gate
-// adjoint, dxe[e] [NX][C] the edge's source-feature adjoint.  XDEP instantiations read x and
-// produce dY / dg; the others produce dxe only (two lean passes instead of one kernel whose
-// live state would not fit in registers at lmax 3).
-// JVP = true (XDEP passes) computes the directional derivative of dg and dY in direction t
-// with dout fixed (the mixed second derivatives, reference structured_product.py:146-158 and
-// the mixed-second mode of ascendc/op_kernel/epilogue_adjoint.cpp):
-//   dg[p]  = sum_k dout_k sum_i (tx_i M[k,i] + x_i tM[k,i])
-//   dY     : x_i g_p replaced by tx_i g_p + x_i tg_p
-// The dxe derivative, sum_p (g_p tM_p^T + tg_p M_p^T) dout, is two plain dxe passes, the
-// second with ACC = true (adds to the rows the first wrote): one fused pass held both gate
-// sets and both bond rows live and needed 256 VGPRs at lmax 3.
-template <int LIN, int LE, int LOUT, bool XDEP, bool JVP = false, bool ACC = false>
-__global__ void __launch_bounds__(kMsgBlock)
-msg_edge_grad_kernel(const float* __restrict__ x, const float* __restrict__ bonds, const float* __restrict__ g,
-                     const MsgTangent t, const float* __restrict__ go, const int64_t* __restrict__ src,
-                     const int64_t* __restrict__ rowptr, const int64_t* __restrict__ perm,
-                     float* __restrict__ dyp, float* __restrict__ dg, float* __restrict__ dxe,
-                     const ictc_tp_desc d, int64_t nodes_src, int64_t nodes_dst, int nchunks) {
-  static_assert(XDEP || !JVP, "the dxe derivative is two plain dxe passes (ACC on the second)");
-  static_assert(!(XDEP && ACC), "ACC applies to the dxe pass");
-  using PS = Paths<LIN, LE, LOUT>;
-  constexpr int NX = PS::NX, NY = PS::NY, NP = PS::N, NOC = PS::NOC, NB = PS::NB;
-  constexpr int NBS = BondStage<NB>::NV * kWave;
-  constexpr int NT = JVP ? 2 : 1;   // input sets per edge: primal (+ direction)
-  __shared__ float sB[kMsgWaves][NT][NBS];
-  __shared__ float sO[NOC * kWave];   // the node's dout chunk, shared by the block's waves
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  // one block per (node, chunk); its waves take every kMsgWaves-th edge of the node;
-  // receivers contiguous per XCD
-  const uint32_t item = xcd_block(blockIdx.x, gridDim.x);
-  const int64_t node = static_cast<int64_t>(item) / nchunks;
-  const int chunk = static_cast<int>(item - node * nchunks);
-  const int C = d.channels;
-  const int c = chunk * kWave + lane;
-  const uint32_t row = static_cast<uint32_t>(C) * 4u;
-  const bool live = c < C;
-  const uint32_t xbytes = static_cast<uint32_t>(nodes_src * NX * row);
-  const rsrc_t rx[2] = {make_rsrc(x, xbytes), make_rsrc(JVP ? t.x : x, xbytes)};
-  const float* gs[2] = {g, t.g};
-  const float* bs_src[2] = {bonds, t.bonds};
-  // lanes past C read channel 0 and zero it (dY sums over lanes); uniform row offsets in soffset
-  const uint32_t vc = static_cast<uint32_t>(live ? c : 0) * 4u;
-  {
-    const rsrc_t ron = make_rsrc(go + node * NOC * C, NOC * row);
-    // read once: non-temporal in the dg/dY pass (measured 1-10 % faster); the dxe pass keeps the
-    // default policy (3 % slower with it at lmax 2)
-    constexpr int kDoutPolicy = XDEP ? kNonTemporal : 0;
-    for (int r = wave; r < NOC; r += kMsgWaves) {
-      const float v = buf_load_vs<kDoutPolicy>(ron, vc, r * row);
-      sO[r * kWave + lane] = live ? v : 0.f;
-    }
-  }
-  __syncthreads();
-  const float* __restrict__ o = sO + lane;   // o[r * kWave]: this lane's channel of dout row r
-
-  BondCoef<LIN, LE, LOUT> bc;
-  bc.init(d, lane);
-  auto fetch = [&](int64_t slot, int64_t& eo, float (*xo)[NX], float (*gvo)[NP], BondStage<NB>* bo) {
-    const int64_t e = perm ? perm[slot] : slot;
-    eo = e;
-#pragma unroll
-    for (int q = 0; q < NT; ++q) bond_row<LIN, LE, LOUT>(bs_src[q], e, lane, bc, bo[q]);   // first
-    const uint32_t xoff = static_cast<uint32_t>(src[e]) * NX * row + vc;   // range-checked gather
-    if constexpr (XDEP) {
-#pragma unroll
-      for (int q = 0; q < NT; ++q)
-#pragma unroll
-        for (int m = 0; m < NX; ++m) {
-          const float v = buf_load_vs(rx[q], xoff, m * row);
-          xo[q][m] = live ? v : 0.f;
-        }
-    }
-#pragma unroll
-    for (int q = 0; q < NT; ++q) {
-      const rsrc_t rg = make_rsrc(gs[q] + e * NP * C, NP * row);
-#pragma unroll
-      for (int p = 0; p < NP; ++p) gvo[q][p] = buf_load_vs<kNonTemporal>(rg, vc, p * row);
-    }
-  };
-
-  auto compute = [&](int64_t e, const float (*xr)[NX], const float (*gv)[NP], const float* bond0,
-                     const float* bond1) {
-    const rsrc_t rdg = make_rsrc(dg ? dg + e * NP * C : nullptr, NP * row);
-    float dyl[NY], dxl[NX];   // dY partials (XDEP) / source-feature adjoint (otherwise)
-#pragma unroll
-    for (int j = 0; j < NY; ++j) dyl[j] = 0.f;
-#pragma unroll
-    for (int m = 0; m < NX; ++m) dxl[m] = 0.f;
-    static_for<0, NP>([&](auto P) {
-      constexpr int p = P;
-      constexpr int l1 = PS::tab.l1[p], l2 = PS::tab.l2[p], l3 = PS::tab.l3[p];
-      constexpr int ni = 2 * l1 + 1, nj = 2 * l2 + 1, no = 2 * l3 + 1;
-      constexpr int boff = PS::tab.bond[p], oo = PS::tab.out[p];
-      using CG = CGTab<l1, l2, l3>;
-      // per-path opaque bases keep the bond and dout reads of a path next to their use
-      // instead of hoisting every path's reads; products with the gate come after them
-      // (g_p o_k for every path would hold NOC extra registers)
-      const float* bp = opaque_lds_row(bond0 + boff);
-      const float* tp = JVP ? opaque_lds_row(bond1 + boff) : bp;
-      const float* op = XDEP ? o + oo * kWave : opaque_lds_row(o + oo * kWave);
-      __builtin_amdgcn_sched_barrier(0);
-      const float gp = live ? gv[0][p] : 0.f;
-      const float tgp = JVP && live ? gv[NT - 1][p] : 0.f;
-      if constexpr (!XDEP && !JVP) {   // source-feature adjoint: dxl_i += g_p sum_k M_p[k][i] o_k
-        static_for<0, ni>([&](auto I) {
-          float u = 0.f;
-          static_for<0, no>([&](auto K) { u = fmaf(bp[K * ni + I], op[K * kWave], u); });
-          dxl[l1 * l1 + I] = fmaf(gp, u, dxl[l1 * l1 + I]);
-        });
-      }
-      if constexpr (XDEP) {
-        float dgv = 0.f;
-        static_for<0, no>([&](auto K) {
-          float base = 0.f;
-          static_for<0, ni>([&](auto I) {
-            base = fmaf(xr[NT - 1][l1 * l1 + I], bp[K * ni + I], base);   // x M (tx M under JVP)
-            if constexpr (JVP) base = fmaf(xr[0][l1 * l1 + I], tp[K * ni + I], base);   // + x tM
-          });
-          dgv = fmaf(base, o[(oo + K) * kWave], dgv);
-        });
-        buf_store_lane(rdg, live, c * 4u + p * row, dgv);   // null dg: empty descriptor
-        if (dyp != nullptr) {
-          float part[nj];
-#pragma unroll
-          for (int j = 0; j < nj; ++j) part[j] = 0.f;
-          static_for<0, ni>([&](auto I) {
-            const float xg = JVP ? fmaf(xr[1][l1 * l1 + I], gp, xr[0][l1 * l1 + I] * tgp)
-                                 : xr[0][l1 * l1 + I] * gp;
-            static_for<0, no>([&](auto K) {
-              const float tt = xg * o[(oo + K) * kWave];
-              static_for<0, nj>([&](auto J) {
-                constexpr float cg = CG::v[(I * nj + J) * no + K];
-                if constexpr (cg != 0.0f) part[J] = fmaf(cg, tt, part[J]);
-              });
-            });
-          });
-          const float sc = d.scale[p];
-#pragma unroll
-          for (int j = 0; j < nj; ++j) dyl[l2 * l2 + j] = fmaf(sc, part[j], dyl[l2 * l2 + j]);
-        }
-      }
-    });
-    if constexpr (!XDEP) {
-      const rsrc_t rde = make_rsrc(dxe ? dxe + e * NX * C : nullptr, NX * row);
-      if constexpr (ACC) {   // add to the dxe rows an earlier launch wrote
-#pragma unroll
-        for (int m = 0; m < NX; ++m) dxl[m] += buf_load_vs(rde, vc, m * row);
-      }
-#pragma unroll
-      for (int m = 0; m < NX; ++m) buf_store_lane(rde, live, c * 4u + m * row, dxl[m]);
-    }
-    if (XDEP && dyp != nullptr) {   // channel sums of the NY partials, one transposing butterfly
-      using WS = WaveSums<NY>;
-      const float tot = WS::reduce(dyl, lane);
-      const int j = WS::index(lane);
-      if (WS::owner(lane) && j < NY) dyp[(e * nchunks + chunk) * NY + j] = tot;
-    }
-  };
-
-  const int64_t s0 = rowptr[node], s1 = rowptr[node + 1];
-  if constexpr (XDEP && !JVP) {
-    // The dg pass stores NP rows per edge; the next edge's loads are requested before them, so
-    // waiting for those loads does not also wait for this edge's stores (one in-order vmcnt).
-    // Measured 4-7 % faster at lmax 2 and 3; the dxe pass (NX stores after the path loop)
-    // gained nothing consistent and stays unpipelined (fewer VGPRs), as do the JVP passes
-    // (twice the per-edge inputs).
-    int64_t slot = s0 + wave;
-    if (slot >= s1) return;
-    float xr[1][NX], gv[1][NP];
-    int64_t e;
-    BondStage<NB> bs[1];
-    fetch(slot, e, xr, gv, bs);
-#pragma clang loop unroll(disable)
-    for (;;) {
-      const int64_t nslot = slot + kMsgWaves;
-      const bool more = nslot < s1;
-      float xn[1][NX], gn[1][NP];
-      int64_t en = e;
-      BondStage<NB> bn[1];
-      if (more) fetch(nslot, en, xn, gn, bn);
-      bond_commit<NB>(bs[0], &sB[wave][0][0], lane);
-      compute(e, xr, gv, &sB[wave][0][0], &sB[wave][0][0]);
-      if (!more) break;
-#pragma unroll
-      for (int m = 0; m < NX; ++m) xr[0][m] = xn[0][m];
-#pragma unroll
-      for (int p = 0; p < NP; ++p) gv[0][p] = gn[0][p];
-      bs[0] = bn[0];
-      e = en;
-      slot = nslot;
-    }
-  } else {
-#pragma clang loop unroll(disable)
-    for (int64_t slot = s0 + wave; slot < s1; slot += kMsgWaves) {
-      float xr[NT][NX], gv[NT][NP];
-      int64_t e;
-      BondStage<NB> bs[NT];
-      fetch(slot, e, xr, gv, bs);
-#pragma unroll
-      for (int q = 0; q < NT; ++q) bond_commit<NB>(bs[q], &sB[wave][q][0], lane);
-      compute(e, xr, gv, &sB[wave][0][0], &sB[wave][NT - 1][0]);
-    }
-  }
-}
-
 // ----------------------------------------------------------------------------- VJP: per source node
 // dx[s] = sum over edges with src(e) = s of dxe[e]  ([NX][C] rows, streamed four edges at a time;
 // each row is read once, with the non-temporal cache policy: 7-11 % faster measured).
@@ -962,7 +754,8 @@ int launch_msg_forward_tangent(const ictc_tp_desc& d, const float* x, const floa
 }
 
 // ----------------------------------------------------------------------------- VJP by degree
-// VJP for degree sets with a bond buffer (lmax 3), in one pass per input degree l1 (the groups of
+// VJP in one pass per input degree l1, for every degree set (bond rows from the buffer or, for
+// small sets, formed in-kernel from the harmonics as the one-degree kernels do) (the groups of
 // msg_forward_degree_kernel: each owns the x rows of degree l1, its paths' gates, bond entries
 // and dout rows, and so its dg columns and dxe rows).  Per edge and path, with
 // w_I = sum_K M[K][I] dout_K (one LDS bond broadcast per (K, I), shared by the lane's CPL channels):
@@ -1026,11 +819,22 @@ msg_edge_grad_degree_kernel(const float* __restrict__ x, const float* __restrict
   const rsrc_t rx[2] = {make_rsrc(xdep ? x : nullptr, xbytes), make_rsrc(JVP ? t.x : nullptr, xbytes)};
   const float* gs[2] = {g, t.g};
   const float* bsrc[2] = {bonds, t.bonds};
-  uint32_t boff[NV];   // byte offsets of the lane's bond entries in a bond row
+  // the lane's bond entries lane + 64 r of the group: their byte offsets in a bond row, or (rows
+  // formed in-kernel) their projection coefficients s_p C_p[i, j - l2^2, k] (zero past the group)
+  constexpr bool INL = BondInline<LIN, LE, LOUT>::value;
+  uint32_t boff[NV];
+  float cf[INL ? NV : 1][INL ? NY : 1];
 #pragma unroll
   for (int r = 0; r < NV; ++r) {
     const int idx = lane + r * kWave;
-    boff[r] = static_cast<uint32_t>(idx < NBG ? kDegreeGroup<LIN, LE, LOUT, L1>.bidx[idx] : 0) * 4u;
+    const int ge = idx < NBG ? kDegreeGroup<LIN, LE, LOUT, L1>.bidx[idx] : 0;
+    boff[r] = static_cast<uint32_t>(ge) * 4u;
+    if constexpr (INL) {
+      const BondDense<LIN, LE, LOUT>& bt = kBondDense<LIN, LE, LOUT>;
+      const float sc = idx < NBG ? d.scale[bt.path[ge]] : 0.f;
+#pragma unroll
+      for (int j = 0; j < NY; ++j) cf[r][j] = bt.cg[ge][j] * sc;
+    }
   }
   const int64_t s0 = rowptr[node], s1 = rowptr[node + 1];
 #pragma clang loop unroll(disable)
@@ -1039,9 +843,24 @@ msg_edge_grad_degree_kernel(const float* __restrict__ x, const float* __restrict
     float bv[NT][NV], xr[NT][CPL][NI], gv[NT][CPL][NPG];
 #pragma unroll
     for (int q = 0; q < NT; ++q) {   // bond entries first (staged into LDS below)
-      const rsrc_t rb = make_rsrc(bsrc[q] + e * NBF, NBF * 4u);
+      if constexpr (INL) {   // from the harmonics row: one load, broadcast from lanes 0..NY-1
+        const float yl = bsrc[q][e * NY + (lane < NY ? lane : NY - 1)];
+        float yv[NY];
 #pragma unroll
-      for (int r = 0; r < NV; ++r) bv[q][r] = buf_load<1>(rb, boff[r]).v[0];
+        for (int j = 0; j < NY; ++j)
+          yv[j] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, yl), j));
+#pragma unroll
+        for (int r = 0; r < NV; ++r) {
+          float acc = 0.f;
+#pragma unroll
+          for (int j = 0; j < NY; ++j) acc = fmaf(yv[j], cf[r][j], acc);
+          bv[q][r] = acc;
+        }
+      } else {
+        const rsrc_t rb = make_rsrc(bsrc[q] + e * NBF, NBF * 4u);
+#pragma unroll
+        for (int r = 0; r < NV; ++r) bv[q][r] = buf_load<1>(rb, boff[r]).v[0];
+      }
     }
     const uint32_t xoff = static_cast<uint32_t>(src[e]) * NX * row;
 #pragma unroll
@@ -1170,11 +989,27 @@ msg_edge_grad_degree_kernel(const float* __restrict__ x, const float* __restrict
   }
 }
 
+// dxe[e, r0 .. r0 + nr) = 0 for every edge e (rows of an input degree without paths); the edge
+// count is read from the receiver CSR's last entry.
+template <int NX>
+__global__ void __launch_bounds__(256)
+msg_zero_rows_kernel(const int64_t* __restrict__ rowptr, int64_t nodes_dst, float* __restrict__ dxe, int r0, int nr,
+                     int channels) {
+  const int64_t edges = rowptr[nodes_dst];
+  const int64_t per = static_cast<int64_t>(nr) * channels;
+  const int64_t total = edges * per;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t e = i / per, q = i - e * per;
+    dxe[e * NX * channels + static_cast<int64_t>(r0) * channels + q] = 0.f;
+  }
+}
+
 // One launch per input degree that has paths (dY partials accumulated across them in launch
 // order); two chunks per lane when the channels span two, except for the tangent passes of the
-// groups with more than 96 bond entries (l1 = 2, 3 at lmax 3), whose doubled inputs need 256
-// VGPRs at two chunks (one wave per SIMD): one chunk per lane there, 156-165 VGPRs (measured
-// at C = 128: 741 / 893 us at two chunks, 517 / 609 us at one).
+// groups l1 >= 2, whose doubled inputs need 196-256 VGPRs at two chunks (one or two waves per
+// SIMD): one chunk per lane there, 126-165 VGPRs (measured at C = 128, lmax 3: 741 / 893 us at
+// two chunks, 517 / 609 us at one).
 template <int LIN, int LE, int LOUT, bool JVP>
 int launch_msg_edge_grad_degrees(const ictc_tp_desc& d, const float* x, const float* bonds, const float* g,
                                  const MsgTangent& t, const float* go, const int64_t* src, const int64_t* rowptr,
@@ -1186,7 +1021,7 @@ int launch_msg_edge_grad_degrees(const ictc_tp_desc& d, const float* x, const fl
     constexpr int L1 = decltype(deg)::value;
     constexpr DegreeGroup GT = DegreeGroupOf<LIN, LE, LOUT, L1>::tab;
     if constexpr (GT.np > 0) {
-      constexpr bool kOneChunk = JVP && GT.nb > 96;
+      constexpr bool kOneChunk = JVP && L1 >= 2;
       const bool two = !kOneChunk && nchunks >= 2;
       const int nblk = two ? (nchunks + 1) / 2 : nchunks;
       const dim3 grid(static_cast<unsigned>(nodes_dst * nblk));
@@ -1205,6 +1040,20 @@ int launch_msg_edge_grad_degrees(const ictc_tp_desc& d, const float* x, const fl
   if constexpr (LIN >= 1) one(Int<1>{});
   if constexpr (LIN >= 2) one(Int<2>{});
   if constexpr (LIN >= 3) one(Int<3>{});
+  // input degrees without paths (e.g. l1 > LE + LOUT) own dxe rows no group writes: zero them
+  if (dxe != nullptr) {
+    auto zero = [&](auto deg) {
+      constexpr int L1 = decltype(deg)::value;
+      if constexpr (DegreeGroupOf<LIN, LE, LOUT, L1>::tab.np == 0) {
+        hipLaunchKernelGGL((msg_zero_rows_kernel<Paths<LIN, LE, LOUT>::NX>), dim3(1024), dim3(256), 0, stream,
+                           rowptr, nodes_dst, dxe, L1 * L1, 2 * L1 + 1, d.channels);
+      }
+    };
+    zero(Int<0>{});
+    if constexpr (LIN >= 1) zero(Int<1>{});
+    if constexpr (LIN >= 2) zero(Int<2>{});
+    if constexpr (LIN >= 3) zero(Int<3>{});
+  }
   return msg_launch_status();
 }
 
@@ -1213,21 +1062,8 @@ int launch_msg_edge_grad(const ictc_tp_desc& d, const float* x, const float* bon
                          const float* go, const int64_t* src, const int64_t* rowptr, const int64_t* perm,
                          float* dyp, float* dg, float* dxe, int64_t nodes_src, int64_t nodes_dst,
                          hipStream_t stream) {
-  if constexpr (!BondInline<LIN, LE, LOUT>::value && Paths<LIN, LE, LOUT>::NB > 0) {
-    return launch_msg_edge_grad_degrees<LIN, LE, LOUT, false>(d, x, bonds, g, MsgTangent{}, go, src, rowptr, perm,
-                                                             dyp, dg, dxe, nodes_src, nodes_dst, stream);
-  } else {
-    const int nchunks = (d.channels + kWave - 1) / kWave;
-    const dim3 grid(static_cast<unsigned>(nodes_dst * nchunks));   // one block per (node, chunk)
-    if (dyp != nullptr || dg != nullptr)
-      hipLaunchKernelGGL((msg_edge_grad_kernel<LIN, LE, LOUT, true>), grid, dim3(kMsgBlock), 0, stream, x, bonds,
-                         g, MsgTangent{}, go, src, rowptr, perm, dyp, dg, nullptr, d, nodes_src, nodes_dst, nchunks);
-    if (dxe != nullptr)
-      hipLaunchKernelGGL((msg_edge_grad_kernel<LIN, LE, LOUT, false>), grid, dim3(kMsgBlock), 0, stream, nullptr,
-                         bonds, g, MsgTangent{}, go, src, rowptr, perm, nullptr, nullptr, dxe, d, nodes_src,
-                         nodes_dst, nchunks);
-    return msg_launch_status();
-  }
+  return launch_msg_edge_grad_degrees<LIN, LE, LOUT, false>(d, x, bonds, g, MsgTangent{}, go, src, rowptr, perm, dyp,
+                                                           dg, dxe, nodes_src, nodes_dst, stream);
 }
 
 template <int LIN, int LE, int LOUT>
@@ -1235,25 +1071,8 @@ int launch_msg_edge_grad_tangent(const ictc_tp_desc& d, const float* x, const fl
                                  const MsgTangent& t, const float* go, const int64_t* src, const int64_t* rowptr,
                                  const int64_t* perm, float* dyp, float* dg, float* dxe, int64_t nodes_src,
                                  int64_t nodes_dst, hipStream_t stream) {
-  if constexpr (!BondInline<LIN, LE, LOUT>::value && Paths<LIN, LE, LOUT>::NB > 0) {
-    return launch_msg_edge_grad_degrees<LIN, LE, LOUT, true>(d, x, bonds, g, t, go, src, rowptr, perm, dyp, dg, dxe,
-                                                            nodes_src, nodes_dst, stream);
-  } else {
-    const int nchunks = (d.channels + kWave - 1) / kWave;
-    const dim3 grid(static_cast<unsigned>(nodes_dst * nchunks));
-    if (dyp != nullptr || dg != nullptr)
-      hipLaunchKernelGGL((msg_edge_grad_kernel<LIN, LE, LOUT, true, true>), grid, dim3(kMsgBlock), 0, stream, x,
-                         bonds, g, t, go, src, rowptr, perm, dyp, dg, nullptr, d, nodes_src, nodes_dst, nchunks);
-    if (dxe != nullptr) {
-      hipLaunchKernelGGL((msg_edge_grad_kernel<LIN, LE, LOUT, false>), grid, dim3(kMsgBlock), 0, stream, nullptr,
-                         t.bonds, g, MsgTangent{}, go, src, rowptr, perm, nullptr, nullptr, dxe, d, nodes_src,
-                         nodes_dst, nchunks);
-      hipLaunchKernelGGL((msg_edge_grad_kernel<LIN, LE, LOUT, false, false, true>), grid, dim3(kMsgBlock), 0,
-                         stream, nullptr, bonds, t.g, MsgTangent{}, go, src, rowptr, perm, nullptr, nullptr, dxe, d,
-                         nodes_src, nodes_dst, nchunks);
-    }
-    return msg_launch_status();
-  }
+  return launch_msg_edge_grad_degrees<LIN, LE, LOUT, true>(d, x, bonds, g, t, go, src, rowptr, perm, dyp, dg, dxe,
+                                                          nodes_src, nodes_dst, stream);
 }
 
 template <int LIN>
