@@ -54,8 +54,10 @@ def _op(c, lin, le, lout, device, layout="ir_mul", paths=None):
     return PackedGraphMessage(tp, input_lmax=lin, edge_lmax=le, layout=layout)
 
 
+# the last two have input degrees without any path (l1 > L_e + L_out): their feature-gradient rows
+# are zero
 CASES = [(64, 2, 2, 2, False), (128, 3, 3, 3, True), (48, 3, 3, 3, False), (96, 1, 2, 2, True),
-         (128, 0, 3, 3, False)]
+         (128, 0, 3, 3, False), (64, 3, 0, 1, True), (32, 2, 1, 0, False)]
 
 
 @pytest.mark.parametrize("c,lin,le,lout,sort", CASES)
