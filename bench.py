@@ -585,8 +585,15 @@ def _bench_mace(device):
         rate = MACE_ATOMS / (ms * 1e-3)
         return {"median_ms": ms, "atom_steps_per_s": rate, f"vs_published_{published / 1e3:.2f}k": rate / published,
                 "execution": mode}
+    floor = {}
+    for name, train, ms in (("inference", False, infer_graph_ms), ("training", True, train_graph_ms)):
+        f = _mace_floor(graph["edge_src"].numel(), MACE_ATOMS, train)
+        floor[name] = {**f, "replay_ms": ms, "frac": f["t_min_ms"] / ms}
     return {"workload": "cfg4 MACE C128/lmax3, 2 interactions, correlation 3, 2,048 atoms, r_c 5 A",
             "edges": graph["edge_src"].numel(),
+            "step_roofline": {"what": "sum of the modelled work at its own roofline (unique bytes at 8 TB/s, "
+                                      "useful FLOPs at 157.3 TFLOP/s) over the HIP-graph replay time",
+                              **floor},
             "inference": leg(infer_ms, 11.0e3, "eager"),
             "training": leg(train_ms, 3.81e3, "eager"),
             "inference_hip_graph": leg(infer_graph_ms, 11.0e3, "HIP graph replay"),
@@ -637,6 +644,50 @@ def _bench_linear(device):
                         "2,048 atoms, fp32",
             "forward": leg(fwd_ms, dense[0], "degree_linear_kernel<true, true, 2>"),
             "input_grad": leg(grad_ms, dense[1], "degree_linear_kernel<false, true, 1>")}
+
+
+def _mace_floor(edges: int, atoms: int, training: bool):
+    """Lower bound on the device time of one cfg-4 step: each modelled piece of work at its own
+    roofline (unique bytes at 8 TB/s for the HBM-bound message kernels, useful FLOPs at
+    157.3 TFLOP/s for the GEMMs, the MFMA message linear and the VALU contraction), summed; the
+    elementwise glue and the design traffic (bond rows, dxe, gathers beyond the first) count zero.
+    Per interaction (input degree 0 then 3; 4 / 23 paths, 16 / 99 message output rows):
+    inference = forward + force backward (message VJP, radial-MLP and linear input adjoints, the
+    contraction's VJP); training adds the loss backward: the energy path's message VJP, the force
+    path's tangent forward and tangent VJP, four more GEMMs per radial layer (the weight gradient
+    and the two adjoints of each force-pass product), four more message-linear and channel-linear
+    products and twice more contraction work (VJP and its directional derivative)."""
+    sys.path.insert(0, os.path.join(ROOT, "ictc-o3-hp-ascend_amd", "csrc"))
+    import gen_sc
+    e, n, c, s = edges, atoms, 128, 10
+    terms = {}
+
+    def add(name, nbytes=0.0, flops=0.0):
+        terms[name] = terms.get(name, 0.0) + max(nbytes / (HBM_PEAK_GBS * 1e9),
+                                                 flops / (MFMA_F32_PEAK_TFLOPS * 1e12)) * 1e3
+    for lin, npath, noc, target in ((0, 4, 16, 3), (3, 23, 99, 0)):
+        nx = (lin + 1) ** 2
+        radial = 2 * e * (8 * 64 + 2 * 64 * 64 + 64 * npath * c)         # radial MLP forward
+        fwd_b = e * (4 * npath * c + 64 + 8) + n * 4 * c * (nx + noc)
+        vjp_b = e * (8 * npath * c + 64 + 64 + 8) + n * 4 * c * (2 * nx + noc)
+        lin_f = 2 * n * c * c * noc                                       # message linear
+        chan_f = 2 * n * c * c * (nx + (target + 1) ** 2 + s)             # linear_up, product, self
+        sc = gen_sc.flop_counts(3, target, 3)
+        sc_f = (sc["forward"] + sc["vjp"]) * n * c
+        add("message kernels", nbytes=fwd_b + vjp_b)
+        add("radial MLP GEMMs", flops=2 * radial)
+        add("message linear", flops=2 * lin_f)
+        add("channel linears", flops=2 * chan_f)
+        add("symmetric contraction", flops=sc_f)
+        if training:
+            tfwd_b = e * (8 * npath * c + 128 + 8) + n * 4 * c * (2 * nx + noc)
+            tvjp_b = e * (12 * npath * c + 128 + 64 + 8) + n * 4 * c * (3 * nx + noc)
+            add("message kernels", nbytes=vjp_b + tfwd_b + tvjp_b)
+            add("radial MLP GEMMs", flops=4 * radial)
+            add("message linear", flops=4 * lin_f)
+            add("channel linears", flops=4 * chan_f)
+            add("symmetric contraction", flops=2 * sc_f)
+    return {"terms_ms": terms, "t_min_ms": sum(terms.values())}
 
 
 def _peak_bytes(fn, device) -> int:
