@@ -8,6 +8,8 @@
 //   y  row n, degree block l:  [O][d]                     (mul_ir, offset O * l^2)
 //   forward:     y[n, o, m]            = alpha * sum_{k, c} W_l[o, k C + c] x[n, k, m, c]
 //   input grad:  gx[n, k, m, c]        = alpha * sum_o gy[n, o, m] W_l[o, k C + c]
+//   mul_ir map:  y[n, o, m]            = alpha * sum_c W_l[o, c] x[n, c, m]   (counts all 1; x
+//                                        mul_ir [N, C (L+1)^2], per degree [C][d] at offset C l^2)
 // i.e. for the rows rho = n d + m, Y = alpha X W^T and gX = alpha gY W, one GEMM per degree with
 // the layout changes folded into the tile loads and stores (no transposed copies, no
 // concatenation, the 1/avg_num_neighbors scale as alpha).
@@ -50,17 +52,22 @@ struct LinearArgs {
   float alpha;
 };
 
-// FWD: A = x rows (K = x columns), B^T = W rows, D -> y.  !FWD: A = gy rows (K = O), B = W,
-// D -> gx columns.  VEC (channels a multiple of 32): each 32-wide K chunk of an x row lies in one
+// MODE kForward: A = x rows (K = x columns), B^T = W rows, D -> y.  kInputGrad: A = gy rows
+// (K = O), B = W, D -> gx columns.  kMulIr: A = mul_ir x rows (K = C, stride d), B^T = W rows,
+// D -> y (mul_ir).  VEC (channels a multiple of 32): each 32-wide K chunk of an x row lies in one
 // path block and weight rows are float4-aligned, so operands are fetched into registers one chunk
 // ahead (their loads in flight while the MFMAs of the current chunk run); with two LDS buffers
 // (NBUF 2) the next chunk is staged into the other buffer right after those MFMAs (one barrier per
 // chunk), with one (NBUF 1, half the LDS and so twice the resident blocks) after a second barrier.
 // The forward's long K (counts C) takes two buffers, the input adjoint's short K (O) one.
 // Without VEC, element by element, one chunk at a time.
-template <bool FWD, bool VEC, int NBUF>
+enum LinearMode { kForward = 0, kInputGrad = 1, kMulIr = 2 };
+
+template <int MODE, bool VEC, int NBUF>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NBUF == 1 ? 8 : 4)))
 degree_linear_kernel(const float* __restrict__ in, float* __restrict__ out, const LinearArgs a) {
+  constexpr bool FWD = MODE != kInputGrad;      // D -> mul_ir y rows, B^T = W rows
+  constexpr bool STRIDED = MODE != kForward;    // A rows read at stride d over K (mul_ir)
   const DegreeGeometry& g = a.g[blockIdx.z];
   const int ncols = FWD ? a.out_channels : g.k;   // output columns
   const int kdim = FWD ? g.k : a.out_channels;    // reduction length
@@ -79,8 +86,9 @@ degree_linear_kernel(const float* __restrict__ in, float* __restrict__ out, cons
   const bool arow = arho < g.rows;
   const int64_t an = arow ? arho / g.d : 0;
   const int am = arow ? static_cast<int>(arho - an * g.d) : 0;
-  const float* __restrict__ abase = FWD ? in + an * a.xwidth + g.xoff + static_cast<int64_t>(am) * C
-                                        : in + an * a.ywidth + g.yoff + am;
+  const float* __restrict__ abase = MODE == kForward   ? in + an * a.xwidth + g.xoff + static_cast<int64_t>(am) * C
+                                    : MODE == kInputGrad ? in + an * a.ywidth + g.yoff + am
+                                                         : in + an * a.xwidth + g.xoff + am;
   // !FWD B staging: thread t holds weight row k0 + t / 8, columns c0 + 8 (t % 8) .. + 7 (two
   // float4 loads), stored transposed element by element.  The k index of B column col is
   // XOR-swizzled by bsw(col) (a multiple of 8 below 32, so every aligned 4-group of k stays
@@ -125,13 +133,21 @@ degree_linear_kernel(const float* __restrict__ in, float* __restrict__ out, cons
       ra1 = f32x4_t{};
       rb0 = f32x4_t{};
       rb1 = f32x4_t{};
-      if constexpr (FWD) {
+      if constexpr (STRIDED) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {   // mul_ir row: stride d over K
+          if (arow && k0 + akq + u < kdim) ra0[u] = abase[static_cast<int64_t>(k0 + akq + u) * g.d];
+          if (arow && k0 + akq + 4 + u < kdim) ra1[u] = abase[static_cast<int64_t>(k0 + akq + 4 + u) * g.d];
+        }
+      } else {
         const int blk = k0 / C, c = k0 - blk * C + akq;
         if (arow && kin) {
           const float* p = abase + static_cast<int64_t>(blk) * g.d * C + c;
           ra0 = *reinterpret_cast<const f32x4_t*>(p);
           ra1 = *reinterpret_cast<const f32x4_t*>(p + 4);
         }
+      }
+      if constexpr (FWD) {
         const int col = c0 + ar;   // weight row col, 8 consecutive k
         if (col < ncols && kin) {
           const float* p = g.w + static_cast<int64_t>(col) * g.k + k0 + akq;
@@ -139,11 +155,6 @@ degree_linear_kernel(const float* __restrict__ in, float* __restrict__ out, cons
           rb1 = *reinterpret_cast<const f32x4_t*>(p + 4);
         }
       } else {
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {   // gy row: stride d over the output channels
-          if (arow && k0 + akq + u < kdim) ra0[u] = abase[static_cast<int64_t>(k0 + akq + u) * g.d];
-          if (arow && k0 + akq + 4 + u < kdim) ra1[u] = abase[static_cast<int64_t>(k0 + akq + 4 + u) * g.d];
-        }
         const int kk = k0 + wk;
         if (kk < kdim && c0 + wc < ncols) {   // ncols (counts C) is a multiple of 32
           const float* p = g.w + static_cast<int64_t>(kk) * g.k + c0 + wc;
@@ -198,8 +209,12 @@ degree_linear_kernel(const float* __restrict__ in, float* __restrict__ out, cons
           const int kk = k0 + akq + u;
           float v = 0.f;
           if (arow && kk < kdim) {
-            const int blk = kk / C, c = kk - blk * C;
-            v = abase[static_cast<int64_t>(blk) * g.d * C + c];
+            if constexpr (STRIDED) {
+              v = abase[static_cast<int64_t>(kk) * g.d];
+            } else {
+              const int blk = kk / C, c = kk - blk * C;
+              v = abase[static_cast<int64_t>(blk) * g.d * C + c];
+            }
           }
           sA[0][ar][akq + u] = v;
           const int col = c0 + ar;
@@ -281,24 +296,30 @@ int prepare(const ictc_degree_linear_desc* desc, const float* const* weights, fl
   return ICTC_OK;
 }
 
-template <bool FWD>
+template <int MODE>
 int launch(const ictc_degree_linear_desc* desc, const float* in, const float* const* weights, float alpha,
            float* out, int64_t nodes, hipStream_t stream) {
   LinearArgs a{};
   int degrees = 0, max_cols = 0;
   int64_t max_rows = 0;
-  const int st = prepare(desc, weights, alpha, nodes, &a, &degrees, &max_rows, &max_cols, FWD);
+  const int st = prepare(desc, weights, alpha, nodes, &a, &degrees, &max_rows, &max_cols, MODE != kInputGrad);
   if (st != ICTC_OK) return st;
+  if (MODE == kMulIr) {   // one channel block per degree: x mul_ir [N, C (L+1)^2]
+    for (int l = 0; l <= desc->lmax; ++l)
+      if (desc->counts[l] != 1) return ICTC_ERR_INVALID_ARGUMENT;
+  }
   if (nodes == 0) return ICTC_OK;
   if (in == nullptr || out == nullptr) return ICTC_ERR_INVALID_ARGUMENT;
   const int64_t row_tiles = (max_rows + kTile - 1) / kTile;
   if (row_tiles > 0x7fffffff) return ICTC_ERR_UNSUPPORTED;
   const dim3 grid(static_cast<unsigned>(row_tiles), static_cast<unsigned>((max_cols + kTile - 1) / kTile),
                   static_cast<unsigned>(degrees));
+  // two LDS buffers for the long K of the forward (counts C), one for the short K of the others
   if (desc->channels % 32 == 0)
-    hipLaunchKernelGGL((degree_linear_kernel<FWD, true, FWD ? 2 : 1>), grid, dim3(256), 0, stream, in, out, a);
+    hipLaunchKernelGGL((degree_linear_kernel<MODE, true, MODE == kForward ? 2 : 1>), grid, dim3(256), 0, stream, in,
+                       out, a);
   else
-    hipLaunchKernelGGL((degree_linear_kernel<FWD, false, 1>), grid, dim3(256), 0, stream, in, out, a);
+    hipLaunchKernelGGL((degree_linear_kernel<MODE, false, 1>), grid, dim3(256), 0, stream, in, out, a);
   return hipGetLastError() == hipSuccess ? ICTC_OK : ICTC_ERR_LAUNCH;
 }
 
@@ -309,13 +330,18 @@ extern "C" {
 
 int ictc_hip_degree_linear_forward(const ictc_degree_linear_desc* desc, const float* x, const float* const* weights,
                                    float alpha, float* y, int64_t nodes, hipStream_t stream) {
-  return ictc::launch<true>(desc, x, weights, alpha, y, nodes, stream);
+  return ictc::launch<ictc::kForward>(desc, x, weights, alpha, y, nodes, stream);
 }
 
 int ictc_hip_degree_linear_input_grad(const ictc_degree_linear_desc* desc, const float* grad_y,
                                       const float* const* weights, float alpha, float* grad_x, int64_t nodes,
                                       hipStream_t stream) {
-  return ictc::launch<false>(desc, grad_y, weights, alpha, grad_x, nodes, stream);
+  return ictc::launch<ictc::kInputGrad>(desc, grad_y, weights, alpha, grad_x, nodes, stream);
+}
+
+int ictc_hip_degree_linear_mul_ir(const ictc_degree_linear_desc* desc, const float* x, const float* const* weights,
+                                  float alpha, float* y, int64_t nodes, hipStream_t stream) {
+  return ictc::launch<ictc::kMulIr>(desc, x, weights, alpha, y, nodes, stream);
 }
 
 }  // extern "C"

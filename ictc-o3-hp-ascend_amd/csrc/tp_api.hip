@@ -63,7 +63,7 @@ const char* ictc_hip_status_string(int status) {
   }
 }
 
-int ictc_hip_abi_version(void) { return 10; }
+int ictc_hip_abi_version(void) { return 11; }
 
 int ictc_hip_tp_slot_count(int input_lmax, int edge_lmax, int output_lmax) {
   if (input_lmax < 0 || edge_lmax < 0 || output_lmax < 0 || input_lmax > 3 || edge_lmax > 3 ||

@@ -15,7 +15,7 @@ import torch  # noqa: F401  (must precede CDLL, see module docstring)
 
 MAX_PATHS = 64
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libictc_hip.so")
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 
 class TpDesc(ctypes.Structure):
@@ -94,6 +94,8 @@ _SIGNATURES = {
                                                       _I64, _P]),
     "ictc_hip_degree_linear_input_grad": (ctypes.c_int, [ctypes.POINTER(DegreeLinearDesc), _P, _P, ctypes.c_float,
                                                          _P, _I64, _P]),
+    "ictc_hip_degree_linear_mul_ir": (ctypes.c_int, [ctypes.POINTER(DegreeLinearDesc), _P, _P, ctypes.c_float, _P,
+                                                     _I64, _P]),
     "ictc_hip_silu_second": (ctypes.c_int, [_P, _P, _P, _P, _P, _I64, _P]),
     "ictc_hip_sgemm": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, _I64, _I64, _I64, ctypes.c_float, _P, _I64, _P,
                                       _I64, ctypes.c_float, _P, _I64, _P]),

@@ -37,6 +37,7 @@ class DegreeLinearPlan:
             self.desc.counts[l] = c
         self.in_width = sum(c * (2 * l + 1) * self.channels for l, c in enumerate(self.counts))
         self.out_width = self.out_channels * (self.lmax + 1) ** 2
+        self._transposed = None
 
     def x_rows(self, x: torch.Tensor, l: int) -> torch.Tensor:
         """Packed x -> the degree-l rows [N (2l+1), counts[l] C] (column k C + c)."""
@@ -44,6 +45,19 @@ class DegreeLinearPlan:
         off = sum(self.counts[j] * (2 * j + 1) * c for j in range(l))
         blk = x[:, off:off + k * d * c].reshape(x.shape[0], k, d, c)
         return blk.transpose(1, 2).reshape(x.shape[0] * d, k * c)
+
+    def transposed(self) -> "DegreeLinearPlan":
+        """The plan of the transposed map (channels and out_channels swapped; one block per degree)."""
+        if self._transposed is None:
+            self._transposed = DegreeLinearPlan(self.counts, self.out_channels, self.channels)
+            self._transposed._transposed = self
+        return self._transposed
+
+    def mul_ir_rows(self, x: torch.Tensor, l: int) -> torch.Tensor:
+        """mul_ir x with one channel block per degree -> the degree-l rows [N (2l+1), C]."""
+        d, c = 2 * l + 1, self.channels
+        blk = x[:, c * l * l:c * (l + 1) ** 2].reshape(x.shape[0], c, d)
+        return blk.transpose(1, 2).reshape(x.shape[0] * d, c)
 
     def y_rows(self, y: torch.Tensor, l: int) -> torch.Tensor:
         """mul_ir y -> the degree-l rows [N (2l+1), O]."""
@@ -123,19 +137,89 @@ class _InputGrad(torch.autograd.Function):
         return (None, None, ggy, *_weight_grads(ctx.plan, gy, z, ctx.alpha, need[1:]))
 
 
+def _check_weights(weights, plan, device):
+    if len(weights) != plan.lmax + 1:
+        raise ValueError("one weight per degree is required")
+    for l, w in enumerate(weights):
+        if w.shape != (plan.out_channels, plan.counts[l] * plan.channels):
+            raise ValueError(f"weight of degree {l} must have shape [O, counts[l] C]")
+        if w.dtype != torch.float32 or w.device != device:
+            raise ValueError("weights must be float32 on the features' device")
+
+
+def _mul_ir_raw(plan: "DegreeLinearPlan", x, weights, alpha):
+    y = torch.empty(x.shape[0], plan.out_width, device=x.device, dtype=torch.float32)
+    _lib.check(_lib.lib().ictc_hip_degree_linear_mul_ir(
+        ctypes.byref(plan.desc), x.data_ptr() if x.numel() else None, _pointers(weights), float(alpha),
+        y.data_ptr() if y.numel() else None, x.shape[0], _lib.stream_of(x.device)), "ictc_hip_degree_linear_mul_ir")
+    return y
+
+
+class _MulIr(torch.autograd.Function):
+    """y = alpha W_l x per degree, mul_ir in and out (one channel block per degree).  Its input
+    adjoint is the same map with the transposed weights (plan.transposed); the weight adjoint is
+    alpha gY_l^T X_l on the [N (2l+1), channels] rows of both; so every derivative order stays on
+    this kernel and dense products."""
+
+    @staticmethod
+    def forward(ctx, plan, alpha, x, *weights):
+        ctx.plan, ctx.alpha = plan, alpha
+        ctx.save_for_backward(x, *weights)
+        return _mul_ir_raw(plan, x, list(weights), alpha)
+
+    @staticmethod
+    def backward(ctx, gy):
+        x, *weights = ctx.saved_tensors
+        need = required_gradients((x, *weights), ctx.needs_input_grad[2:])
+        if gy is None or not any(need):
+            return (None, None, None) + (None,) * len(weights)
+        gy = gy.contiguous()
+        plan = ctx.plan
+        gx = None
+        if need[0]:
+            gx = _MulIr.apply(plan.transposed(), ctx.alpha, gy, *[w.t().contiguous() for w in weights])
+        gw = [mm(plan.y_rows(gy, l).t(), plan.mul_ir_rows(x, l)) * ctx.alpha if n else None
+              for l, n in enumerate(need[1:])]
+        return (None, None, gx, *gw)
+
+
+def degree_linear_mul_ir(x: torch.Tensor, weights: Sequence[torch.Tensor], plan: "DegreeLinearPlan",
+                         alpha: float = 1.0) -> torch.Tensor:
+    """Per-degree channel linear on mul_ir rows in and out: x [N, C (L+1)^2] (per degree
+    [C][2l+1]), weights[l] [O, C] -> alpha W_l x per degree, [N, O (L+1)^2] (the e3nn o3.Linear of
+    the MACE product block); the plan must have one channel block per degree."""
+    if any(k != 1 for k in plan.counts):
+        raise ValueError("the mul_ir map takes one channel block per degree")
+    if x.ndim != 2 or x.shape[1] != plan.in_width:
+        raise ValueError("features must have shape [N, C (L+1)^2]")
+    _check_weights(weights, plan, x.device)
+    if x.dtype != torch.float32 or not x.is_cuda:
+        raise ValueError("features must be float32 on a ROCm GPU")
+    return _MulIr.apply(plan, float(alpha), x.contiguous(), *[w.contiguous() for w in weights])
+
+
+def degree_linear_adjoint(y: torch.Tensor, weights: Sequence[torch.Tensor], plan: DegreeLinearPlan,
+                          alpha: float = 1.0) -> torch.Tensor:
+    """The adjoint map of ``degree_linear`` in its first argument, as an operator of its own:
+    y [N, plan.out_width] (mul_ir, per degree [O][2l+1]) -> alpha * W_l^T y per degree,
+    [N, plan.in_width] (per degree counts[l] blocks of [2l+1][C], ir_mul).  With counts all 1 and
+    the weights transposed this is a per-degree C x C channel linear from mul_ir to ir_mul (the
+    MACE interaction's linear_up feeding the message kernels)."""
+    if y.ndim != 2 or y.shape[1] != plan.out_width:
+        raise ValueError("features must have shape [N, O (L+1)^2]")
+    _check_weights(weights, plan, y.device)
+    if y.dtype != torch.float32 or not y.is_cuda:
+        raise ValueError("features must be float32 on a ROCm GPU")
+    return _InputGrad.apply(plan, float(alpha), y.contiguous(), *[w.contiguous() for w in weights])
+
+
 def degree_linear(x: torch.Tensor, weights: Sequence[torch.Tensor], plan: DegreeLinearPlan,
                   alpha: float = 1.0) -> torch.Tensor:
     """x [N, plan.in_width] (packed per-degree path blocks [count][2l+1][C]), weights[l]
     [O, counts[l] C] -> alpha * per-degree linear [N, O (L+1)^2] (mul_ir)."""
     if x.ndim != 2 or x.shape[1] != plan.in_width:
         raise ValueError("features must have shape [N, sum_l counts[l] (2l+1) C]")
-    if len(weights) != plan.lmax + 1:
-        raise ValueError("one weight per degree is required")
-    for l, w in enumerate(weights):
-        if w.shape != (plan.out_channels, plan.counts[l] * plan.channels):
-            raise ValueError(f"weight of degree {l} must have shape [O, counts[l] C]")
-        if w.dtype != torch.float32 or w.device != x.device:
-            raise ValueError("weights must be float32 on the features' device")
+    _check_weights(weights, plan, x.device)
     if x.dtype != torch.float32 or not x.is_cuda:
         raise ValueError("features must be float32 on a ROCm GPU")
     return _Forward.apply(plan, float(alpha), x.contiguous(), *[w.contiguous() for w in weights])

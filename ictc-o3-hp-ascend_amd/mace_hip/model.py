@@ -41,7 +41,8 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from ictc_o3.backends.hip.degree_linear import DegreeLinearPlan, degree_linear
+from ictc_o3.backends.hip.degree_linear import (DegreeLinearPlan, degree_linear, degree_linear_adjoint,
+                                                 degree_linear_mul_ir)
 from ictc_o3.backends.hip.graph_message import packed_graph_message
 from ictc_o3.backends.hip.harmonics import direction_harmonics_packed
 from ictc_o3.backends.hip.radial_message import fold_projection, packed_radial_graph_message
@@ -54,24 +55,6 @@ from .linear import Linear, linear
 from .radial import bessel_embedding
 
 SILU_SCALE = 1.6791767923989418   # _Normalize2MomSiLU (pure_cartesian_ictd_fix.py:610-619)
-
-
-def split_mul_ir(x: torch.Tensor, channels: int, lmax: int) -> Dict[int, torch.Tensor]:
-    widths = [channels * (2 * l + 1) for l in range(lmax + 1)]
-    parts = x.split([*widths, x.shape[-1] - sum(widths)], dim=-1)
-    return {l: parts[l].reshape(x.shape[0], channels, 2 * l + 1) for l in range(lmax + 1)}
-
-
-def merge_mul_ir(blocks: Dict[int, torch.Tensor]) -> torch.Tensor:
-    n = next(iter(blocks.values())).shape[0]
-    return torch.cat([blocks[l].reshape(n, -1) for l in sorted(blocks)], dim=-1)
-
-
-def degree_rows(block: torch.Tensor) -> torch.Tensor:
-    """mul_ir degree block [N, C, 2l+1] -> rows [N (2l+1), C] (one row per (node, m)), so that a
-    per-degree channel map is one plain GEMM; torch.matmul on the strided [N, 2l+1, C] view can
-    fall back to a batched GEMM over N tiny matrices."""
-    return block.transpose(1, 2).reshape(-1, block.shape[1])
 
 
 def tp_paths(input_lmax: int, edge_lmax: int, target_lmax: int):
@@ -98,12 +81,16 @@ class ChannelLinear(nn.Module):
         super().__init__()
         self.channels, self.lmax = channels, lmax
         self.weights = nn.ParameterList([nn.Parameter(torch.eye(channels)) for _ in range(lmax + 1)])
+        self.plan = DegreeLinearPlan([1] * (lmax + 1), channels, channels)
 
     def to_ir_mul(self, x: torch.Tensor) -> torch.Tensor:
-        """mul_ir [N, C(L+1)^2] -> ir_mul [N, sum_l (2l+1) C]: out[n, m, o] = sum_c W[o,c] x[n,c,m]."""
-        blocks = split_mul_ir(x, self.channels, self.lmax)
-        return torch.cat([linear(degree_rows(blocks[l]), self.weights[l]).reshape(x.shape[0], -1)
-                          for l in range(self.lmax + 1)], dim=-1)
+        """mul_ir [N, C(L+1)^2] -> ir_mul [N, sum_l (2l+1) C]: out[n, m, o] = sum_c W[o,c] x[n,c,m],
+        one fp32-MFMA launch over every degree (the message linear's adjoint kernel with the
+        weights transposed; the layout change folded into its tile loads and stores)."""
+        width = self.channels * (self.lmax + 1) ** 2
+        if x.shape[1] != width:
+            x = x[:, :width]
+        return degree_linear_adjoint(x, [w.t() for w in self.weights], self.plan)
 
 
 class MessageLinear(nn.Module):
@@ -154,13 +141,11 @@ class IrrepsLinear(nn.Module):
         super().__init__()
         self.channels, self.lmax = channels, lmax
         self.weights = nn.ParameterList([nn.Parameter(torch.randn(channels, channels)) for _ in range(lmax + 1)])
+        self.plan = DegreeLinearPlan([1] * (lmax + 1), channels, channels)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        blocks = split_mul_ir(x, self.channels, self.lmax)
-        scale = 1.0 / math.sqrt(self.channels)
-        n = x.shape[0]
-        return merge_mul_ir({l: linear(degree_rows(b), self.weights[l] * scale)
-                             .reshape(n, 2 * l + 1, self.channels).transpose(1, 2) for l, b in blocks.items()})
+        """One fp32-MFMA launch over every degree, mul_ir in and out, 1/sqrt(C) as its alpha."""
+        return degree_linear_mul_ir(x, list(self.weights), self.plan, 1.0 / math.sqrt(self.channels))
 
 
 class Interaction(nn.Module):

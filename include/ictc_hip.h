@@ -453,6 +453,19 @@ int ictc_hip_degree_linear_input_grad(const ictc_degree_linear_desc* desc, const
                                       int64_t nodes, hipStream_t stream);
 
 /*
+ * The same per-degree channel map on mul_ir rows in and out, with one channel block per degree
+ * (counts[l] = 1 for every l, else ICTC_ERR_INVALID_ARGUMENT): for x [nodes, C (lmax+1)^2] and
+ * y [nodes, O (lmax+1)^2], both per degree [channels][2l+1] at offsets C l^2 / O l^2,
+ *   y[n, o, m] = alpha sum_c weights[l][o, c] x[n, c, m]
+ * The e3nn o3.Linear of the MACE product block (reference pure_cartesian_ictd_fix.py:1145-1195,
+ * an irreps-preserving C x C map per degree); its input adjoint is this map with the weights
+ * transposed (and the roles of C and O swapped).
+ */
+int ictc_hip_degree_linear_mul_ir(const ictc_degree_linear_desc* desc, const float* x,
+                                  const float* const* weights, float alpha, float* y,
+                                  int64_t nodes, hipStream_t stream);
+
+/*
  * Row-major fp32 product C[m,n] = alpha * op(A) op(B) + beta * C on rocBLAS, for the dense
  * channel linears around the operators.  op(A) is [m,k]: A is stored [m,k] (lda >= k) or,
  * with trans_a != 0, [k,m] (lda >= m); likewise B with op(B) [k,n].  Each host thread uses
