@@ -78,14 +78,39 @@ class FactorizedPlan:
     def __init__(self, matrices: List[List[torch.Tensor]], reconstruction: List[float]):
         self.matrices = matrices
         self.reconstruction_relative = reconstruction
+        rows = sum(a.shape[0] for mats in matrices for a in mats)
+        cols = sum(a.shape[1] for mats in matrices for a in mats)
+        # every (target degree, order) projection on the diagonal of one [KTOT, K_module] matrix
+        first = matrices[0][0]
+        self.block = torch.zeros(rows, cols, dtype=first.dtype, device=first.device)
+        r = c = 0
+        for mats in matrices:
+            for a in mats:
+                self.block[r:r + a.shape[0], c:c + a.shape[1]] = a
+                r, c = r + a.shape[0], c + a.shape[1]
+        self._table_key, self._table = None, None
 
     def weight_table(self, contractions) -> torch.Tensor:
-        """[S, KTOT, C] kernel weights from the modules' live weights (differentiable)."""
-        blocks = []
-        for mats, con in zip(self.matrices, contractions):
-            for a, w in zip(mats, [con.weights_max, *con.weights]):
-                blocks.append(torch.einsum("pk,skc->spc", a, w))
-        return torch.cat(blocks, 1)
+        """[S, KTOT, C] kernel weights from the modules' live weights (differentiable): one product
+        of the block-diagonal projection with the concatenated module weights.  When no weight
+        requires a gradient the table is kept until a weight is replaced or modified in place."""
+        from ictc_o3.backends.hip.linear import mm
+        ws = [w for con in contractions for w in (con.weights_max, *con.weights)]
+        frozen = not (torch.is_grad_enabled() and any(w.requires_grad for w in ws))
+        key = tuple((id(w), w.data_ptr(), w._version) for w in ws) if frozen else None
+        if frozen and key == self._table_key:
+            return self._table
+        w = torch.cat(ws, 1)                                    # [S, K_module, C]
+        s, k, c = w.shape
+        flat = w.transpose(0, 1).reshape(k, s * c)
+        # rocBLAS on the GPU; a module built on the host (the factory's reconstruction gate) uses torch
+        table = mm(self.block, flat) if flat.is_cuda else self.block @ flat
+        table = table.reshape(-1, s, c).transpose(0, 1).contiguous()
+        if frozen:
+            self._table_key, self._table = key, table
+        else:
+            self._table_key, self._table = None, None
+        return table
 
 
 def constant_key(owner, device) -> tuple:
