@@ -37,7 +37,7 @@ reference) and three launches of each TP kernel at the benchmark sizes, for
 rocprofv3 --pmc passes.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--kernels-only]
-                      [--only tp|message|sc|mace|graph]
+                      [--only tp|tp0|message|sc|mace|graph|linear|generic]
 """
 from __future__ import annotations
 
@@ -360,6 +360,53 @@ def _bench_tp_cfg0(device):
                          "algorithmic_bytes_per_launch": BYTES_TP0 * TP0_ROWS, "achieved": gbs,
                          "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS,
                          "traffic": traffic, "traffic_unit": "bytes/launch"}}
+
+
+GEN_C, GEN_L, GEN_ROWS = 64, 4, 65536
+
+
+def _bench_generic(device):
+    """Degree-generic kernels (run-time path tables; every degree set with a degree above 3): the
+    TP forward and VJP at C = 64, degrees (4, 4, 4) (42 paths), 65,536 instances.  Reported
+    against both bounds: algorithmic HBM bytes (x, Y, g read and out written; the VJP also reads
+    dout and writes dx, dY, dg) and the FMA work the kernels execute (forward 2·NB·C per instance
+    plus 2·Σ_p n1 n2 n3 for the bond rows; the VJP 2·2·NB·C for dg and dx, 2·Σ_p n1 n2 n3·C for
+    the per-channel dY contraction, and the bond rows)."""
+    from ictc_o3 import EdgeTensorProduct
+    from ictc_o3.backends.hip.harmonics import direction_harmonics_packed
+    from ictc_o3.backends.hip.tensor_product import _backward_raw, _forward_raw
+    op = EdgeTensorProduct.create(channels=GEN_C, input_lmax=GEN_L, edge_lmax=GEN_L, device=device)
+    plan = op.plan
+    assert plan.generic
+    gen = torch.Generator(device=device).manual_seed(5)
+    x = torch.randn(GEN_ROWS, plan.x_width, device=device, generator=gen)
+    n = torch.nn.functional.normalize(torch.randn(GEN_ROWS, 3, device=device, generator=gen), dim=-1)
+    y = direction_harmonics_packed(n, GEN_L).contiguous()
+    g = torch.randn(GEN_ROWS, plan.full_gate_width, device=device, generator=gen)
+    go = torch.randn(GEN_ROWS, plan.full_out_width, device=device, generator=gen)
+    fwd_ms = _event_ms(lambda: _forward_raw(plan, x, y, g), device, reps=10)
+    vjp_ms = _event_ms(lambda: _backward_raw(plan, (True, True, True), x, y, g, go), device, reps=10)
+    paths = plan.full_paths
+    nb = sum((2 * a + 1) * (2 * c + 1) for a, _, c in paths)
+    dense = sum((2 * a + 1) * (2 * b + 1) * (2 * c + 1) for a, b, c in paths)
+    xw, yw, gw, ow = plan.x_width, plan.y_width, plan.full_gate_width, plan.full_out_width
+    fwd_bytes, vjp_bytes = 4 * (xw + yw + gw + ow), 4 * (ow + 2 * (xw + yw + gw))
+    fwd_flops = 2 * nb * GEN_C + 2 * dense
+    vjp_flops = 2 * 2 * nb * GEN_C + 2 * dense * GEN_C + 2 * dense
+
+    def leg(ms, nbytes, flops):
+        gbs = nbytes * GEN_ROWS / (ms * 1e-3) / 1e9
+        tf = flops * GEN_ROWS / (ms * 1e-3) / 1e12
+        return {"mean_launch_ms": ms, "instances_per_s": GEN_ROWS / (ms * 1e-3),
+                "hbm": {"algorithmic_bytes_per_instance": nbytes, "achieved": gbs, "peak": HBM_PEAK_GBS,
+                        "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS},
+                "valu": {"fma_flops_per_instance": flops, "achieved": tf, "peak": VALU_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": tf / VALU_PEAK_TFLOPS}}
+
+    return {"workload": f"degree-generic TP C{GEN_C}, degrees ({GEN_L},{GEN_L},{GEN_L}), {len(paths)} paths, "
+                        f"{GEN_ROWS:,} instances, ir_mul",
+            "kernels": "gen_tp_forward_kernel, gen_tp_backward_kernel",
+            "forward": leg(fwd_ms, fwd_bytes, fwd_flops), "vjp": leg(vjp_ms, vjp_bytes, vjp_flops)}
 
 
 def _cpu_tp_cfg0(budget_s: float = 10.0, rows: int = 8192):
@@ -813,7 +860,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--kernels-only", action="store_true")
-    ap.add_argument("--only", choices=("tp", "tp0", "message", "sc", "mace", "graph", "linear"), default=None,
+    ap.add_argument("--only", choices=("tp", "tp0", "message", "sc", "mace", "graph", "linear", "generic"),
+                    default=None,
                     help="run one section and print its JSON (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -827,9 +875,9 @@ def main() -> int:
     if args.kernels_only:
         _kernels_only(op.plan, device)
         return 0
-    if args.only in ("tp0", "message", "sc", "mace", "graph", "linear"):
+    if args.only in ("tp0", "message", "sc", "mace", "graph", "linear", "generic"):
         fn = {"tp0": _bench_tp_cfg0, "message": _bench_message, "sc": _bench_sc, "mace": _bench_mace,
-              "graph": _bench_graph, "linear": _bench_linear}[args.only]
+              "graph": _bench_graph, "linear": _bench_linear, "generic": _bench_generic}[args.only]
         print(json.dumps({args.only: fn(device)}), flush=True)
         return 0
     elapsed, vjp_ms, fwd_ms = _time_gpu(args, op.plan, device)
@@ -845,7 +893,7 @@ def main() -> int:
         others = {"tp_cfg0": _bench_tp_cfg0(device), "message_cfg2": _bench_message(device),
                   "sc_cfg3": _bench_sc(device),
                   "mace_cfg4": _bench_mace(device), "message_linear_cfg4": _bench_linear(device),
-                  "radius_graph": _bench_graph(device)}
+                  "radius_graph": _bench_graph(device), "tp_generic_l4": _bench_generic(device)}
         if not args.no_cpu:
             others["tp_cfg0"]["cpu_baseline"] = _cpu_tp_cfg0()
             others["message_cfg2"]["cpu_baseline"] = _cpu_message()

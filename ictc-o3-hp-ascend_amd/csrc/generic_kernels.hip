@@ -1,0 +1,439 @@
+// Degree-generic tensor-product and graph-message kernels (every degree <= 6).
+//
+// The mathematics of tp_kernels.hpp and message_kernels.hpp (reference ictd_irreps.py:2669-2748,
+// backends/ascend/tensor_product.py:30-55 and 159-218, structured_product.py:7-87):
+//   M_p[k][i] = s_p * sum_j Y[l2^2 + j] * Chat_p[i][j][k]                 (bond, stored [k][i])
+//   out[o_p + k, c] = g[p, c] * sum_i x[l1^2 + i, c] * M_p[k][i]
+// with the path set, the output and bond offsets and the CG tensors read at run time instead of
+// compiled per degree set, so one kernel serves every (input_lmax, edge_lmax, output_lmax).
+//
+// Launch shape: one wave per workgroup and one instance (TP row, or receiver-CSR edge of the
+// message kernels) at a time, grid-stride over instances.  Per instance the wave builds M_p of
+// every path into LDS (lanes over bond entries), then walks the channels in chunks of 64 with
+// lane = channel.  Paths are enumerated in ascending l1, so the x rows of one input degree are
+// loaded into registers once per chunk and serve every path of that degree; the loops over the
+// components of one degree are unrolled to the largest degree (13 components) with the rows past
+// a degree's width zeroed or clamped, so their loads issue together.
+//
+// VJP per path p, with go_k = g_p * dout_k:
+//   dg[p]      = sum_k dout_k * sum_i M_p[k][i] x_i
+//   dx[l1, i] += sum_k M_p[k][i] go_k                  (registers, one input degree at a time)
+//   dY[l2, j] += s_p * sum_{i,k} Chat_p[i][j][k] x_i go_k   (per lane, then summed over lanes)
+// The dY term is contracted per lane against the CG rows Chat_p[i][k][0..n2) (stored [i][k][j],
+// read with wave-uniform scalar loads), and the path's n2 lane partials are summed over the wave
+// by one transposing butterfly (a fixed order).  (The ICTC coupling tensors are dense -- 49,684
+// of the 52,570 entries up to degree 6 are nonzero -- so this costs sum_p n1 n2 n3 FMAs per
+// channel; it measured faster than first reducing the per-entry products x_i go_k over the
+// channels, which is bound by the latency of one cross-lane sum per 16 bond entries.)
+#include "generic.hpp"
+
+#include "ictc_common.hpp"
+#include "generated/ictc_cg_generic.hpp"
+
+namespace ictc {
+namespace {
+
+constexpr int kLanes = 64;
+constexpr int64_t kGridCap = 16384;
+constexpr int kMaxN = 2 * kGenericMaxL + 1;   // components of the largest degree
+constexpr int kHead = 2 * kLanes;              // LDS head: sY [64] | sDY [64]
+
+static_assert(kGenericMaxL == kCGGenericMaxL, "generic CG table degree");
+static_assert(ICTC_MAX_PATHS >= 106, "the (6,6,6) path set has 106 paths");
+
+// Run-time path table of one descriptor (kernel argument, read with scalar loads).
+struct GenTable {
+  int np, nb, noc, nx, ny, channels, lin, lout;
+  int meta[ICTC_MAX_PATHS];    // l1 | l2 << 4 | l3 << 8 | first output row << 12
+  int bond[ICTC_MAX_PATHS];    // first bond entry of M_p
+  int cg[ICTC_MAX_PATHS];      // first kCGGeneric index of Chat_p ([i][k][j])
+  float scale[ICTC_MAX_PATHS];
+};
+
+struct PathInfo {
+  int l1, l2, l3, n1, n2, n3, out;
+};
+
+__device__ __forceinline__ PathInfo path_info(const GenTable& t, int p) {
+  const int m = t.meta[p];
+  PathInfo r;
+  r.l1 = m & 15;
+  r.l2 = (m >> 4) & 15;
+  r.l3 = (m >> 8) & 15;
+  r.n1 = 2 * r.l1 + 1;
+  r.n2 = 2 * r.l2 + 1;
+  r.n3 = 2 * r.l3 + 1;
+  r.out = m >> 12;
+  return r;
+}
+
+// M_p of every path into sM from the harmonics in sY (lanes over the bond entries of a path).
+// An entry's coefficients Chat_p[i][k][0..n2) are contiguous; all kMaxN are loaded (the table is
+// padded, so a row read never leaves it) and those past n2 are not used.
+__device__ void build_bonds(const GenTable& t, const float* sY, float* sM, int lane) {
+  for (int p = 0; p < t.np; ++p) {
+    const PathInfo q = path_info(t, p);
+    const float* cg = kCGGeneric + t.cg[p];
+    const float s = t.scale[p];
+    float* bond = sM + t.bond[p];
+    for (int e = lane; e < q.n1 * q.n3; e += kLanes) {
+      const int k = e / q.n1, i = e - k * q.n1;
+      const float* row = cg + (i * q.n3 + k) * q.n2;
+      float c[kMaxN];
+#pragma unroll
+      for (int j = 0; j < kMaxN; ++j) c[j] = row[j];
+      float acc = 0.f;
+#pragma unroll
+      for (int j = 0; j < kMaxN; ++j)
+        if (j < q.n2) acc = fmaf(sY[q.l2 * q.l2 + j], c[j], acc);
+      bond[e] = acc * s;
+    }
+  }
+}
+
+// x rows [l1^2, l1^2 + n1) of this lane's channel into xr[0..n1) (xr past n1 and lanes past C
+// get 0).  rx spans the instance's feature row [NX][C]; an empty descriptor (no x, or a source
+// index out of range) reads zeros.  All kMaxN row loads are issued together; those past n1
+// repeat row n1 - 1 (the wave-uniform row offset is not range checked, so it stays inside the
+// degree block).
+__device__ __forceinline__ void stage_x(rsrc_t rx, int l1, int n1, int C, int c, bool on, float (&xr)[kMaxN]) {
+  const uint32_t lc = static_cast<uint32_t>(on ? c : 0) * 4u;
+#pragma unroll
+  for (int i = 0; i < kMaxN; ++i)
+    xr[i] = buf_load_vs(rx, lc, static_cast<uint32_t>((l1 * l1 + (i < n1 ? i : n1 - 1)) * C) * 4u);
+#pragma unroll
+  for (int i = 0; i < kMaxN; ++i) xr[i] = (on && i < n1) ? xr[i] : 0.f;
+}
+
+// Feature row of one instance: x + row * NX * C, or an empty descriptor.
+__device__ __forceinline__ rsrc_t x_row(const float* x, int64_t row, bool valid, const GenTable& t) {
+  const uint32_t bytes = static_cast<uint32_t>(t.nx * t.channels) * 4u;
+  return make_rsrc(x && valid ? x + row * t.nx * t.channels : nullptr, bytes);
+}
+
+// Gate of path p at channel c (0 for lanes past C; p past the last path reads path 0).
+__device__ __forceinline__ float gate(const float* g, int p, int np, int C, int c, bool on) {
+  return on ? g[static_cast<int64_t>(p < np ? p : 0) * C + c] : 0.f;
+}
+
+// sum_i xr[i] * M[k][i] over the kMaxN register rows (xr is zero past n1; the bond reads past n1
+// are clamped into row k).
+__device__ __forceinline__ float bond_row_dot(const float* bond, int k, int n1, const float (&xr)[kMaxN],
+                                              float (&bv)[kMaxN]) {
+  const float* b = bond + k * n1;
+#pragma unroll
+  for (int i = 0; i < kMaxN; ++i) bv[i] = b[i < n1 ? i : n1 - 1];
+  float acc = 0.f;
+#pragma unroll
+  for (int i = 0; i < kMaxN; ++i) acc = fmaf(xr[i], bv[i], acc);
+  return acc;
+}
+
+// Forward of one instance: out rows [NOC][C] written, or added to when accumulate is set.  The
+// next path's gate is requested before the current path is computed.
+__device__ void forward_instance(const GenTable& t, const float* sM, rsrc_t x, const float* g, float* out,
+                                 bool accumulate, int lane) {
+  const int C = t.channels;
+  for (int c0 = 0; c0 < C; c0 += kLanes) {
+    const int c = c0 + lane;
+    const bool on = c < C;
+    int staged = -1;
+    float xr[kMaxN], bv[kMaxN];
+    float gnext = gate(g, 0, t.np, C, c, on);
+    for (int p = 0; p < t.np; ++p) {
+      const PathInfo q = path_info(t, p);
+      if (q.l1 != staged) {
+        stage_x(x, q.l1, q.n1, C, c, on, xr);
+        staged = q.l1;
+      }
+      const float gv = gnext;
+      gnext = gate(g, p + 1, t.np, C, c, on);
+      const float* bond = sM + t.bond[p];
+      for (int k = 0; k < q.n3; ++k) {
+        const float acc = bond_row_dot(bond, k, q.n1, xr, bv);
+        if (on) {
+          float* dst = out + static_cast<int64_t>(q.out + k) * C + c;
+          *dst = accumulate ? *dst + acc * gv : acc * gv;
+        }
+      }
+    }
+  }
+}
+
+struct BwdLds {
+  float* sG;     // [2 lout + 1][64] go_k of the current path (lane columns)
+  float* sDY;    // [64] dY of the instance
+};
+
+// VJP of one instance (sM built, L.sDY zeroed): dg and dx rows written when their pointers are
+// set, the dY contributions added to L.sDY when want_dy (x is needed for dg and dY).  Every
+// lane takes part in the dY butterflies whatever its channel, so the call is wave-uniform.
+__device__ void backward_instance(const GenTable& t, const float* sM, const BwdLds& L, rsrc_t x,
+                                  const float* g, const float* go, float* dx, float* dg, bool want_dy, int lane) {
+  using WS = WaveSums<16>;
+  static_assert(kMaxN <= 16, "dY butterfly width");
+  const int C = t.channels;
+  for (int c0 = 0; c0 < C; c0 += kLanes) {
+    const int c = c0 + lane;
+    const bool on = c < C;
+    int staged = -1;
+    unsigned seen = 0;   // input degrees with at least one path
+    float xr[kMaxN], dxr[kMaxN], bv[kMaxN];
+    auto flush = [&](int l) {
+#pragma unroll
+      for (int i = 0; i < kMaxN; ++i)
+        if (i < 2 * l + 1) dx[static_cast<int64_t>(l * l + i) * C + c] = dxr[i];
+    };
+    for (int p = 0; p < t.np; ++p) {
+      const PathInfo q = path_info(t, p);
+      if (q.l1 != staged) {
+        if (staged >= 0 && dx && on) flush(staged);
+        stage_x(x, q.l1, q.n1, C, c, on, xr);
+#pragma unroll
+        for (int i = 0; i < kMaxN; ++i) dxr[i] = 0.f;
+        staged = q.l1;
+        seen |= 1u << q.l1;
+      }
+      const float gv = gate(g, p, t.np, C, c, on);
+      float o[kMaxN];
+#pragma unroll
+      for (int k = 0; k < kMaxN; ++k)
+        o[k] = on ? go[static_cast<int64_t>(q.out + (k < q.n3 ? k : 0)) * C + c] : 0.f;
+      const float* bond = sM + t.bond[p];
+      float dgv = 0.f;
+#pragma unroll
+      for (int k = 0; k < kMaxN; ++k) {
+        if (k < q.n3) {
+          const float base = bond_row_dot(bond, k, q.n1, xr, bv);
+          dgv = fmaf(base, o[k], dgv);
+          const float gk = gv * o[k];
+          L.sG[k * kLanes + lane] = gk;
+#pragma unroll
+          for (int i = 0; i < kMaxN; ++i) dxr[i] = fmaf(bv[i], gk, dxr[i]);
+        }
+      }
+      if (dg && on) dg[static_cast<int64_t>(p) * C + c] = dgv;
+      if (want_dy) {
+        // this lane's sum_{i,k} Chat[i][k][j] x_i go_k, against the CG rows (scalar loads)
+        const float* cg = kCGGeneric + t.cg[p];
+        float part[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) part[j] = 0.f;
+#pragma unroll
+        for (int i = 0; i < kMaxN; ++i) {
+          if (i < q.n1) {
+            for (int k = 0; k < q.n3; ++k) {
+              const float tk = xr[i] * L.sG[k * kLanes + lane];
+              const float* row = cg + (i * q.n3 + k) * q.n2;
+              float cv[kMaxN];
+#pragma unroll
+              for (int j = 0; j < kMaxN; ++j) cv[j] = row[j];
+#pragma unroll
+              for (int j = 0; j < kMaxN; ++j)
+                if (j < q.n2) part[j] = fmaf(cv[j], tk, part[j]);
+            }
+          }
+        }
+        // summed over the lanes (fixed butterfly order), added by the owner lanes
+        const float tot = WS::reduce(part, lane);
+        const int j = WS::index(lane);
+        if (WS::owner(lane) && j < q.n2) L.sDY[q.l2 * q.l2 + j] = fmaf(t.scale[p], tot, L.sDY[q.l2 * q.l2 + j]);
+      }
+    }
+    if (dx && on) {
+      if (staged >= 0) flush(staged);
+      for (int l = 0; l <= t.lin; ++l)        // degrees without a path: zero adjoint
+        if (!((seen >> l) & 1u))
+          for (int i = 0; i < 2 * l + 1; ++i) dx[static_cast<int64_t>(l * l + i) * C + c] = 0.f;
+    }
+  }
+}
+
+// LDS carve-up, in floats: sY | sDY | sM | (sG)
+__host__ __device__ __forceinline__ int bond_floats(const GenTable& t) { return (t.nb + 3) & ~3; }
+__host__ __device__ __forceinline__ int fwd_lds_floats(const GenTable& t) { return kHead + bond_floats(t); }
+__host__ __device__ __forceinline__ int bwd_lds_floats(const GenTable& t) {
+  return fwd_lds_floats(t) + (2 * t.lout + 1) * kLanes;
+}
+
+__device__ __forceinline__ BwdLds carve(float* lds, const GenTable& t) {
+  BwdLds L;
+  L.sDY = lds + kLanes;
+  L.sG = lds + kHead + bond_floats(t);
+  return L;
+}
+
+// Harmonics of row r into sY and sDY zeroed, barrier, bonds, barrier.
+__device__ __forceinline__ void begin_instance(const GenTable& t, const float* y, int64_t r, float* lds, int lane) {
+  if (lane < t.ny) lds[lane] = y[r * t.ny + lane];
+  lds[kLanes + lane] = 0.f;
+  __syncthreads();
+  build_bonds(t, lds, lds + kHead, lane);
+  __syncthreads();
+}
+
+__global__ void __launch_bounds__(kLanes)
+gen_tp_forward_kernel(const GenTable t, const float* __restrict__ x, const float* __restrict__ y,
+                      const float* __restrict__ g, float* __restrict__ out, int64_t rows) {
+  extern __shared__ float lds[];
+  const int lane = threadIdx.x;
+  const int C = t.channels;
+  for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+    begin_instance(t, y, r, lds, lane);
+    forward_instance(t, lds + kHead, x_row(x, r, true, t), g + r * t.np * C, out + r * t.noc * C, false, lane);
+    __syncthreads();
+  }
+}
+
+__global__ void __launch_bounds__(kLanes)
+gen_tp_backward_kernel(const GenTable t, const float* __restrict__ x, const float* __restrict__ y,
+                       const float* __restrict__ g, const float* __restrict__ go, float* __restrict__ dx,
+                       float* __restrict__ dy, float* __restrict__ dg, int64_t rows) {
+  extern __shared__ float lds[];
+  const int lane = threadIdx.x;
+  const int C = t.channels;
+  const BwdLds L = carve(lds, t);
+  for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+    begin_instance(t, y, r, lds, lane);
+    backward_instance(t, lds + kHead, L, x_row(x, r, true, t), g + r * t.np * C, go + r * t.noc * C,
+                      dx ? dx + r * t.nx * C : nullptr, dg ? dg + r * t.np * C : nullptr, dy != nullptr, lane);
+    __syncthreads();
+    if (dy && lane < t.ny) dy[r * t.ny + lane] = L.sDY[lane];
+  }
+}
+
+// Receiver-CSR message forward: one node at a time per workgroup, its edges in CSR order.
+__global__ void __launch_bounds__(kLanes)
+gen_msg_forward_kernel(const GenTable t, const float* __restrict__ x, const float* __restrict__ y,
+                       const float* __restrict__ g, const int64_t* __restrict__ src,
+                       const int64_t* __restrict__ rowptr, const int64_t* __restrict__ perm, float* __restrict__ out,
+                       int64_t nodes_src, int64_t nodes_dst) {
+  extern __shared__ float lds[];
+  const int lane = threadIdx.x;
+  const int C = t.channels;
+  for (int64_t n = blockIdx.x; n < nodes_dst; n += gridDim.x) {
+    const int64_t q0 = rowptr[n], q1 = rowptr[n + 1];
+    float* orow = out + n * t.noc * C;
+    if (q0 == q1) {
+      for (int64_t i = lane; i < static_cast<int64_t>(t.noc) * C; i += kLanes) orow[i] = 0.f;
+      continue;
+    }
+    for (int64_t q = q0; q < q1; ++q) {
+      const int64_t e = perm ? perm[q] : q;
+      begin_instance(t, y, e, lds, lane);
+      const int64_t s = src[e];
+      forward_instance(t, lds + kHead, x_row(x, s, s >= 0 && s < nodes_src, t), g + e * t.np * C, orow, q != q0,
+                       lane);
+      __syncthreads();
+    }
+  }
+}
+
+// Receiver-CSR edge adjoint: per edge e of node n, the TP VJP with dout = go[n].
+__global__ void __launch_bounds__(kLanes)
+gen_msg_edge_grad_kernel(const GenTable t, const float* __restrict__ x, const float* __restrict__ y,
+                         const float* __restrict__ g, const float* __restrict__ go,
+                         const int64_t* __restrict__ src, const int64_t* __restrict__ rowptr,
+                         const int64_t* __restrict__ perm, float* __restrict__ dyp, float* __restrict__ dg,
+                         float* __restrict__ dxe, int64_t nodes_src, int64_t nodes_dst, int chunks) {
+  extern __shared__ float lds[];
+  const int lane = threadIdx.x;
+  const int C = t.channels;
+  const BwdLds L = carve(lds, t);
+  for (int64_t n = blockIdx.x; n < nodes_dst; n += gridDim.x) {
+    const int64_t q0 = rowptr[n], q1 = rowptr[n + 1];
+    for (int64_t q = q0; q < q1; ++q) {
+      const int64_t e = perm ? perm[q] : q;
+      begin_instance(t, y, e, lds, lane);
+      const int64_t s = src[e];
+      backward_instance(t, lds + kHead, L, x_row(x, s, s >= 0 && s < nodes_src, t), g + e * t.np * C,
+                        go + n * t.noc * C, dxe ? dxe + e * t.nx * C : nullptr, dg ? dg + e * t.np * C : nullptr,
+                        dyp != nullptr, lane);
+      __syncthreads();
+      if (dyp) {
+        float* d = dyp + e * chunks * t.ny;
+        for (int i = lane; i < chunks * t.ny; i += kLanes) d[i] = i < t.ny ? L.sDY[i] : 0.f;
+      }
+    }
+  }
+}
+
+int make_table(const ictc_tp_desc& d, GenTable* t) {
+  if (d.input_lmax > kGenericMaxL || d.edge_lmax > kGenericMaxL || d.output_lmax > kGenericMaxL)
+    return ICTC_ERR_UNSUPPORTED;
+  const PathTable pt = make_paths(d.input_lmax, d.edge_lmax, d.output_lmax);
+  *t = GenTable{};
+  t->np = pt.n;
+  t->nb = pt.nbond;
+  t->noc = pt.noc;
+  t->nx = (d.input_lmax + 1) * (d.input_lmax + 1);
+  t->ny = (d.edge_lmax + 1) * (d.edge_lmax + 1);
+  t->channels = d.channels;
+  t->lin = d.input_lmax;
+  t->lout = d.output_lmax;
+  constexpr int G = kCGGenericMaxL + 1;
+  for (int p = 0; p < pt.n; ++p) {
+    const int off = kCGGenericOffset[(pt.l1[p] * G + pt.l2[p]) * G + pt.l3[p]];
+    if (off < 0) return ICTC_ERR_INVALID_ARGUMENT;
+    t->meta[p] = pt.l1[p] | pt.l2[p] << 4 | pt.l3[p] << 8 | pt.out[p] << 12;
+    t->bond[p] = pt.bond[p];
+    t->cg[p] = off;
+    t->scale[p] = d.scale[p];
+  }
+  return ICTC_OK;
+}
+
+unsigned grid_for(int64_t instances) {
+  return static_cast<unsigned>(instances < kGridCap ? instances : kGridCap);
+}
+
+int status() { return hipGetLastError() == hipSuccess ? ICTC_OK : ICTC_ERR_LAUNCH; }
+
+}  // namespace
+
+int generic_tp_forward(const ictc_tp_desc& d, const float* x, const float* y, const float* g, float* out,
+                       int64_t rows, hipStream_t stream) {
+  GenTable t;
+  const int st = make_table(d, &t);
+  if (st != ICTC_OK) return st;
+  hipLaunchKernelGGL(gen_tp_forward_kernel, dim3(grid_for(rows)), dim3(kLanes),
+                     fwd_lds_floats(t) * sizeof(float), stream, t, x, y, g, out, rows);
+  return status();
+}
+
+int generic_tp_backward(const ictc_tp_desc& d, const float* x, const float* y, const float* g, const float* go,
+                        float* dx, float* dy, float* dg, int64_t rows, hipStream_t stream) {
+  GenTable t;
+  const int st = make_table(d, &t);
+  if (st != ICTC_OK) return st;
+  hipLaunchKernelGGL(gen_tp_backward_kernel, dim3(grid_for(rows)), dim3(kLanes),
+                     bwd_lds_floats(t) * sizeof(float), stream, t, x, y, g, go, dx, dy, dg, rows);
+  return status();
+}
+
+int generic_msg_forward(const ictc_tp_desc& d, const float* x, const float* y, const float* g, const int64_t* src,
+                        const int64_t* rowptr, const int64_t* perm, float* out, int64_t nodes_src,
+                        int64_t nodes_dst, hipStream_t stream) {
+  GenTable t;
+  const int st = make_table(d, &t);
+  if (st != ICTC_OK) return st;
+  hipLaunchKernelGGL(gen_msg_forward_kernel, dim3(grid_for(nodes_dst)), dim3(kLanes),
+                     fwd_lds_floats(t) * sizeof(float), stream, t, x, y, g, src, rowptr, perm, out, nodes_src,
+                     nodes_dst);
+  return status();
+}
+
+int generic_msg_edge_grad(const ictc_tp_desc& d, const float* x, const float* y, const float* g, const float* go,
+                          const int64_t* src, const int64_t* rowptr, const int64_t* perm, float* dyp, float* dg,
+                          float* dxe, int64_t nodes_src, int64_t nodes_dst, hipStream_t stream) {
+  GenTable t;
+  const int st = make_table(d, &t);
+  if (st != ICTC_OK) return st;
+  const int chunks = (d.channels + kLanes - 1) / kLanes;
+  hipLaunchKernelGGL(gen_msg_edge_grad_kernel, dim3(grid_for(nodes_dst)), dim3(kLanes),
+                     bwd_lds_floats(t) * sizeof(float), stream, t, x, y, g, go, src, rowptr, perm, dyp, dg, dxe,
+                     nodes_src, nodes_dst, chunks);
+  return status();
+}
+
+}  // namespace ictc

@@ -3,6 +3,7 @@
 // source-node segmented sum (which depends on the input degree only) here.
 #include <mutex>
 
+#include "generic.hpp"
 #include "message_kernels.hpp"
 
 namespace ictc {
@@ -66,8 +67,10 @@ const MsgEdgeT kMsgEdgeT[64] = {
 #include "generated/tp_instances.def"
 };
 #undef ICTC_DECLARE
-const MsgNode kMsgNode[4] = {&launch_msg_node_grad<0>, &launch_msg_node_grad<1>, &launch_msg_node_grad<2>,
-                             &launch_msg_node_grad<3>};
+const MsgNode kMsgNode[kGenericMaxL + 1] = {&launch_msg_node_grad<0>, &launch_msg_node_grad<1>,
+                                            &launch_msg_node_grad<2>, &launch_msg_node_grad<3>,
+                                            &launch_msg_node_grad<4>, &launch_msg_node_grad<5>,
+                                            &launch_msg_node_grad<6>};
 
 int tp_check_desc(const ictc_tp_desc* d);  // tp_api.hip
 
@@ -93,6 +96,7 @@ inline int bond_row_floats(const ictc_tp_desc* d) {
 
 // width of the caller's bond buffer: 0 when the kernels build the rows from the harmonics
 inline int bond_width(const ictc_tp_desc* d) {
+  if (generic_degrees(*d)) return 0;
   const int nb = bond_row_floats(d), ny = (d->edge_lmax + 1) * (d->edge_lmax + 1);
   return bond_inline(nb, ny) ? 0 : nb;
 }
@@ -192,6 +196,9 @@ int ictc_hip_message_forward(const ictc_tp_desc* desc, const float* node_feature
   if (nodes_dst == 0) return ICTC_OK;
   if (!node_out || !dst_rowptr || (edges > 0 && (!node_features || !bonds || !gates || !src)))
     return ICTC_ERR_INVALID_ARGUMENT;
+  if (ictc::generic_degrees(*desc))
+    return ictc::generic_msg_forward(*desc, node_features, bonds, gates, src, dst_rowptr, dst_perm, node_out,
+                                     nodes_src, nodes_dst, stream);
   const ictc::MsgFwd fn = ictc::kMsgFwd[ictc::msg_index(desc)];
   if (fn == nullptr) return ICTC_ERR_UNSUPPORTED;
   return fn(*desc, node_features, bonds, gates, src, dst_rowptr, dst_perm, node_out, nodes_src, nodes_dst,
@@ -209,6 +216,10 @@ int ictc_hip_message_edge_grad(const ictc_tp_desc* desc, const float* node_featu
     return ICTC_OK;
   if (!bonds || !gates || !grad_out || !src || !dst_rowptr) return ICTC_ERR_INVALID_ARGUMENT;
   if ((grad_harmonics_partial || grad_gates) && !node_features) return ICTC_ERR_INVALID_ARGUMENT;
+  if (ictc::generic_degrees(*desc))
+    return ictc::generic_msg_edge_grad(*desc, node_features, bonds, gates, grad_out, src, dst_rowptr, dst_perm,
+                                       grad_harmonics_partial, grad_gates, edge_grad_features, nodes_src,
+                                       nodes_dst, stream);
   const ictc::MsgEdge fn = ictc::kMsgEdge[ictc::msg_index(desc)];
   if (fn == nullptr) return ICTC_ERR_UNSUPPORTED;
   return fn(*desc, node_features, bonds, gates, grad_out, src, dst_rowptr, dst_perm, grad_harmonics_partial,
@@ -225,8 +236,9 @@ int ictc_hip_message_edge_grad_static(const ictc_tp_desc* desc, const float* nod
   if (edges == 0 || nodes_dst == 0 || (!grad_harmonics && !grad_gates && !edge_grad_features)) return ICTC_OK;
   if (!bonds || !gates || !grad_out || !src || !dst_rowptr) return ICTC_ERR_INVALID_ARGUMENT;
   if ((grad_harmonics || grad_gates) && !node_features) return ICTC_ERR_INVALID_ARGUMENT;
-  const ictc::MsgEdge fn = ictc::kMsgEdge[ictc::msg_index(desc)];
-  if (fn == nullptr) return ICTC_ERR_UNSUPPORTED;
+  const bool generic = ictc::generic_degrees(*desc);
+  const ictc::MsgEdge fn = generic ? nullptr : ictc::kMsgEdge[ictc::msg_index(desc)];
+  if (!generic && fn == nullptr) return ICTC_ERR_UNSUPPORTED;
   const int chunks = ictc_hip_message_chunks(desc->channels);
   const int ny = (desc->edge_lmax + 1) * (desc->edge_lmax + 1);
   float* partial = grad_harmonics;   // one chunk: the kernel writes the sums itself
@@ -235,8 +247,11 @@ int ictc_hip_message_edge_grad_static(const ictc_tp_desc* desc, const float* nod
     const int sst = ictc::static_scratch(stream, &partial);
     if (sst != ICTC_OK) return sst;
   }
-  const int r = fn(*desc, node_features, bonds, gates, grad_out, src, dst_rowptr, dst_perm, partial, grad_gates,
-                   edge_grad_features, nodes_src, nodes_dst, stream);
+  const int r = generic ? ictc::generic_msg_edge_grad(*desc, node_features, bonds, gates, grad_out, src, dst_rowptr,
+                                                      dst_perm, partial, grad_gates, edge_grad_features, nodes_src,
+                                                      nodes_dst, stream)
+                        : fn(*desc, node_features, bonds, gates, grad_out, src, dst_rowptr, dst_perm, partial,
+                             grad_gates, edge_grad_features, nodes_src, nodes_dst, stream);
   if (r != ICTC_OK || partial == grad_harmonics) return r;
   const int64_t total = edges * ny;
   hipLaunchKernelGGL(ictc::chunk_sum_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0,
@@ -256,6 +271,7 @@ int ictc_hip_message_forward_tangent(const ictc_tp_desc* desc, const float* node
       (edges > 0 && (!node_features || !bonds || !gates || !tangent_features || !tangent_bonds ||
                      !tangent_gates || !src)))
     return ICTC_ERR_INVALID_ARGUMENT;
+  if (ictc::generic_degrees(*desc)) return ICTC_ERR_UNSUPPORTED;
   const ictc::MsgFwdT fn = ictc::kMsgFwdT[ictc::msg_index(desc)];
   if (fn == nullptr) return ICTC_ERR_UNSUPPORTED;
   const ictc::MsgTangent t{tangent_features, tangent_bonds, tangent_gates};
@@ -277,6 +293,7 @@ int ictc_hip_message_edge_grad_tangent(const ictc_tp_desc* desc, const float* no
   if (!node_features || !bonds || !gates || !tangent_features || !tangent_bonds || !tangent_gates || !grad_out ||
       !src || !dst_rowptr)
     return ICTC_ERR_INVALID_ARGUMENT;
+  if (ictc::generic_degrees(*desc)) return ICTC_ERR_UNSUPPORTED;
   const ictc::MsgEdgeT fn = ictc::kMsgEdgeT[ictc::msg_index(desc)];
   if (fn == nullptr) return ICTC_ERR_UNSUPPORTED;
   const ictc::MsgTangent t{tangent_features, tangent_bonds, tangent_gates};

@@ -1,5 +1,6 @@
 // extern "C" entry points of the tensor-product family: descriptor validation and
 // dispatch to the per-degree instantiations compiled in generated/tp_inst_*.hip.
+#include "generic.hpp"
 #include "tp_kernels.hpp"
 
 namespace ictc {
@@ -14,8 +15,9 @@ namespace ictc {
 #include "generated/tp_instances.def"
 #undef ICTC_DECLARE
 
-// Dispatch tables indexed by input_lmax*16 + edge_lmax*4 + output_lmax; entries of
-// combinations left out of a (development) build are null and report UNSUPPORTED.
+// Dispatch tables of the per-degree instantiations (every degree <= 3), indexed by
+// input_lmax*16 + edge_lmax*4 + output_lmax; entries of combinations left out of a
+// (development) build are null and report UNSUPPORTED.
 #define ICTC_DECLARE(A, B, C) [A * 16 + B * 4 + C] = &launch_forward<A, B, C>,
 const FwdLaunch kFwdTable[64] = {
 #include "generated/tp_instances.def"
@@ -33,9 +35,10 @@ int tp_check_desc(const ictc_tp_desc* d) {
   if (d->channels < 1 || d->num_paths < 0 || d->num_paths > ICTC_MAX_PATHS || d->out_components < 0)
     return ICTC_ERR_INVALID_ARGUMENT;
   if (d->input_lmax < 0 || d->edge_lmax < 0 || d->output_lmax < 0) return ICTC_ERR_INVALID_ARGUMENT;
-  if (d->input_lmax > 3 || d->edge_lmax > 3 || d->output_lmax > 3) return ICTC_ERR_UNSUPPORTED;
-  // The kernels compile the full path set of the degrees with its canonical layout;
-  // the descriptor must state exactly that (path subsets are mapped by the caller).
+  if (d->input_lmax > kGenericMaxL || d->edge_lmax > kGenericMaxL || d->output_lmax > kGenericMaxL)
+    return ICTC_ERR_UNSUPPORTED;
+  // The kernels run the full path set of the degrees with its canonical layout; the
+  // descriptor must state exactly that (path subsets are mapped by the caller).
   const PathTable t = make_paths(d->input_lmax, d->edge_lmax, d->output_lmax);
   if (d->num_paths != t.n || d->out_components != t.noc) return ICTC_ERR_INVALID_ARGUMENT;
   for (int s = 0; s < t.n; ++s)
@@ -63,11 +66,11 @@ const char* ictc_hip_status_string(int status) {
   }
 }
 
-int ictc_hip_abi_version(void) { return 11; }
+int ictc_hip_abi_version(void) { return 12; }
 
 int ictc_hip_tp_slot_count(int input_lmax, int edge_lmax, int output_lmax) {
-  if (input_lmax < 0 || edge_lmax < 0 || output_lmax < 0 || input_lmax > 3 || edge_lmax > 3 ||
-      output_lmax > 3)
+  constexpr int L = ictc::kGenericMaxL;
+  if (input_lmax < 0 || edge_lmax < 0 || output_lmax < 0 || input_lmax > L || edge_lmax > L || output_lmax > L)
     return -1;
   return ictc::make_paths(input_lmax, edge_lmax, output_lmax).n;
 }
@@ -79,6 +82,8 @@ int ictc_hip_tp_forward(const ictc_tp_desc* desc, const float* features, const f
   if (rows < 0) return ICTC_ERR_INVALID_ARGUMENT;
   if (rows == 0) return ICTC_OK;
   if (!features || !harmonics || !gates || !out) return ICTC_ERR_INVALID_ARGUMENT;
+  if (ictc::generic_degrees(*desc))
+    return ictc::generic_tp_forward(*desc, features, harmonics, gates, out, rows, stream);
   const ictc::FwdLaunch fn = ictc::kFwdTable[ictc::table_index(desc)];
   if (fn == nullptr) return ICTC_ERR_UNSUPPORTED;
   return fn(*desc, features, harmonics, gates, out, rows, stream);
@@ -94,6 +99,9 @@ int ictc_hip_tp_backward(const ictc_tp_desc* desc, const float* features, const 
   if (!harmonics || !gates || !grad_out) return ICTC_ERR_INVALID_ARGUMENT;
   if ((grad_harmonics || grad_gates) && !features) return ICTC_ERR_INVALID_ARGUMENT;
   if (!grad_features && !grad_harmonics && !grad_gates) return ICTC_OK;
+  if (ictc::generic_degrees(*desc))
+    return ictc::generic_tp_backward(*desc, features, harmonics, gates, grad_out, grad_features, grad_harmonics,
+                                     grad_gates, rows, stream);
   const ictc::BwdLaunch fn = ictc::kBwdTable[ictc::table_index(desc)];
   if (fn == nullptr) return ICTC_ERR_UNSUPPORTED;
   return fn(*desc, features, harmonics, gates, grad_out, grad_features, grad_harmonics, grad_gates,

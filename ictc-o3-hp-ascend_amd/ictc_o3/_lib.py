@@ -13,9 +13,9 @@ import threading
 
 import torch  # noqa: F401  (must precede CDLL, see module docstring)
 
-MAX_PATHS = 64
+MAX_PATHS = 128
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libictc_hip.so")
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 
 class TpDesc(ctypes.Structure):

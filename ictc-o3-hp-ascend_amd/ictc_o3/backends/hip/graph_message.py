@@ -212,8 +212,9 @@ def _second_order_raw(plan: TensorProductPlan, graph: MessageGraph, need, x, y, 
 
 
 # The double backward uses the fused tangent kernels when no further derivative is recorded
-# (grad mode off inside backward) and all three tangents are present; otherwise it applies the
-# differentiable one-argument substitutions.  Tests switch this off to compare the two.
+# (grad mode off inside backward), all three tangents are present and the degrees have them
+# (every degree <= 3); otherwise it applies the differentiable one-argument substitutions.
+# Tests switch this off to compare the two.
 FUSED_SECOND_ORDER = True
 
 
@@ -271,7 +272,7 @@ class _Backward(torch.autograd.Function):
         hy = hy if need_out[1] else None
         hg = hg if need_out[2] else None
         nx, ny, ng, no = required_gradients((x, y, g, go), ctx.needs_input_grad[3:7])
-        if (FUSED_SECOND_ORDER and not torch.is_grad_enabled() and graph.edges > 0
+        if (FUSED_SECOND_ORDER and not plan.generic and not torch.is_grad_enabled() and graph.edges > 0
                 and hx is not None and hy is not None and hg is not None and (nx or ny or ng or no)):
             gx, gy, gg, ggo = _second_order_raw(plan, graph, (nx, ny, ng, no), x, y, g, go, hx.contiguous(),
                                                 hy.contiguous(), hg.contiguous(), bonds)

@@ -25,6 +25,10 @@ from ...autograd.adjoint_requirements import required_gradients
 from ...basis.ictd_irreps import PathPlan, triangle_paths
 
 
+MAX_DEGREE = 6            # degree-generic kernels (run-time path tables)
+COMPILED_MAX_DEGREE = 3   # per-degree kernels
+
+
 def _canonical_layout(full):
     """First output component of each full-set path: ascending l3, enumeration order
     within one l3 (the owner's path_offset order)."""
@@ -40,9 +44,11 @@ def _canonical_layout(full):
 class TensorProductPlan:
     """Immutable launch description of one owner (paths, channels, degrees).
 
-    The kernels are compiled for the full triangle/parity path set of
-    (input_lmax, edge_lmax, output_lmax).  An owner with a path subset runs the full
-    set with zero gates on the absent paths and keeps only its own output rows."""
+    The kernels run the full triangle/parity path set of (input_lmax, edge_lmax,
+    output_lmax).  An owner with a path subset runs the full set with zero gates on the
+    absent paths and keeps only its own output rows.  Degrees up to 3 run the per-degree
+    kernels; a degree of 4 to 6 runs the degree-generic ones (``generic``), which have no
+    fused message tangent kernels."""
 
     def __init__(self, paths: Sequence[Tuple[int, int, int]], channels: int, input_lmax: int,
                  edge_lmax: int, lmax: Optional[int] = None):
@@ -54,8 +60,9 @@ class TensorProductPlan:
         self.lmax = max(lmax if lmax is not None else 0, self.input_lmax, self.edge_lmax, self.output_lmax)
         if any(i > self.input_lmax or j > self.edge_lmax for i, j, _ in paths):
             raise ValueError("Declared input degrees must cover every tensor-product path")
-        if max(self.input_lmax, self.edge_lmax, self.output_lmax) > 3:
-            raise ValueError("the HIP tensor-product kernels support degrees up to 3")
+        if max(self.input_lmax, self.edge_lmax, self.output_lmax) > MAX_DEGREE:
+            raise ValueError(f"the HIP tensor-product kernels support degrees up to {MAX_DEGREE}")
+        self.generic = max(self.input_lmax, self.edge_lmax, self.output_lmax) > COMPILED_MAX_DEGREE
         self.plan = PathPlan(paths, channels)
         self.plan.path_counts_by_l = {l: self.plan.path_counts_by_l.get(l, 0) for l in range(self.lmax + 1)}
         self.paths = self.plan.paths

@@ -29,12 +29,12 @@
 extern "C" {
 #endif
 
-#define ICTC_MAX_PATHS 64
+#define ICTC_MAX_PATHS 128   /* the full (6,6,6) path set has 106 paths */
 
 typedef enum ictc_status {
     ICTC_OK = 0,
     ICTC_ERR_INVALID_ARGUMENT = 1,   /* null pointer, negative size, bad descriptor */
-    ICTC_ERR_UNSUPPORTED = 2,        /* degree combination not compiled in */
+    ICTC_ERR_UNSUPPORTED = 2,        /* degree combination or mode not supported */
     ICTC_ERR_LAUNCH = 3,             /* hipLaunchKernel / hipGetLastError failed */
     ICTC_ERR_INDEX = 4,              /* graph or species index out of range (checked kernels) */
     ICTC_ERR_CAPACITY = 5            /* input exceeds a static scratch array (nothing launched) */
@@ -57,12 +57,18 @@ typedef enum ictc_status {
  *                  the library carry the 'component' normalisation (ictd_irreps.py:136-142).
  * An owner with a path subset runs the full set with zero gates on the absent paths
  * and keeps its own output rows.
+ *
+ * Degrees: every degree <= 6.  Degree sets with all degrees <= 3 run kernels compiled per
+ * degree set (path loops unrolled, CG constants folded); the others run degree-generic
+ * kernels that read the path table and the CG tensors at run time (one wave per instance),
+ * behind every tensor-product and graph-message entry point except the two message tangent
+ * entry points, which return ICTC_ERR_UNSUPPORTED for such degree sets.
  */
 typedef struct ictc_tp_desc {
     int32_t channels;          /* C >= 1 */
-    int32_t input_lmax;        /* 0..3 */
-    int32_t edge_lmax;         /* 0..3 */
-    int32_t output_lmax;       /* 0..3 */
+    int32_t input_lmax;        /* 0..6 */
+    int32_t edge_lmax;         /* 0..6 */
+    int32_t output_lmax;       /* 0..6 */
     int32_t num_paths;         /* P: number of owner paths (gate blocks) */
     int32_t out_components;    /* NOC */
     int32_t gate_index[ICTC_MAX_PATHS];
@@ -120,7 +126,8 @@ int ictc_hip_tp_backward(const ictc_tp_desc* desc,
  * (the reference's bond projection Y @ P: backends/ascend/tensor_product.py:9-57,
  * structured_product.py:7-22).  The same buffer serves the forward and both VJP kernels.
  * For small degree sets (at most 32 projection coefficients per lane, e.g. lmax 2 or an
- * input lmax of 0) the kernels form the bond rows from the harmonics themselves:
+ * input lmax of 0) and for every degree set with a degree above 3 the kernels form the bond
+ * rows from the harmonics themselves:
  * ictc_hip_message_bond_width then returns 0, ictc_hip_message_bonds does nothing, and the
  * caller passes the harmonics [edges, (L_e+1)^2] as the `bonds` argument.
  *

@@ -38,7 +38,10 @@ def test_status_strings_and_slot_counts():
     assert lib.ictc_hip_tp_slot_count(2, 2, 2) == 11
     assert lib.ictc_hip_tp_slot_count(3, 3, 3) == 23
     assert lib.ictc_hip_tp_slot_count(0, 3, 3) == 4
-    assert lib.ictc_hip_tp_slot_count(4, 3, 3) == -1
+    assert lib.ictc_hip_tp_slot_count(4, 4, 4) == 42      # degree-generic kernels
+    assert lib.ictc_hip_tp_slot_count(5, 5, 5) == 69
+    assert lib.ictc_hip_tp_slot_count(6, 6, 6) == 106
+    assert lib.ictc_hip_tp_slot_count(7, 3, 3) == -1
 
 
 def _desc(c=64, lmax=2):
@@ -64,7 +67,10 @@ def test_descriptor_validation_rejects_before_launch():
     bad.out_offset[0] = bad.out_components          # output block past the end
     assert fwd(ctypes.byref(bad), fake, fake, fake, fake, 4, None) == 1
     bad = _desc()
-    bad.input_lmax = 4
+    bad.input_lmax = 4                              # path count no longer matches
+    assert fwd(ctypes.byref(bad), fake, fake, fake, fake, 4, None) == 1
+    bad = _desc()
+    bad.input_lmax = 7                              # above every kernel
     assert fwd(ctypes.byref(bad), fake, fake, fake, fake, 4, None) == 2
     assert fwd(ctypes.byref(d), fake, fake, fake, fake, -1, None) == 1
     assert fwd(ctypes.byref(d), None, fake, fake, fake, 4, None) == 1
@@ -73,6 +79,21 @@ def test_descriptor_validation_rejects_before_launch():
     bwd = lib.ictc_hip_tp_backward
     # gradients to harmonics need the features operand
     assert bwd(ctypes.byref(d), None, fake, fake, fake, None, fake, None, 4, None) == 1
+
+
+def test_generic_degree_validation_before_launch():
+    """Degree sets above 3 pass descriptor validation; the message tangent entry points, which have
+    no degree-generic kernels, report UNSUPPORTED before any launch; bond rows are built in-kernel."""
+    from ictc_o3 import _lib
+    lib = _lib.lib()
+    fake = ctypes.c_void_p(16)  # never dereferenced
+    d = _desc(16, 4)
+    assert lib.ictc_hip_tp_forward(ctypes.byref(d), None, fake, fake, fake, 4, None) == 1
+    assert lib.ictc_hip_message_bond_width(ctypes.byref(d)) == 0
+    f = fake
+    assert lib.ictc_hip_message_forward_tangent(ctypes.byref(d), f, f, f, f, f, f, f, f, None, f, 1, 1, 1, None) == 2
+    assert lib.ictc_hip_message_edge_grad_tangent(ctypes.byref(d), f, f, f, f, f, f, f, f, f, None, f, None, None,
+                                                  1, 1, 1, None) == 2
 
 
 def test_python_guards_reject_cpu_tensors():

@@ -58,7 +58,8 @@ def test_basis_is_gram_orthonormal_and_harmonic():
 
 
 @pytest.mark.parametrize("l1,l2,l3", [(1, 1, 0), (1, 1, 2), (2, 2, 2), (3, 3, 2), (1, 2, 3), (2, 3, 3),
-                                      (3, 3, 6), (2, 2, 4), (0, 3, 3), (3, 1, 2)])
+                                      (3, 3, 6), (2, 2, 4), (0, 3, 3), (3, 1, 2), (4, 4, 4), (5, 3, 6),
+                                      (6, 6, 6)])
 def test_cg_equivariant(l1, l2, l3):
     c = B.cg_tensor(l1, l2, l3)
     for seed in (1, 2):
@@ -70,8 +71,8 @@ def test_cg_equivariant(l1, l2, l3):
 
 
 def test_cg_forbidden_paths_are_zero_and_normalisation():
-    for l1 in range(4):
-        for l2 in range(4):
+    for l1 in range(7):
+        for l2 in range(7):
             for l3 in range(7):
                 c = B.cg_tensor(l1, l2, l3)
                 ok = abs(l1 - l2) <= l3 <= l1 + l2 and (l1 + l2 + l3) % 2 == 0
@@ -114,9 +115,9 @@ def test_cg_sign_and_size_closed_form(source):
     n = torch.nn.functional.normalize(torch.randn(64, 3, generator=g, dtype=torch.float64), dim=-1)
     ys = B.direction_harmonics_all(n, 6)
     checked = 0
-    for l1 in range(4):
-        for l2 in range(4):
-            for l3 in range(abs(l1 - l2), l1 + l2 + 1):
+    for l1 in range(7):          # every triple the kernels use (all degrees <= 6)
+        for l2 in range(7):
+            for l3 in range(abs(l1 - l2), min(l1 + l2, 6) + 1):
                 if (l1 + l2 + l3) % 2:
                     continue
                 raw = (B.cg_tensor(l1, l2, l3) if source == "oracle"
@@ -128,7 +129,7 @@ def test_cg_sign_and_size_closed_form(source):
                 assert (f - want * ys[l3]).abs().max() < 1e-12 * max(1.0, float(ys[l3].abs().max())) * 50, \
                     (l1, l2, l3)
                 checked += 1
-    assert checked == 30
+    assert checked == 106
 
 
 def test_harmonics_closed_forms_and_normalisation():
@@ -170,9 +171,9 @@ def test_path_enumeration_sizes():
 
 def test_product_host_constants_match_oracle():
     from ictc_o3.basis import ictd_irreps as P
-    for l1 in range(4):
-        for l2 in range(4):
-            for l3 in range(abs(l1 - l2), l1 + l2 + 1):
+    for l1 in range(7):
+        for l2 in range(7):
+            for l3 in range(abs(l1 - l2), min(l1 + l2, 6) + 1):
                 assert np.abs(P.coupling_tensor(l1, l2, l3) - B.cg_tensor(l1, l2, l3).numpy()).max() < 1e-12
     for l in range(6):
         mons, proj, scale = P.harmonics_tables(l)
