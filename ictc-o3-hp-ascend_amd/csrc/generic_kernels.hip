@@ -67,27 +67,44 @@ __device__ __forceinline__ PathInfo path_info(const GenTable& t, int p) {
   return r;
 }
 
-// M_p of every path into sM from the harmonics in sY (lanes over the bond entries of a path).
-// An entry's coefficients Chat_p[i][k][0..n2) are contiguous; all kMaxN are loaded (the table is
-// padded, so a row read never leaves it) and those past n2 are not used.
+// Calls f(Int<n>{}) for the odd width n = 2 l + 1 <= kMaxN of a degree (a wave-uniform switch), so
+// loops over one degree's components run exactly n times.
+template <typename F>
+__device__ __forceinline__ void with_width(int n1, F&& f) {
+  static_assert(kMaxN == 13, "widths 1..13");
+  switch (n1) {
+    case 1: f(Int<1>{}); break;
+    case 3: f(Int<3>{}); break;
+    case 5: f(Int<5>{}); break;
+    case 7: f(Int<7>{}); break;
+    case 9: f(Int<9>{}); break;
+    case 11: f(Int<11>{}); break;
+    default: f(Int<13>{}); break;
+  }
+}
+
+// M_p of every path into sM from the harmonics in sY (lanes over the bond entries of a path);
+// an entry's coefficients Chat_p[i][k][0..n2) are contiguous.
 __device__ void build_bonds(const GenTable& t, const float* sY, float* sM, int lane) {
   for (int p = 0; p < t.np; ++p) {
     const PathInfo q = path_info(t, p);
     const float* cg = kCGGeneric + t.cg[p];
     const float s = t.scale[p];
     float* bond = sM + t.bond[p];
-    for (int e = lane; e < q.n1 * q.n3; e += kLanes) {
-      const int k = e / q.n1, i = e - k * q.n1;
-      const float* row = cg + (i * q.n3 + k) * q.n2;
-      float c[kMaxN];
+    const float* y = sY + q.l2 * q.l2;
+    with_width(q.n2, [&](auto N2) {
+      for (int e = lane; e < q.n1 * q.n3; e += kLanes) {
+        const int k = e / q.n1, i = e - k * q.n1;
+        const float* row = cg + (i * q.n3 + k) * N2;
+        float c[N2];
 #pragma unroll
-      for (int j = 0; j < kMaxN; ++j) c[j] = row[j];
-      float acc = 0.f;
+        for (int j = 0; j < N2; ++j) c[j] = row[j];
+        float acc = 0.f;
 #pragma unroll
-      for (int j = 0; j < kMaxN; ++j)
-        if (j < q.n2) acc = fmaf(sY[q.l2 * q.l2 + j], c[j], acc);
-      bond[e] = acc * s;
-    }
+        for (int j = 0; j < N2; ++j) acc = fmaf(y[j], c[j], acc);
+        bond[e] = acc * s;
+      }
+    });
   }
 }
 
@@ -116,16 +133,15 @@ __device__ __forceinline__ float gate(const float* g, int p, int np, int C, int 
   return on ? g[static_cast<int64_t>(p < np ? p : 0) * C + c] : 0.f;
 }
 
-// sum_i xr[i] * M[k][i] over the kMaxN register rows (xr is zero past n1; the bond reads past n1
-// are clamped into row k).
-__device__ __forceinline__ float bond_row_dot(const float* bond, int k, int n1, const float (&xr)[kMaxN],
-                                              float (&bv)[kMaxN]) {
-  const float* b = bond + k * n1;
+// sum_i xr[i] * b[i] over the N1 components of the degree (the bond row k of a path); the row
+// is left in bv for the dx update.
+template <int N1>
+__device__ __forceinline__ float row_dot(const float* b, const float (&xr)[kMaxN], float (&bv)[kMaxN]) {
 #pragma unroll
-  for (int i = 0; i < kMaxN; ++i) bv[i] = b[i < n1 ? i : n1 - 1];
+  for (int i = 0; i < N1; ++i) bv[i] = b[i];
   float acc = 0.f;
 #pragma unroll
-  for (int i = 0; i < kMaxN; ++i) acc = fmaf(xr[i], bv[i], acc);
+  for (int i = 0; i < N1; ++i) acc = fmaf(xr[i], bv[i], acc);
   return acc;
 }
 
@@ -149,19 +165,23 @@ __device__ void forward_instance(const GenTable& t, const float* sM, rsrc_t x, c
       const float gv = gnext;
       gnext = gate(g, p + 1, t.np, C, c, on);
       const float* bond = sM + t.bond[p];
-      for (int k = 0; k < q.n3; ++k) {
-        const float acc = bond_row_dot(bond, k, q.n1, xr, bv);
-        if (on) {
-          float* dst = out + static_cast<int64_t>(q.out + k) * C + c;
-          *dst = accumulate ? *dst + acc * gv : acc * gv;
+      with_width(q.n1, [&](auto N1) {
+        for (int k = 0; k < q.n3; ++k) {
+          const float acc = row_dot<N1>(bond + k * N1, xr, bv);
+          if (on) {
+            float* dst = out + static_cast<int64_t>(q.out + k) * C + c;
+            *dst = accumulate ? *dst + acc * gv : acc * gv;
+          }
         }
-      }
+      });
     }
   }
 }
 
 struct BwdLds {
-  float* sG;     // [2 lout + 1][64] go_k of the current path (lane columns)
+  float* sX;     // [2 lin + 1][64] x rows of the current input degree (lane columns)
+  float* sG;     // [2 lout + 1][64] go_k of the current path
+  float* sO;     // [2 lout + 1][64] dout_k of the current path
   float* sDY;    // [64] dY of the instance
 };
 
@@ -170,7 +190,6 @@ struct BwdLds {
 // lane takes part in the dY butterflies whatever its channel, so the call is wave-uniform.
 __device__ void backward_instance(const GenTable& t, const float* sM, const BwdLds& L, rsrc_t x,
                                   const float* g, const float* go, float* dx, float* dg, bool want_dy, int lane) {
-  using WS = WaveSums<16>;
   static_assert(kMaxN <= 16, "dY butterfly width");
   const int C = t.channels;
   for (int c0 = 0; c0 < C; c0 += kLanes) {
@@ -189,6 +208,11 @@ __device__ void backward_instance(const GenTable& t, const float* sM, const BwdL
       if (q.l1 != staged) {
         if (staged >= 0 && dx && on) flush(staged);
         stage_x(x, q.l1, q.n1, C, c, on, xr);
+        if (want_dy) {
+#pragma unroll
+          for (int i = 0; i < kMaxN; ++i)
+            if (i < q.n1) L.sX[i * kLanes + lane] = xr[i];
+        }
 #pragma unroll
         for (int i = 0; i < kMaxN; ++i) dxr[i] = 0.f;
         staged = q.l1;
@@ -199,46 +223,48 @@ __device__ void backward_instance(const GenTable& t, const float* sM, const BwdL
 #pragma unroll
       for (int k = 0; k < kMaxN; ++k)
         o[k] = on ? go[static_cast<int64_t>(q.out + (k < q.n3 ? k : 0)) * C + c] : 0.f;
-      const float* bond = sM + t.bond[p];
-      float dgv = 0.f;
 #pragma unroll
-      for (int k = 0; k < kMaxN; ++k) {
+      for (int k = 0; k < kMaxN; ++k)
         if (k < q.n3) {
-          const float base = bond_row_dot(bond, k, q.n1, xr, bv);
-          dgv = fmaf(base, o[k], dgv);
-          const float gk = gv * o[k];
-          L.sG[k * kLanes + lane] = gk;
-#pragma unroll
-          for (int i = 0; i < kMaxN; ++i) dxr[i] = fmaf(bv[i], gk, dxr[i]);
+          L.sO[k * kLanes + lane] = o[k];
+          L.sG[k * kLanes + lane] = gv * o[k];
         }
-      }
-      if (dg && on) dg[static_cast<int64_t>(p) * C + c] = dgv;
+      const float* bond = sM + t.bond[p];
+      const float* cg = kCGGeneric + t.cg[p];
+      float dgv = 0.f;
+      with_width(q.n1, [&](auto N1) {
+        for (int k = 0; k < q.n3; ++k) {
+          const float base = row_dot<N1>(bond + k * N1, xr, bv);
+          dgv = fmaf(base, L.sO[k * kLanes + lane], dgv);
+          const float gk = L.sG[k * kLanes + lane];
+#pragma unroll
+          for (int i = 0; i < N1; ++i) dxr[i] = fmaf(bv[i], gk, dxr[i]);
+        }
+      });
       if (want_dy) {
-        // this lane's sum_{i,k} Chat[i][k][j] x_i go_k, against the CG rows (scalar loads)
-        const float* cg = kCGGeneric + t.cg[p];
-        float part[16];
+        with_width(q.n2, [&](auto N2) {
+          // this lane's sum_{i,k} Chat[i][k][j] x_i go_k against the CG rows (scalar loads), then
+          // summed over the lanes (a fixed butterfly) and added by the owner lanes
+          using WS = WaveSums<N2>;
+          float part[N2];
 #pragma unroll
-        for (int j = 0; j < 16; ++j) part[j] = 0.f;
-#pragma unroll
-        for (int i = 0; i < kMaxN; ++i) {
-          if (i < q.n1) {
+          for (int j = 0; j < N2; ++j) part[j] = 0.f;
+          for (int i = 0; i < q.n1; ++i) {
+            const float xi = L.sX[i * kLanes + lane];
+#pragma unroll 4
             for (int k = 0; k < q.n3; ++k) {
-              const float tk = xr[i] * L.sG[k * kLanes + lane];
-              const float* row = cg + (i * q.n3 + k) * q.n2;
-              float cv[kMaxN];
+              const float tk = xi * L.sG[k * kLanes + lane];
+              const float* row = cg + (i * q.n3 + k) * N2;
 #pragma unroll
-              for (int j = 0; j < kMaxN; ++j) cv[j] = row[j];
-#pragma unroll
-              for (int j = 0; j < kMaxN; ++j)
-                if (j < q.n2) part[j] = fmaf(cv[j], tk, part[j]);
+              for (int j = 0; j < N2; ++j) part[j] = fmaf(row[j], tk, part[j]);
             }
           }
-        }
-        // summed over the lanes (fixed butterfly order), added by the owner lanes
-        const float tot = WS::reduce(part, lane);
-        const int j = WS::index(lane);
-        if (WS::owner(lane) && j < q.n2) L.sDY[q.l2 * q.l2 + j] = fmaf(t.scale[p], tot, L.sDY[q.l2 * q.l2 + j]);
+          const float tot = WS::reduce(part, lane);
+          const int j = WS::index(lane);
+          if (WS::owner(lane) && j < N2) L.sDY[q.l2 * q.l2 + j] = fmaf(t.scale[p], tot, L.sDY[q.l2 * q.l2 + j]);
+        });
       }
+      if (dg && on) dg[static_cast<int64_t>(p) * C + c] = dgv;
     }
     if (dx && on) {
       if (staged >= 0) flush(staged);
@@ -249,17 +275,19 @@ __device__ void backward_instance(const GenTable& t, const float* sM, const BwdL
   }
 }
 
-// LDS carve-up, in floats: sY | sDY | sM | (sG)
+// LDS carve-up, in floats: sY | sDY | sM | (sX | sG | sO)
 __host__ __device__ __forceinline__ int bond_floats(const GenTable& t) { return (t.nb + 3) & ~3; }
 __host__ __device__ __forceinline__ int fwd_lds_floats(const GenTable& t) { return kHead + bond_floats(t); }
 __host__ __device__ __forceinline__ int bwd_lds_floats(const GenTable& t) {
-  return fwd_lds_floats(t) + (2 * t.lout + 1) * kLanes;
+  return fwd_lds_floats(t) + ((2 * t.lin + 1) + 2 * (2 * t.lout + 1)) * kLanes;
 }
 
 __device__ __forceinline__ BwdLds carve(float* lds, const GenTable& t) {
   BwdLds L;
   L.sDY = lds + kLanes;
-  L.sG = lds + kHead + bond_floats(t);
+  L.sX = lds + kHead + bond_floats(t);
+  L.sG = L.sX + (2 * t.lin + 1) * kLanes;
+  L.sO = L.sG + (2 * t.lout + 1) * kLanes;
   return L;
 }
 
