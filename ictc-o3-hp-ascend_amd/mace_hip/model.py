@@ -18,7 +18,8 @@ Architecture (reference ``mace_ictc/models/pure_cartesian_ictd_fix.py``; factory
   layer 0 has input degree 0 (paths (0,l,l)); the last product targets l = 0.
 
 Dense layers (radial MLP, channel linears, readouts) go through ``mace_hip.linear`` (one GEMM
-per layer and degree; weight gradients reduced in row blocks).
+per layer and degree; weight gradients reduced in row blocks).  The edge directions and the
+Bessel x cutoff embedding come from ``mace_hip.embedding`` (one HIP kernel per derivative order).
 
 Layouts.  Node features between blocks are the reference's flat mul_ir layout
 ``[N, C*(L+1)^2]`` (degree blocks ``[C, 2l+1]``), which the symmetric-contraction
@@ -50,6 +51,7 @@ from ictc_o3.basis.ictd_irreps import EdgeWeightedPathPreservingTensorProduct
 from ictc_o3.ops.symmetric_contraction import ICTDBridgeUSymmetricContractionSO3
 
 from .activation import silu
+from .embedding import edge_embedding
 from .geometry import edge_vectors, one_hot_rows
 from .linear import Linear, linear
 from .radial import bessel_embedding
@@ -278,11 +280,19 @@ class MaceICTC(nn.Module):
         shift_vecs = (edge_shifts.to(pos.dtype).unsqueeze(-1) * edge_cell).sum(1)
         # pos[dst] - pos[src] with a fixed-order (atomic-free) adjoint: forces are reproducible
         vec = edge_vectors(pos, edge_src, edge_dst) + shift_vecs
-        length = vec.norm(dim=1)
-        directions = vec / length.clamp(min=1e-8).unsqueeze(-1)
-        mask = (length <= self.cutoff).to(pos.dtype)
+        if vec.dtype == torch.float32 and self.cutoff_p is not None:
+            # directions and the radial embedding in one kernel per derivative order; the interaction
+            # takes no cutoff mask (its gates are exactly zero from r_max on, see Interaction.forward)
+            directions, edge_feats = edge_embedding(vec, r_max=self.cutoff, num_basis=self.num_basis,
+                                                    cutoff_p=self.cutoff_p)
+            mask = None
+        else:
+            length = vec.norm(dim=1)
+            directions = vec / length.clamp(min=1e-8).unsqueeze(-1)
+            mask = (length <= self.cutoff).to(pos.dtype)
+            edge_feats = bessel_embedding(length, r_max=self.cutoff, num_basis=self.num_basis,
+                                          cutoff_p=self.cutoff_p)
         harmonics = direction_harmonics_packed(directions, self.lmax)
-        edge_feats = bessel_embedding(length, r_max=self.cutoff, num_basis=self.num_basis, cutoff_p=self.cutoff_p)
         if species is None:
             species = self.species_index(atomic_numbers)
         # the embedding as the product one_hot(species) @ W^T (the reference's node_embedding on

@@ -415,6 +415,34 @@ int ictc_hip_edge_vector_grad(int dtype, const void* grad_vec, const int64_t* ds
                               hipStream_t stream);
 
 /*
+ * Edge embedding of the MACE interaction, one elementwise pass per derivative order.  From the
+ * edge vectors v [edges, 3] (r = |v|):
+ *   directions n = v / max(r, 1e-8)                                           [edges, 3]
+ *   embedding  emb_b = sqrt(2 / r_max) sin(b pi r / r_max) / max(r, 1e-12) u(r / r_max)
+ *              (b = 1..num_basis; u the polynomial cutoff envelope of power cutoff_p, zero
+ *              from r_max on)                                                  [edges, num_basis]
+ * Modes (f = (n, emb)):
+ *   ICTC_EMBED_VALUE: out_directions = n, out_embedding = emb
+ *   ICTC_EMBED_VJP  : out_directions = d<(grad_directions, grad_embedding), f>/dv   (either
+ *                     cotangent may be null: zero)
+ *   ICTC_EMBED_JVP  : out_directions = dn[tangent], out_embedding = demb[tangent] (either may be
+ *                     null)
+ *   ICTC_EMBED_HVP  : out_directions = d/dv <(grad_directions, grad_embedding), df[tangent]>
+ * Replaces the edge length / direction of reference mace_ictc/models/pure_cartesian_ictd_fix.py:
+ * 2935-2936 and mace_polynomial_cutoff / mace_radial_embedding (Bessel, no sqrt(num_basis)
+ * factor) of mace_ictc/models/radial_basis.py:11-92, whose library-op compositions take some
+ * twenty passes per derivative order.  num_basis <= ICTC_EMBED_MAX_BASIS, 1 <= cutoff_p <=
+ * ICTC_EMBED_MAX_POWER, r_max > 0.
+ */
+enum ictc_embed_mode { ICTC_EMBED_VALUE = 0, ICTC_EMBED_VJP = 1, ICTC_EMBED_JVP = 2, ICTC_EMBED_HVP = 3 };
+#define ICTC_EMBED_MAX_BASIS 64
+#define ICTC_EMBED_MAX_POWER 16
+int ictc_hip_edge_embedding(int mode, const float* vectors, const float* grad_directions,
+                            const float* grad_embedding, const float* tangent, float* out_directions,
+                            float* out_embedding, int num_basis, int cutoff_p, float r_max, int64_t edges,
+                            hipStream_t stream);
+
+/*
  * SiLU derivative forms of force training's double backward through the radial MLP: for the
  * first-order backward y = grad * silu'(x) and a cotangent of y, one elementwise pass over n
  * floats writes
