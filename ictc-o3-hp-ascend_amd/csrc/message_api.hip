@@ -205,7 +205,7 @@ int ictc_hip_message_forward(const ictc_tp_desc* desc, const float* node_feature
             stream);
 }
 
-int ictc_hip_message_edge_grad(const ictc_tp_desc* desc, const float* node_features, const float* bonds,
+int ictc_hip_message_edge_grad(const ictc_tp_desc* desc, const float* node_features, const float* harmonics,
                                const float* gates, const float* grad_out, const int64_t* src,
                                const int64_t* dst_rowptr, const int64_t* dst_perm,
                                float* grad_harmonics_partial, float* grad_gates, float* edge_grad_features,
@@ -214,19 +214,19 @@ int ictc_hip_message_edge_grad(const ictc_tp_desc* desc, const float* node_featu
   if (st != ICTC_OK) return st;
   if (edges == 0 || nodes_dst == 0 || (!grad_harmonics_partial && !grad_gates && !edge_grad_features))
     return ICTC_OK;
-  if (!bonds || !gates || !grad_out || !src || !dst_rowptr) return ICTC_ERR_INVALID_ARGUMENT;
+  if (!harmonics || !gates || !grad_out || !src || !dst_rowptr) return ICTC_ERR_INVALID_ARGUMENT;
   if ((grad_harmonics_partial || grad_gates) && !node_features) return ICTC_ERR_INVALID_ARGUMENT;
   if (ictc::generic_degrees(*desc))
-    return ictc::generic_msg_edge_grad(*desc, node_features, bonds, gates, grad_out, src, dst_rowptr, dst_perm,
+    return ictc::generic_msg_edge_grad(*desc, node_features, harmonics, gates, grad_out, src, dst_rowptr, dst_perm,
                                        grad_harmonics_partial, grad_gates, edge_grad_features, nodes_src,
                                        nodes_dst, stream);
   const ictc::MsgEdge fn = ictc::kMsgEdge[ictc::msg_index(desc)];
   if (fn == nullptr) return ICTC_ERR_UNSUPPORTED;
-  return fn(*desc, node_features, bonds, gates, grad_out, src, dst_rowptr, dst_perm, grad_harmonics_partial,
+  return fn(*desc, node_features, harmonics, gates, grad_out, src, dst_rowptr, dst_perm, grad_harmonics_partial,
             grad_gates, edge_grad_features, nodes_src, nodes_dst, stream);
 }
 
-int ictc_hip_message_edge_grad_static(const ictc_tp_desc* desc, const float* node_features, const float* bonds,
+int ictc_hip_message_edge_grad_static(const ictc_tp_desc* desc, const float* node_features, const float* harmonics,
                                       const float* gates, const float* grad_out, const int64_t* src,
                                       const int64_t* dst_rowptr, const int64_t* dst_perm, float* grad_harmonics,
                                       float* grad_gates, float* edge_grad_features, int64_t nodes_src,
@@ -234,7 +234,7 @@ int ictc_hip_message_edge_grad_static(const ictc_tp_desc* desc, const float* nod
   const int st = ictc::msg_common(desc, nodes_src, nodes_dst, edges);
   if (st != ICTC_OK) return st;
   if (edges == 0 || nodes_dst == 0 || (!grad_harmonics && !grad_gates && !edge_grad_features)) return ICTC_OK;
-  if (!bonds || !gates || !grad_out || !src || !dst_rowptr) return ICTC_ERR_INVALID_ARGUMENT;
+  if (!harmonics || !gates || !grad_out || !src || !dst_rowptr) return ICTC_ERR_INVALID_ARGUMENT;
   if ((grad_harmonics || grad_gates) && !node_features) return ICTC_ERR_INVALID_ARGUMENT;
   const bool generic = ictc::generic_degrees(*desc);
   const ictc::MsgEdge fn = generic ? nullptr : ictc::kMsgEdge[ictc::msg_index(desc)];
@@ -247,10 +247,10 @@ int ictc_hip_message_edge_grad_static(const ictc_tp_desc* desc, const float* nod
     const int sst = ictc::static_scratch(stream, &partial);
     if (sst != ICTC_OK) return sst;
   }
-  const int r = generic ? ictc::generic_msg_edge_grad(*desc, node_features, bonds, gates, grad_out, src, dst_rowptr,
+  const int r = generic ? ictc::generic_msg_edge_grad(*desc, node_features, harmonics, gates, grad_out, src, dst_rowptr,
                                                       dst_perm, partial, grad_gates, edge_grad_features, nodes_src,
                                                       nodes_dst, stream)
-                        : fn(*desc, node_features, bonds, gates, grad_out, src, dst_rowptr, dst_perm, partial,
+                        : fn(*desc, node_features, harmonics, gates, grad_out, src, dst_rowptr, dst_perm, partial,
                              grad_gates, edge_grad_features, nodes_src, nodes_dst, stream);
   if (r != ICTC_OK || partial == grad_harmonics) return r;
   const int64_t total = edges * ny;
@@ -279,9 +279,9 @@ int ictc_hip_message_forward_tangent(const ictc_tp_desc* desc, const float* node
             stream);
 }
 
-int ictc_hip_message_edge_grad_tangent(const ictc_tp_desc* desc, const float* node_features, const float* bonds,
+int ictc_hip_message_edge_grad_tangent(const ictc_tp_desc* desc, const float* node_features, const float* harmonics,
                                        const float* gates, const float* tangent_features,
-                                       const float* tangent_bonds, const float* tangent_gates,
+                                       const float* tangent_harmonics, const float* tangent_gates,
                                        const float* grad_out, const int64_t* src, const int64_t* dst_rowptr,
                                        const int64_t* dst_perm, float* grad_harmonics_partial, float* grad_gates,
                                        float* edge_grad_features, int64_t nodes_src, int64_t nodes_dst,
@@ -290,14 +290,14 @@ int ictc_hip_message_edge_grad_tangent(const ictc_tp_desc* desc, const float* no
   if (st != ICTC_OK) return st;
   if (edges == 0 || nodes_dst == 0 || (!grad_harmonics_partial && !grad_gates && !edge_grad_features))
     return ICTC_OK;
-  if (!node_features || !bonds || !gates || !tangent_features || !tangent_bonds || !tangent_gates || !grad_out ||
+  if (!node_features || !harmonics || !gates || !tangent_features || !tangent_harmonics || !tangent_gates || !grad_out ||
       !src || !dst_rowptr)
     return ICTC_ERR_INVALID_ARGUMENT;
   if (ictc::generic_degrees(*desc)) return ICTC_ERR_UNSUPPORTED;
   const ictc::MsgEdgeT fn = ictc::kMsgEdgeT[ictc::msg_index(desc)];
   if (fn == nullptr) return ICTC_ERR_UNSUPPORTED;
-  const ictc::MsgTangent t{tangent_features, tangent_bonds, tangent_gates};
-  return fn(*desc, node_features, bonds, gates, t, grad_out, src, dst_rowptr, dst_perm, grad_harmonics_partial,
+  const ictc::MsgTangent t{tangent_features, nullptr, tangent_gates, tangent_harmonics};
+  return fn(*desc, node_features, harmonics, gates, t, grad_out, src, dst_rowptr, dst_perm, grad_harmonics_partial,
             grad_gates, edge_grad_features, nodes_src, nodes_dst, stream);
 }
 

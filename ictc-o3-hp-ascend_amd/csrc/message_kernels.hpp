@@ -21,10 +21,11 @@
 //   * msg_forward_degree_kernel (degree sets with a bond buffer): the forward and its tangent,
 //     one launch per input degree with two channel chunks per lane;
 //   * msg_edge_grad_degree_kernel (receiver CSR, every degree set): one block per (node, channel
-//     chunks) stages the node's dout rows in LDS once and its waves split the node's edges;
-//     per edge dg, dY partials and the edge's contribution to the source-feature adjoint
-//     dxe[e] = sum_p g_p M_p^T dout[dst(e)] (so dout is never gathered per edge), in one pass
-//     per input degree (first order or tangent);
+//     chunk) contracts the node's dout rows with the CG tensors once, into LDS, and its waves
+//     split the node's edges; per edge dg, dY partials and the edge's contribution to the
+//     source-feature adjoint dxe[e] = sum_p g_p M_p^T dout[dst(e)] (so dout is never gathered
+//     per edge), from the edge's harmonics row (no bond rows), in one pass per input degree
+//     (first order or tangent);
 //   * msg_node_grad_kernel (source CSR): dx[s] = sum over the out-edges of s of dxe[e],
 //     a streaming segmented sum.
 // Node-feature gathers go through buffer descriptors spanning the whole node tensor,
@@ -277,13 +278,14 @@ __device__ __forceinline__ void bond_commit(const BondStage<NB>& s, float* __res
 // wave count is what a one-wave-per-receiver launch is limited by).
 constexpr int kMsgReduceRows = 16;
 
-// Direction of the message inputs for the tangent (JVP) kernels: x [nodes_src, NX*C], the bond
-// rows of the harmonics direction (the harmonics direction itself when the rows are built
-// in-kernel) and g [edges, NP*C]; all three are required.
+// Direction of the message inputs for the tangent (JVP) kernels: x [nodes_src, NX*C], g [edges,
+// NP*C] and the harmonics direction, as bond rows (the harmonics direction itself when the rows
+// are built in-kernel) for the forward tangent and as harmonics rows for the VJP tangent.
 struct MsgTangent {
   const float* x;
-  const float* bonds;
+  const float* bonds;   // forward tangent: the bond rows of the harmonics direction
   const float* g;
+  const float* y;       // VJP tangent: the harmonics direction [edges, (L_e+1)^2]
 };
 
 // JVP = true computes the directional derivative of the message in direction t:
@@ -754,237 +756,271 @@ int launch_msg_forward_tangent(const ictc_tp_desc& d, const float* x, const floa
 }
 
 // ----------------------------------------------------------------------------- VJP by degree
-// VJP in one pass per input degree l1, for every degree set (bond rows from the buffer or, for
-// small sets, formed in-kernel from the harmonics as the one-degree kernels do) (the groups of
-// msg_forward_degree_kernel: each owns the x rows of degree l1, its paths' gates, bond entries
-// and dout rows, and so its dg columns and dxe rows).  Per edge and path, with
-// w_I = sum_K M[K][I] dout_K (one LDS bond broadcast per (K, I), shared by the lane's CPL channels):
-//   dg_p   = sum_I x_I w_I                        (= sum_K dout_K sum_I x_I M[K][I])
-//   dxe_I += g_p w_I
-//   dY_j  += s_p sum_{I,K} C_p[I, j, K] (sum over the lane's channels of x_I g_p dout_K)
-// so the gates and bond rows are read once for all three outputs (the one-degree kernels read
-// them once in the dg/dY pass and again in the dxe pass).  JVP = true gives the directional
-// derivative of all three in direction t = (tx, tM, tg) with dout fixed (the mixed second
-// derivatives; tw_I = sum_K tM[K][I] dout_K):
-//   dg_p = sum_I (tx_I w_I + x_I tw_I),  dxe_I += g_p tw_I + tg_p w_I,  x_I g_p -> tx_I g_p + x_I tg_p in dY.
-// dY partials: group launches run in order on one stream; the first writes a block's channel sum
-// into the slot of its first chunk (and zero into its second), later groups add to it (a fixed
-// order).
-template <int LIN, int LE, int LOUT, int L1, int CPL, bool JVP>
+// VJP in one pass per input degree l1 (the groups of msg_forward_degree_kernel: each owns the x rows
+// of degree l1, its paths' gates and dout rows, and so its dg columns and dxe rows).  With the bond
+// matrices M_p[K][I] = s_p sum_J Y_{l2^2 + J} C_p[I, J, K] the per-edge, per-path adjoints are
+//   w_I = sum_K M[K][I] dout_K,  dg_p = sum_I x_I w_I,  dxe_I += g_p w_I,
+//   dY_{l2^2 + J} += s_p sum_{I,K} C_p[I, J, K] x_I g_p dout_K   (summed over the channels).
+// For receiver n the factor U_p[I][J] = s_p sum_K C_p[I, J, K] dout_n[K] is the same for every edge
+// into n: built once per block in LDS, it turns both contractions into ni * nj products per channel,
+//   w_I = sum_J Y_{l2^2 + J} U_p[I][J],  v_J = sum_I x_I U_p[I][J],
+//   dg_p = sum_J Y_{l2^2 + J} v_J,  dY_{l2^2 + J} += g_p v_J,
+// where the bond form costs ni * no for w and ni * no * nj (shared by the lane's channels) for the
+// harmonics partials, and each edge needs its harmonics row instead of its bond row (measured at
+// C = 128, lmax 3, 105,634 edges: 1.07 -> 1.01 ms for the four launches, the tangent 1.57 -> 1.33 ms;
+// C = 64, lmax 2, 855,792 edges: 1.82 -> 1.66 and 2.32 -> 2.11 ms; outputs within 2.5e-7
+// relative).  JVP = true gives the directional derivative of all three in direction
+// t = (tx, tY, tg) with dout fixed (the mixed second derivatives): tw_I = sum_J tY_{l2^2 + J} U_p[I][J],
+//   dg_p = sum_I (tx_I w_I + x_I tw_I),  dxe_I += g_p tw_I + tg_p w_I,
+//   dY_{l2^2 + J} += sum_I (tx_I g_p + x_I tg_p) U_p[I][J].
+// One block per (receiver, 64-channel chunk); path k's U block is built by wave k mod 4, then every
+// wave walks every fourth edge of the receiver.  dY partials [edges, chunks, NY]: group launches run
+// in order on one stream; the first writes each (edge, chunk) slot, later groups add to it (a fixed
+// order; the caller sums the chunk axis).
+struct NodeU {
+  int nu = 0;
+  int off[ICTC_MAX_PATHS] = {};   // first U entry of each path of the group
+};
+
+template <int LIN, int LE, int LOUT, int L1>
+constexpr NodeU make_node_u() {
+  NodeU u{};
+  constexpr DegreeGroup GT = DegreeGroupOf<LIN, LE, LOUT, L1>::tab;
+  constexpr PathTable pt = Paths<LIN, LE, LOUT>::tab;
+  for (int k = 0; k < GT.np; ++k) {
+    u.off[k] = u.nu;
+    u.nu += GT.nx * (2 * pt.l2[GT.path[k]] + 1);
+  }
+  return u;
+}
+
+template <int LIN, int LE, int LOUT, int L1>
+struct NodeUOf {
+  static constexpr NodeU tab = make_node_u<LIN, LE, LOUT, L1>();
+};
+
+template <int LIN, int LE, int LOUT, int L1, bool JVP>
 __global__ void __launch_bounds__(kMsgBlock)
-msg_edge_grad_degree_kernel(const float* __restrict__ x, const float* __restrict__ bonds,
-                            const float* __restrict__ g, const MsgTangent t, const float* __restrict__ go,
-                            const int64_t* __restrict__ src, const int64_t* __restrict__ rowptr,
-                            const int64_t* __restrict__ perm, float* __restrict__ dyp, float* __restrict__ dg,
-                            float* __restrict__ dxe, const ictc_tp_desc d, int64_t nodes_src, int nblk,
-                            int nchunks, int first) {
+msg_edge_grad_degree_kernel(const float* __restrict__ x, const float* __restrict__ y, const float* __restrict__ g,
+                          const MsgTangent t, const float* __restrict__ go, const int64_t* __restrict__ src,
+                          const int64_t* __restrict__ rowptr, const int64_t* __restrict__ perm,
+                          float* __restrict__ dyp, float* __restrict__ dg, float* __restrict__ dxe,
+                          const ictc_tp_desc d, int64_t nodes_src, int nchunks, int first) {
   using PS = Paths<LIN, LE, LOUT>;
   constexpr DegreeGroup GT = DegreeGroupOf<LIN, LE, LOUT, L1>::tab;
-  constexpr int NX = PS::NX, NY = PS::NY, NP = PS::N, NOCF = PS::NOC, NBF = PS::NB;
-  constexpr int NPG = GT.np, NOC = GT.noc, NBG = GT.nb, NI = GT.nx;
-  constexpr int NV = (NBG + kWave - 1) / kWave;
+  constexpr NodeU UT = NodeUOf<LIN, LE, LOUT, L1>::tab;
+  constexpr int NX = PS::NX, NY = PS::NY, NP = PS::N, NOCF = PS::NOC;
+  constexpr int NPG = GT.np, NI = GT.nx, NU = UT.nu;
   constexpr int NT = JVP ? 2 : 1;   // input sets per edge: primal (+ direction)
   static_assert(NPG > 0, "an input degree without paths has no launch");
-  __shared__ float sB[kMsgWaves][NT][NV * kWave];
-  __shared__ float sO[NOC][CPL * kWave];   // the group's dout rows of the node, for the block's chunks
+  static_assert(NU * kWave * 4 <= 65536, "the node contraction table exceeds 64 KiB of LDS");
+  __shared__ float sU[NU * kWave];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const uint32_t item = xcd_block(blockIdx.x, gridDim.x);   // receivers contiguous per XCD
-  const int64_t node = static_cast<int64_t>(item) / nblk;
-  const int chunk0 = static_cast<int>(item - node * nblk) * CPL;
+  const int64_t node = static_cast<int64_t>(item) / nchunks;
+  const int chunk = static_cast<int>(item - node * nchunks);
   const int C = d.channels;
   const uint32_t row = static_cast<uint32_t>(C) * 4u;
-  bool live[CPL];
-  uint32_t vc[CPL];   // lanes past C read channel 0, zero it and store nothing
-#pragma unroll
-  for (int h = 0; h < CPL; ++h) {
-    const int c = (chunk0 + h) * kWave + lane;
-    live[h] = c < C;
-    vc[h] = static_cast<uint32_t>(live[h] ? c : 0) * 4u;
-  }
+  const int c = chunk * kWave + lane;
+  const bool live = c < C;
+  const uint32_t vc = static_cast<uint32_t>(live ? c : 0) * 4u;   // lanes past C read channel 0, zero it
   {
     const rsrc_t ron = make_rsrc(go + node * NOCF * C, NOCF * row);
-    for (int r = wave; r < NOC; r += kMsgWaves) {
-      const uint32_t soff = static_cast<uint32_t>(kDegreeGroup<LIN, LE, LOUT, L1>.rowmap[r]) * row;
-#pragma unroll
-      for (int h = 0; h < CPL; ++h) {
-        const float v = buf_load_vs<kNonTemporal>(ron, vc[h], soff);
-        sO[r][h * kWave + lane] = live[h] ? v : 0.f;
+    static_for<0, NPG>([&](auto Q) {
+      constexpr int k = Q;
+      if (wave == k % kMsgWaves) {   // wave-uniform
+        constexpr int p = GT.path[k];
+        constexpr int l2 = PS::tab.l2[p], l3 = PS::tab.l3[p];
+        constexpr int nj = 2 * l2 + 1, no = 2 * l3 + 1, oo = GT.out[k], uo = UT.off[k];
+        using CG = CGTab<L1, l2, l3>;
+        float ov[no];
+        static_for<0, no>([&](auto K) {
+          constexpr uint32_t r = static_cast<uint32_t>(GT.rowmap[oo + K]);
+          const float v = buf_load_vs<kNonTemporal>(ron, vc, r * row);
+          ov[K] = live ? v : 0.f;
+        });
+        const float sc = d.scale[p];
+        static_for<0, NI>([&](auto I) {
+          static_for<0, nj>([&](auto J) {
+            float u = 0.f;
+            static_for<0, no>([&](auto K) {
+              constexpr float cg = CG::v[(I * nj + J) * no + K];
+              if constexpr (cg != 0.0f) u = fmaf(cg, ov[K], u);
+            });
+            sU[(uo + I * nj + J) * kWave + lane] = sc * u;
+          });
+        });
       }
-    }
+    });
   }
   __syncthreads();
   const uint32_t xbytes = static_cast<uint32_t>(nodes_src * NX * row);
   const bool xdep = JVP || dg != nullptr || dyp != nullptr;   // the plain dxe needs no x
   const rsrc_t rx[2] = {make_rsrc(xdep ? x : nullptr, xbytes), make_rsrc(JVP ? t.x : nullptr, xbytes)};
   const float* gs[2] = {g, t.g};
-  const float* bsrc[2] = {bonds, t.bonds};
-  // the lane's bond entries lane + 64 r of the group: their byte offsets in a bond row, or (rows
-  // formed in-kernel) their projection coefficients s_p C_p[i, j - l2^2, k] (zero past the group)
-  constexpr bool INL = BondInline<LIN, LE, LOUT>::value;
-  uint32_t boff[NV];
-  float cf[INL ? NV : 1][INL ? NY : 1];
-#pragma unroll
-  for (int r = 0; r < NV; ++r) {
-    const int idx = lane + r * kWave;
-    const int ge = idx < NBG ? kDegreeGroup<LIN, LE, LOUT, L1>.bidx[idx] : 0;
-    boff[r] = static_cast<uint32_t>(ge) * 4u;
-    if constexpr (INL) {
-      const BondDense<LIN, LE, LOUT>& bt = kBondDense<LIN, LE, LOUT>;
-      const float sc = idx < NBG ? d.scale[bt.path[ge]] : 0.f;
-#pragma unroll
-      for (int j = 0; j < NY; ++j) cf[r][j] = bt.cg[ge][j] * sc;
-    }
-  }
-  const int64_t s0 = rowptr[node], s1 = rowptr[node + 1];
-#pragma clang loop unroll(disable)
-  for (int64_t slot = s0 + wave; slot < s1; slot += kMsgWaves) {
-    const int64_t e = perm ? perm[slot] : slot;
-    float bv[NT][NV], xr[NT][CPL][NI], gv[NT][CPL][NPG];
-#pragma unroll
-    for (int q = 0; q < NT; ++q) {   // bond entries first (staged into LDS below)
-      if constexpr (INL) {   // from the harmonics row: one load, broadcast from lanes 0..NY-1
-        const float yl = bsrc[q][e * NY + (lane < NY ? lane : NY - 1)];
-        float yv[NY];
-#pragma unroll
-        for (int j = 0; j < NY; ++j)
-          yv[j] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, yl), j));
-#pragma unroll
-        for (int r = 0; r < NV; ++r) {
-          float acc = 0.f;
-#pragma unroll
-          for (int j = 0; j < NY; ++j) acc = fmaf(yv[j], cf[r][j], acc);
-          bv[q][r] = acc;
-        }
-      } else {
-        const rsrc_t rb = make_rsrc(bsrc[q] + e * NBF, NBF * 4u);
-#pragma unroll
-        for (int r = 0; r < NV; ++r) bv[q][r] = buf_load<1>(rb, boff[r]).v[0];
-      }
-    }
-    const uint32_t xoff = static_cast<uint32_t>(src[e]) * NX * row;
+  const float* ys[2] = {y, t.y};
+  const bool wy = dyp != nullptr;
+  using WS = WaveSums<NY>;
+  const int wj = WS::index(lane);   // the harmonic whose channel sum this lane ends up holding
+  const bool wown = wy && WS::owner(lane) && wj < NY;
+  const int wjc = wj < NY ? wj : NY - 1;
+  // One edge's inputs: its harmonics rows (wave-uniform loads), the source features of degree l1,
+  // the group's gates and the harmonics partial that earlier degree launches left in the slot.
+  struct EdgeIn {
+    float yv[NT][NY];
+    float xr[NT][NI];
+    float gv[NT][NPG];
+    float prev;
+  };
+  auto fetch = [&](int64_t e, int64_t s, EdgeIn& in) {
 #pragma unroll
     for (int q = 0; q < NT; ++q)
 #pragma unroll
-      for (int h = 0; h < CPL; ++h)
+      for (int j = 0; j < NY; ++j) in.yv[q][j] = ys[q][e * NY + j];
+    const uint32_t xoff = static_cast<uint32_t>(s) * NX * row;
 #pragma unroll
-        for (int m = 0; m < NI; ++m) {
-          const float v = buf_load_vs(rx[q], xoff + vc[h], (L1 * L1 + m) * row);
-          xr[q][h][m] = live[h] ? v : 0.f;
-        }
+    for (int q = 0; q < NT; ++q)
+#pragma unroll
+      for (int m = 0; m < NI; ++m) {
+        const float v = buf_load_vs(rx[q], xoff + vc, (L1 * L1 + m) * row);
+        in.xr[q][m] = live ? v : 0.f;
+      }
 #pragma unroll
     for (int q = 0; q < NT; ++q) {
       const rsrc_t rg = make_rsrc(gs[q] + e * NP * C, NP * row);
 #pragma unroll
-      for (int h = 0; h < CPL; ++h)
-#pragma unroll
-        for (int k = 0; k < NPG; ++k) gv[q][h][k] = buf_load_vs<kNonTemporal>(rg, vc[h], GT.path[k] * row);
+      for (int k = 0; k < NPG; ++k) in.gv[q][k] = buf_load_vs<kNonTemporal>(rg, vc, GT.path[k] * row);
     }
-#pragma unroll
-    for (int q = 0; q < NT; ++q)
-#pragma unroll
-      for (int r = 0; r < NV; ++r) sB[wave][q][lane + r * kWave] = bv[q][r];
-    wave_lds_sync();
+    in.prev = (wy && !first) ? dyp[(e * nchunks + chunk) * NY + wjc] : 0.f;
+  };
+  auto compute = [&](int64_t e, const EdgeIn& in) {
     const rsrc_t rdg = make_rsrc(dg ? dg + e * NP * C : nullptr, NP * row);
-    float dyl[NY], dxl[CPL][NI];
+    float dyl[NY], dxl[NI];
 #pragma unroll
     for (int j = 0; j < NY; ++j) dyl[j] = 0.f;
 #pragma unroll
-    for (int h = 0; h < CPL; ++h)
-#pragma unroll
-      for (int m = 0; m < NI; ++m) dxl[h][m] = 0.f;
+    for (int m = 0; m < NI; ++m) dxl[m] = 0.f;
     static_for<0, NPG>([&](auto Q) {
       constexpr int k = Q;
       constexpr int p = GT.path[k];
-      constexpr int l2 = PS::tab.l2[p], l3 = PS::tab.l3[p];
-      constexpr int ni = NI, nj = 2 * l2 + 1, no = 2 * l3 + 1;
-      constexpr int bo = GT.bond[k], oo = GT.out[k];
-      using CG = CGTab<L1, l2, l3>;
-      const float* bp = opaque_lds_row(&sB[wave][0][bo]);
-      const float* tp = JVP ? opaque_lds_row(&sB[wave][NT - 1][bo]) : bp;
+      constexpr int l2 = PS::tab.l2[p];
+      constexpr int nj = 2 * l2 + 1, uo = UT.off[k];
+      const float* up = opaque_lds_row(sU + uo * kWave);
       __builtin_amdgcn_sched_barrier(0);
-      float w[CPL][ni], tw[CPL][ni];
+      float w[NI], tw[NI];
 #pragma unroll
-      for (int h = 0; h < CPL; ++h)
+      for (int i = 0; i < NI; ++i) w[i] = tw[i] = 0.f;
+      float dgv = 0.f;
+      if constexpr (JVP) {
+        // harmonics partials from xg_I = tx_I g_p + x_I tg_p
+        auto contract = [&](auto WY) {
+          float xg[NI], part[nj];
+          if constexpr (WY) {
 #pragma unroll
-        for (int i = 0; i < ni; ++i) w[h][i] = tw[h][i] = 0.f;
-      static_for<0, no>([&](auto K) {
-        float ov[CPL];
+            for (int i = 0; i < NI; ++i) xg[i] = fmaf(in.xr[1][i], in.gv[0][k], in.xr[0][i] * in.gv[1][k]);
 #pragma unroll
-        for (int h = 0; h < CPL; ++h) ov[h] = sO[oo + K][h * kWave + lane];
-        static_for<0, ni>([&](auto I) {
-          const float b = bp[K * ni + I];
-          const float tb = JVP ? tp[K * ni + I] : 0.f;
-#pragma unroll
-          for (int h = 0; h < CPL; ++h) {
-            w[h][I] = fmaf(b, ov[h], w[h][I]);
-            if constexpr (JVP) tw[h][I] = fmaf(tb, ov[h], tw[h][I]);
+            for (int j = 0; j < nj; ++j) part[j] = 0.f;
           }
-        });
-      });
-#pragma unroll
-      for (int h = 0; h < CPL; ++h) {
-        float dgv = 0.f;
-#pragma unroll
-        for (int i = 0; i < ni; ++i) {
-          if constexpr (JVP) {
-            dgv = fmaf(xr[1][h][i], w[h][i], dgv);
-            dgv = fmaf(xr[0][h][i], tw[h][i], dgv);
-            dxl[h][i] = fmaf(gv[0][h][k], tw[h][i], dxl[h][i]);
-            dxl[h][i] = fmaf(gv[1][h][k], w[h][i], dxl[h][i]);
-          } else {
-            dgv = fmaf(xr[0][h][i], w[h][i], dgv);
-            dxl[h][i] = fmaf(gv[0][h][k], w[h][i], dxl[h][i]);
-          }
-        }
-        buf_store_lane(rdg, live[h], vc[h] + p * row, dgv);   // null dg: empty descriptor
-      }
-      if (dyp != nullptr) {
-        float part[nj];
-#pragma unroll
-        for (int j = 0; j < nj; ++j) part[j] = 0.f;
-        static_for<0, ni>([&](auto I) {
-          float xg[CPL];
-#pragma unroll
-          for (int h = 0; h < CPL; ++h)
-            xg[h] = JVP ? fmaf(xr[1][h][I], gv[0][h][k], xr[0][h][I] * gv[1][h][k]) : xr[0][h][I] * gv[0][h][k];
-          static_for<0, no>([&](auto K) {
-            float tt = xg[0] * sO[oo + K][lane];
-#pragma unroll
-            for (int h = 1; h < CPL; ++h) tt = fmaf(xg[h], sO[oo + K][h * kWave + lane], tt);
+          static_for<0, NI>([&](auto I) {
+            __builtin_amdgcn_sched_barrier(0);   // one row of U in registers at a time
             static_for<0, nj>([&](auto J) {
-              constexpr float cg = CG::v[(I * nj + J) * no + K];
-              if constexpr (cg != 0.0f) part[J] = fmaf(cg, tt, part[J]);
+              const float u = up[(I * nj + J) * kWave + lane];
+              w[I] = fmaf(in.yv[0][l2 * l2 + J], u, w[I]);
+              tw[I] = fmaf(in.yv[1][l2 * l2 + J], u, tw[I]);
+              if constexpr (WY) part[J] = fmaf(xg[I], u, part[J]);
             });
           });
-        });
-        const float sc = d.scale[p];
+          if constexpr (WY) {
 #pragma unroll
-        for (int j = 0; j < nj; ++j) dyl[l2 * l2 + j] = fmaf(sc, part[j], dyl[l2 * l2 + j]);
+            for (int j = 0; j < nj; ++j) dyl[l2 * l2 + j] += part[j];
+          }
+        };
+        if (wy)
+          contract(Int<1>{});
+        else
+          contract(Int<0>{});
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+          dgv = fmaf(in.xr[1][i], w[i], dgv);
+          dgv = fmaf(in.xr[0][i], tw[i], dgv);
+          dxl[i] = fmaf(in.gv[0][k], tw[i], dxl[i]);
+          dxl[i] = fmaf(in.gv[1][k], w[i], dxl[i]);
+        }
+      } else {
+        // with v_J = sum_I x_I U[I][J]: dg_p = sum_J Y_J v_J and the partials are g_p v_J
+        auto contract = [&](auto WY) {
+          float v[nj];
+          if constexpr (WY) {
+#pragma unroll
+            for (int j = 0; j < nj; ++j) v[j] = 0.f;
+          }
+          static_for<0, NI>([&](auto I) {
+            __builtin_amdgcn_sched_barrier(0);   // one row of U in registers at a time
+            static_for<0, nj>([&](auto J) {
+              const float u = up[(I * nj + J) * kWave + lane];
+              w[I] = fmaf(in.yv[0][l2 * l2 + J], u, w[I]);
+              if constexpr (WY) v[J] = fmaf(in.xr[0][I], u, v[J]);
+            });
+          });
+          if constexpr (WY) {
+#pragma unroll
+            for (int j = 0; j < nj; ++j) {
+              dgv = fmaf(in.yv[0][l2 * l2 + j], v[j], dgv);
+              dyl[l2 * l2 + j] = fmaf(in.gv[0][k], v[j], dyl[l2 * l2 + j]);
+            }
+          } else {
+#pragma unroll
+            for (int i = 0; i < NI; ++i) dgv = fmaf(in.xr[0][i], w[i], dgv);
+          }
+        };
+        if (wy)
+          contract(Int<1>{});
+        else
+          contract(Int<0>{});
+#pragma unroll
+        for (int i = 0; i < NI; ++i) dxl[i] = fmaf(in.gv[0][k], w[i], dxl[i]);
       }
+      buf_store_lane(rdg, live, vc + p * row, dgv);   // null dg: empty descriptor
     });
     if (dxe != nullptr) {
       const rsrc_t rde = make_rsrc(dxe + e * NX * C, NX * row);
 #pragma unroll
-      for (int h = 0; h < CPL; ++h)
-#pragma unroll
-        for (int m = 0; m < NI; ++m) buf_store_lane(rde, live[h], vc[h] + (L1 * L1 + m) * row, dxl[h][m]);
+      for (int m = 0; m < NI; ++m) buf_store_lane(rde, live, vc + (L1 * L1 + m) * row, dxl[m]);
     }
-    if (dyp != nullptr) {   // channel sums of the NY partials, one transposing butterfly
-      using WS = WaveSums<NY>;
+    if (wy) {   // channel sums of the NY partials, one transposing butterfly
       const float tot = WS::reduce(dyl, lane);
-      const int j = WS::index(lane);
-      if (WS::owner(lane) && j < NY) {
-        float* q = dyp + (e * nchunks + chunk0) * NY + j;
-        if (first) {
-          q[0] = tot;
-#pragma unroll
-          for (int h = 1; h < CPL; ++h)
-            if (chunk0 + h < nchunks) q[h * NY] = 0.f;
-        } else {
-          q[0] += tot;
-        }
+      if (wown) dyp[(e * nchunks + chunk) * NY + wj] = in.prev + tot;
+    }
+  };
+  // Software pipeline over the receiver's edges: the next edge's index and source (and, where the
+  // registers allow, its loads) are requested before the current edge is computed and stored.
+  constexpr bool kPrefetch = !JVP || L1 == 0;
+  const int64_t s0 = rowptr[node], s1 = rowptr[node + 1];
+  int64_t slot = s0 + wave;
+  if (slot < s1) {
+    int64_t e = perm ? perm[slot] : slot;
+    EdgeIn cur;
+    fetch(e, src[e], cur);
+#pragma clang loop unroll(disable)
+    for (;;) {
+      const int64_t nslot = slot + kMsgWaves;
+      const bool more = nslot < s1;
+      int64_t ne = e, ns = 0;
+      EdgeIn nxt;
+      if (more) {
+        ne = perm ? perm[nslot] : nslot;
+        ns = src[ne];
+        if constexpr (kPrefetch) fetch(ne, ns, nxt);
       }
+      compute(e, cur);
+      if (!more) break;
+      slot = nslot;
+      e = ne;
+      if constexpr (kPrefetch)
+        cur = nxt;
+      else
+        fetch(e, ns, cur);
     }
   }
 }
@@ -1005,34 +1041,20 @@ msg_zero_rows_kernel(const int64_t* __restrict__ rowptr, int64_t nodes_dst, floa
   }
 }
 
-// One launch per input degree that has paths (dY partials accumulated across them in launch
-// order); two chunks per lane when the channels span two, except for the tangent passes of the
-// groups l1 >= 2, whose doubled inputs need 196-256 VGPRs at two chunks (one or two waves per
-// SIMD): one chunk per lane there, 126-165 VGPRs (measured at C = 128, lmax 3: 741 / 893 us at
-// two chunks, 517 / 609 us at one).
+// One launch per input degree that has paths (dY partials accumulated across them in launch order).
 template <int LIN, int LE, int LOUT, bool JVP>
-int launch_msg_edge_grad_degrees(const ictc_tp_desc& d, const float* x, const float* bonds, const float* g,
+int launch_msg_edge_grad_degrees(const ictc_tp_desc& d, const float* x, const float* y, const float* g,
                                  const MsgTangent& t, const float* go, const int64_t* src, const int64_t* rowptr,
                                  const int64_t* perm, float* dyp, float* dg, float* dxe, int64_t nodes_src,
                                  int64_t nodes_dst, hipStream_t stream) {
   const int nchunks = (d.channels + kWave - 1) / kWave;
+  const dim3 grid(static_cast<unsigned>(nodes_dst * nchunks));   // one block per (receiver, chunk)
   int first = 1;
   auto one = [&](auto deg) {
     constexpr int L1 = decltype(deg)::value;
-    constexpr DegreeGroup GT = DegreeGroupOf<LIN, LE, LOUT, L1>::tab;
-    if constexpr (GT.np > 0) {
-      constexpr bool kOneChunk = JVP && L1 >= 2;
-      const bool two = !kOneChunk && nchunks >= 2;
-      const int nblk = two ? (nchunks + 1) / 2 : nchunks;
-      const dim3 grid(static_cast<unsigned>(nodes_dst * nblk));
-      if (two)
-        hipLaunchKernelGGL((msg_edge_grad_degree_kernel<LIN, LE, LOUT, L1, 2, JVP>), grid, dim3(kMsgBlock), 0,
-                           stream, x, bonds, g, t, go, src, rowptr, perm, dyp, dg, dxe, d, nodes_src, nblk, nchunks,
-                           first);
-      else
-        hipLaunchKernelGGL((msg_edge_grad_degree_kernel<LIN, LE, LOUT, L1, 1, JVP>), grid, dim3(kMsgBlock), 0,
-                           stream, x, bonds, g, t, go, src, rowptr, perm, dyp, dg, dxe, d, nodes_src, nblk, nchunks,
-                           first);
+    if constexpr (DegreeGroupOf<LIN, LE, LOUT, L1>::tab.np > 0) {
+      hipLaunchKernelGGL((msg_edge_grad_degree_kernel<LIN, LE, LOUT, L1, JVP>), grid, dim3(kMsgBlock), 0, stream, x,
+                         y, g, t, go, src, rowptr, perm, dyp, dg, dxe, d, nodes_src, nchunks, first);
       first = 0;
     }
   };
@@ -1057,21 +1079,22 @@ int launch_msg_edge_grad_degrees(const ictc_tp_desc& d, const float* x, const fl
   return msg_launch_status();
 }
 
+// y: the harmonics [edges, (L_e+1)^2]; t.y the harmonics direction of the tangent pass
 template <int LIN, int LE, int LOUT>
-int launch_msg_edge_grad(const ictc_tp_desc& d, const float* x, const float* bonds, const float* g,
+int launch_msg_edge_grad(const ictc_tp_desc& d, const float* x, const float* y, const float* g,
                          const float* go, const int64_t* src, const int64_t* rowptr, const int64_t* perm,
                          float* dyp, float* dg, float* dxe, int64_t nodes_src, int64_t nodes_dst,
                          hipStream_t stream) {
-  return launch_msg_edge_grad_degrees<LIN, LE, LOUT, false>(d, x, bonds, g, MsgTangent{}, go, src, rowptr, perm, dyp,
-                                                           dg, dxe, nodes_src, nodes_dst, stream);
+  return launch_msg_edge_grad_degrees<LIN, LE, LOUT, false>(d, x, y, g, MsgTangent{}, go, src, rowptr, perm, dyp, dg,
+                                                           dxe, nodes_src, nodes_dst, stream);
 }
 
 template <int LIN, int LE, int LOUT>
-int launch_msg_edge_grad_tangent(const ictc_tp_desc& d, const float* x, const float* bonds, const float* g,
+int launch_msg_edge_grad_tangent(const ictc_tp_desc& d, const float* x, const float* y, const float* g,
                                  const MsgTangent& t, const float* go, const int64_t* src, const int64_t* rowptr,
                                  const int64_t* perm, float* dyp, float* dg, float* dxe, int64_t nodes_src,
                                  int64_t nodes_dst, hipStream_t stream) {
-  return launch_msg_edge_grad_degrees<LIN, LE, LOUT, true>(d, x, bonds, g, t, go, src, rowptr, perm, dyp, dg, dxe,
+  return launch_msg_edge_grad_degrees<LIN, LE, LOUT, true>(d, x, y, g, t, go, src, rowptr, perm, dyp, dg, dxe,
                                                           nodes_src, nodes_dst, stream);
 }
 

@@ -7,9 +7,10 @@ The map is trilinear in (node features x, edge harmonics Y, edge gates g) for a
 fixed graph, so its VJP and every mixed derivative reuse the same three kernels
 with substituted operands (as for the plain TP):
 
-    bonds     : msg_bond     (per-edge bond matrices from Y, once per edge)
+    bonds     : msg_bond     (per-edge bond matrices from Y, once per edge; forward only)
     forward   : msg_forward  (receiver CSR, per-node register accumulation)
-    dY, dg    : msg_edge_grad (receiver CSR, dout[n] in registers, x[src] gathered)
+    dY, dg    : msg_edge_grad (receiver CSR, dout[n] contracted with the CG tensors once
+                per receiver, x[src] gathered, Y read per edge)
     dx        : msg_edge_grad writes each edge's feature adjoint, msg_node_grad sums
                 them per source node (source CSR), so dout is never gathered per edge
 
@@ -135,12 +136,11 @@ def _forward_raw(plan: TensorProductPlan, graph: MessageGraph, x, y, g, bonds=No
     return out
 
 
-def _backward_raw(plan: TensorProductPlan, graph: MessageGraph, need, x, y, g, go, bonds=None):
+def _backward_raw(plan: TensorProductPlan, graph: MessageGraph, need, x, y, g, go):
+    """First-order adjoints; the edge kernels read the harmonics y (not bond rows)."""
     dev = go.device
     lib = _lib.lib()
     stream = _lib.stream_of(dev)
-    if bonds is None:
-        bonds = _bonds(plan, graph, y)
     dx = dy = dg = None
     dyp = dxe = None
     if graph.edges:
@@ -154,7 +154,7 @@ def _backward_raw(plan: TensorProductPlan, graph: MessageGraph, need, x, y, g, g
         if need[0] or need[1] or need[2]:
             xp = x.data_ptr() if (need[1] or need[2]) else None
             _lib.check(lib.ictc_hip_message_edge_grad(
-                ctypes.byref(plan.desc), xp, _p(bonds), _p(g), go.data_ptr(), graph.src.data_ptr(),
+                ctypes.byref(plan.desc), xp, _p(y), _p(g), go.data_ptr(), graph.src.data_ptr(),
                 graph.rowptr_dst.data_ptr(), _p(graph.perm_dst), _p(dyp), _p(dg), _p(dxe), graph.nodes_src,
                 graph.nodes_dst, graph.edges, stream), "ictc_hip_message_edge_grad")
         if dyp is not None:
@@ -181,11 +181,11 @@ def _second_order_raw(plan: TensorProductPlan, graph: MessageGraph, need, x, y, 
     dev = go.device
     lib = _lib.lib()
     stream = _lib.stream_of(dev)
-    if bonds is None:
-        bonds = _bonds(plan, graph, y)
-    tbonds = _bonds(plan, graph, ty)
     gx = gy = gg = ggo = None
-    if no:
+    if no:   # the forward tangent reads bond rows, the edge tangent pass the harmonics
+        if bonds is None:
+            bonds = _bonds(plan, graph, y)
+        tbonds = _bonds(plan, graph, ty)
         ggo = torch.empty(graph.nodes_dst, plan.full_out_width, device=dev, dtype=torch.float32)
         _lib.check(lib.ictc_hip_message_forward_tangent(
             ctypes.byref(plan.desc), x.data_ptr(), _p(bonds), _p(g), tx.data_ptr(), _p(tbonds), _p(tg),
@@ -197,7 +197,7 @@ def _second_order_raw(plan: TensorProductPlan, graph: MessageGraph, need, x, y, 
     dxe = torch.empty(graph.edges, plan.x_width, device=dev, dtype=torch.float32) if nx else None
     if nx or ny or ng:
         _lib.check(lib.ictc_hip_message_edge_grad_tangent(
-            ctypes.byref(plan.desc), x.data_ptr(), _p(bonds), _p(g), tx.data_ptr(), _p(tbonds), _p(tg),
+            ctypes.byref(plan.desc), x.data_ptr(), _p(y), _p(g), tx.data_ptr(), _p(ty), _p(tg),
             go.data_ptr(), graph.src.data_ptr(), graph.rowptr_dst.data_ptr(), _p(graph.perm_dst), _p(dyp),
             _p(gg), _p(dxe), graph.nodes_src, graph.nodes_dst, graph.edges, stream),
             "ictc_hip_message_edge_grad_tangent")
@@ -251,11 +251,9 @@ class _Backward(torch.autograd.Function):
     def forward(ctx, plan, graph, need, x, y, g, go, bonds=None):
         ctx.plan, ctx.graph, ctx.need = plan, graph, need
         ctx.set_materialize_grads(False)
-        if bonds is None:
-            bonds = _bonds(plan, graph, y)
-        ctx.bonds = bonds
+        ctx.bonds = bonds   # for the forward passes of the double backward (formed there if None)
         ctx.save_for_backward(x, y, g, go)
-        outs = _backward_raw(plan, graph, need, x, y, g, go, bonds)
+        outs = _backward_raw(plan, graph, need, x, y, g, go)
         empty = go.new_empty(0)
         outs = tuple(t if t is not None else empty for t in outs)
         for t, n in zip(outs, need):
@@ -307,7 +305,7 @@ def vjp(plan, graph, need, x, y, g, go, bonds=None):
     if not any(need):
         return None, None, None
     if not torch.is_grad_enabled():       # nothing recorded: skip the autograd Function
-        return _backward_raw(plan, graph, need, x, y, g, go, bonds)
+        return _backward_raw(plan, graph, need, x, y, g, go)
     outs = _Backward.apply(plan, graph, need, x, y, g, go, bonds)
     return tuple(o if n else None for o, n in zip(outs, need))
 

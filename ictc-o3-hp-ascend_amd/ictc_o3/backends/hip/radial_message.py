@@ -133,13 +133,13 @@ def _backward_raw(plan, graph, ranges: RangePlan, need, x, y, hidden, weight, bi
         if rows == 0:
             continue
         g = _range_gates(hidden, weight, bias, mask, s0, s1)
-        bonds = _range_bonds(plan, y, s0, s1)
+        yr = y[s0:s1]   # the edge kernels read the harmonics rows
         dyp = torch.empty(rows, nch, plan.y_width, device=dev, dtype=torch.float32) if ny else None
         dg = torch.empty(rows, plan.full_gate_width, device=dev, dtype=torch.float32) if need_dg else None
         dxe = torch.empty(rows, plan.x_width, device=dev, dtype=torch.float32) if nx else None
         go_r = go[n0:n1]
         _lib.check(lib.ictc_hip_message_edge_grad(
-            ctypes.byref(plan.desc), x.data_ptr() if (ny or need_dg) else None, bonds.data_ptr(), g.data_ptr(),
+            ctypes.byref(plan.desc), x.data_ptr() if (ny or need_dg) else None, yr.data_ptr(), g.data_ptr(),
             go_r.data_ptr(), ranges.src_sorted[s0:s1].data_ptr(), rowptr.data_ptr(), None, _lib.ptr(dyp),
             _lib.ptr(dg), _lib.ptr(dxe), graph.nodes_src, n1 - n0, rows, stream), "ictc_hip_message_edge_grad")
         if ny:

@@ -124,10 +124,11 @@ int ictc_hip_tp_backward(const ictc_tp_desc* desc,
  * ictc_hip_message_bonds into a caller-owned buffer [edges, ictc_hip_message_bond_width]:
  *   bonds[e][bond_p + k*(2 l1 + 1) + i] = scale_p * sum_j harmonics[e][l2^2 + j] C_p[i, j, k]
  * (the reference's bond projection Y @ P: backends/ascend/tensor_product.py:9-57,
- * structured_product.py:7-22).  The same buffer serves the forward and both VJP kernels.
- * For small degree sets (at most 32 projection coefficients per lane, e.g. lmax 2 or an
- * input lmax of 0) and for every degree set with a degree above 3 the kernels form the bond
- * rows from the harmonics themselves:
+ * structured_product.py:7-22).  The buffer serves the forward and its tangent; the VJP entry
+ * points take the harmonics themselves (they contract grad_out with the CG tensors once per
+ * receiver instead).  For small degree sets (at most 32 projection coefficients per lane,
+ * e.g. lmax 2 or an input lmax of 0) and for every degree set with a degree above 3 the
+ * kernels form the bond rows from the harmonics themselves:
  * ictc_hip_message_bond_width then returns 0, ictc_hip_message_bonds does nothing, and the
  * caller passes the harmonics [edges, (L_e+1)^2] as the `bonds` argument.
  *
@@ -157,14 +158,15 @@ int ictc_hip_message_forward(const ictc_tp_desc* desc, const float* node_feature
 int ictc_hip_message_chunks(int channels);
 
 /*
- * Message VJP, per-edge part (receiver CSR, grad_out[n] read once per node): for every edge
+ * Message VJP, per-edge part (receiver CSR, grad_out[n] read once per node), from the
+ * harmonics [edges, (L_e+1)^2] (not the bond rows): for every edge
  *   grad_gates[e]               = d<grad_out, node_out>/d gates[e]            [edges, P*C]
  *   grad_harmonics_partial[e,q] = partial sums over the channels of the harmonics
  *                                 gradient of edge e              [edges, chunks, NY];
  *                                 their sum over q (which the caller forms) is the
  *                                 gradient.  Which channels a slot holds depends on
- *                                 the kernel schedule (a slot may hold two chunks'
- *                                 sum, its neighbour zero); it is fixed per degree set.
+ *                                 the kernel schedule (64-channel chunk q for the
+ *                                 degrees up to 3); it is fixed per degree set.
  *   edge_grad_features[e]       = sum_p gates[e,p] M_p[e]^T grad_out[dst(e)], the edge's
  *                                 contribution to the source-feature gradient
  *                                 [edges, C*(L_in+1)^2] (features layout)
@@ -173,7 +175,7 @@ int ictc_hip_message_chunks(int channels);
  * (ascendc/op_kernel/epilogue_adjoint.cpp:6-208).
  */
 int ictc_hip_message_edge_grad(const ictc_tp_desc* desc, const float* node_features,
-                               const float* bonds, const float* gates, const float* grad_out,
+                               const float* harmonics, const float* gates, const float* grad_out,
                                const int64_t* src, const int64_t* dst_rowptr,
                                const int64_t* dst_perm, float* grad_harmonics_partial,
                                float* grad_gates, float* edge_grad_features, int64_t nodes_src,
@@ -195,7 +197,7 @@ int ictc_hip_message_edge_grad(const ictc_tp_desc* desc, const float* node_featu
  */
 #define ICTC_MSG_STATIC_SCRATCH_FLOATS 4194304
 int ictc_hip_message_edge_grad_static(const ictc_tp_desc* desc, const float* node_features,
-                                      const float* bonds, const float* gates, const float* grad_out,
+                                      const float* harmonics, const float* gates, const float* grad_out,
                                       const int64_t* src, const int64_t* dst_rowptr,
                                       const int64_t* dst_perm, float* grad_harmonics,
                                       float* grad_gates, float* edge_grad_features,
@@ -205,8 +207,10 @@ int ictc_hip_message_edge_grad_static(const ictc_tp_desc* desc, const float* nod
 /*
  * Mixed second derivatives of the message, as directional derivatives (JVPs) in the
  * direction (tangent_features [nodes_src, C*(L_in+1)^2], tangent harmonics, tangent_gates
- * [edges, P*C]); tangent_bonds are the bond rows of the tangent harmonics from
- * ictc_hip_message_bonds (or the tangent harmonics themselves when the bond width is 0).
+ * [edges, P*C]).  ictc_hip_message_forward_tangent takes bond rows (bonds, and tangent_bonds
+ * from ictc_hip_message_bonds on the tangent harmonics, or the harmonics themselves when the
+ * bond width is 0); ictc_hip_message_edge_grad_tangent takes the harmonics and the tangent
+ * harmonics [edges, (L_e+1)^2], as ictc_hip_message_edge_grad does.
  *   ictc_hip_message_forward_tangent: node_out = d/de message(x + e tx, Y + e tY, g + e tg)
  *     = sum over each argument replaced by its tangent, the others kept;
  *   ictc_hip_message_edge_grad_tangent: the same derivative of each edge_grad output with
@@ -226,8 +230,8 @@ int ictc_hip_message_forward_tangent(const ictc_tp_desc* desc, const float* node
                                      int64_t edges, hipStream_t stream);
 
 int ictc_hip_message_edge_grad_tangent(const ictc_tp_desc* desc, const float* node_features,
-                                       const float* bonds, const float* gates,
-                                       const float* tangent_features, const float* tangent_bonds,
+                                       const float* harmonics, const float* gates,
+                                       const float* tangent_features, const float* tangent_harmonics,
                                        const float* tangent_gates, const float* grad_out,
                                        const int64_t* src, const int64_t* dst_rowptr,
                                        const int64_t* dst_perm, float* grad_harmonics_partial,

@@ -152,7 +152,7 @@ def test_message_bond_width_and_tangent_validation():
         assert fwd_t(ctypes.byref(d3), *bad, 4, 4, 8, None) == 1, f"forward_tangent accepted null arg {i}"
     assert fwd_t(ctypes.byref(d3), *args, 4, 4, -1, None) == 1
     edge_t = lib.ictc_hip_message_edge_grad_tangent
-    args = [fake] * 13                 # x, bonds, g, tx, tb, tg, dout, src, rowptr, perm, dyp, dg, dxe
+    args = [fake] * 13                 # x, y, g, tx, ty, tg, dout, src, rowptr, perm, dyp, dg, dxe
     for i in (0, 1, 2, 3, 4, 5, 6, 7, 8):
         bad = list(args)
         bad[i] = None

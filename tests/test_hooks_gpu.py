@@ -95,7 +95,7 @@ def test_graph_message_hook(gpu):
     xs = {l: v.float().to(gpu).requires_grad_() for l, v in x.items()}
     empty = graph_message(owner, xs, {l: v[:0].float().to(gpu) for l, v in y.items()},
                           g[:0].float().to(gpu), src[:0].to(gpu), dst[:0].to(gpu))
-    assert all(float(v.abs().sum()) == 0.0 for v in empty.values())
+    assert all(float(v.detach().abs().sum()) == 0.0 for v in empty.values())
     total = sum(v.sum() for v in empty.values())
     grads = torch.autograd.grad(total, list(xs.values()), allow_unused=True)
     assert all(gr is None or float(gr.abs().sum()) == 0.0 for gr in grads)

@@ -40,15 +40,14 @@ def _inputs(plan, nodes, edges, seed, dev):
 
 def _edge_grads(plan, nodes, edges, seed, dev):
     from ictc_o3 import _lib
-    from ictc_o3.backends.hip.graph_message import _bonds, message_graph
+    from ictc_o3.backends.hip.graph_message import message_graph
     lib = _lib.lib()
     src, dst, x, y, gates, go = _inputs(plan, nodes, edges, seed, dev)
     graph = message_graph(src, dst, nodes, nodes)
-    bonds = _bonds(plan, graph, y)
     stream = _lib.stream_of(dev)
     chunks = lib.ictc_hip_message_chunks(plan.channels)
     ny = plan.y_width
-    common = (ctypes.byref(plan.desc), x.data_ptr(), bonds.data_ptr(), gates.data_ptr(), go.data_ptr(),
+    common = (ctypes.byref(plan.desc), x.data_ptr(), y.data_ptr(), gates.data_ptr(), go.data_ptr(),
               graph.src.data_ptr(), graph.rowptr_dst.data_ptr(), _lib.ptr(graph.perm_dst))
     dyp = torch.empty(edges, chunks, ny, device=dev)
     dg = torch.empty(edges, plan.full_gate_width, device=dev)
