@@ -299,7 +299,9 @@ class EdgeWeightedPathPreservingTensorProduct(nn.Module):
         """gates * weight as [E, P*C] (weight folded only when it is not a frozen all-ones).
 
         Whether a frozen weight is all ones is checked once (a host read) and cached on the
-        weight's identity, storage address and version counter."""
+        weight's identity, storage address and version counter.  An in-place write through
+        ``weight.data`` does not advance that counter and is not seen; change a frozen weight
+        with ``torch.no_grad()`` + ``weight.copy_(...)`` or ``load_state_dict`` (both do)."""
         w = self.weight
         if gates is None:
             return w.reshape(1, -1).expand(rows, -1).contiguous()
