@@ -76,11 +76,21 @@ def force_loss(prediction, atoms: int):
     return (prediction["energy"] / atoms).square().mean() + prediction["forces"].square().mean()
 
 
+def backward_to_parameters(loss: torch.Tensor, model) -> None:
+    """loss.backward() restricted to the model's trainable parameters.  energy_and_forces
+    differentiates through a private copy of the positions, and the loss gradient with respect
+    to that copy is never read; naming the parameters as the backward's inputs lets every
+    adjoint that only leads there (the harmonics and edge-geometry terms of the message VJPs and
+    of their double backward, the radial MLP's input adjoints) be skipped.  The parameters'
+    gradients are the same as those of loss.backward()."""
+    loss.backward(inputs=[p for p in model.parameters() if p.requires_grad])
+
+
 def training_step(model, optimizer, graph: dict, *, species=None):
     """One force-loss step; returns the loss (a device tensor, not synchronised)."""
     prediction = energy_and_forces(model, **graph, training=True, species=species)
     loss = force_loss(prediction, graph["positions"].shape[0])
-    loss.backward()
+    backward_to_parameters(loss, model)
     optimizer.step()
     optimizer.zero_grad(set_to_none=True)
     return loss.detach()
@@ -153,7 +163,7 @@ class CapturedTrainingStep:
         with pin_graphs() as self._message_graphs, torch.cuda.graph(self.graph):
             prediction = energy_and_forces(model, **self._graph, training=True, species=self._species)
             self._loss = force_loss(prediction, self._graph["positions"].shape[0])
-            self._loss.backward()
+            backward_to_parameters(self._loss, model)
             optimizer.step()
 
     def __call__(self, positions: torch.Tensor, cell=None) -> torch.Tensor:

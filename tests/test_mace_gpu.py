@@ -61,13 +61,20 @@ def test_energy_and_forces_match_oracle(gpu, channels):
 
 
 @pytest.mark.parametrize("channels", [32, 128])
-def test_force_loss_gradients_match_oracle(gpu, channels):
+@pytest.mark.parametrize("to_parameters", [False, True], ids=["backward", "backward_to_parameters"])
+def test_force_loss_gradients_match_oracle(gpu, channels, to_parameters):
+    """Both the plain loss.backward() and the parameter-restricted backward of training_step
+    (which skips every adjoint that only leads to the positions) against the oracle."""
     from mace_hip import energy_and_forces, force_loss
+    from mace_hip.runtime import backward_to_parameters
     model, graph, oracle, cpu = _setup(gpu, channels=channels, seed=5)
     atoms = graph["positions"].shape[0]
     pred = energy_and_forces(model, **graph, training=True)
     loss = force_loss(pred, atoms)
-    loss.backward()
+    if to_parameters:
+        backward_to_parameters(loss, model)
+    else:
+        loss.backward()
     names = [n for n, p in model.named_parameters() if p.requires_grad]
     for n in names:
         oracle.p[n].requires_grad_(True)
@@ -78,6 +85,24 @@ def test_force_loss_gradients_match_oracle(gpu, channels):
     params = dict(model.named_parameters())
     for n, g in zip(names, grads):
         assert_rel(params[n].grad, g, rtol=RTOL_FORCE, what=f"d loss / d {n}")
+
+
+def test_backward_to_parameters_equals_full_backward(gpu):
+    """The parameter-restricted backward gives the parameters the gradients of loss.backward()."""
+    from mace_hip import energy_and_forces, force_loss
+    from mace_hip.runtime import backward_to_parameters
+    grads = []
+    for restricted in (False, True):
+        model, graph, _, _ = _setup(gpu, channels=64, seed=7)
+        loss = force_loss(energy_and_forces(model, **graph, training=True), graph["positions"].shape[0])
+        if restricted:
+            backward_to_parameters(loss, model)
+        else:
+            loss.backward()
+        grads.append({n: p.grad.clone() for n, p in model.named_parameters() if p.grad is not None})
+    assert grads[0].keys() == grads[1].keys()
+    for n in grads[0]:
+        assert_rel(grads[1][n], grads[0][n], rtol=1e-6, what=f"d loss / d {n}")
 
 
 def _rotation(om):
