@@ -90,6 +90,11 @@ def _input_grad_raw(plan: DegreeLinearPlan, gy, weights, alpha):
     return gx
 
 
+def _scaled(t: torch.Tensor, alpha: float) -> torch.Tensor:
+    """alpha * t, without a launch when alpha is 1."""
+    return t if alpha == 1.0 else t * alpha
+
+
 def _weight_grads(plan: DegreeLinearPlan, gy, x, alpha, need):
     """alpha * gY_l^T X_l per degree (dense products on rearranged rows; differentiable)."""
     out = []
@@ -97,7 +102,7 @@ def _weight_grads(plan: DegreeLinearPlan, gy, x, alpha, need):
         if not n or plan.counts[l] == 0:
             out.append(None)
             continue
-        out.append(mm(plan.y_rows(gy, l).t(), plan.x_rows(x, l)) * alpha)
+        out.append(_scaled(mm(plan.y_rows(gy, l).t(), plan.x_rows(x, l)), alpha))
     return out
 
 
@@ -178,7 +183,7 @@ class _MulIr(torch.autograd.Function):
         gx = None
         if need[0]:
             gx = _MulIr.apply(plan.transposed(), ctx.alpha, gy, *[w.t().contiguous() for w in weights])
-        gw = [mm(plan.y_rows(gy, l).t(), plan.mul_ir_rows(x, l)) * ctx.alpha if n else None
+        gw = [_scaled(mm(plan.y_rows(gy, l).t(), plan.mul_ir_rows(x, l)), ctx.alpha) if n else None
               for l, n in enumerate(need[1:])]
         return (None, None, gx, *gw)
 
