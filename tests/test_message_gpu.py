@@ -57,7 +57,7 @@ def _op(c, lin, le, lout, device, layout="ir_mul", paths=None):
 # the last two have input degrees without any path (l1 > L_e + L_out): their feature-gradient rows
 # are zero
 CASES = [(64, 2, 2, 2, False), (128, 3, 3, 3, True), (48, 3, 3, 3, False), (96, 1, 2, 2, True),
-         (128, 0, 3, 3, False), (64, 3, 0, 1, True), (32, 2, 1, 0, False)]
+         (128, 0, 3, 3, False), (64, 3, 0, 1, True), (32, 2, 1, 0, False), (192, 3, 3, 3, False)]
 
 
 @pytest.mark.parametrize("c,lin,le,lout,sort", CASES)
@@ -105,7 +105,7 @@ def test_mask_destinations_and_mul_ir(gpu):
 
 
 @pytest.mark.parametrize("c,lin,le,lout", [(64, 2, 2, 2), (128, 3, 3, 3), (48, 3, 3, 3), (96, 0, 3, 3),
-                                           (64, 1, 2, 1)])
+                                           (64, 1, 2, 1), (192, 3, 3, 3)])
 @pytest.mark.parametrize("fused", [True, False], ids=["tangent_kernels", "substitution"])
 def test_mixed_second_derivatives(gpu, c, lin, le, lout, fused, monkeypatch):
     """Second derivatives of <dout, message> contracted with (hx, hY, hg), against the float64
