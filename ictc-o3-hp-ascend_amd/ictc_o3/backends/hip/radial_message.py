@@ -250,10 +250,9 @@ def fold_projection(owner, plan: TensorProductPlan, weight: torch.Tensor, bias: 
     c, p = owner.channels, owner.num_paths
     weight = weight.reshape(p, c, -1)
     bias = None if bias is None else bias.reshape(p, c)
-    w = owner.weight
-    if w.requires_grad or not bool(torch.all(w == 1)):
-        weight = weight * w[:, :, None]
-        bias = None if bias is None else bias * w
+    w = owner.weight              # always folded (a [P, C, H] product), so every change is seen
+    weight = weight * w[:, :, None]
+    bias = None if bias is None else bias * w
     if not plan.is_full:
         slots = torch.tensor(plan.slot_of_path, device=weight.device)
         full = len(plan.full_paths)

@@ -330,6 +330,16 @@ def check_message_operands(owner, device, harmonics_rows, gates, src, dst, mask,
     return edges
 
 
+def message_gates(owner, gates: Optional[torch.Tensor], edges: int):
+    """(gates [E, P*C], receiver-row weight or None) for the message kernels.  The owner's
+    per-(path, channel) weight is applied to the message's receiver rows
+    (``owner.output_weight_rows``, always, so every change of the weight is seen) rather than
+    folded into every edge's gates; ``gates=None`` means the weight alone."""
+    if gates is None:
+        return owner.effective_gates(None, edges), None
+    return gates.reshape(edges, owner.num_paths * owner.channels), owner.output_weight_rows()
+
+
 def graph_message(owner, features, harmonics, gates, src, dst, mask=None, *, edge_chunk_size=16384):
     """The reference's message hook (``backends/ascend/tensor_product.py:159-218``, called by the
     interaction block at ``pure_cartesian_ictd_fix.py:1787-1800``):
@@ -346,6 +356,6 @@ def graph_message(owner, features, harmonics, gates, src, dst, mask=None, *, edg
     x = pack_features(owner, features, nodes)
     y = pack_harmonics(owner, harmonics, edges, sample)
     plan = owner.hip_plan(*owner_degrees(owner))
-    out = packed_graph_message(plan, x, y, owner.effective_gates(gates, edges), src, dst,
-                               nodes_dst=destination_nodes(owner, nodes), mask=mask)
-    return packed_to_blocks(plan, out)
+    gates, row_weight = message_gates(owner, gates, edges)
+    out = packed_graph_message(plan, x, y, gates, src, dst, nodes_dst=destination_nodes(owner, nodes), mask=mask)
+    return packed_to_blocks(plan, out if row_weight is None else out * row_weight)

@@ -284,36 +284,33 @@ class EdgeWeightedPathPreservingTensorProduct(nn.Module):
             self._plans[key] = plan
         return plan
 
-    def invalidate_weight_cache(self) -> None:
-        """Forget that the frozen weight was found to be all ones.  Needed only after writing the
-        weight through ``weight.data`` (such writes bypass the version counter that the cache
-        checks); ``load_state_dict``, in-place updates of the parameter and replacing its
-        storage are detected without it."""
-        self._unit_weight_key = None
-
-    def _load_from_state_dict(self, *args, **kwargs):
-        self._unit_weight_key = None
-        super()._load_from_state_dict(*args, **kwargs)
-
     def effective_gates(self, gates: Optional[torch.Tensor], rows: int) -> torch.Tensor:
-        """gates * weight as [E, P*C] (weight folded only when it is not a frozen all-ones).
-
-        Whether a frozen weight is all ones is checked once (a host read) and cached on the
-        weight's identity, storage address and version counter.  An in-place write through
-        ``weight.data`` does not advance that counter and is not seen; change a frozen weight
-        with ``torch.no_grad()`` + ``weight.copy_(...)`` or ``load_state_dict`` (both do)."""
+        """gates * weight as [E, P*C]: the per-(path, channel) weight is always folded, as the
+        reference does (``backends/ascend/packed_tensor_product.py:163-164``), so any change of
+        the weight -- including writes through ``weight.data`` -- is seen by the next call.
+        A unit weight multiplies exactly (g * 1 == g), so the result equals the gates then."""
         w = self.weight
         if gates is None:
             return w.reshape(1, -1).expand(rows, -1).contiguous()
-        gates = gates.reshape(rows, self.num_paths * self.channels)
-        if not w.requires_grad:
-            key = (id(w), w.data_ptr(), w._version)
-            if getattr(self, "_unit_weight_key", None) == key:
-                return gates
-            if bool(torch.all(w == 1)):
-                self._unit_weight_key = key
-                return gates
-        return (gates.reshape(rows, self.num_paths, self.channels) * w[None]).reshape(rows, self.num_paths * self.channels)
+        gates = gates.reshape(rows, self.num_paths, self.channels)
+        return (gates * w[None]).reshape(rows, self.num_paths * self.channels)
+
+    def output_weight_rows(self) -> torch.Tensor:
+        """The weight laid out along the packed ir_mul output: entry (l3 block, path offset, m, c)
+        holds weight[p, c] of the path p that writes that row.  The message is linear in each
+        path's gate and sums over edges, so ``message(g * weight) == weight_rows * message(g)``:
+        a receiver-level product instead of one over every edge's gates (the reference folds
+        into the gates, ``packed_tensor_product.py:163-164``; the results agree to rounding).
+        Differentiable with respect to a live weight."""
+        parts = []
+        for l3 in range(self.lmax + 1):
+            ordered = sorted((self.path_offset[p], p) for p in range(self.num_paths) if self.paths[p][2] == l3)
+            if not ordered:
+                continue
+            idx = torch.tensor([p for _, p in ordered], device=self.weight.device)
+            rows = self.weight.index_select(0, idx)                     # [count, C]
+            parts.append(rows[:, None, :].expand(len(ordered), 2 * l3 + 1, self.channels).reshape(-1))
+        return torch.cat(parts) if parts else self.weight.new_zeros(0)
 
     def forward(self, x1: Dict[int, torch.Tensor], x2: Dict[int, torch.Tensor],
                 gates: Optional[torch.Tensor] = None) -> Dict[int, torch.Tensor]:

@@ -183,7 +183,7 @@ class PackedGraphMessage(EdgeTensorProduct):
 
     def _message(self, features, harmonics, gates, src, dst, mask):
         from ictc_o3.backends.hip.graph_message import packed_graph_message
-        from ictc_o3.backends.hip.tensor_product import check_message_operands, destination_nodes
+        from ictc_o3.backends.hip.tensor_product import check_message_operands, destination_nodes, message_gates
         edges = check_message_operands(self.tp, features.device, [harmonics.shape[0]], gates, src, dst, mask,
                                        self.edge_chunk_size)
         require_gpu_fp32(features, harmonics, self.tp.weight)
@@ -192,8 +192,10 @@ class PackedGraphMessage(EdgeTensorProduct):
         if harmonics.shape != (edges, (self.edge_lmax + 1) ** 2):
             raise ValueError("Harmonics must have shape [E,(L_edge+1)^2]")
         nodes = destination_nodes(self.tp, features.shape[0])
-        return packed_graph_message(self.plan, self._to_ir_mul_features(features), harmonics,
-                                    self.tp.effective_gates(gates, edges), src, dst, nodes_dst=nodes, mask=mask)
+        gates, row_weight = message_gates(self.tp, gates, edges)
+        out = packed_graph_message(self.plan, self._to_ir_mul_features(features), harmonics, gates, src, dst,
+                                   nodes_dst=nodes, mask=mask)
+        return out if row_weight is None else out * row_weight
 
     def forward(self, features, harmonics, gates, src, dst, mask=None):
         return self._from_ir_mul_output(self._message(features, harmonics, gates, src, dst, mask))

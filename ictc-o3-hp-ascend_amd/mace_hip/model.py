@@ -186,6 +186,13 @@ class Interaction(nn.Module):
         hidden, weight = self.radial_hidden(edge_feats)
         return linear(hidden, weight)
 
+    def message_gates(self, edge_feats):
+        """The gates times the TP's frozen path weight (the reference's gates * weight,
+        ``backends/ascend/packed_tensor_product.py:163-164``), folded into the rows of the radial
+        MLP's last weight ([P*C, 64]) rather than applied to the [E, P*C] gates."""
+        hidden, weight = self.radial_hidden(edge_feats)
+        return linear(hidden, weight * self.tp.weight.reshape(-1, 1))
+
     def forward(self, h, harmonics, edge_feats, src, dst, mask, species):
         """mask: the reference multiplies the gates by (r <= r_max) (:1801-1808).  The radial
         features carry the cutoff envelope, exactly 0 from r_max on, and fc has no biases, so
@@ -195,7 +202,7 @@ class Interaction(nn.Module):
         x1 = self.linear_up.to_ir_mul(h)
         plan = self.tp.hip_plan(self.input_lmax, self.edge_lmax)
         if self.edge_chunk_size is None:
-            gates = self.tp.effective_gates(self.radial_mlp(edge_feats), edge_feats.shape[0])
+            gates = self.message_gates(edge_feats)
             m = packed_graph_message(plan, x1, harmonics, gates, src, dst, nodes_dst=n)
         else:
             # the radial MLP's last layer produced one receiver range at a time inside the message

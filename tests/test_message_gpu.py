@@ -234,3 +234,41 @@ def test_full_size_matches_tp_plus_scatter(gpu):
     b = torch.autograd.grad(ref, (x, y, g), go)
     for name, u, v in zip(("x", "Y", "g"), a, b):
         assert_rel(u, v, what=f"fused vs TP+scatter grad {name}")
+
+
+@pytest.mark.parametrize("layout", ["ir_mul", "mul_ir"])
+def test_frozen_weight_written_through_data(gpu, layout):
+    """A frozen path weight changed through ``weight.data`` (no version bump) after a first call:
+    the TP folds it into the gates and the message applies it to the receiver rows, both on
+    every call (reference gates * weight, packed_tensor_product.py:163-164); values and all
+    three gradients against the oracle with that weight, also for the dict hook."""
+    from ictc_o3 import EdgeTensorProduct, GraphMessage
+    c, lin, le, lout = 64, 2, 2, 2
+    paths = [p for i, p in enumerate(enumerate_paths(lin, le, lout)) if i != 3]
+    op = _op(c, lin, le, lout, gpu, layout=layout, paths=paths)
+    nodes, edges = 20, 160
+    src, dst = _graph(nodes, edges, 11)
+    plain = TensorProductOracle(c, lin, le, lout, layout=layout, paths=paths)
+    x, y, g = _edge_inputs(plain, nodes, edges, 12)
+    dev = [t.to(gpu) for t in (x, y, g)]
+    op(*dev, src.to(gpu), dst.to(gpu))                       # a first call with the unit weight
+    w = torch.randn(plain.num_paths, c, generator=torch.Generator().manual_seed(13))
+    op.tp.weight.data.copy_(w.to(gpu))                       # invisible to the version counter
+    ref = TensorProductOracle(c, lin, le, lout, layout=layout, paths=paths, weight=w.double())
+    go = torch.randn(nodes, ref.output_width, generator=torch.Generator().manual_seed(14))
+    cpu = [t.double().requires_grad_() for t in (x, y, g)]
+    expect = ref.graph_message(*cpu, src, dst)
+    egrads = torch.autograd.grad(expect, cpu, go.double())
+    leaves = [t.clone().requires_grad_() for t in dev]
+    out = op(*leaves, src.to(gpu), dst.to(gpu))
+    assert_rel(out, expect, what="weighted message")
+    for name, a, b in zip(("x", "Y", "g"), torch.autograd.grad(out, leaves, go.to(gpu)), egrads):
+        assert_rel(a, b, what=f"weighted message grad {name}")
+    hook = GraphMessage(op.tp, input_lmax=lin, edge_lmax=le, layout=layout)
+    blocks = hook(plain.blocks(dev[0]), plain.harmonics(dev[1]), dev[2], src.to(gpu), dst.to(gpu))
+    for l, v in ref.unpack_output(expect.detach()).items():
+        assert_rel(blocks[l], v, what=f"weighted dict message l={l}")
+    tp = EdgeTensorProduct(op.tp, input_lmax=lin, edge_lmax=le, layout=layout)
+    xe = x[src]
+    assert_rel(tp(xe.to(gpu), dev[1], dev[2]), ref.forward(xe.double(), y.double(), g.double()),
+               what="weighted TP")
