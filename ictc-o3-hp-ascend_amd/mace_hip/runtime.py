@@ -4,7 +4,8 @@ Mirrors reference ``mace_ictc/hp/runtime.py``: ``create_model`` (:7-81; channels
 num_interactions, correlation 1-3, atomic_numbers, cutoff, avg_num_neighbors) and
 ``energy_and_forces`` (:84-119; forces = -dE/dpos through autograd, ``create_graph``
 when training, detached results otherwise, zero-edge graphs keep the coordinate
-dependency).  ``training_step`` is the pattern of ``examples/model.py:35-41``: energy and
+dependency).  ``check_model`` / ``configure_model`` (:123-145) report and select the HIP
+operators.  ``training_step`` is the pattern of ``examples/model.py:35-41``: energy and
 forces with ``training=True``, loss = mean((E/N)^2) + mean(F^2), backward, AdamW step.
 
 ``CapturedEnergyAndForces`` / ``CapturedTrainingStep`` record one fixed-shape step into a
@@ -18,7 +19,7 @@ from __future__ import annotations
 import torch
 
 from ictc_o3.backends.hip.graph_message import pin_graphs
-from ictc_o3.backends.hip.runtime import require_gpu_fp32
+from ictc_o3.backends.hip.runtime import require_gpu_fp32, strict_fp32
 
 from .geometry import one_hot_rows
 from .linear import mm
@@ -59,6 +60,7 @@ def energy_and_forces(model, positions, atomic_numbers, batch, edge_src, edge_ds
     if atomic_numbers.shape != (n,) or batch.shape != (n,):
         raise ValueError("atomic numbers and batch must have shape [N]")
     require_gpu_fp32(positions)
+    _validate_batch(batch, cell.shape[0])
     with torch.enable_grad():
         pos = positions if positions.requires_grad else positions.detach().requires_grad_(True)
         atomic = model(pos, atomic_numbers, batch, edge_src, edge_dst, edge_shifts, cell, species=species)
@@ -72,28 +74,104 @@ def energy_and_forces(model, positions, atomic_numbers, batch, edge_src, edge_ds
     return result if training else {k: v.detach() for k, v in result.items()}
 
 
+def _validate_batch(batch: torch.Tensor, structures: int) -> None:
+    """Per-structure energies are one_hot(batch)^T @ atomic energies, which would silently drop an
+    atom whose batch index is outside [0, structures) (an index_add would raise): check the range
+    once per batch tensor (one host read), cached on its identity, address and version."""
+    key = (id(batch), batch.data_ptr(), batch._version, int(structures))
+    if _validate_batch.last == key:
+        return
+    if batch.numel() and (int(batch.min()) < 0 or int(batch.max()) >= structures):
+        raise ValueError(f"batch indices must lie in [0, {structures}) (one per cell)")
+    _validate_batch.last = key
+
+
+_validate_batch.last = None
+
+
 def force_loss(prediction, atoms: int):
     return (prediction["energy"] / atoms).square().mean() + prediction["forces"].square().mean()
 
 
-def backward_to_parameters(loss: torch.Tensor, model) -> None:
-    """loss.backward() restricted to the model's trainable parameters.  energy_and_forces
-    differentiates through a private copy of the positions, and the loss gradient with respect
-    to that copy is never read; naming the parameters as the backward's inputs lets every
-    adjoint that only leads there (the harmonics and edge-geometry terms of the message VJPs and
-    of their double backward, the radial MLP's input adjoints) be skipped.  The parameters'
+def backward_to_parameters(loss: torch.Tensor, model, positions: torch.Tensor = None) -> None:
+    """loss.backward() restricted to the model's trainable parameters (and to ``positions`` when
+    the caller passes positions that require a gradient, so their ``.grad`` fills as with
+    loss.backward()).  For positions without a gradient, energy_and_forces differentiates through
+    a private copy whose loss gradient is never read; leaving it out of the backward's inputs lets
+    every adjoint that only leads there (the harmonics and edge-geometry terms of the message VJPs
+    and of their double backward, the radial MLP's input adjoints) be skipped.  The parameters'
     gradients are the same as those of loss.backward()."""
-    loss.backward(inputs=[p for p in model.parameters() if p.requires_grad])
+    inputs = [p for p in model.parameters() if p.requires_grad]
+    if positions is not None and positions.requires_grad:
+        inputs.append(positions)
+    loss.backward(inputs=inputs)
 
 
 def training_step(model, optimizer, graph: dict, *, species=None):
     """One force-loss step; returns the loss (a device tensor, not synchronised)."""
     prediction = energy_and_forces(model, **graph, training=True, species=species)
     loss = force_loss(prediction, graph["positions"].shape[0])
-    backward_to_parameters(loss, model)
+    backward_to_parameters(loss, model, graph["positions"])
     optimizer.step()
     optimizer.zero_grad(set_to_none=True)
     return loss.detach()
+
+
+def check_model(model, *, training=False, capture=False) -> dict:
+    """Coverage of the HIP operators for this model, without modifying it (reference
+    ``hp/runtime.py:123-130`` and its backend check ``mace_ictc/ascend/runtime.py:10-39``):
+    {"supported": bool, "backend": "hip", "reasons": [...]}.  Training (force-loss second
+    derivatives) and HIP-graph capture (``CapturedEnergyAndForces``, ``CapturedTrainingStep``)
+    are both covered, so ``training`` and ``capture`` add no reasons."""
+    if not isinstance(model, MaceICTC):
+        return {"supported": False, "backend": "hip", "reasons": ["Expected the MACE-ICTC model (mace_hip.MaceICTC)"]}
+    reasons = []
+    if any(p.device.type != "cuda" or p.dtype != torch.float32 for p in model.parameters()):
+        reasons.append("All model parameters must already be ROCm GPU FP32")
+    try:
+        from ictc_o3 import _lib
+        _lib.lib()
+    except (OSError, RuntimeError) as exc:
+        reasons.append(f"The HIP operator library is unavailable: {exc}")
+    if not 0 <= model.lmax <= 3:
+        reasons.append("The message tangent kernels and the symmetric contraction are compiled for lmax <= 3")
+    for product in model.products:
+        if product.symmetric_contractions.correlation not in (1, 2, 3):
+            reasons.append("The symmetric contraction supports correlation 1, 2 and 3")
+    for interaction in model.interactions:
+        if interaction.tp.internal_compute_dtype != torch.float32:
+            reasons.append("Tensor-product internal compute dtype must be FP32")
+    return {"supported": not reasons, "backend": "hip", "reasons": reasons}
+
+
+def configure_model(model, *, training=False, policy="auto", layout="packed", capture=False,
+                    message_chunk_edges=None, electrostatics_backend="auto") -> dict:
+    """Select the HIP operators for a model (reference ``hp/runtime.py:133-145`` and
+    ``mace_ictc/ascend/runtime.py:42-89``; same arguments).  ``message_chunk_edges`` switches
+    radial streaming on (receiver ranges of at most that many edges; the reference's
+    ``edge_chunk_size``) or off (None).  There is no reference backend to fall back to (no CPU
+    path in this build), so ``policy="reference"`` and an unsupported model raise."""
+    if layout not in ("packed", "fused_pack"):
+        raise ValueError("layout must be packed or fused_pack")
+    if policy not in ("auto", "generated", "reference"):
+        raise ValueError("policy must be auto, generated or reference")
+    if message_chunk_edges is not None and (not isinstance(message_chunk_edges, int)
+                                            or isinstance(message_chunk_edges, bool) or message_chunk_edges < 1):
+        raise ValueError("edge_chunk_size must be a positive integer or None for automatic sizing")
+    if electrostatics_backend not in ("auto", "none"):
+        raise ValueError("electrostatics is not part of this model; electrostatics_backend must be auto or none")
+    if policy == "reference":
+        raise ValueError("this build has no reference (CPU) backend; use policy='auto' or 'generated'")
+    coverage = check_model(model, training=training, capture=capture)
+    if not coverage["supported"]:
+        raise ValueError("HIP HP unavailable: " + "; ".join(coverage["reasons"]))
+    strict_fp32()
+    model.set_message_streaming(message_chunk_edges)
+    return {"requested": policy, "selected": "generated", "backend": "hip", "reasons": [],
+            "electrostatics": None, "arithmetic": "strict FP32; TF32 and autocast disabled",
+            "edge_chunk_size": message_chunk_edges, "kernel_backend": "hip",
+            "tensor_product_adjoint": "analytic",
+            "counts": {"interactions": len(model.interactions)}}
 
 
 def _warm_up(fn, calls: int, device) -> None:
@@ -163,7 +241,7 @@ class CapturedTrainingStep:
         with pin_graphs() as self._message_graphs, torch.cuda.graph(self.graph):
             prediction = energy_and_forces(model, **self._graph, training=True, species=self._species)
             self._loss = force_loss(prediction, self._graph["positions"].shape[0])
-            backward_to_parameters(self._loss, model)
+            backward_to_parameters(self._loss, model, self._graph["positions"])
             optimizer.step()
 
     def __call__(self, positions: torch.Tensor, cell=None) -> torch.Tensor:

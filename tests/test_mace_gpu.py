@@ -139,3 +139,26 @@ def test_full_size_rotation_and_training_step(gpu):
     assert math.isfinite(float(loss))
     moved = [n for n, p in model.named_parameters() if p.requires_grad and not torch.equal(p, before[n])]
     assert len(moved) == len(before)
+
+
+def test_configure_model_selects_hip_and_streaming(gpu):
+    """configure_model (reference hp/runtime.py:133-145) on a GPU model: supported, the message
+    chunk size switches radial streaming on and off, and the configured model still matches the
+    oracle; positions that require a gradient get it from the restricted training backward."""
+    from mace_hip import check_model, configure_model, energy_and_forces, force_loss
+    from mace_hip.runtime import backward_to_parameters
+    model, graph, oracle, cpu = _setup(gpu)
+    assert check_model(model, training=True, capture=True) == {"supported": True, "backend": "hip", "reasons": []}
+    info = configure_model(model, training=True, message_chunk_edges=64)
+    assert info["selected"] == "generated" and info["edge_chunk_size"] == 64
+    assert all(i.edge_chunk_size == 64 for i in model.interactions)
+    got = energy_and_forces(model, **graph)
+    e, f, _ = oracle.energy_and_forces(**cpu)
+    assert_rel(got["energy"], e, what="streamed energy")
+    assert_rel(got["forces"], f, rtol=RTOL_FORCE, what="streamed forces")
+    configure_model(model)
+    assert all(i.edge_chunk_size is None for i in model.interactions)
+    pos = graph["positions"].clone().requires_grad_()
+    pred = energy_and_forces(model, **{**graph, "positions": pos}, training=True)
+    backward_to_parameters(force_loss(pred, pos.shape[0]), model, pos)
+    assert pos.grad is not None and torch.isfinite(pos.grad).all()
