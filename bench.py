@@ -143,11 +143,11 @@ def _copy_gbs(device, nbytes: int = 1 << 30, reps: int = 5) -> float:
 
 
 def _stream_mix_gbs(device, reads: int, writes: int, total_bytes: int, reps: int = 5):
-    """Best bandwidth of an ideal grid-stride float4 streaming kernel (csrc/stream_probe.hip)
+    """Best bandwidth of an ideal grid-stride float4 streaming kernel (stream_probe.hip)
     moving total_bytes in the given read:write mix, over three grid sizes and both load cache
     policies (default, non-temporal); None if the probe library is absent."""
     import ctypes
-    path = os.path.join(ROOT, "ictc-o3-hp-ascend_amd", "ictc_o3", "lib", "libictc_stream_probe.so")
+    path = os.path.join(ROOT, "libictc_stream_probe.so")
     if not os.path.exists(path):
         return None
     lib = ctypes.CDLL(path)
@@ -295,7 +295,7 @@ def _event_ms(fn, device, reps: int = 10, warmup: int = 3) -> float:
 
 def _probe_lib():
     import ctypes
-    path = os.path.join(ROOT, "ictc-o3-hp-ascend_amd", "ictc_o3", "lib", "libictc_stream_probe.so")
+    path = os.path.join(ROOT, "libictc_stream_probe.so")
     if not os.path.exists(path):
         return None
     lib = ctypes.CDLL(path)
@@ -306,7 +306,7 @@ def _probe_lib():
 
 def _valu_fma_tflops(device, grid: int = 16384, iters: int = 2048, reps: int = 5):
     """fp32 FMA rate of register-only kernels of scalar (non-packed) fma chains
-    (csrc/stream_probe.hip) in both instruction forms the compiler emits: v_fma_f32 with SGPR
+    (stream_probe.hip) in both instruction forms the compiler emits: v_fma_f32 with SGPR
     operands (VOP3) and v_fmac_f32 with every operand in a VGPR (VOP2); None if the probe
     library is absent."""
     import ctypes
@@ -521,8 +521,7 @@ def _sc_inputs(device, nodes=SC_NODES):
 
 
 def _bench_sc(device):
-    sys.path.insert(0, os.path.join(ROOT, "ictc-o3-hp-ascend_amd", "csrc"))
-    import gen_sc
+    import sc_flops
     from ictc_o3.backends.hip.symmetric_contraction import ContractionPlan, _forward_raw, _vjp_raw
     plan = ContractionPlan(SC_L, SC_T, SC_K, SC_C, SC_S)
     x, species, go = _sc_inputs(device)
@@ -537,7 +536,7 @@ def _bench_sc(device):
     w = torch.cat(blocks, 1).to(device).contiguous()
     fwd_ms = _event_ms(lambda: _forward_raw(plan, x, species, w), device)
     vjp_ms = _event_ms(lambda: _vjp_raw(plan, x, species, w, go), device)
-    flops = gen_sc.flop_counts(SC_L, SC_T, SC_K)          # useful FLOPs per (node, channel)
+    flops = sc_flops.flop_counts(SC_L, SC_T, SC_K)        # useful FLOPs per (node, channel)
     executed = _sc_executed_flops()                        # per lane, from the committed VALU counters
     probe = _valu_fma_tflops(device)
     d, o = (SC_L + 1) ** 2, (SC_T + 1) ** 2
@@ -704,8 +703,7 @@ def _mace_floor(edges: int, atoms: int, training: bool):
     path's tangent forward and tangent VJP, four more GEMMs per radial layer (the weight gradient
     and the two adjoints of each force-pass product), four more message-linear and channel-linear
     products and twice more contraction work (VJP and its directional derivative)."""
-    sys.path.insert(0, os.path.join(ROOT, "ictc-o3-hp-ascend_amd", "csrc"))
-    import gen_sc
+    import sc_flops
     e, n, c, s = edges, atoms, 128, 10
     terms = {}
 
@@ -719,7 +717,7 @@ def _mace_floor(edges: int, atoms: int, training: bool):
         vjp_b = e * (8 * npath * c + 64 + 64 + 8) + n * 4 * c * (2 * nx + noc)
         lin_f = 2 * n * c * c * noc                                       # message linear
         chan_f = 2 * n * c * c * (nx + (target + 1) ** 2 + s)             # linear_up, product, self
-        sc = gen_sc.flop_counts(3, target, 3)
+        sc = sc_flops.flop_counts(3, target, 3)
         sc_f = (sc["forward"] + sc["vjp"]) * n * c
         add("message kernels", nbytes=fwd_b + vjp_b)
         add("radial MLP GEMMs", flops=2 * radial)

@@ -7,8 +7,9 @@ Steps:
      listing the compiled combinations for the dispatch tables;
   3. compile every TU to an object in parallel, largest first;
   4. link the objects and the API TUs into ``ictc_o3/lib/libictc_hip.so``;
-  5. build ``ictc_o3/lib/libictc_stream_probe.so`` from ``stream_probe.hip`` (bench.py's
-     streaming-bandwidth reference; not part of the operator library).
+  5. build ``libictc_stream_probe.so`` beside bench.py from the repository root's
+     ``stream_probe.hip`` (bench.py's streaming-bandwidth and FMA-rate reference; not part of
+     the operator library).
 
 Every HIP TU is compiled with ``-Xclang -target-feature -Xclang -packed-fp32-ops``
 (no packed FP32 VALU instructions are generated).
@@ -35,7 +36,8 @@ GEN = os.path.join(HERE, "generated")
 OBJ = os.path.join(HERE, "_build")
 LIB_DIR = os.path.join(PKG, "ictc_o3", "lib")
 LIB = os.path.join(LIB_DIR, "libictc_hip.so")
-PROBE_LIB = os.path.join(LIB_DIR, "libictc_stream_probe.so")
+PROBE_SRC = os.path.join(REPO, "stream_probe.hip")
+PROBE_LIB = os.path.join(REPO, "libictc_stream_probe.so")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
@@ -201,7 +203,7 @@ def build(jobs: int | None = None, verbose: bool = True, incremental: bool = Fal
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
     os.replace(tmp, LIB)
-    res = subprocess.run([HIPCC, *FLAGS, "-shared", os.path.join(HERE, "stream_probe.hip"), "-o", PROBE_LIB + ".tmp"],
+    res = subprocess.run([HIPCC, *FLAGS, "-shared", PROBE_SRC, "-o", PROBE_LIB + ".tmp"],
                          capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"stream probe build failed:\n{res.stderr}")

@@ -435,15 +435,6 @@ def weight_columns(lmax: int, target: int, corr: int) -> int:
     return _columns(lmax, target, corr)[2]
 
 
-def flop_counts(lmax: int, target: int, corr: int) -> Dict[str, int]:
-    """Useful floating-point operations per (node, channel) of the emitted float forward and
-    VJP (sc_flops.py: products with an exact zero or +-1 and sums with an exact zero are free;
-    an fma is its product plus its sum)."""
-    import sc_flops
-    D, NO, ktot = (lmax + 1) ** 2, (target + 1) ** 2, weight_columns(lmax, target, corr)
-    return sc_flops.useful_flops(emit(lmax, target, corr), D, NO, ktot)
-
-
 def configs():
     return [(l, t, k) for l in range(4) for t in range(l + 1) for k in (1, 2, 3)]
 

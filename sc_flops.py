@@ -16,7 +16,9 @@ not executed instructions; the hardware's executed counts come from the VALU cou
 """
 from __future__ import annotations
 
+import os
 import re
+import sys
 from typing import Dict, List
 
 _SKIP = ("//", "#pragma", "asm ", "switch", "case ", "default:", "for (int step", "int Cs = C;")
@@ -170,3 +172,15 @@ def useful_flops(text: str, D: int, NO: int, KTOT: int) -> Dict[str, int]:
         exec(src, env)  # noqa: S102 - statements emitted by this repository's own generator
         out[name] = tally.flops
     return out
+
+
+def flop_counts(lmax: int, target: int, corr: int) -> Dict[str, int]:
+    """Useful floating-point operations per (node, channel) of the emitted float forward and VJP
+    of one (lmax, target, correlation) configuration (products with an exact zero or +-1 and
+    sums with an exact zero are free; an fma is its product plus its sum)."""
+    csrc = os.path.join(os.path.dirname(os.path.abspath(__file__)), "ictc-o3-hp-ascend_amd", "csrc")
+    if csrc not in sys.path:
+        sys.path.insert(0, csrc)
+    import gen_sc
+    D, NO, ktot = (lmax + 1) ** 2, (target + 1) ** 2, gen_sc.weight_columns(lmax, target, corr)
+    return useful_flops(gen_sc.emit(lmax, target, corr), D, NO, ktot)
