@@ -50,10 +50,17 @@ extern "C" int ictc_hip_sgemm(int trans_a, int trans_b, int64_t m, int64_t n, in
   if (rocblas_set_stream(h, stream) != rocblas_status_success) return ICTC_ERR_LAUNCH;
   const rocblas_operation op_a = trans_a ? rocblas_operation_transpose : rocblas_operation_none;
   const rocblas_operation op_b = trans_b ? rocblas_operation_transpose : rocblas_operation_none;
+  // k == 0 leaves C = beta * C and reads neither operand, but rocBLAS still checks their leading
+  // dimensions (at least the stored rows of the column-major views, and 1) and pointers: pass
+  // the smallest legal ones and a valid address instead of whatever the caller gave
+  const int64_t ldb_rb = k > 0 ? ldb : (trans_b ? 1 : (n > 1 ? n : 1));
+  const int64_t lda_rb = k > 0 ? lda : (trans_a ? (m > 1 ? m : 1) : 1);
+  const float* a_rb = k > 0 ? a : c;
+  const float* b_rb = k > 0 ? b : c;
   // column-major view: C^T [n, m] = op(B)^T [n, k] * op(A)^T [k, m]
   const rocblas_status st = rocblas_sgemm(h, op_b, op_a, static_cast<rocblas_int>(n), static_cast<rocblas_int>(m),
-                                          static_cast<rocblas_int>(k), &alpha, b, static_cast<rocblas_int>(ldb > 0 ? ldb : 1),
-                                          a, static_cast<rocblas_int>(lda > 0 ? lda : 1), &beta, c,
+                                          static_cast<rocblas_int>(k), &alpha, b_rb, static_cast<rocblas_int>(ldb_rb),
+                                          a_rb, static_cast<rocblas_int>(lda_rb), &beta, c,
                                           static_cast<rocblas_int>(ldc));
   return st == rocblas_status_success ? ICTC_OK : ICTC_ERR_LAUNCH;
 }

@@ -226,6 +226,11 @@ int ictc_hip_message_edge_grad(const ictc_tp_desc* desc, const float* node_featu
             grad_gates, edge_grad_features, nodes_src, nodes_dst, stream);
 }
 
+int ictc_hip_message_static_prepare(void) {
+  float* address = nullptr;
+  return ictc::static_scratch(nullptr, &address);
+}
+
 int ictc_hip_message_edge_grad_static(const ictc_tp_desc* desc, const float* node_features, const float* harmonics,
                                       const float* gates, const float* grad_out, const int64_t* src,
                                       const int64_t* dst_rowptr, const int64_t* dst_perm, float* grad_harmonics,

@@ -3,10 +3,13 @@
  *
  * libictc_hip.so exports plain extern "C" entry points taking device pointers,
  * sizes and a hipStream_t.  Nothing here allocates device memory (the caller owns
- * every input, output and workspace buffer) except ictc_hip_sgemm, whose rocBLAS
- * handle may allocate its own workspace.  Launches are asynchronous on the given
- * stream; every entry point is reentrant and keeps no mutable global state other
- * than ictc_hip_sgemm's per-thread rocBLAS handles.
+ * every input, output and workspace buffer), with two exceptions: ictc_hip_sgemm's
+ * rocBLAS handles (one per host thread and device) allocate their own workspace, and
+ * ictc_hip_message_edge_grad_static stages partial sums in a library-owned static
+ * device array (16 MiB per GPU, held for the life of the process) that every call on
+ * that GPU shares, so overlapping calls on one GPU must be serialised.  Launches are
+ * asynchronous on the given stream; every other entry point is reentrant, and the only
+ * mutable global state is those rocBLAS handles and the static array's per-device address.
  *
  * Data layout (all float32, row-major, channel-contiguous "ir_mul" packing):
  *   features   [rows, C*(L_in+1)^2]     per degree l: (2l+1) rows of C channels
@@ -193,9 +196,14 @@ int ictc_hip_message_edge_grad(const ictc_tp_desc* desc, const float* node_featu
  * before any launch.  Every row the call reads from the array it first writes (a receiver CSR
  * that covers every edge once, as for the entry point above).  The stream must belong to the
  * current device.  Allocates nothing.  Calls that overlap on one GPU (concurrent streams or
- * host threads) share the array and race: serialise them.
+ * host threads) share the array and race: serialise them.  The array's device address is
+ * looked up (hipGetSymbolAddress) on the first call on each device, or earlier by
+ * ictc_hip_message_static_prepare: call that once per device, with the device current, before
+ * capturing a HIP graph that contains this entry point, so that the capture records launches
+ * only.
  */
 #define ICTC_MSG_STATIC_SCRATCH_FLOATS 4194304
+int ictc_hip_message_static_prepare(void);
 int ictc_hip_message_edge_grad_static(const ictc_tp_desc* desc, const float* node_features,
                                       const float* harmonics, const float* gates, const float* grad_out,
                                       const int64_t* src, const int64_t* dst_rowptr,

@@ -107,3 +107,22 @@ def test_sgemm_storage_orders(ta, tb):
     got = L._sgemm(av, bv).double().cpu()
     err = (got - a @ b).abs().max() / (a @ b).abs().max()
     assert err < 1e-6, f"relative error {err:.2e}"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_sgemm_k_zero_scales_c(ta, tb):
+    """ictc_hip_sgemm with k = 0 through the C ABI: C = beta * C whatever leading dimensions and
+    operand pointers the caller passes (rocBLAS's own checks do not apply to unread operands)."""
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from ictc_o3 import _lib
+    dev = torch.device("cuda", 0)
+    m, n = 37, 23
+    c = torch.randn(m, n, device=dev)
+    want = c * 0.5
+    st = _lib.lib().ictc_hip_sgemm(ta, tb, m, n, 0, 1.0, None, 0, None, 0, 0.5, c.data_ptr(), n,
+                                   _lib.stream_of(dev))
+    torch.cuda.synchronize()
+    assert st == 0
+    assert torch.equal(c, want)

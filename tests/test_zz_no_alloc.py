@@ -87,3 +87,58 @@ def test_static_edge_grad_refuses_beyond_capacity(gpu):
     args = (ctypes.byref(plan.desc),) + (fake,) * 10
     assert lib.ictc_hip_message_edge_grad_static(*args, 8, 8, capacity + 1, None) == 5
     assert lib.ictc_hip_status_string(5) == b"input exceeds the static scratch capacity"
+
+
+def test_static_edge_grad_under_graph_capture(gpu):
+    """The entry point captured into a HIP graph (after ictc_hip_message_static_prepare resolved
+    the array's address, so the capture records launches only), replayed three times on inputs
+    changed in place, with eager work in between: every replay equals the allocating entry point
+    on the same inputs."""
+    from ictc_o3 import _lib
+    from ictc_o3.backends.hip.graph_message import message_graph
+    lib = _lib.lib()
+    plan = _plan(128, 3)
+    nodes, edges = 200, 3000
+    src, dst, x, y, gates, go = _inputs(plan, nodes, edges, 5, gpu)
+    graph = message_graph(src, dst, nodes, nodes)
+    assert lib.ictc_hip_message_static_prepare() == 0
+    ny = plan.y_width
+    dy = torch.empty(edges, ny, device=gpu)
+    dg = torch.empty(edges, plan.full_gate_width, device=gpu)
+    dxe = torch.empty(edges, plan.x_width, device=gpu)
+
+    def call(stream):
+        return lib.ictc_hip_message_edge_grad_static(
+            ctypes.byref(plan.desc), x.data_ptr(), y.data_ptr(), gates.data_ptr(), go.data_ptr(),
+            graph.src.data_ptr(), graph.rowptr_dst.data_ptr(), _lib.ptr(graph.perm_dst), dy.data_ptr(),
+            dg.data_ptr(), dxe.data_ptr(), nodes, nodes, edges, stream)
+
+    side = torch.cuda.Stream(device=gpu)
+    side.wait_stream(torch.cuda.current_stream(gpu))
+    with torch.cuda.stream(side):
+        assert call(side.cuda_stream) == 0                          # warm-up outside the capture
+    torch.cuda.current_stream(gpu).wait_stream(side)
+    torch.cuda.synchronize(gpu)
+    g = torch.cuda.CUDAGraph()
+    print("static edge grad: capture", flush=True)
+    with torch.cuda.graph(g):
+        assert call(_lib.stream_of(gpu)) == 0
+    gen = torch.Generator(device=gpu).manual_seed(9)
+    for replay in range(3):
+        with torch.no_grad():
+            x.copy_(torch.randn(x.shape, device=gpu, generator=gen))
+            go.copy_(torch.randn(go.shape, device=gpu, generator=gen))
+        g.replay()
+        torch.cuda.synchronize(gpu)
+        chunks = lib.ictc_hip_message_chunks(plan.channels)
+        dyp = torch.empty(edges, chunks, ny, device=gpu)
+        dg_ref = torch.empty_like(dg)
+        dxe_ref = torch.empty_like(dxe)
+        _lib.check(lib.ictc_hip_message_edge_grad(
+            ctypes.byref(plan.desc), x.data_ptr(), y.data_ptr(), gates.data_ptr(), go.data_ptr(),
+            graph.src.data_ptr(), graph.rowptr_dst.data_ptr(), _lib.ptr(graph.perm_dst), dyp.data_ptr(),
+            dg_ref.data_ptr(), dxe_ref.data_ptr(), nodes, nodes, edges, _lib.stream_of(gpu)),
+            "ictc_hip_message_edge_grad")
+        torch.cuda.synchronize(gpu)
+        assert torch.equal(dg, dg_ref) and torch.equal(dxe, dxe_ref), f"replay {replay}"
+        assert torch.equal(dy, dyp.sum(1)), f"replay {replay}"
