@@ -41,6 +41,7 @@ Usage: python gen_sc.py <out_dir> [configs...]   (config = "LTK", e.g. "313")
 from __future__ import annotations
 
 import os
+import re
 import sys
 from typing import Dict, List, Tuple
 
@@ -160,6 +161,57 @@ def _schedule(lmax: int, target: int, corr: int):
     return order1, vanishing, groups, out, o2_only
 
 
+def _split_args(text: str) -> List[str]:
+    """Top-level comma-separated arguments of a call's argument text."""
+    args, depth, cur = [], 0, ""
+    for ch in text:
+        if ch == "," and depth == 0:
+            args.append(cur.strip())
+            cur = ""
+            continue
+        depth += (ch == "(") - (ch == ")")
+        cur += ch
+    args.append(cur.strip())
+    return args
+
+
+_ASSIGN = re.compile(r"^(\s*)(?:\{ )?(\w+\[\d+\]) = (.*);( \})?$")
+_ZERO_LOOP = re.compile(r"for \(int i = 0; i < (\d+); \+\+i\) (\w+)\[i\] = 0\.0f;")
+
+
+def _fold_zero_starts(lines: List[str]) -> List[str]:
+    """Rewrite the first accumulation into an accumulator known to hold exactly 0,
+    ``X = sfma(a, b, X)``, as the product ``X = a * b``.  fma(a, b, +0) needs a VOP3 encoding
+    that cannot hold a literal operand, so the compiler moves the constant into an SGPR, and on
+    gfx950 a VALU instruction with an SGPR operand issues at half the rate of one whose operands
+    are VGPRs or a literal (4.1 against 2.1 cycles per wave64 instruction, measured); the product
+    has a VOP2 form with the literal.  The value only differs in the sign of an exact zero
+    product, which no later sum can tell.  Straight-line statements only: the known zeros are
+    those assigned 0.0f earlier in the same list of lines."""
+    zero, out = set(), []
+    for raw in lines:
+        for line in raw.split("\n"):
+            m = _ZERO_LOOP.search(line)
+            if m:
+                zero.update(f"{m.group(2)}[{i}]" for i in range(int(m.group(1))))
+                out.append(line)
+                continue
+            m = _ASSIGN.match(line)
+            if m:
+                indent, target, rhs, close = m.groups()
+                if rhs == "0.0f":
+                    zero.add(target)
+                else:
+                    if rhs.startswith("sfma(") and rhs.endswith(")") and target in zero:
+                        args = _split_args(rhs[5:-1])
+                        if len(args) == 3 and args[2] == target:
+                            opened = "{ " if line.strip().startswith("{ ") else ""
+                            line = f"{indent}{opened}{target} = {args[0]} * ({args[1]});{close or ''}"
+                    zero.discard(target)
+            out.append(line)
+    return out
+
+
 def emit(lmax: int, target: int, corr: int) -> str:
     D, NO = (lmax + 1) ** 2, (target + 1) ** 2
     _, offsets, ktot = _columns(lmax, target, corr)
@@ -182,9 +234,11 @@ def emit(lmax: int, target: int, corr: int) -> str:
     qn = max([1] + [off + 2 * t[0] + 1 for b in batches for t, off in b["triples"]])
 
     def nested(pairs):
-        """sum of coef * operand as one nested sfma chain ([(coef, operand)], coef a literal)."""
-        expr = "0.0f"
-        for v, operand in pairs:
+        """sum of coef * operand as one nested sfma chain ([(coef, operand)], coef a literal),
+        started by a plain product (see _fold_zero_starts)."""
+        (v0, op0), rest = pairs[0], pairs[1:]
+        expr = f"{_f(v0)} * {op0}"
+        for v, operand in rest:
             expr = f"sfma({_f(v)}, {operand}, {expr})"
         return expr
 
@@ -254,10 +308,11 @@ def emit(lmax: int, target: int, corr: int) -> str:
             qm.setdefault(q, {}).setdefault(m, []).append((v, X(lc, k)))
         lines = []
         for q in range(2 * mid + 1):
-            expr = "0.0f"
+            expr = None
             for m, terms in sorted(qm.get(q, {}).items()):
-                expr = f"sfma({U(lo, m)}, {nested(terms)}, {expr})"
-            lines.append(f"    Q[{off + q}] = {expr};")
+                expr = (f"{U(lo, m)} * ({nested(terms)})" if expr is None
+                        else f"sfma({U(lo, m)}, {nested(terms)}, {expr})")
+            lines.append(f"    Q[{off + q}] = {expr or '0.0f'};")
         return lines
 
     fsteps, bsteps, asteps = [], [], []
@@ -351,7 +406,7 @@ def emit(lmax: int, target: int, corr: int) -> str:
             out.append(f"  {{  // step {k}")
             out.extend(body)
             out.append("  }")
-        return [ln.replace("* Cs]", "* C]") for ln in out]
+        return _fold_zero_starts([ln.replace("* Cs]", "* C]") for ln in out])
 
     def merged(steps, sizes):
         """Concatenate consecutive steps into one step per group (sizes sum to len(steps))."""
@@ -381,7 +436,7 @@ def emit(lmax: int, target: int, corr: int) -> str:
         out.append("    switch (step) {")
         for k, body in enumerate(steps):
             out.append(f"    case {k}: {{")
-            out.extend("  " + line for line in body)
+            out.extend("  " + line for line in _fold_zero_starts(body))
             out.append("    } break;")
         out += ["    default: break;", "    }", "  }"]
         return out
