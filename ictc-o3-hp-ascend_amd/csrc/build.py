@@ -67,7 +67,7 @@ INSTANCE_KINDS = {
             "int64_t, int64_t, hipStream_t);\n"
             "template int launch_msg_edge_grad<{a}, {b}, {c}>(const ictc_tp_desc&, const float*, "
             "const float*, const float*, const float*, const int64_t*, const int64_t*, const int64_t*, "
-            "float*, float*, float*, int64_t, int64_t, hipStream_t);\n"
+            "float*, float*, float*, int64_t, int64_t, hipStream_t, int);\n"
             "template int launch_msg_forward_tangent<{a}, {b}, {c}>(const ictc_tp_desc&, const float*, "
             "const float*, const float*, const MsgTangent&, const int64_t*, const int64_t*, const int64_t*, "
             "float*, int64_t, int64_t, hipStream_t);\n"

@@ -18,7 +18,7 @@ namespace ictc {
   extern template int launch_msg_edge_grad<A, B, C>(const ictc_tp_desc&, const float*, const float*, \
                                                     const float*, const float*, const int64_t*,     \
                                                     const int64_t*, const int64_t*, float*, float*,  \
-                                                    float*, int64_t, int64_t, hipStream_t);          \
+                                                    float*, int64_t, int64_t, hipStream_t, int);     \
   extern template int launch_msg_forward_tangent<A, B, C>(                                          \
       const ictc_tp_desc&, const float*, const float*, const float*, const MsgTangent&,             \
       const int64_t*, const int64_t*, const int64_t*, float*, int64_t, int64_t, hipStream_t);       \
@@ -34,7 +34,7 @@ using MsgFwd = int (*)(const ictc_tp_desc&, const float*, const float*, const fl
                        const int64_t*, const int64_t*, float*, int64_t, int64_t, hipStream_t);
 using MsgEdge = int (*)(const ictc_tp_desc&, const float*, const float*, const float*, const float*,
                         const int64_t*, const int64_t*, const int64_t*, float*, float*, float*, int64_t,
-                        int64_t, hipStream_t);
+                        int64_t, hipStream_t, int);
 using MsgNode = int (*)(int, const float*, const int64_t*, const int64_t*, float*, int64_t, hipStream_t);
 using MsgFwdT = int (*)(const ictc_tp_desc&, const float*, const float*, const float*, const MsgTangent&,
                         const int64_t*, const int64_t*, const int64_t*, float*, int64_t, int64_t, hipStream_t);
@@ -209,21 +209,25 @@ int ictc_hip_message_edge_grad(const ictc_tp_desc* desc, const float* node_featu
                                const float* gates, const float* grad_out, const int64_t* src,
                                const int64_t* dst_rowptr, const int64_t* dst_perm,
                                float* grad_harmonics_partial, float* grad_gates, float* edge_grad_features,
-                               int64_t nodes_src, int64_t nodes_dst, int64_t edges, hipStream_t stream) {
+                               int64_t nodes_src, int64_t nodes_dst, int64_t edges, int accumulate_gates,
+                               hipStream_t stream) {
   const int st = ictc::msg_common(desc, nodes_src, nodes_dst, edges);
   if (st != ICTC_OK) return st;
+  if (accumulate_gates != 0 && accumulate_gates != 1) return ICTC_ERR_INVALID_ARGUMENT;
   if (edges == 0 || nodes_dst == 0 || (!grad_harmonics_partial && !grad_gates && !edge_grad_features))
     return ICTC_OK;
   if (!harmonics || !gates || !grad_out || !src || !dst_rowptr) return ICTC_ERR_INVALID_ARGUMENT;
   if ((grad_harmonics_partial || grad_gates) && !node_features) return ICTC_ERR_INVALID_ARGUMENT;
-  if (ictc::generic_degrees(*desc))
+  if (ictc::generic_degrees(*desc)) {
+    if (accumulate_gates && grad_gates) return ICTC_ERR_UNSUPPORTED;
     return ictc::generic_msg_edge_grad(*desc, node_features, harmonics, gates, grad_out, src, dst_rowptr, dst_perm,
                                        grad_harmonics_partial, grad_gates, edge_grad_features, nodes_src,
                                        nodes_dst, stream);
+  }
   const ictc::MsgEdge fn = ictc::kMsgEdge[ictc::msg_index(desc)];
   if (fn == nullptr) return ICTC_ERR_UNSUPPORTED;
   return fn(*desc, node_features, harmonics, gates, grad_out, src, dst_rowptr, dst_perm, grad_harmonics_partial,
-            grad_gates, edge_grad_features, nodes_src, nodes_dst, stream);
+            grad_gates, edge_grad_features, nodes_src, nodes_dst, stream, accumulate_gates);
 }
 
 int ictc_hip_message_static_prepare(void) {
@@ -256,7 +260,7 @@ int ictc_hip_message_edge_grad_static(const ictc_tp_desc* desc, const float* nod
                                                       dst_perm, partial, grad_gates, edge_grad_features, nodes_src,
                                                       nodes_dst, stream)
                         : fn(*desc, node_features, harmonics, gates, grad_out, src, dst_rowptr, dst_perm, partial,
-                             grad_gates, edge_grad_features, nodes_src, nodes_dst, stream);
+                             grad_gates, edge_grad_features, nodes_src, nodes_dst, stream, 0);
   if (r != ICTC_OK || partial == grad_harmonics) return r;
   const int64_t total = edges * ny;
   hipLaunchKernelGGL(ictc::chunk_sum_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0,

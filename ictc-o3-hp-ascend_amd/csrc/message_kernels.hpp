@@ -799,7 +799,7 @@ struct NodeUOf {
   static constexpr NodeU tab = make_node_u<LIN, LE, LOUT, L1>();
 };
 
-template <int LIN, int LE, int LOUT, int L1, bool JVP>
+template <int LIN, int LE, int LOUT, int L1, bool JVP, bool ACC = false>
 __global__ void __launch_bounds__(kMsgBlock)
 msg_edge_grad_degree_kernel(const float* __restrict__ x, const float* __restrict__ y, const float* __restrict__ g,
                           const MsgTangent t, const float* __restrict__ go, const int64_t* __restrict__ src,
@@ -871,6 +871,7 @@ msg_edge_grad_degree_kernel(const float* __restrict__ x, const float* __restrict
     float yv[NT][NY];
     float xr[NT][NI];
     float gv[NT][NPG];
+    float dgp[ACC ? NPG : 1];   // ACC: the gate gradients already in dg (this pass adds to them)
     float prev;
   };
   auto fetch = [&](int64_t e, int64_t s, EdgeIn& in) {
@@ -891,6 +892,11 @@ msg_edge_grad_degree_kernel(const float* __restrict__ x, const float* __restrict
       const rsrc_t rg = make_rsrc(gs[q] + e * NP * C, NP * row);
 #pragma unroll
       for (int k = 0; k < NPG; ++k) in.gv[q][k] = buf_load_vs<kNonTemporal>(rg, vc, GT.path[k] * row);
+    }
+    if constexpr (ACC) {
+      const rsrc_t rdg = make_rsrc(dg + e * NP * C, NP * row);
+#pragma unroll
+      for (int k = 0; k < NPG; ++k) in.dgp[k] = buf_load_vs(rdg, vc, GT.path[k] * row);
     }
     in.prev = (wy && !first) ? dyp[(e * nchunks + chunk) * NY + wjc] : 0.f;
   };
@@ -981,6 +987,7 @@ msg_edge_grad_degree_kernel(const float* __restrict__ x, const float* __restrict
 #pragma unroll
         for (int i = 0; i < NI; ++i) dxl[i] = fmaf(in.gv[0][k], w[i], dxl[i]);
       }
+      if constexpr (ACC) dgv += in.dgp[k];
       buf_store_lane(rdg, live, vc + p * row, dgv);   // null dg: empty descriptor
     });
     if (dxe != nullptr) {
@@ -1042,17 +1049,27 @@ msg_zero_rows_kernel(const int64_t* __restrict__ rowptr, int64_t nodes_dst, floa
 }
 
 // One launch per input degree that has paths (dY partials accumulated across them in launch order).
+// accumulate (first order only, dg non-null): add the gate gradients into dg instead of overwriting
+// it (each edge's prior dg values are requested with its other loads).
 template <int LIN, int LE, int LOUT, bool JVP>
 int launch_msg_edge_grad_degrees(const ictc_tp_desc& d, const float* x, const float* y, const float* g,
                                  const MsgTangent& t, const float* go, const int64_t* src, const int64_t* rowptr,
                                  const int64_t* perm, float* dyp, float* dg, float* dxe, int64_t nodes_src,
-                                 int64_t nodes_dst, hipStream_t stream) {
+                                 int64_t nodes_dst, hipStream_t stream, bool accumulate = false) {
   const int nchunks = (d.channels + kWave - 1) / kWave;
   const dim3 grid(static_cast<unsigned>(nodes_dst * nchunks));   // one block per (receiver, chunk)
   int first = 1;
   auto one = [&](auto deg) {
     constexpr int L1 = decltype(deg)::value;
     if constexpr (DegreeGroupOf<LIN, LE, LOUT, L1>::tab.np > 0) {
+      if constexpr (!JVP) {
+        if (accumulate) {
+          hipLaunchKernelGGL((msg_edge_grad_degree_kernel<LIN, LE, LOUT, L1, false, true>), grid, dim3(kMsgBlock), 0,
+                             stream, x, y, g, t, go, src, rowptr, perm, dyp, dg, dxe, d, nodes_src, nchunks, first);
+          first = 0;
+          return;
+        }
+      }
       hipLaunchKernelGGL((msg_edge_grad_degree_kernel<LIN, LE, LOUT, L1, JVP>), grid, dim3(kMsgBlock), 0, stream, x,
                          y, g, t, go, src, rowptr, perm, dyp, dg, dxe, d, nodes_src, nchunks, first);
       first = 0;
@@ -1084,9 +1101,10 @@ template <int LIN, int LE, int LOUT>
 int launch_msg_edge_grad(const ictc_tp_desc& d, const float* x, const float* y, const float* g,
                          const float* go, const int64_t* src, const int64_t* rowptr, const int64_t* perm,
                          float* dyp, float* dg, float* dxe, int64_t nodes_src, int64_t nodes_dst,
-                         hipStream_t stream) {
+                         hipStream_t stream, int accumulate_gates) {
   return launch_msg_edge_grad_degrees<LIN, LE, LOUT, false>(d, x, y, g, MsgTangent{}, go, src, rowptr, perm, dyp, dg,
-                                                           dxe, nodes_src, nodes_dst, stream);
+                                                           dxe, nodes_src, nodes_dst, stream,
+                                                           accumulate_gates != 0 && dg != nullptr);
 }
 
 template <int LIN, int LE, int LOUT>

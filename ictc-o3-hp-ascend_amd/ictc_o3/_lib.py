@@ -15,7 +15,7 @@ import torch  # noqa: F401  (must precede CDLL, see module docstring)
 
 MAX_PATHS = 128
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libictc_hip.so")
-ABI_VERSION = 15
+ABI_VERSION = 16
 
 
 class TpDesc(ctypes.Structure):
@@ -81,7 +81,7 @@ _SIGNATURES = {
     "ictc_hip_message_forward": (ctypes.c_int, [ctypes.POINTER(TpDesc), _P, _P, _P, _P, _P, _P, _P,
                                                 _I64, _I64, _I64, _P]),
     "ictc_hip_message_edge_grad": (ctypes.c_int, [ctypes.POINTER(TpDesc), _P, _P, _P, _P, _P, _P, _P,
-                                                  _P, _P, _P, _I64, _I64, _I64, _P]),
+                                                  _P, _P, _P, _I64, _I64, _I64, ctypes.c_int, _P]),
     "ictc_hip_message_static_prepare": (ctypes.c_int, []),
     "ictc_hip_message_edge_grad_static": (ctypes.c_int, [ctypes.POINTER(TpDesc), _P, _P, _P, _P, _P, _P, _P,
                                                          _P, _P, _P, _I64, _I64, _I64, _P]),

@@ -136,8 +136,10 @@ def _forward_raw(plan: TensorProductPlan, graph: MessageGraph, x, y, g, bonds=No
     return out
 
 
-def _backward_raw(plan: TensorProductPlan, graph: MessageGraph, need, x, y, g, go):
-    """First-order adjoints; the edge kernels read the harmonics y (not bond rows)."""
+def _backward_raw(plan: TensorProductPlan, graph: MessageGraph, need, x, y, g, go, dg_into=None):
+    """First-order adjoints; the edge kernels read the harmonics y (not bond rows).  dg_into: a gate
+    gradient [E, P*C] already computed for the same gates, which the kernel adds this one into (the
+    returned dg is then that buffer)."""
     dev = go.device
     lib = _lib.lib()
     stream = _lib.stream_of(dev)
@@ -148,7 +150,8 @@ def _backward_raw(plan: TensorProductPlan, graph: MessageGraph, need, x, y, g, g
         if need[1]:
             dyp = torch.empty(graph.edges, nch, plan.y_width, device=dev, dtype=torch.float32)
         if need[2]:
-            dg = torch.empty(graph.edges, plan.full_gate_width, device=dev, dtype=torch.float32)
+            dg = dg_into if dg_into is not None else torch.empty(graph.edges, plan.full_gate_width, device=dev,
+                                                                 dtype=torch.float32)
         if need[0]:
             dxe = torch.empty(graph.edges, plan.x_width, device=dev, dtype=torch.float32)
         if need[0] or need[1] or need[2]:
@@ -156,7 +159,8 @@ def _backward_raw(plan: TensorProductPlan, graph: MessageGraph, need, x, y, g, g
             _lib.check(lib.ictc_hip_message_edge_grad(
                 ctypes.byref(plan.desc), xp, _p(y), _p(g), go.data_ptr(), graph.src.data_ptr(),
                 graph.rowptr_dst.data_ptr(), _p(graph.perm_dst), _p(dyp), _p(dg), _p(dxe), graph.nodes_src,
-                graph.nodes_dst, graph.edges, stream), "ictc_hip_message_edge_grad")
+                graph.nodes_dst, graph.edges, int(dg_into is not None and need[2]), stream),
+                "ictc_hip_message_edge_grad")
         if dyp is not None:
             dy = dyp[:, 0] if nch == 1 else dyp.sum(1)
     else:
@@ -224,6 +228,45 @@ def _add(acc, value):
     return value if acc is None else acc + value
 
 
+class _GateGradSlot:
+    """Hand-over of a gate gradient between the two autograd nodes that both produce a gradient
+    for the same message gates in a force-loss double backward: the message forward's node (the
+    energy path) and the node of its VJP (the force path, recorded when the forces are taken with
+    create_graph).  Without it the engine sums the two [E, P*C] gradients with one more pass over
+    three such tensors.  When the VJP's node runs first and the forward's node is still to run and
+    will produce a gate gradient, the VJP's node leaves its gate gradient here and returns none;
+    the forward's node then has the edge kernel add its own gradient into that buffer
+    (``ictc_hip_message_edge_grad`` accumulate mode) and returns the sum.  In any other order
+    both return their gradients and the engine adds them as usual."""
+    __slots__ = ("stash", "forward_done")
+
+    def __init__(self):
+        self.stash = None            # a gate gradient deferred to the forward's node
+        self.forward_done = False    # the forward's node ran in a backward that records nothing
+
+
+# The hand-over of _GateGradSlot (tests switch it off to compare: the results are bit-identical,
+# a float add being commutative).
+GATE_GRAD_HANDOVER = True
+
+
+def _defer_gate_grad(ctx, plan: TensorProductPlan, graph: MessageGraph, g) -> bool:
+    """Whether the VJP node (ctx) hands its gate gradient to the message forward's node."""
+    slot, fwd = getattr(ctx, "slot", None), getattr(ctx, "forward_node", None)
+    if (not GATE_GRAD_HANDOVER or torch.is_grad_enabled() or slot is None or fwd is None or slot.stash is not None
+            or slot.forward_done):
+        return False
+    if plan.generic or graph.edges == 0 or not fwd.needs_input_grad[4]:
+        return False
+    query = getattr(torch._C, "_will_engine_execute_node", None)
+    if query is None:
+        return False
+    try:
+        return bool(query(fwd)) and required_gradients((g,), (True,))[0]
+    except (RuntimeError, AttributeError, AssertionError):
+        return False
+
+
 class _Forward(torch.autograd.Function):
     """bonds: the bond rows of y when the caller has them (derived data, not an input)."""
 
@@ -233,23 +276,36 @@ class _Forward(torch.autograd.Function):
         if bonds is None:
             bonds = _bonds(plan, graph, y)
         ctx.bonds = bonds
+        ctx.slot = _GateGradSlot()
         ctx.save_for_backward(x, y, g)
         return _forward_raw(plan, graph, x, y, g, bonds)
 
     @staticmethod
     def backward(ctx, go):
         x, y, g = ctx.saved_tensors
+        stash = None
+        if not torch.is_grad_enabled():          # a backward that records nothing (the last one)
+            stash, ctx.slot.stash = ctx.slot.stash, None
+            ctx.slot.forward_done = True
         need = required_gradients((x, y, g), ctx.needs_input_grad[2:5])
         if go is None or not any(need):
-            return None, None, None, None, None, None
-        dx, dy, dg = vjp(ctx.plan, ctx.graph, need, x, y, g, go.contiguous(), ctx.bonds)
+            return None, None, None, None, stash, None
+        if stash is not None and need[2] and not ctx.plan.generic and ctx.graph.edges:
+            # add this gate gradient into the one the VJP's node deferred here (inside the kernel)
+            dx, dy, dg = _backward_raw(ctx.plan, ctx.graph, need, x, y, g, go.contiguous(), dg_into=stash)
+        else:
+            dx, dy, dg = vjp(ctx.plan, ctx.graph, need, x, y, g, go.contiguous(), ctx.bonds, slot=ctx.slot,
+                             forward_node=ctx)
+            if stash is not None:
+                dg = stash if dg is None else dg + stash
         return None, None, dx, dy, dg, None
 
 
 class _Backward(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, plan, graph, need, x, y, g, go, bonds=None):
+    def forward(ctx, plan, graph, need, x, y, g, go, bonds=None, slot=None, forward_node=None):
         ctx.plan, ctx.graph, ctx.need = plan, graph, need
+        ctx.slot, ctx.forward_node = slot, forward_node   # see _GateGradSlot
         ctx.set_materialize_grads(False)
         ctx.bonds = bonds   # for the forward passes of the double backward (formed there if None)
         ctx.save_for_backward(x, y, g, go)
@@ -274,7 +330,9 @@ class _Backward(torch.autograd.Function):
                 and hx is not None and hy is not None and hg is not None and (nx or ny or ng or no)):
             gx, gy, gg, ggo = _second_order_raw(plan, graph, (nx, ny, ng, no), x, y, g, go, hx.contiguous(),
                                                 hy.contiguous(), hg.contiguous(), bonds)
-            return None, None, None, gx, gy, gg, ggo, None
+            if gg is not None and _defer_gate_grad(ctx, plan, graph, g):
+                ctx.slot.stash, gg = gg, None
+            return None, None, None, gx, gy, gg, ggo, None, None, None
         gx = gy = gg = ggo = None
         if hx is not None:
             hx = hx.contiguous()
@@ -297,16 +355,18 @@ class _Backward(torch.autograd.Function):
                 gx, gy = _add(gx, a), _add(gy, b)
             if no:
                 ggo = _add(ggo, _Forward.apply(plan, graph, x, y, hg, bonds))
-        return None, None, None, gx, gy, gg, ggo, None
+        if gg is not None and _defer_gate_grad(ctx, plan, graph, g):
+            ctx.slot.stash, gg = gg, None
+        return None, None, None, gx, gy, gg, ggo, None, None, None
 
 
-def vjp(plan, graph, need, x, y, g, go, bonds=None):
+def vjp(plan, graph, need, x, y, g, go, bonds=None, slot=None, forward_node=None):
     need = tuple(bool(n) for n in need)
     if not any(need):
         return None, None, None
     if not torch.is_grad_enabled():       # nothing recorded: skip the autograd Function
         return _backward_raw(plan, graph, need, x, y, g, go)
-    outs = _Backward.apply(plan, graph, need, x, y, g, go, bonds)
+    outs = _Backward.apply(plan, graph, need, x, y, g, go, bonds, slot, forward_node)
     return tuple(o if n else None for o, n in zip(outs, need))
 
 

@@ -141,7 +141,7 @@ def _backward_raw(plan, graph, ranges: RangePlan, need, x, y, hidden, weight, bi
         _lib.check(lib.ictc_hip_message_edge_grad(
             ctypes.byref(plan.desc), x.data_ptr() if (ny or need_dg) else None, yr.data_ptr(), g.data_ptr(),
             go_r.data_ptr(), ranges.src_sorted[s0:s1].data_ptr(), rowptr.data_ptr(), None, _lib.ptr(dyp),
-            _lib.ptr(dg), _lib.ptr(dxe), graph.nodes_src, n1 - n0, rows, stream), "ictc_hip_message_edge_grad")
+            _lib.ptr(dg), _lib.ptr(dxe), graph.nodes_src, n1 - n0, rows, 0, stream), "ictc_hip_message_edge_grad")
         if ny:
             dy[s0:s1] = dyp[:, 0] if nch == 1 else dyp.sum(1)
         if need_dg:

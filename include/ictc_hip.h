@@ -174,15 +174,19 @@ int ictc_hip_message_chunks(int channels);
  *                                 contribution to the source-feature gradient
  *                                 [edges, C*(L_in+1)^2] (features layout)
  * Any output may be null; node_features may be null when only edge_grad_features is
- * requested.  Replaces the dr/dg terms of ictc_epilogue_adjoint
- * (ascendc/op_kernel/epilogue_adjoint.cpp:6-208).
+ * requested.  accumulate_gates = 1 adds the gate gradients into grad_gates (which then holds
+ * a gradient already, e.g. the other contribution to the same gates in a force-loss double
+ * backward) instead of overwriting it; 0 overwrites.  Degree sets with a degree above 3
+ * return ICTC_ERR_UNSUPPORTED for accumulate_gates = 1.  Replaces the dr/dg terms of
+ * ictc_epilogue_adjoint (ascendc/op_kernel/epilogue_adjoint.cpp:6-208).
  */
 int ictc_hip_message_edge_grad(const ictc_tp_desc* desc, const float* node_features,
                                const float* harmonics, const float* gates, const float* grad_out,
                                const int64_t* src, const int64_t* dst_rowptr,
                                const int64_t* dst_perm, float* grad_harmonics_partial,
                                float* grad_gates, float* edge_grad_features, int64_t nodes_src,
-                               int64_t nodes_dst, int64_t edges, hipStream_t stream);
+                               int64_t nodes_dst, int64_t edges, int accumulate_gates,
+                               hipStream_t stream);
 
 /*
  * No counterpart in the reference: for callers that cannot allocate device memory (code under

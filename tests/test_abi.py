@@ -177,4 +177,4 @@ def test_message_rejects_node_tensors_beyond_32bit_offsets():
     assert lib.ictc_hip_message_forward_tangent(ctypes.byref(d3), *([fake] * 8), None, fake,
                                                 too_many, 4, 8, None) == 2
     assert lib.ictc_hip_message_edge_grad(ctypes.byref(d3), fake, fake, fake, fake, fake, fake, None,
-                                          fake, fake, fake, too_many, 4, 8, None) == 2
+                                          fake, fake, fake, too_many, 4, 8, 0, None) == 2

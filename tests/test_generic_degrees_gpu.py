@@ -185,7 +185,7 @@ def test_message_vjp_allocation_free_entry_point(gpu):
                   graph.rowptr_dst.data_ptr(), perm)
         stream = _lib.stream_of(gpu)
         _lib.check(lib.ictc_hip_message_edge_grad(ctypes.byref(plan.desc), *common, dyp.data_ptr(), dg1.data_ptr(),
-                                                  dx1.data_ptr(), nodes, nodes, edges, stream), "edge_grad")
+                                                  dx1.data_ptr(), nodes, nodes, edges, 0, stream), "edge_grad")
         _lib.check(lib.ictc_hip_message_edge_grad_static(ctypes.byref(plan.desc), *common, dy2.data_ptr(),
                                                          dg2.data_ptr(), dx2.data_ptr(), nodes, nodes, edges, stream),
                    "edge_grad_static")

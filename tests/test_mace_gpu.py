@@ -162,3 +162,34 @@ def test_configure_model_selects_hip_and_streaming(gpu):
     pred = energy_and_forces(model, **{**graph, "positions": pos}, training=True)
     backward_to_parameters(force_loss(pred, pos.shape[0]), model, pos)
     assert pos.grad is not None and torch.isfinite(pos.grad).all()
+
+
+def test_gate_gradient_handover(gpu, monkeypatch):
+    """Force-loss backward: the force path's gate gradient (the message VJP's double backward) is
+    handed to the energy path's message VJP, whose edge kernel adds its own gate gradient into it,
+    instead of the engine adding two [E, P*C] tensors.  The parameter gradients are bit-identical
+    to those of the engine's sum (a float add is commutative), and the hand-over is taken."""
+    import ictc_o3.backends.hip.graph_message as GM
+    from mace_hip import energy_and_forces, force_loss
+    from mace_hip.runtime import backward_to_parameters
+    accumulated = []
+    raw = GM._backward_raw
+
+    def spy(*args, dg_into=None, **kw):
+        accumulated.append(dg_into is not None)
+        return raw(*args, dg_into=dg_into, **kw)
+
+    monkeypatch.setattr(GM, "_backward_raw", spy)
+    grads = []
+    for handover in (False, True):
+        monkeypatch.setattr(GM, "GATE_GRAD_HANDOVER", handover)
+        accumulated.clear()
+        model, graph, _, _ = _setup(gpu, channels=64, seed=9)
+        loss = force_loss(energy_and_forces(model, **graph, training=True), graph["positions"].shape[0])
+        backward_to_parameters(loss, model, graph["positions"])
+        grads.append({n: p.grad.clone() for n, p in model.named_parameters() if p.grad is not None})
+        print(f"handover={handover}: accumulate-mode edge kernels {sum(accumulated)}", flush=True)
+        assert sum(accumulated) == (len(model.interactions) if handover else 0)
+    assert grads[0].keys() == grads[1].keys()
+    for n in grads[0]:
+        assert torch.equal(grads[1][n], grads[0][n]), n

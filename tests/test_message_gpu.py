@@ -272,3 +272,42 @@ def test_frozen_weight_written_through_data(gpu, layout):
     xe = x[src]
     assert_rel(tp(xe.to(gpu), dev[1], dev[2]), ref.forward(xe.double(), y.double(), g.double()),
                what="weighted TP")
+
+
+@pytest.mark.parametrize("c,lin,le,lout", [(64, 2, 2, 2), (128, 3, 3, 3), (96, 0, 3, 3)])
+def test_edge_grad_accumulate_mode(gpu, c, lin, le, lout):
+    """ictc_hip_message_edge_grad with accumulate_gates = 1 through the C ABI: grad_gates ends as
+    its prior contents plus the gate gradient (bit-identical to adding them afterwards); the
+    other outputs are those of the overwriting call."""
+    import ctypes
+    from ictc_o3 import _lib
+    from ictc_o3.backends.hip.graph_message import message_graph
+    from ictc_o3.backends.hip.tensor_product import TensorProductPlan
+    from ictc_o3.basis.ictd_irreps import triangle_paths
+    plan = TensorProductPlan(triangle_paths(lin, le, lout), c, lin, le)
+    lib = _lib.lib()
+    nodes, edges = 40, 700
+    src, dst = _graph(nodes, edges, c + lin)
+    g = torch.Generator().manual_seed(21)
+    x = torch.randn(nodes, plan.x_width, generator=g).to(gpu)
+    n = torch.nn.functional.normalize(torch.randn(edges, 3, generator=g, dtype=torch.float64), dim=-1)
+    y = B.direction_harmonics_packed(n, le).float().to(gpu)
+    gates = torch.randn(edges, plan.full_gate_width, generator=g).to(gpu)
+    go = torch.randn(nodes, plan.full_out_width, generator=g).to(gpu)
+    prior = torch.randn(edges, plan.full_gate_width, generator=g).to(gpu)
+    graph = message_graph(src.to(gpu), dst.to(gpu), nodes, nodes)
+    chunks = lib.ictc_hip_message_chunks(c)
+    outs = []
+    for acc in (0, 1):
+        dyp = torch.empty(edges, chunks, plan.y_width, device=gpu)
+        dg = prior.clone() if acc else torch.empty_like(prior)
+        dxe = torch.empty(edges, plan.x_width, device=gpu)
+        print(f"edge grad accumulate={acc}: C={c} degrees={(lin, le, lout)}", flush=True)
+        _lib.check(lib.ictc_hip_message_edge_grad(
+            ctypes.byref(plan.desc), x.data_ptr(), y.data_ptr(), gates.data_ptr(), go.data_ptr(),
+            graph.src.data_ptr(), graph.rowptr_dst.data_ptr(), _lib.ptr(graph.perm_dst), dyp.data_ptr(),
+            dg.data_ptr(), dxe.data_ptr(), nodes, nodes, edges, acc, _lib.stream_of(gpu)), "edge_grad")
+        outs.append((dyp, dg, dxe))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[1][1], outs[0][1] + prior)
+    assert torch.equal(outs[1][0], outs[0][0]) and torch.equal(outs[1][2], outs[0][2])

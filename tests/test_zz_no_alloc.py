@@ -53,7 +53,7 @@ def _edge_grads(plan, nodes, edges, seed, dev):
     dg = torch.empty(edges, plan.full_gate_width, device=dev)
     dxe = torch.empty(edges, plan.x_width, device=dev)
     _lib.check(lib.ictc_hip_message_edge_grad(*common, dyp.data_ptr(), dg.data_ptr(), dxe.data_ptr(), nodes,
-                                              nodes, edges, stream), "ictc_hip_message_edge_grad")
+                                              nodes, edges, 0, stream), "ictc_hip_message_edge_grad")
     dy2 = torch.full((edges, ny), float("nan"), device=dev)
     dg2 = torch.full_like(dg, float("nan"))
     dxe2 = torch.full_like(dxe, float("nan"))
@@ -137,7 +137,7 @@ def test_static_edge_grad_under_graph_capture(gpu):
         _lib.check(lib.ictc_hip_message_edge_grad(
             ctypes.byref(plan.desc), x.data_ptr(), y.data_ptr(), gates.data_ptr(), go.data_ptr(),
             graph.src.data_ptr(), graph.rowptr_dst.data_ptr(), _lib.ptr(graph.perm_dst), dyp.data_ptr(),
-            dg_ref.data_ptr(), dxe_ref.data_ptr(), nodes, nodes, edges, _lib.stream_of(gpu)),
+            dg_ref.data_ptr(), dxe_ref.data_ptr(), nodes, nodes, edges, 0, _lib.stream_of(gpu)),
             "ictc_hip_message_edge_grad")
         torch.cuda.synchronize(gpu)
         assert torch.equal(dg, dg_ref) and torch.equal(dxe, dxe_ref), f"replay {replay}"
