@@ -509,6 +509,55 @@ def _bench_message(device):
                     **real.get("vjp", {})}}
 
 
+def _bench_message3(device):
+    """The MACE layer-1 message at lmax 3 on the cfg-4 graph (C = 128, 2,048 atoms): forward, VJP,
+    and the tangent forward and tangent VJP of the force-loss double backward, each one call of
+    the raw launchers on HBM-resident inputs.  Unique-byte models: per edge the harmonics, gates
+    and source index read once and the per-edge outputs (dg, dY) written once; per node the
+    features and cotangent read once and the node outputs written once; the tangent passes also
+    read the tangent harmonics, gates and features.  Bond rows and x[src] gathers beyond the
+    first are design traffic outside the models."""
+    from ictc_o3 import EdgeTensorProduct
+    from ictc_o3.backends.hip.graph_message import _backward_raw, _bonds, _forward_raw, _second_order_raw, message_graph
+    c, l = 128, 3
+    op = EdgeTensorProduct.create(channels=c, input_lmax=l, edge_lmax=l, device=device)
+    plan = op.plan
+    _, graph_in = _mace_graph(device)
+    src, dst = graph_in["edge_src"], graph_in["edge_dst"]
+    n, e = MACE_ATOMS, src.numel()
+    pos = graph_in["positions"]
+    vec = pos[dst] - pos[src] + graph_in["edge_shifts"].to(pos.dtype) @ graph_in["cell"][0]
+    from ictc_o3.backends.hip.harmonics import direction_harmonics_packed
+    y = direction_harmonics_packed((vec / vec.norm(dim=1, keepdim=True)).contiguous(), l).contiguous()
+    gen = torch.Generator(device="cpu").manual_seed(3)
+    nx, ny, ng, no = 16 * c, 16, 23 * c, 99 * c
+    x, tx = (torch.randn(n, nx, generator=gen).to(device) for _ in range(2))
+    g, tg = (torch.randn(e, ng, generator=gen).to(device) / math.sqrt(23) for _ in range(2))
+    ty = torch.randn(e, ny, generator=gen).to(device)
+    go = torch.randn(n, no, generator=gen).to(device)
+    graph = message_graph(src, dst, n, n)
+    bonds = _bonds(plan, graph, y)
+    need3, need4 = (True, True, True), (True, True, True, True)
+    calls = {
+        "forward": (lambda: _forward_raw(plan, graph, x, y, g, bonds),
+                    e * (4 * (ny + ng) + 8) + n * 4 * (nx + no)),
+        "vjp": (lambda: _backward_raw(plan, graph, need3, x, y, g, go),
+                e * (4 * 2 * (ny + ng) + 8) + n * 4 * (2 * nx + no)),
+        "tangent_forward": (lambda: _second_order_raw(plan, graph, (False, False, False, True), x, y, g, go, tx, ty,
+                                                      tg, bonds),
+                            e * (4 * 2 * (ny + ng) + 8) + n * 4 * (2 * nx + no)),
+        "tangent_vjp": (lambda: _second_order_raw(plan, graph, (True, True, True, False), x, y, g, go, tx, ty, tg,
+                                                  bonds),
+                        e * (4 * (2 * (ny + ng) + ny + ng) + 8) + n * 4 * (3 * nx + no)),
+    }
+    out = {"workload": "cfg4 graph, MACE layer-1 message C128/lmax3, 2,048 atoms, r_c 5 A", "edges": e}
+    for name, (fn, nbytes) in calls.items():
+        ms = _event_ms(fn, device)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {"mean_ms": ms, "algorithmic_bytes": nbytes, "achieved_gbs": gbs, "frac": gbs / HBM_PEAK_GBS}
+    return out
+
+
 SC_C, SC_L, SC_T, SC_K, SC_NODES, SC_S = 128, 3, 1, 3, 65536, 10
 
 
@@ -858,7 +907,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--kernels-only", action="store_true")
-    ap.add_argument("--only", choices=("tp", "tp0", "message", "sc", "mace", "graph", "linear", "generic"),
+    ap.add_argument("--only", choices=("tp", "tp0", "message", "message3", "sc", "mace", "graph", "linear",
+                                       "generic"),
                     default=None,
                     help="run one section and print its JSON (for profiling)")
     args = ap.parse_args()
@@ -873,9 +923,10 @@ def main() -> int:
     if args.kernels_only:
         _kernels_only(op.plan, device)
         return 0
-    if args.only in ("tp0", "message", "sc", "mace", "graph", "linear", "generic"):
-        fn = {"tp0": _bench_tp_cfg0, "message": _bench_message, "sc": _bench_sc, "mace": _bench_mace,
-              "graph": _bench_graph, "linear": _bench_linear, "generic": _bench_generic}[args.only]
+    if args.only in ("tp0", "message", "message3", "sc", "mace", "graph", "linear", "generic"):
+        fn = {"tp0": _bench_tp_cfg0, "message": _bench_message, "message3": _bench_message3, "sc": _bench_sc,
+              "mace": _bench_mace, "graph": _bench_graph, "linear": _bench_linear,
+              "generic": _bench_generic}[args.only]
         print(json.dumps({args.only: fn(device)}), flush=True)
         return 0
     elapsed, vjp_ms, fwd_ms = _time_gpu(args, op.plan, device)
@@ -889,7 +940,7 @@ def main() -> int:
     others = {}
     if args.only is None:
         others = {"tp_cfg0": _bench_tp_cfg0(device), "message_cfg2": _bench_message(device),
-                  "sc_cfg3": _bench_sc(device),
+                  "message_cfg4_lmax3": _bench_message3(device), "sc_cfg3": _bench_sc(device),
                   "mace_cfg4": _bench_mace(device), "message_linear_cfg4": _bench_linear(device),
                   "radius_graph": _bench_graph(device), "tp_generic_l4": _bench_generic(device)}
         if not args.no_cpu:
