@@ -301,7 +301,37 @@ def _probe_lib():
     lib = ctypes.CDLL(path)
     lib.ictc_probe_valu_fma.restype = ctypes.c_int
     lib.ictc_probe_valu_fma.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    lib.ictc_probe_valu_form.restype = ctypes.c_int
+    lib.ictc_probe_valu_form.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
     return lib
+
+
+VALU_FORMS = ("v_fmac_f32_e32 v,v,v", "v_fmac_f32_e32 v,literal,v", "v_fma_f32 v,v,v,v (VOP3)",
+              "v_fmac_f32_e32 v,s,v (SGPR operand)", "v_fmac_f32_e64 v,v,v (VOP3 encoding)", "v_fmac_f32_dpp",
+              "v_cndmask_b32_e64 (SGPR-pair mask)", "v_readlane_b32")
+
+
+def _valu_form_cycles(device, grid: int = 16384, iters: int = 2048, clock_ghz: float = 2.4):
+    """Issue cost of VALU instruction forms (stream_probe.hip valu_form_kernel): nanoseconds per
+    wave instruction per SIMD at full occupancy, and the same in cycles of the 2.4 GHz peak
+    clock; None if the probe library is absent."""
+    import ctypes
+    lib = _probe_lib()
+    if lib is None:
+        return None
+    out = torch.empty(grid * 256, device=device)
+    stream = torch.cuda.current_stream(device)
+    simds = torch.cuda.get_device_properties(device).multi_processor_count * 4
+    res = {}
+    for form, name in enumerate(VALU_FORMS):
+        def launch():
+            if lib.ictc_probe_valu_form(out.data_ptr(), form, iters, grid, ctypes.c_void_p(stream.cuda_stream)) != 0:
+                raise RuntimeError("VALU form probe launch failed")
+        ms = _event_ms(launch, device, reps=5, warmup=2)
+        wave_insts = grid * 4 * iters * 16
+        ns = ms * 1e6 / (wave_insts / simds)
+        res[name] = {"ns_per_wave_instruction_per_simd": ns, "cycles_at_2.4GHz": ns * clock_ghz}
+    return res
 
 
 def _valu_fma_tflops(device, grid: int = 16384, iters: int = 2048, reps: int = 5):
@@ -908,7 +938,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--kernels-only", action="store_true")
     ap.add_argument("--only", choices=("tp", "tp0", "message", "message3", "sc", "mace", "graph", "linear",
-                                       "generic"),
+                                       "generic", "valu"),
                     default=None,
                     help="run one section and print its JSON (for profiling)")
     args = ap.parse_args()
@@ -923,10 +953,10 @@ def main() -> int:
     if args.kernels_only:
         _kernels_only(op.plan, device)
         return 0
-    if args.only in ("tp0", "message", "message3", "sc", "mace", "graph", "linear", "generic"):
+    if args.only in ("tp0", "message", "message3", "sc", "mace", "graph", "linear", "generic", "valu"):
         fn = {"tp0": _bench_tp_cfg0, "message": _bench_message, "message3": _bench_message3, "sc": _bench_sc,
               "mace": _bench_mace, "graph": _bench_graph, "linear": _bench_linear,
-              "generic": _bench_generic}[args.only]
+              "generic": _bench_generic, "valu": _valu_form_cycles}[args.only]
         print(json.dumps({args.only: fn(device)}), flush=True)
         return 0
     elapsed, vjp_ms, fwd_ms = _time_gpu(args, op.plan, device)

@@ -11,7 +11,8 @@
 // A second probe measures the fp32 vector (VALU) FMA rate this build can reach: every lane
 // runs 16 independent fma chains on registers (scalar v_fma/v_fmac: the library is compiled
 // without packed FP32, so no v_pk_fma_f32 can appear) and writes one float, so the work is
-// 32 FLOPs per lane per iteration and memory traffic is negligible.
+// 32 FLOPs per lane per iteration and memory traffic is negligible.  A third gives the issue
+// cost of individual VALU instruction forms (operand kinds and encodings).
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 
@@ -57,6 +58,44 @@ __global__ void __launch_bounds__(256) valu_fma_kernel(float* __restrict__ out, 
   out[blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x] = s;
 }
 
+// Issue cost of one VALU instruction form: every lane runs 16 independent chains of that
+// instruction (inline asm, so the form is exactly the one named), iters times.  Forms:
+//   0 v_fmac_f32_e32 v, v, v      (VOP2, all operands VGPRs)
+//   1 v_fmac_f32_e32 v, literal, v
+//   2 v_fma_f32 v, v, v, v        (VOP3, all VGPRs, destination distinct from the addend)
+//   3 v_fmac_f32_e32 v, s, v      (an SGPR operand)
+//   4 v_fmac_f32_e64 v, v, v      (the VOP3 encoding of fmac)
+//   5 v_fmac_f32_dpp v, v, v      (a DPP lane permutation)
+//   6 v_cndmask_b32_e64 v, v, v, s[..]   (a lane mask in an SGPR pair)
+//   7 v_readlane_b32 s, v, 1
+template <int FORM>
+__global__ void __launch_bounds__(256) valu_form_kernel(float* __restrict__ out, int iters, float b, float c) {
+  float a[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) a[i] = static_cast<float>(threadIdx.x + i);
+  const float vb = b + 1e-7f * static_cast<float>(threadIdx.x & 1);
+  const float vc = c * static_cast<float>(1 + (threadIdx.x & 1));
+  const unsigned long long mask = __ballot(threadIdx.x & 1);
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if constexpr (FORM == 0) asm volatile("v_fmac_f32_e32 %0, %1, %2" : "+v"(a[i]) : "v"(vb), "v"(vc));
+      if constexpr (FORM == 1) asm volatile("v_fmac_f32_e32 %0, 0x3f7fbe77, %1" : "+v"(a[i]) : "v"(vc));
+      if constexpr (FORM == 2) asm volatile("v_fma_f32 %0, %1, %2, %3" : "=v"(a[i]) : "v"(vb), "v"(vc), "v"(a[(i + 1) & 15]));
+      if constexpr (FORM == 3) asm volatile("v_fmac_f32_e32 %0, %1, %2" : "+v"(a[i]) : "s"(b), "v"(vc));
+      if constexpr (FORM == 4) asm volatile("v_fmac_f32_e64 %0, %1, %2" : "+v"(a[i]) : "v"(vb), "v"(vc));
+      if constexpr (FORM == 5)
+        asm volatile("v_fmac_f32_dpp %0, %1, %2 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf" : "+v"(a[i]) : "v"(vb), "v"(vc));
+      if constexpr (FORM == 6) asm volatile("v_cndmask_b32_e64 %0, %0, %1, %2" : "+v"(a[i]) : "v"(vb), "s"(mask));
+      if constexpr (FORM == 7) asm volatile("v_readlane_b32 s0, %0, 1" ::"v"(a[i]) : "s0");
+    }
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) s += a[i];
+  out[blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x] = s;
+}
+
 template <int R, int W, bool NT>
 int launch(const void* a, void* b, size_t units, int grid, hipStream_t stream) {
   hipLaunchKernelGGL((stream_mix_kernel<R, W, NT>), dim3(grid), dim3(256), 0, stream, static_cast<const f4*>(a),
@@ -91,5 +130,24 @@ extern "C" int ictc_probe_valu_fma(void* out, int iters, int grid, int vgpr_oper
   else
     hipLaunchKernelGGL(valu_fma_kernel<false>, dim3(grid), dim3(256), 0, stream, static_cast<float*>(out), iters,
                        0.999f, 1e-3f);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+// Issue cost of VALU instruction form `form` (valu_form_kernel above): grid blocks of 256 lanes,
+// 16 instructions x iters per lane; out must hold grid * 256 floats.  Returns 0 or -1.
+extern "C" int ictc_probe_valu_form(void* out, int form, int iters, int grid, hipStream_t stream) {
+  if (out == nullptr || iters <= 0 || grid <= 0) return -1;
+  float* o = static_cast<float*>(out);
+  switch (form) {
+    case 0: hipLaunchKernelGGL(valu_form_kernel<0>, dim3(grid), dim3(256), 0, stream, o, iters, 0.999f, 1e-3f); break;
+    case 1: hipLaunchKernelGGL(valu_form_kernel<1>, dim3(grid), dim3(256), 0, stream, o, iters, 0.999f, 1e-3f); break;
+    case 2: hipLaunchKernelGGL(valu_form_kernel<2>, dim3(grid), dim3(256), 0, stream, o, iters, 0.999f, 1e-3f); break;
+    case 3: hipLaunchKernelGGL(valu_form_kernel<3>, dim3(grid), dim3(256), 0, stream, o, iters, 0.999f, 1e-3f); break;
+    case 4: hipLaunchKernelGGL(valu_form_kernel<4>, dim3(grid), dim3(256), 0, stream, o, iters, 0.999f, 1e-3f); break;
+    case 5: hipLaunchKernelGGL(valu_form_kernel<5>, dim3(grid), dim3(256), 0, stream, o, iters, 0.999f, 1e-3f); break;
+    case 6: hipLaunchKernelGGL(valu_form_kernel<6>, dim3(grid), dim3(256), 0, stream, o, iters, 0.999f, 1e-3f); break;
+    case 7: hipLaunchKernelGGL(valu_form_kernel<7>, dim3(grid), dim3(256), 0, stream, o, iters, 0.999f, 1e-3f); break;
+    default: return -1;
+  }
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
