@@ -303,6 +303,9 @@ def _probe_lib():
     lib.ictc_probe_valu_fma.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
     lib.ictc_probe_valu_form.restype = ctypes.c_int
     lib.ictc_probe_valu_form.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    lib.ictc_probe_valu_chains.restype = ctypes.c_int
+    lib.ictc_probe_valu_chains.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                           ctypes.c_void_p]
     return lib
 
 
@@ -331,6 +334,22 @@ def _valu_form_cycles(device, grid: int = 16384, iters: int = 2048, clock_ghz: f
         wave_insts = grid * 4 * iters * 16
         ns = ms * 1e6 / (wave_insts / simds)
         res[name] = {"ns_per_wave_instruction_per_simd": ns, "cycles_at_2.4GHz": ns * clock_ghz}
+    # one wave's issue rate: independent FMA chains at 1, 2 and 4 resident waves per SIMD
+    cus, chain_iters = simds // 4, 20000
+    out = torch.empty(cus * 4 * 256, device=device)
+    chains = {}
+    for waves in (1, 2, 4):
+        for k in (1, 2, 4, 8):
+            def launch():
+                if lib.ictc_probe_valu_chains(out.data_ptr(), k, waves, cus, chain_iters,
+                                              ctypes.c_void_p(stream.cuda_stream)) != 0:
+                    raise RuntimeError("VALU chain probe launch failed")
+            ms = _event_ms(launch, device, reps=2, warmup=1)
+            cycles = ms * 1e-3 * clock_ghz * 1e9
+            chains[f"{waves}_waves_per_simd_{k}_chains"] = {
+                "cycles_per_wave_instruction_per_wave": cycles / (chain_iters * 16),
+                "cycles_per_wave_instruction_per_simd": cycles / (chain_iters * 16 * waves)}
+    res["fma_chains_by_occupancy"] = chains
     return res
 
 

@@ -51,8 +51,14 @@ __device__ __forceinline__ void sc_store_mul_ir(float* __restrict__ row, int C, 
 //   mode 3: JVP                               out [N, C*(T+1)^2]   = J(x) t
 //   mode 4: Hessian-vector product            out [N, C*(L+1)^2]   = d/dx <u, J(x) t>
 //   mode 5: weight-feature JVP                out [N, KTOT, C]     <u, d chain_p(x)[t]>
+// The straight-line float forward of the largest plans would take ~200 VGPRs (two waves per SIMD);
+// it runs better at three (168 VGPRs, a few values spilled; cfg 3 forward 0.511 -> 0.494 ms, the
+// VALU pairing more instructions with a third wave ready).  Every other mode keeps the compiler's
+// own allocation.
+constexpr int sc_min_waves(int l, int t, int k, int mode) { return (mode == 0 && l == 3 && k == 3 && t <= 1) ? 3 : 1; }
+
 template <int L, int T, int K, int MODE>
-__global__ void __launch_bounds__(kScBlock)
+__global__ void __launch_bounds__(kScBlock) __attribute__((amdgpu_waves_per_eu(sc_min_waves(L, T, K, MODE))))
 sc_kernel(const float* __restrict__ x, const float* __restrict__ t, const int64_t* __restrict__ species,
           const float* __restrict__ w, const float* __restrict__ u, float* __restrict__ out, int C,
           int64_t nodes, int num_species, int nchunks) {

@@ -96,6 +96,32 @@ __global__ void __launch_bounds__(256) valu_form_kernel(float* __restrict__ out,
   out[blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x] = s;
 }
 
+// Issue rate of one wave: CHAINS independent v_fmac_f32 chains (16 instructions per iteration in
+// total) in blocks of 256 lanes whose dynamic LDS allocation limits residency to a chosen number of
+// blocks per CU, i.e. waves per SIMD.
+template <int CHAINS>
+__global__ void __launch_bounds__(256) valu_chain_kernel(float* __restrict__ out, int iters, float b, float c) {
+  extern __shared__ float pad[];
+  float a[CHAINS];
+#pragma unroll
+  for (int i = 0; i < CHAINS; ++i) a[i] = static_cast<float>(threadIdx.x + i);
+  const float vb = b + 1e-7f * static_cast<float>(threadIdx.x & 1);
+  const float vc = c * static_cast<float>(1 + (threadIdx.x & 1));
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int r = 0; r < 16 / CHAINS; ++r) {
+#pragma unroll
+      for (int k = 0; k < CHAINS; ++k) asm volatile("v_fmac_f32_e32 %0, %1, %2" : "+v"(a[k]) : "v"(vb), "v"(vc));
+    }
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < CHAINS; ++i) s += a[i];
+  if (threadIdx.x == 0) pad[0] = s;
+  __syncthreads();
+  out[blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x] = s + pad[threadIdx.x & 1];
+}
+
 template <int R, int W, bool NT>
 int launch(const void* a, void* b, size_t units, int grid, hipStream_t stream) {
   hipLaunchKernelGGL((stream_mix_kernel<R, W, NT>), dim3(grid), dim3(256), 0, stream, static_cast<const f4*>(a),
@@ -147,6 +173,27 @@ extern "C" int ictc_probe_valu_form(void* out, int form, int iters, int grid, hi
     case 5: hipLaunchKernelGGL(valu_form_kernel<5>, dim3(grid), dim3(256), 0, stream, o, iters, 0.999f, 1e-3f); break;
     case 6: hipLaunchKernelGGL(valu_form_kernel<6>, dim3(grid), dim3(256), 0, stream, o, iters, 0.999f, 1e-3f); break;
     case 7: hipLaunchKernelGGL(valu_form_kernel<7>, dim3(grid), dim3(256), 0, stream, o, iters, 0.999f, 1e-3f); break;
+    default: return -1;
+  }
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+// One wave's issue rate: chains (1, 2, 4 or 8) independent FMA chains, waves_per_simd (1, 2 or 4)
+// resident waves per SIMD (blocks per CU limited through their LDS allocation), cus * waves_per_simd
+// blocks of 256 lanes, 16 instructions x iters per lane; out must hold that many blocks x 256
+// floats.  Returns 0 or -1.
+extern "C" int ictc_probe_valu_chains(void* out, int chains, int waves_per_simd, int cus, int iters,
+                                      hipStream_t stream) {
+  if (out == nullptr || iters <= 0 || cus <= 0) return -1;
+  if (waves_per_simd != 1 && waves_per_simd != 2 && waves_per_simd != 4) return -1;
+  const size_t lds = (160u * 1024u) / static_cast<unsigned>(waves_per_simd) - 1024u;
+  const dim3 grid(static_cast<unsigned>(cus * waves_per_simd));
+  float* o = static_cast<float*>(out);
+  switch (chains) {
+    case 1: hipLaunchKernelGGL(valu_chain_kernel<1>, grid, dim3(256), lds, stream, o, iters, 0.999f, 1e-3f); break;
+    case 2: hipLaunchKernelGGL(valu_chain_kernel<2>, grid, dim3(256), lds, stream, o, iters, 0.999f, 1e-3f); break;
+    case 4: hipLaunchKernelGGL(valu_chain_kernel<4>, grid, dim3(256), lds, stream, o, iters, 0.999f, 1e-3f); break;
+    case 8: hipLaunchKernelGGL(valu_chain_kernel<8>, grid, dim3(256), lds, stream, o, iters, 0.999f, 1e-3f); break;
     default: return -1;
   }
   return hipGetLastError() == hipSuccess ? 0 : -1;
