@@ -30,7 +30,8 @@
 namespace ictc {
 namespace {
 
-constexpr int kTile = 64;   // rows and columns per block
+constexpr int kTile = 64;   // rows per block, and columns per block of the forward modes
+constexpr int kTileIg = 128;   // columns per block of the input adjoint
 constexpr int kKc = 32;     // K per LDS chunk
 constexpr int kPitch = kKc + 4;   // LDS row pitch in floats (16-byte aligned rows)
 
@@ -54,29 +55,34 @@ struct LinearArgs {
 
 // MODE kForward: A = x rows (K = x columns), B^T = W rows, D -> y.  kInputGrad: A = gy rows
 // (K = O), B = W, D -> gx columns.  kMulIr: A = mul_ir x rows (K = C, stride d), B^T = W rows,
-// D -> y (mul_ir).  VEC (channels a multiple of 32): each 32-wide K chunk of an x row lies in one
-// path block and weight rows are float4-aligned, so operands are fetched into registers one chunk
-// ahead (their loads in flight while the MFMAs of the current chunk run); with two LDS buffers
+// D -> y (mul_ir).  VEC (channels, and for kInputGrad out_channels, multiples of 32): every
+// 32-wide K chunk is full, each K chunk of an x row lies in one path block and weight rows are
+// float4-aligned, so operands are fetched into registers one chunk ahead (their loads in flight
+// while the MFMAs of the current chunk run); with two LDS buffers
 // (NBUF 2) the next chunk is staged into the other buffer right after those MFMAs (one barrier per
 // chunk), with one (NBUF 1, half the LDS and so twice the resident blocks) after a second barrier.
 // The forward's long K (counts C) takes two buffers, the input adjoint's short K (O) one.
 // Without VEC, element by element, one chunk at a time.
 enum LinearMode { kForward = 0, kInputGrad = 1, kMulIr = 2 };
 
-template <int MODE, bool VEC, int NBUF>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NBUF == 1 ? 8 : 4)))
+template <int MODE, bool VEC, int NBUF, int TN>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NBUF == 1 ? (TN > kTile ? 5 : 8) : 4)))
 degree_linear_kernel(const float* __restrict__ in, float* __restrict__ out, const LinearArgs a) {
   constexpr bool FWD = MODE != kInputGrad;      // D -> mul_ir y rows, B^T = W rows
+  constexpr int NT = TN / 16;                   // 16-column MFMA tiles per wave
+  static_assert(FWD ? TN == kTile : (TN == kTile || TN == kTileIg), "column tile");
   constexpr bool STRIDED = MODE != kForward;    // A rows read at stride d over K (mul_ir)
-  const DegreeGeometry& g = a.g[blockIdx.z];
+  // the degree's geometry in registers (read once from the kernel arguments)
+  const DegreeGeometry g = a.g[blockIdx.z];
+  const int d = g.d;
   const int ncols = FWD ? a.out_channels : g.k;   // output columns
   const int kdim = FWD ? g.k : a.out_channels;    // reduction length
   const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kTile;
-  const int c0 = blockIdx.y * kTile;
+  const int c0 = blockIdx.y * TN;
   // uniform per block; a degree without path blocks (kdim 0) writes its zero forward rows
   if (r0 >= g.rows || c0 >= ncols) return;
   __shared__ __align__(16) float sA[NBUF][kTile][kPitch];   // [buffer][row][k]
-  __shared__ __align__(16) float sB[NBUF][kTile][kPitch];   // [buffer][column][k]
+  __shared__ __align__(16) float sB[NBUF][TN][kPitch];      // [buffer][column][k]
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int C = a.channels;
@@ -84,19 +90,22 @@ degree_linear_kernel(const float* __restrict__ in, float* __restrict__ out, cons
   const int ar = tid >> 2, akq = (tid & 3) * 8;
   const int64_t arho = r0 + ar;
   const bool arow = arho < g.rows;
-  const int64_t an = arow ? arho / g.d : 0;
-  const int am = arow ? static_cast<int>(arho - an * g.d) : 0;
+  const int64_t an = arow ? arho / d : 0;
+  const int am = arow ? static_cast<int>(arho - an * d) : 0;
   const float* __restrict__ abase = MODE == kForward   ? in + an * a.xwidth + g.xoff + static_cast<int64_t>(am) * C
                                     : MODE == kInputGrad ? in + an * a.ywidth + g.yoff + am
                                                          : in + an * a.xwidth + g.xoff + am;
-  // !FWD B staging: thread t holds weight row k0 + t / 8, columns c0 + 8 (t % 8) .. + 7 (two
-  // float4 loads), stored transposed element by element.  The k index of B column col is
-  // XOR-swizzled by bsw(col) (a multiple of 8 below 32, so every aligned 4-group of k stays
-  // contiguous and in its row): the transposed stores of a wave then meet at most two lanes per
-  // bank, and with the 36-float pitch the 16-byte MFMA operand reads stay conflict-free.
-  const int wk = tid >> 3, wc = (tid & 7) * 8;
-  auto bsw = [](int col) { return FWD ? 0 : ((col >> 3) & 3) * 8; };
-  f32x4_t acc[4] = {};
+  // !FWD B staging: thread t holds weight row k0 + t / 8, columns c0 + CPT (t % 8) .. + CPT - 1
+  // (CPT = TN / 8: two or four float4 loads), stored transposed element by element.  The k index
+  // of B column col is XOR-swizzled by bsw(col) (a multiple of 8 below 32, so every aligned
+  // 4-group of k stays contiguous and in its row; it follows col / 8 for CPT 8, col / 16 for
+  // CPT 16, the bits that tell the lanes of one store apart): the transposed stores of a wave
+  // then meet at most two lanes per bank, and with the 36-float pitch the 16-byte MFMA operand
+  // reads stay conflict-free.
+  constexpr int CPT = TN / 8;
+  const int wk = tid >> 3, wc = (tid & 7) * CPT;
+  auto bsw = [](int col) { return FWD ? 0 : ((col >> (CPT == 16 ? 4 : 3)) & 3) * 8; };
+  f32x4_t acc[NT] = {};
   const int fr = lane & 15, fq = (lane >> 4) * 4;
   auto mfma_chunk = [&](int buf) {
 #pragma unroll
@@ -106,99 +115,102 @@ degree_linear_kernel(const float* __restrict__ in, float* __restrict__ out, cons
         // one B operand live at a time (the register budget of 8 waves per SIMD); the
         // accumulation chains of the other resident waves fill the MFMA pipe
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const f32x4_t bv = *reinterpret_cast<const f32x4_t*>(&sB[buf][t * 16 + fr][(kg + fq) ^ bsw(t * 16 + fr)]);
+        for (int t = 0; t < NT; t += 2) {
+          const f32x4_t bv0 = *reinterpret_cast<const f32x4_t*>(&sB[buf][t * 16 + fr][(kg + fq) ^ bsw(t * 16 + fr)]);
+          const f32x4_t bv1 = *reinterpret_cast<const f32x4_t*>(&sB[buf][t * 16 + 16 + fr][(kg + fq) ^ bsw(t * 16 + 16 + fr)]);
 #pragma unroll
-          for (int j = 0; j < 4; ++j) acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j], bv[j], acc[t], 0, 0, 0);
+          for (int j = 0; j < 4; ++j) {
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j], bv0[j], acc[t], 0, 0, 0);
+            acc[t + 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j], bv1[j], acc[t + 1], 0, 0, 0);
+          }
         }
       } else {
-        f32x4_t bv[4];
+        f32x4_t bv[NT];
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
+        for (int t = 0; t < NT; ++t)
           bv[t] = *reinterpret_cast<const f32x4_t*>(&sB[buf][t * 16 + fr][(kg + fq) ^ bsw(t * 16 + fr)]);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
 #pragma unroll
-          for (int t = 0; t < 4; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j], bv[t][j], acc[t], 0, 0, 0);
+          for (int t = 0; t < NT; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j], bv[t][j], acc[t], 0, 0, 0);
         }
       }
     }
   };
   if constexpr (VEC) {
-    // registers of one chunk: A (8 floats of the thread's row), B (8 floats)
-    f32x4_t ra0, ra1, rb0, rb1;
+    // registers of one chunk: A (8 floats of the thread's row), B (8 floats, or CPT of the
+    // input adjoint's weight row)
+    constexpr int NRB = FWD ? 2 : CPT / 4;
+    f32x4_t ra0, ra1, rb[NRB];
+    // Every K chunk is full under VEC (kdim a multiple of 32), and no load is conditional on the
+    // lane: a select or a branch on a loaded value would wait for the load at the fetch instead of
+    // at the stage.  Rows past the end read row 0 and columns past the end read the last valid
+    // weight columns: their products land in output rows / columns that are never stored.
     auto fetch = [&](int k0) {
-      const bool kin = k0 + akq < kdim;
-      ra0 = f32x4_t{};
-      ra1 = f32x4_t{};
-      rb0 = f32x4_t{};
-      rb1 = f32x4_t{};
-      if constexpr (STRIDED) {
+      if constexpr (STRIDED) {   // mul_ir row: stride d over K
+        const float* p = abase + (k0 + akq) * d;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {   // mul_ir row: stride d over K
-          if (arow && k0 + akq + u < kdim) ra0[u] = abase[static_cast<int64_t>(k0 + akq + u) * g.d];
-          if (arow && k0 + akq + 4 + u < kdim) ra1[u] = abase[static_cast<int64_t>(k0 + akq + 4 + u) * g.d];
+        for (int u = 0; u < 4; ++u) {
+          ra0[u] = p[u * d];
+          ra1[u] = p[(u + 4) * d];
         }
       } else {
         const int blk = k0 / C, c = k0 - blk * C + akq;
-        if (arow && kin) {
-          const float* p = abase + static_cast<int64_t>(blk) * g.d * C + c;
-          ra0 = *reinterpret_cast<const f32x4_t*>(p);
-          ra1 = *reinterpret_cast<const f32x4_t*>(p + 4);
-        }
+        const float* p = abase + blk * d * C + c;
+        ra0 = *reinterpret_cast<const f32x4_t*>(p);
+        ra1 = *reinterpret_cast<const f32x4_t*>(p + 4);
       }
       if constexpr (FWD) {
-        const int col = c0 + ar;   // weight row col, 8 consecutive k
-        if (col < ncols && kin) {
-          const float* p = g.w + static_cast<int64_t>(col) * g.k + k0 + akq;
-          rb0 = *reinterpret_cast<const f32x4_t*>(p);
-          rb1 = *reinterpret_cast<const f32x4_t*>(p + 4);
-        }
+        const int col = c0 + ar < ncols ? c0 + ar : ncols - 1;   // weight row col, 8 consecutive k
+        const float* p = g.w + static_cast<int64_t>(col) * g.k + k0 + akq;
+        rb[0] = *reinterpret_cast<const f32x4_t*>(p);
+        rb[1] = *reinterpret_cast<const f32x4_t*>(p + 4);
       } else {
-        const int kk = k0 + wk;
-        if (kk < kdim && c0 + wc < ncols) {   // ncols (counts C) is a multiple of 32
-          const float* p = g.w + static_cast<int64_t>(kk) * g.k + c0 + wc;
-          rb0 = *reinterpret_cast<const f32x4_t*>(p);
-          rb1 = *reinterpret_cast<const f32x4_t*>(p + 4);
-        }
+        // ncols (counts C) is a multiple of 32 and CPT is 8 or 16: the clamped run of CPT
+        // columns stays in range
+        const int col = c0 + wc < ncols ? c0 + wc : ncols - CPT;
+        const float* p = g.w + static_cast<int64_t>(k0 + wk) * g.k + col;
+#pragma unroll
+        for (int q = 0; q < NRB; ++q) rb[q] = *reinterpret_cast<const f32x4_t*>(p + 4 * q);
       }
     };
     auto stage = [&](int buf) {
       *reinterpret_cast<f32x4_t*>(&sA[buf][ar][akq]) = ra0;
       *reinterpret_cast<f32x4_t*>(&sA[buf][ar][akq + 4]) = ra1;
       if constexpr (FWD) {
-        *reinterpret_cast<f32x4_t*>(&sB[buf][ar][akq]) = rb0;
-        *reinterpret_cast<f32x4_t*>(&sB[buf][ar][akq + 4]) = rb1;
+        *reinterpret_cast<f32x4_t*>(&sB[buf][ar][akq]) = rb[0];
+        *reinterpret_cast<f32x4_t*>(&sB[buf][ar][akq + 4]) = rb[1];
       } else {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          sB[buf][wc + u][wk ^ bsw(wc + u)] = rb0[u];
-          sB[buf][wc + 4 + u][wk ^ bsw(wc + 4 + u)] = rb1[u];
-        }
+        for (int q = 0; q < NRB; ++q)
+#pragma unroll
+          for (int u = 0; u < 4; ++u) sB[buf][wc + 4 * q + u][wk ^ bsw(wc + 4 * q + u)] = rb[q][u];
       }
     };
-    fetch(0);
-    if constexpr (NBUF == 2) {
-      // buffer c & 1 holds chunk c; chunk c + 1 is fetched before and staged after chunk c's
-      // MFMAs, into the buffer every wave finished reading at the previous barrier
-      stage(0);
-      __syncthreads();
-      int buf = 0;
-      for (int k0 = 0; k0 < kdim; k0 += kKc) {
-        const bool more = k0 + kKc < kdim;
-        if (more) fetch(k0 + kKc);
-        mfma_chunk(buf);
-        if (more) stage(buf ^ 1);
-        __syncthreads();
-        buf ^= 1;
-      }
-    } else {
-      for (int k0 = 0; k0 < kdim; k0 += kKc) {
+    if (kdim > 0) {   // uniform
+      fetch(0);
+      if constexpr (NBUF == 2) {
+        // buffer c & 1 holds chunk c; chunk c + 1 is fetched before and staged after chunk c's
+        // MFMAs, into the buffer every wave finished reading at the previous barrier
         stage(0);
         __syncthreads();
-        if (k0 + kKc < kdim) fetch(k0 + kKc);
-        mfma_chunk(0);
-        __syncthreads();
+        int buf = 0;
+        for (int k0 = 0; k0 < kdim; k0 += kKc) {
+          const bool more = k0 + kKc < kdim;
+          if (more) fetch(k0 + kKc);
+          mfma_chunk(buf);
+          if (more) stage(buf ^ 1);
+          __syncthreads();
+          buf ^= 1;
+        }
+      } else {
+        for (int k0 = 0; k0 < kdim; k0 += kKc) {
+          stage(0);
+          __syncthreads();
+          if (k0 + kKc < kdim) fetch(k0 + kKc);
+          mfma_chunk(0);
+          __syncthreads();
+        }
       }
     }
   } else {
@@ -239,22 +251,28 @@ degree_linear_kernel(const float* __restrict__ in, float* __restrict__ out, cons
       __syncthreads();
     }
   }
+  // the lane's four output rows rho0 .. rho0 + 3: one division, then (n, m) stepped
+  const int64_t rho0 = r0 + wave * 16 + 4 * (lane >> 4);
+  int64_t n = rho0 / d;
+  int m = static_cast<int>(rho0 - n * d);
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
-    const int64_t rho = r0 + wave * 16 + 4 * (lane >> 4) + v;
-    if (rho >= g.rows) continue;
-    const int64_t n = rho / g.d;
-    const int m = static_cast<int>(rho - n * g.d);
+    if (v > 0 && ++m == d) {
+      m = 0;
+      ++n;
+    }
+    if (rho0 + v >= g.rows) continue;
+    float* __restrict__ orow = FWD ? out + n * a.ywidth + g.yoff + m : out + n * a.xwidth + g.xoff + m * C;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
+    for (int t = 0; t < NT; ++t) {
       const int col = c0 + t * 16 + (lane & 15);
       if (col >= ncols) continue;
       const float val = a.alpha * acc[t][v];
       if (FWD) {
-        out[n * a.ywidth + g.yoff + static_cast<int64_t>(col) * g.d + m] = val;
+        orow[col * d] = val;
       } else {
         const int blk = col / C, c = col - blk * C;
-        out[n * a.xwidth + g.xoff + (static_cast<int64_t>(blk) * g.d + m) * C + c] = val;
+        orow[blk * d * C + c] = val;
       }
     }
   }
@@ -312,14 +330,19 @@ int launch(const ictc_degree_linear_desc* desc, const float* in, const float* co
   if (in == nullptr || out == nullptr) return ICTC_ERR_INVALID_ARGUMENT;
   const int64_t row_tiles = (max_rows + kTile - 1) / kTile;
   if (row_tiles > 0x7fffffff) return ICTC_ERR_UNSUPPORTED;
-  const dim3 grid(static_cast<unsigned>(row_tiles), static_cast<unsigned>((max_cols + kTile - 1) / kTile),
+  // two LDS buffers for the long K of the forward (counts C), one for the short K of the others;
+  // the input adjoint's vector path takes 128 columns per block (its B tile is read once per
+  // 64 x 128 outputs instead of 64 x 64)
+  const bool vec = desc->channels % 32 == 0 && (MODE != kInputGrad || desc->out_channels % 32 == 0);
+  constexpr int kTn = MODE == kInputGrad ? kTileIg : kTile;
+  const int tn = vec ? kTn : kTile;
+  const dim3 grid(static_cast<unsigned>(row_tiles), static_cast<unsigned>((max_cols + tn - 1) / tn),
                   static_cast<unsigned>(degrees));
-  // two LDS buffers for the long K of the forward (counts C), one for the short K of the others
-  if (desc->channels % 32 == 0)
-    hipLaunchKernelGGL((degree_linear_kernel<MODE, true, MODE == kForward ? 2 : 1>), grid, dim3(256), 0, stream, in,
-                       out, a);
+  if (vec)
+    hipLaunchKernelGGL((degree_linear_kernel<MODE, true, MODE == kForward ? 2 : 1, kTn>), grid, dim3(256), 0, stream,
+                       in, out, a);
   else
-    hipLaunchKernelGGL((degree_linear_kernel<MODE, false, 1>), grid, dim3(256), 0, stream, in, out, a);
+    hipLaunchKernelGGL((degree_linear_kernel<MODE, false, 1, kTile>), grid, dim3(256), 0, stream, in, out, a);
   return hipGetLastError() == hipSuccess ? ICTC_OK : ICTC_ERR_LAUNCH;
 }
 

@@ -32,7 +32,12 @@ def _reference(x, weights, counts, c, o, alpha):
     return torch.cat(out, -1)
 
 
-CASES = [((4, 6, 7, 6), 128, 128, 2048, 1 / 50.0), ((3, 4, 4), 64, 64, 77, 0.3), ((2, 0, 3), 40, 24, 33, 1.0),
+# the vector path (C a multiple of 32) at the cfg-4 shape, with column counts that end inside a
+# 128-column tile (32, 96, 64: the clamped weight runs), with a degree without path blocks, and
+# with O not a multiple of 32 (its input adjoint on the element-wise path); the element-wise path
+# with odd C and O
+CASES = [((4, 6, 7, 6), 128, 128, 2048, 1 / 50.0), ((3, 4, 4), 64, 64, 77, 0.3), ((1, 3, 2), 32, 64, 45, 0.7),
+         ((3, 0, 2), 64, 96, 70, 1.5), ((1, 1), 96, 40, 29, 1.0), ((2, 0, 3), 40, 24, 33, 1.0),
          ((1,), 16, 8, 5, 2.0)]
 
 
