@@ -278,11 +278,19 @@ def _median_call_ms(fn, device, *, warmup_s: float = 2.0, warmup_calls: int = 3,
     return sorted(times)[len(times) // 2]
 
 
-def _event_ms(fn, device, reps: int = 10, warmup: int = 3) -> float:
-    """Mean duration of fn's launches between HIP events on the current stream."""
+def _event_ms(fn, device, reps: int = 10, warmup: int = 3, warm_s: float = 0.05) -> float:
+    """Mean duration of fn's launches between HIP events on the current stream, after `warmup`
+    calls and at least `warm_s` seconds of back-to-back calls (the GPU clocks ramp up over the
+    first milliseconds of work: a few warm-up calls alone time a short leg partly at lower
+    clocks)."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize(device)
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < warm_s:
+        for _ in range(4):
+            fn()
+        torch.cuda.synchronize(device)
     stream = torch.cuda.current_stream(device)
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     s.record(stream)

@@ -67,19 +67,25 @@ __device__ __forceinline__ PathInfo path_info(const GenTable& t, int p) {
   return r;
 }
 
-// Calls f(Int<n>{}) for the odd width n = 2 l + 1 <= kMaxN of a degree (a wave-uniform switch), so
+// Calls f(Int<n>{}) for the odd width n = 2 l + 1 <= NM of a degree (a wave-uniform switch), so
 // loops over one degree's components run exactly n times.
-template <typename F>
+template <int NM = kMaxN, typename F>
 __device__ __forceinline__ void with_width(int n1, F&& f) {
-  static_assert(kMaxN == 13, "widths 1..13");
+  static_assert(kMaxN == 13 && (NM == 9 || NM == 13), "widths 1..13");
   switch (n1) {
     case 1: f(Int<1>{}); break;
     case 3: f(Int<3>{}); break;
     case 5: f(Int<5>{}); break;
     case 7: f(Int<7>{}); break;
     case 9: f(Int<9>{}); break;
-    case 11: f(Int<11>{}); break;
-    default: f(Int<13>{}); break;
+    default:
+      if constexpr (NM == 13) {
+        if (n1 == 11)
+          f(Int<11>{});
+        else
+          f(Int<13>{});
+      }
+      break;
   }
 }
 
@@ -108,35 +114,54 @@ __device__ void build_bonds(const GenTable& t, const float* sY, float* sM, int l
   }
 }
 
-// x rows [l1^2, l1^2 + n1) of this lane's channel into xr[0..n1) (xr past n1 and lanes past C
-// get 0).  rx spans the instance's feature row [NX][C]; an empty descriptor (no x, or a source
-// index out of range) reads zeros.  All kMaxN row loads are issued together; those past n1
+// Per-lane byte offset of channel c in a row, or for lanes past C an offset beyond every
+// descriptor's range (their loads return 0 and their values are never stored).
+__device__ __forceinline__ uint32_t lane_off(int c, bool on) { return on ? static_cast<uint32_t>(c) * 4u : 0xFFFFFFF0u; }
+
+// x rows [l1^2, l1^2 + n1) of the lane's channel into xr[0..n1); the NM - n1 loads past n1
 // repeat row n1 - 1 (the wave-uniform row offset is not range checked, so it stays inside the
-// degree block).
-__device__ __forceinline__ void stage_x(rsrc_t rx, int l1, int n1, int C, int c, bool on, float (&xr)[kMaxN]) {
-  const uint32_t lc = static_cast<uint32_t>(on ? c : 0) * 4u;
+// degree block).  rx spans the instance's feature row [NX][C]; an empty descriptor (no x, or a
+// source index out of range) reads zeros.  No value is inspected here: the loads stay in flight
+// until the degree's first path uses them.
+template <int NM>
+__device__ __forceinline__ void load_x(const GenTable& t, int l1, rsrc_t rx, uint32_t lo, float (&xr)[NM]) {
+  const int n1 = 2 * l1 + 1;
+  const uint32_t row = static_cast<uint32_t>(t.channels) * 4u;
 #pragma unroll
-  for (int i = 0; i < kMaxN; ++i)
-    xr[i] = buf_load_vs(rx, lc, static_cast<uint32_t>((l1 * l1 + (i < n1 ? i : n1 - 1)) * C) * 4u);
-#pragma unroll
-  for (int i = 0; i < kMaxN; ++i) xr[i] = (on && i < n1) ? xr[i] : 0.f;
+  for (int i = 0; i < NM; ++i) xr[i] = buf_load_vs(rx, lo, static_cast<uint32_t>(l1 * l1 + (i < n1 ? i : n1 - 1)) * row);
 }
 
-// Feature row of one instance: x + row * NX * C, or an empty descriptor.
+// A path's gate and its n3 dout rows (rows past n3 repeat row n3 - 1), requested one path ahead.
+template <int NM>
+struct PathIn {
+  float gv;
+  float o[NM];
+};
+
+template <int NM>
+__device__ __forceinline__ void load_path(const GenTable& t, int p, rsrc_t rg, rsrc_t rgo, uint32_t lo,
+                                          PathIn<NM>& in) {
+  const PathInfo q = path_info(t, p);
+  const uint32_t row = static_cast<uint32_t>(t.channels) * 4u;
+  in.gv = buf_load_vs(rg, lo, static_cast<uint32_t>(p) * row);
+#pragma unroll
+  for (int k = 0; k < NM; ++k) in.o[k] = buf_load_vs(rgo, lo, static_cast<uint32_t>(q.out + (k < q.n3 ? k : q.n3 - 1)) * row);
+}
+
+// Rows of one instance: x + row * NX * C (or an empty descriptor), and [n][C] blocks.
 __device__ __forceinline__ rsrc_t x_row(const float* x, int64_t row, bool valid, const GenTable& t) {
   const uint32_t bytes = static_cast<uint32_t>(t.nx * t.channels) * 4u;
   return make_rsrc(x && valid ? x + row * t.nx * t.channels : nullptr, bytes);
 }
 
-// Gate of path p at channel c (0 for lanes past C; p past the last path reads path 0).
-__device__ __forceinline__ float gate(const float* g, int p, int np, int C, int c, bool on) {
-  return on ? g[static_cast<int64_t>(p < np ? p : 0) * C + c] : 0.f;
+__device__ __forceinline__ rsrc_t block_rows(const float* base, int64_t row, int n, int C) {
+  return make_rsrc(base ? base + row * n * C : nullptr, static_cast<uint32_t>(n * C) * 4u);
 }
 
 // sum_i xr[i] * b[i] over the N1 components of the degree (the bond row k of a path); the row
 // is left in bv for the dx update.
-template <int N1>
-__device__ __forceinline__ float row_dot(const float* b, const float (&xr)[kMaxN], float (&bv)[kMaxN]) {
+template <int N1, int NM>
+__device__ __forceinline__ float row_dot(const float* b, const float (&xr)[NM], float (&bv)[NM]) {
 #pragma unroll
   for (int i = 0; i < N1; ++i) bv[i] = b[i];
   float acc = 0.f;
@@ -146,26 +171,35 @@ __device__ __forceinline__ float row_dot(const float* b, const float (&xr)[kMaxN
 }
 
 // Forward of one instance: out rows [NOC][C] written, or added to when accumulate is set.  The
-// next path's gate is requested before the current path is computed.
-__device__ void forward_instance(const GenTable& t, const float* sM, rsrc_t x, const float* g, float* out,
-                                 bool accumulate, int lane) {
+// next path's gate, and the next input degree's x rows, are requested before the current path
+// is computed.  `prepare` (the bond build) runs once, after the first chunk's first loads are
+// issued.
+template <int NM, typename Prepare>
+__device__ void forward_instance(const GenTable& t, const float* sM, rsrc_t rx, rsrc_t rg, float* out,
+                                 bool accumulate, int lane, Prepare&& prepare) {
   const int C = t.channels;
+  const uint32_t row = static_cast<uint32_t>(C) * 4u;
+  bool first = true;
   for (int c0 = 0; c0 < C; c0 += kLanes) {
     const int c = c0 + lane;
     const bool on = c < C;
-    int staged = -1;
-    float xr[kMaxN], bv[kMaxN];
-    float gnext = gate(g, 0, t.np, C, c, on);
+    const uint32_t lo = lane_off(c, on);
+    float xr[NM], xn[NM], bv[NM];
+    int lcur = path_info(t, 0).l1;
+    load_x<NM>(t, lcur, rx, lo, xr);
+    float gv = buf_load_vs(rg, lo, 0u);
+    if (first) {
+      prepare();
+      first = false;
+    }
     for (int p = 0; p < t.np; ++p) {
       const PathInfo q = path_info(t, p);
-      if (q.l1 != staged) {
-        stage_x(x, q.l1, q.n1, C, c, on, xr);
-        staged = q.l1;
-      }
-      const float gv = gnext;
-      gnext = gate(g, p + 1, t.np, C, c, on);
+      const bool more = p + 1 < t.np;
+      const int lnext = more ? path_info(t, p + 1).l1 : q.l1;
+      const float gnext = more ? buf_load_vs(rg, lo, static_cast<uint32_t>(p + 1) * row) : 0.f;
+      if (lnext != q.l1) load_x<NM>(t, lnext, rx, lo, xn);
       const float* bond = sM + t.bond[p];
-      with_width(q.n1, [&](auto N1) {
+      with_width<NM>(q.n1, [&](auto N1) {
         for (int k = 0; k < q.n3; ++k) {
           const float acc = row_dot<N1>(bond + k * N1, xr, bv);
           if (on) {
@@ -174,6 +208,11 @@ __device__ void forward_instance(const GenTable& t, const float* sM, rsrc_t x, c
           }
         }
       });
+      gv = gnext;
+      if (lnext != q.l1) {
+#pragma unroll
+        for (int i = 0; i < NM; ++i) xr[i] = xn[i];
+      }
     }
   }
 }
@@ -185,54 +224,64 @@ struct BwdLds {
   float* sDY;    // [64] dY of the instance
 };
 
-// VJP of one instance (sM built, L.sDY zeroed): dg and dx rows written when their pointers are
-// set, the dY contributions added to L.sDY when want_dy (x is needed for dg and dY).  Every
-// lane takes part in the dY butterflies whatever its channel, so the call is wave-uniform.
-__device__ void backward_instance(const GenTable& t, const float* sM, const BwdLds& L, rsrc_t x,
-                                  const float* g, const float* go, float* dx, float* dg, bool want_dy, int lane) {
-  static_assert(kMaxN <= 16, "dY butterfly width");
+// VJP of one instance (L.sDY zeroed): dg and dx rows written when their pointers are set, the dY
+// contributions added to L.sDY when want_dy (x is needed for dg and dY).  Every lane takes part
+// in the dY butterflies whatever its channel, so the call is wave-uniform.  The next path's gate
+// and dout rows, and the next input degree's x rows, are requested before the current path is
+// computed; `prepare` (the bond build) runs once, after the first chunk's first loads are issued.
+template <int NM, typename Prepare>
+__device__ void backward_instance(const GenTable& t, const float* sM, const BwdLds& L, rsrc_t rx, rsrc_t rg,
+                                  rsrc_t rgo, float* dx, float* dg, bool want_dy, int lane, Prepare&& prepare) {
+  static_assert(NM <= 16, "dY butterfly width");
   const int C = t.channels;
+  bool first = true;
   for (int c0 = 0; c0 < C; c0 += kLanes) {
     const int c = c0 + lane;
     const bool on = c < C;
+    const uint32_t lo = lane_off(c, on);
     int staged = -1;
     unsigned seen = 0;   // input degrees with at least one path
-    float xr[kMaxN], dxr[kMaxN], bv[kMaxN];
+    float xr[NM], xn[NM], dxr[NM], bv[NM];
+    PathIn<NM> cur, nxt;
+    load_x<NM>(t, path_info(t, 0).l1, rx, lo, xr);
+    load_path<NM>(t, 0, rg, rgo, lo, cur);
+    if (first) {
+      prepare();
+      first = false;
+    }
     auto flush = [&](int l) {
 #pragma unroll
-      for (int i = 0; i < kMaxN; ++i)
+      for (int i = 0; i < NM; ++i)
         if (i < 2 * l + 1) dx[static_cast<int64_t>(l * l + i) * C + c] = dxr[i];
     };
     for (int p = 0; p < t.np; ++p) {
       const PathInfo q = path_info(t, p);
+      const bool more = p + 1 < t.np;
+      const int lnext = more ? path_info(t, p + 1).l1 : q.l1;
+      if (more) load_path<NM>(t, p + 1, rg, rgo, lo, nxt);
+      if (lnext != q.l1) load_x<NM>(t, lnext, rx, lo, xn);
       if (q.l1 != staged) {
         if (staged >= 0 && dx && on) flush(staged);
-        stage_x(x, q.l1, q.n1, C, c, on, xr);
-        if (want_dy) {
+        if (want_dy) {   // lanes past C contribute nothing to the dY sums
 #pragma unroll
-          for (int i = 0; i < kMaxN; ++i)
-            if (i < q.n1) L.sX[i * kLanes + lane] = xr[i];
+          for (int i = 0; i < NM; ++i)
+            if (i < q.n1) L.sX[i * kLanes + lane] = on ? xr[i] : 0.f;
         }
 #pragma unroll
-        for (int i = 0; i < kMaxN; ++i) dxr[i] = 0.f;
+        for (int i = 0; i < NM; ++i) dxr[i] = 0.f;
         staged = q.l1;
         seen |= 1u << q.l1;
       }
-      const float gv = gate(g, p, t.np, C, c, on);
-      float o[kMaxN];
 #pragma unroll
-      for (int k = 0; k < kMaxN; ++k)
-        o[k] = on ? go[static_cast<int64_t>(q.out + (k < q.n3 ? k : 0)) * C + c] : 0.f;
-#pragma unroll
-      for (int k = 0; k < kMaxN; ++k)
+      for (int k = 0; k < NM; ++k)
         if (k < q.n3) {
-          L.sO[k * kLanes + lane] = o[k];
-          L.sG[k * kLanes + lane] = gv * o[k];
+          L.sO[k * kLanes + lane] = cur.o[k];
+          L.sG[k * kLanes + lane] = on ? cur.gv * cur.o[k] : 0.f;
         }
       const float* bond = sM + t.bond[p];
       const float* cg = kCGGeneric + t.cg[p];
       float dgv = 0.f;
-      with_width(q.n1, [&](auto N1) {
+      with_width<NM>(q.n1, [&](auto N1) {
         for (int k = 0; k < q.n3; ++k) {
           const float base = row_dot<N1>(bond + k * N1, xr, bv);
           dgv = fmaf(base, L.sO[k * kLanes + lane], dgv);
@@ -242,7 +291,7 @@ __device__ void backward_instance(const GenTable& t, const float* sM, const BwdL
         }
       });
       if (want_dy) {
-        with_width(q.n2, [&](auto N2) {
+        with_width<NM>(q.n2, [&](auto N2) {
           // this lane's sum_{i,k} Chat[i][k][j] x_i go_k against the CG rows (scalar loads), then
           // summed over the lanes (a fixed butterfly) and added by the owner lanes
           using WS = WaveSums<N2>;
@@ -265,6 +314,13 @@ __device__ void backward_instance(const GenTable& t, const float* sM, const BwdL
         });
       }
       if (dg && on) dg[static_cast<int64_t>(p) * C + c] = dgv;
+      if (more) {
+        cur = nxt;
+        if (lnext != q.l1) {
+#pragma unroll
+          for (int i = 0; i < NM; ++i) xr[i] = xn[i];
+        }
+      }
     }
     if (dx && on) {
       if (staged >= 0) flush(staged);
@@ -291,28 +347,41 @@ __device__ __forceinline__ BwdLds carve(float* lds, const GenTable& t) {
   return L;
 }
 
-// Harmonics of row r into sY and sDY zeroed, barrier, bonds, barrier.
-__device__ __forceinline__ void begin_instance(const GenTable& t, const float* y, int64_t r, float* lds, int lane) {
-  if (lane < t.ny) lds[lane] = y[r * t.ny + lane];
+// Harmonics of an instance (requested one instance ahead into yv: lanes below NY) into sY, sDY
+// zeroed, barrier.  The bonds are built by the instance functions' `prepare` step.
+__device__ __forceinline__ void stage_y(float yv, float* lds, int lane) {
+  lds[lane] = yv;
   lds[kLanes + lane] = 0.f;
-  __syncthreads();
-  build_bonds(t, lds, lds + kHead, lane);
   __syncthreads();
 }
 
+__device__ __forceinline__ float load_y(const GenTable& t, const float* y, int64_t r, bool valid, int lane) {
+  float v = 0.f;
+  if (valid && lane < t.ny) v = y[r * t.ny + lane];
+  return v;
+}
+
+template <int NM>
 __global__ void __launch_bounds__(kLanes)
 gen_tp_forward_kernel(const GenTable t, const float* __restrict__ x, const float* __restrict__ y,
                       const float* __restrict__ g, float* __restrict__ out, int64_t rows) {
   extern __shared__ float lds[];
   const int lane = threadIdx.x;
   const int C = t.channels;
+  float yv = load_y(t, y, blockIdx.x, blockIdx.x < rows, lane);
   for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
-    begin_instance(t, y, r, lds, lane);
-    forward_instance(t, lds + kHead, x_row(x, r, true, t), g + r * t.np * C, out + r * t.noc * C, false, lane);
+    stage_y(yv, lds, lane);
+    yv = load_y(t, y, r + gridDim.x, r + gridDim.x < rows, lane);
+    forward_instance<NM>(t, lds + kHead, x_row(x, r, true, t), block_rows(g, r, t.np, C), out + r * t.noc * C,
+                         false, lane, [&] {
+                           build_bonds(t, lds, lds + kHead, lane);
+                           __syncthreads();
+                         });
     __syncthreads();
   }
 }
 
+template <int NM>
 __global__ void __launch_bounds__(kLanes)
 gen_tp_backward_kernel(const GenTable t, const float* __restrict__ x, const float* __restrict__ y,
                        const float* __restrict__ g, const float* __restrict__ go, float* __restrict__ dx,
@@ -321,16 +390,23 @@ gen_tp_backward_kernel(const GenTable t, const float* __restrict__ x, const floa
   const int lane = threadIdx.x;
   const int C = t.channels;
   const BwdLds L = carve(lds, t);
+  float yv = load_y(t, y, blockIdx.x, blockIdx.x < rows, lane);
   for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
-    begin_instance(t, y, r, lds, lane);
-    backward_instance(t, lds + kHead, L, x_row(x, r, true, t), g + r * t.np * C, go + r * t.noc * C,
-                      dx ? dx + r * t.nx * C : nullptr, dg ? dg + r * t.np * C : nullptr, dy != nullptr, lane);
+    stage_y(yv, lds, lane);
+    yv = load_y(t, y, r + gridDim.x, r + gridDim.x < rows, lane);
+    backward_instance<NM>(t, lds + kHead, L, x_row(x, r, true, t), block_rows(g, r, t.np, C),
+                          block_rows(go, r, t.noc, C), dx ? dx + r * t.nx * C : nullptr,
+                          dg ? dg + r * t.np * C : nullptr, dy != nullptr, lane, [&] {
+                            build_bonds(t, lds, lds + kHead, lane);
+                            __syncthreads();
+                          });
     __syncthreads();
     if (dy && lane < t.ny) dy[r * t.ny + lane] = L.sDY[lane];
   }
 }
 
 // Receiver-CSR message forward: one node at a time per workgroup, its edges in CSR order.
+template <int NM>
 __global__ void __launch_bounds__(kLanes)
 gen_msg_forward_kernel(const GenTable t, const float* __restrict__ x, const float* __restrict__ y,
                        const float* __restrict__ g, const int64_t* __restrict__ src,
@@ -346,18 +422,26 @@ gen_msg_forward_kernel(const GenTable t, const float* __restrict__ x, const floa
       for (int64_t i = lane; i < static_cast<int64_t>(t.noc) * C; i += kLanes) orow[i] = 0.f;
       continue;
     }
+    int64_t e = perm ? perm[q0] : q0;
+    float yv = load_y(t, y, e, true, lane);
     for (int64_t q = q0; q < q1; ++q) {
-      const int64_t e = perm ? perm[q] : q;
-      begin_instance(t, y, e, lds, lane);
+      stage_y(yv, lds, lane);
       const int64_t s = src[e];
-      forward_instance(t, lds + kHead, x_row(x, s, s >= 0 && s < nodes_src, t), g + e * t.np * C, orow, q != q0,
-                       lane);
+      const int64_t en = q + 1 < q1 ? (perm ? perm[q + 1] : q + 1) : e;
+      yv = load_y(t, y, en, q + 1 < q1, lane);
+      forward_instance<NM>(t, lds + kHead, x_row(x, s, s >= 0 && s < nodes_src, t), block_rows(g, e, t.np, C),
+                           orow, q != q0, lane, [&] {
+                             build_bonds(t, lds, lds + kHead, lane);
+                             __syncthreads();
+                           });
       __syncthreads();
+      e = en;
     }
   }
 }
 
 // Receiver-CSR edge adjoint: per edge e of node n, the TP VJP with dout = go[n].
+template <int NM>
 __global__ void __launch_bounds__(kLanes)
 gen_msg_edge_grad_kernel(const GenTable t, const float* __restrict__ x, const float* __restrict__ y,
                          const float* __restrict__ g, const float* __restrict__ go,
@@ -370,18 +454,27 @@ gen_msg_edge_grad_kernel(const GenTable t, const float* __restrict__ x, const fl
   const BwdLds L = carve(lds, t);
   for (int64_t n = blockIdx.x; n < nodes_dst; n += gridDim.x) {
     const int64_t q0 = rowptr[n], q1 = rowptr[n + 1];
+    if (q0 == q1) continue;
+    const rsrc_t rgo = block_rows(go, n, t.noc, C);
+    int64_t e = perm ? perm[q0] : q0;
+    float yv = load_y(t, y, e, true, lane);
     for (int64_t q = q0; q < q1; ++q) {
-      const int64_t e = perm ? perm[q] : q;
-      begin_instance(t, y, e, lds, lane);
+      stage_y(yv, lds, lane);
       const int64_t s = src[e];
-      backward_instance(t, lds + kHead, L, x_row(x, s, s >= 0 && s < nodes_src, t), g + e * t.np * C,
-                        go + n * t.noc * C, dxe ? dxe + e * t.nx * C : nullptr, dg ? dg + e * t.np * C : nullptr,
-                        dyp != nullptr, lane);
+      const int64_t en = q + 1 < q1 ? (perm ? perm[q + 1] : q + 1) : e;
+      yv = load_y(t, y, en, q + 1 < q1, lane);
+      backward_instance<NM>(t, lds + kHead, L, x_row(x, s, s >= 0 && s < nodes_src, t), block_rows(g, e, t.np, C),
+                            rgo, dxe ? dxe + e * t.nx * C : nullptr, dg ? dg + e * t.np * C : nullptr,
+                            dyp != nullptr, lane, [&] {
+                              build_bonds(t, lds, lds + kHead, lane);
+                              __syncthreads();
+                            });
       __syncthreads();
       if (dyp) {
         float* d = dyp + e * chunks * t.ny;
         for (int i = lane; i < chunks * t.ny; i += kLanes) d[i] = i < t.ny ? L.sDY[i] : 0.f;
       }
+      e = en;
     }
   }
 }
@@ -417,6 +510,9 @@ unsigned grid_for(int64_t instances) {
 
 int status() { return hipGetLastError() == hipSuccess ? ICTC_OK : ICTC_ERR_LAUNCH; }
 
+// Every degree <= 4: the kernels keep 9 components per degree in registers instead of 13.
+bool narrow(const ictc_tp_desc& d) { return d.input_lmax <= 4 && d.edge_lmax <= 4 && d.output_lmax <= 4; }
+
 }  // namespace
 
 int generic_tp_forward(const ictc_tp_desc& d, const float* x, const float* y, const float* g, float* out,
@@ -424,8 +520,12 @@ int generic_tp_forward(const ictc_tp_desc& d, const float* x, const float* y, co
   GenTable t;
   const int st = make_table(d, &t);
   if (st != ICTC_OK) return st;
-  hipLaunchKernelGGL(gen_tp_forward_kernel, dim3(grid_for(rows)), dim3(kLanes),
-                     fwd_lds_floats(t) * sizeof(float), stream, t, x, y, g, out, rows);
+  const dim3 grid(grid_for(rows)), block(kLanes);
+  const size_t lds = fwd_lds_floats(t) * sizeof(float);
+  if (narrow(d))
+    hipLaunchKernelGGL(gen_tp_forward_kernel<9>, grid, block, lds, stream, t, x, y, g, out, rows);
+  else
+    hipLaunchKernelGGL(gen_tp_forward_kernel<13>, grid, block, lds, stream, t, x, y, g, out, rows);
   return status();
 }
 
@@ -434,8 +534,12 @@ int generic_tp_backward(const ictc_tp_desc& d, const float* x, const float* y, c
   GenTable t;
   const int st = make_table(d, &t);
   if (st != ICTC_OK) return st;
-  hipLaunchKernelGGL(gen_tp_backward_kernel, dim3(grid_for(rows)), dim3(kLanes),
-                     bwd_lds_floats(t) * sizeof(float), stream, t, x, y, g, go, dx, dy, dg, rows);
+  const dim3 grid(grid_for(rows)), block(kLanes);
+  const size_t lds = bwd_lds_floats(t) * sizeof(float);
+  if (narrow(d))
+    hipLaunchKernelGGL(gen_tp_backward_kernel<9>, grid, block, lds, stream, t, x, y, g, go, dx, dy, dg, rows);
+  else
+    hipLaunchKernelGGL(gen_tp_backward_kernel<13>, grid, block, lds, stream, t, x, y, g, go, dx, dy, dg, rows);
   return status();
 }
 
@@ -445,9 +549,14 @@ int generic_msg_forward(const ictc_tp_desc& d, const float* x, const float* y, c
   GenTable t;
   const int st = make_table(d, &t);
   if (st != ICTC_OK) return st;
-  hipLaunchKernelGGL(gen_msg_forward_kernel, dim3(grid_for(nodes_dst)), dim3(kLanes),
-                     fwd_lds_floats(t) * sizeof(float), stream, t, x, y, g, src, rowptr, perm, out, nodes_src,
-                     nodes_dst);
+  const dim3 grid(grid_for(nodes_dst)), block(kLanes);
+  const size_t lds = fwd_lds_floats(t) * sizeof(float);
+  if (narrow(d))
+    hipLaunchKernelGGL(gen_msg_forward_kernel<9>, grid, block, lds, stream, t, x, y, g, src, rowptr, perm, out,
+                       nodes_src, nodes_dst);
+  else
+    hipLaunchKernelGGL(gen_msg_forward_kernel<13>, grid, block, lds, stream, t, x, y, g, src, rowptr, perm, out,
+                       nodes_src, nodes_dst);
   return status();
 }
 
@@ -458,9 +567,14 @@ int generic_msg_edge_grad(const ictc_tp_desc& d, const float* x, const float* y,
   const int st = make_table(d, &t);
   if (st != ICTC_OK) return st;
   const int chunks = (d.channels + kLanes - 1) / kLanes;
-  hipLaunchKernelGGL(gen_msg_edge_grad_kernel, dim3(grid_for(nodes_dst)), dim3(kLanes),
-                     bwd_lds_floats(t) * sizeof(float), stream, t, x, y, g, go, src, rowptr, perm, dyp, dg, dxe,
-                     nodes_src, nodes_dst, chunks);
+  const dim3 grid(grid_for(nodes_dst)), block(kLanes);
+  const size_t lds = bwd_lds_floats(t) * sizeof(float);
+  if (narrow(d))
+    hipLaunchKernelGGL(gen_msg_edge_grad_kernel<9>, grid, block, lds, stream, t, x, y, g, go, src, rowptr, perm, dyp,
+                       dg, dxe, nodes_src, nodes_dst, chunks);
+  else
+    hipLaunchKernelGGL(gen_msg_edge_grad_kernel<13>, grid, block, lds, stream, t, x, y, g, go, src, rowptr, perm,
+                       dyp, dg, dxe, nodes_src, nodes_dst, chunks);
   return status();
 }
 

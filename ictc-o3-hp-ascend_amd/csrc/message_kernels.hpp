@@ -825,6 +825,7 @@ msg_edge_grad_degree_kernel(const float* __restrict__ x, const float* __restrict
   const int c = chunk * kWave + lane;
   const bool live = c < C;
   const uint32_t vc = static_cast<uint32_t>(live ? c : 0) * 4u;   // lanes past C read channel 0, zero it
+  const uint32_t xdead = live ? 0u : 0xFFFFFFF0u;   // OR-ed into x gather offsets: out of range
   {
     const rsrc_t ron = make_rsrc(go + node * NOCF * C, NOCF * row);
     static_for<0, NPG>([&](auto Q) {
@@ -879,14 +880,14 @@ msg_edge_grad_degree_kernel(const float* __restrict__ x, const float* __restrict
     for (int q = 0; q < NT; ++q)
 #pragma unroll
       for (int j = 0; j < NY; ++j) in.yv[q][j] = ys[q][e * NY + j];
-    const uint32_t xoff = static_cast<uint32_t>(s) * NX * row;
+    // Lanes past C get a voffset beyond the descriptor's range (xdead), so the hardware returns
+    // 0: a select on the loaded value instead would make the wave wait for this (prefetched)
+    // gather before computing the current edge.
+    const uint32_t xoff = (static_cast<uint32_t>(s) * NX * row + vc) | xdead;
 #pragma unroll
     for (int q = 0; q < NT; ++q)
 #pragma unroll
-      for (int m = 0; m < NI; ++m) {
-        const float v = buf_load_vs(rx[q], xoff + vc, (L1 * L1 + m) * row);
-        in.xr[q][m] = live ? v : 0.f;
-      }
+      for (int m = 0; m < NI; ++m) in.xr[q][m] = buf_load_vs(rx[q], xoff, (L1 * L1 + m) * row);
 #pragma unroll
     for (int q = 0; q < NT; ++q) {
       const rsrc_t rg = make_rsrc(gs[q] + e * NP * C, NP * row);
