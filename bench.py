@@ -762,9 +762,9 @@ LIN_COUNTS, LIN_C, MFMA_F32_PEAK_TFLOPS = (4, 6, 7, 6), 128, 157.3   # fp32 MFMA
 def _bench_linear(device):
     """The second interaction's message linear of the cfg-4 MACE step (per degree 4 / 6 / 7 / 6
     path blocks of C = 128 channels into 128, 2,048 atoms, alpha = 1/avg_num_neighbors) on the
-    fp32-MFMA kernel, forward and input adjoint, beside the dense-GEMM route it replaced
-    (per-degree rearranged copies, rocBLAS products, concatenation)."""
-    from ictc_o3.backends.hip.degree_linear import DegreeLinearPlan, _forward_raw, _input_grad_raw
+    fp32-MFMA kernels, forward, input adjoint and weight adjoint, beside the dense-GEMM routes
+    they replaced (per-degree rearranged copies, rocBLAS products, concatenation)."""
+    from ictc_o3.backends.hip.degree_linear import DegreeLinearPlan, _forward_raw, _input_grad_raw, _weight_grad_raw
     from ictc_o3.backends.hip.linear import mm
     n, c, alpha = MACE_ATOMS, LIN_C, 1.0 / 50.0
     plan = DegreeLinearPlan(LIN_COUNTS, c, c)
@@ -780,10 +780,16 @@ def _bench_linear(device):
     def dense_input_grad():
         return torch.cat([mm(plan.y_rows(gy, l), ws[l]).reshape(n, 2 * l + 1, k, c).transpose(1, 2)
                           .reshape(n, -1) for l, k in enumerate(LIN_COUNTS)], 1) * alpha
+
+    def dense_weight_grad():   # the rearranged-rows route: copies of both operands, one product per degree
+        return [mm(plan.y_rows(gy, l).t(), plan.x_rows(x, l)) * alpha for l in range(len(LIN_COUNTS))]
+    need = [True] * len(LIN_COUNTS)
     # 30 warm-up launches (about 3 ms of work) first: the clocks ramp up over the first launches
     fwd_ms = _event_ms(lambda: _forward_raw(plan, x, ws, alpha), device, reps=100, warmup=30)
     grad_ms = _event_ms(lambda: _input_grad_raw(plan, gy, ws, alpha), device, reps=100, warmup=30)
-    dense = (_event_ms(dense_forward, device, reps=20), _event_ms(dense_input_grad, device, reps=20))
+    wgrad_ms = _event_ms(lambda: _weight_grad_raw(plan, 0, gy, x, alpha, need), device, reps=100, warmup=30)
+    dense = (_event_ms(dense_forward, device, reps=20), _event_ms(dense_input_grad, device, reps=20),
+             _event_ms(dense_weight_grad, device, reps=20))
     flops = 2 * n * c * sum((2 * l + 1) * k * c for l, k in enumerate(LIN_COUNTS))
     nbytes = 4 * (n * (plan.in_width + plan.out_width) + sum(w.numel() for w in ws))
 
@@ -796,7 +802,8 @@ def _bench_linear(device):
     return {"workload": "cfg4 MACE message linear (interaction 2): per-degree path blocks 4/6/7/6 x C128 -> C128, "
                         "2,048 atoms, fp32",
             "forward": leg(fwd_ms, dense[0], "degree_linear_kernel<0, true, 2, 64>"),
-            "input_grad": leg(grad_ms, dense[1], "degree_linear_kernel<1, true, 1, 128>")}
+            "input_grad": leg(grad_ms, dense[1], "degree_linear_kernel<1, true, 1, 128>"),
+            "weight_grad": leg(wgrad_ms, dense[2], "degree_linear_wgrad_kernel<0> + degree_linear_wgrad_sum_kernel")}
 
 
 def _mace_floor(edges: int, atoms: int, training: bool):

@@ -25,6 +25,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "ictc_common.hpp"
 #include "ictc_hip.h"
 
 namespace ictc {
@@ -346,6 +347,268 @@ int launch(const ictc_degree_linear_desc* desc, const float* in, const float* co
   return hipGetLastError() == hipSuccess ? ICTC_OK : ICTC_ERR_LAUNCH;
 }
 
+// Weight adjoint per degree (the dense product the layouts above otherwise need rearranged
+// copies for):  gW_l[o, j] = alpha * sum_{rows rho = n d + m} gy[n, o, m] * x[rho, j], with the x
+// rows of the forward (kWgIrMul: x[n, k, m, c], j = k C + c) or of the mul_ir map (kWgMulIr:
+// x[n, c, m] at offset C l^2, j = c).  The rows of a degree are split into ranges (range_rows, a
+// multiple of the 32-row chunk sized so that every block of the launch is resident at once: the
+// LDS of three blocks fits a CU, and a second partial round of blocks would idle most CUs); a
+// block of kWgWaves waves computes the 128 (o) x 64 (j) partial of one range (each wave 128 /
+// kWgWaves o x 64 j, v_mfma_f32_16x16x4_f32 over 32-row chunks staged through LDS, the next
+// chunk's loads in flight
+// during the current chunk's MFMAs) and stores it into the workspace; a second kernel sums the
+// ranges in order and scales by alpha (fixed order: bit-identical run to run).  Rows past the end
+// read zeros from the buffer range check (their offsets lie past the tensors).
+enum WgLayout { kWgIrMul = 0, kWgMulIr = 1 };
+constexpr int kWgMinRows = 256;   // shortest range (8 chunks)
+constexpr int kWgBlocksPerCu = 3;  // 51,200 B of LDS per block
+constexpr int kWgO = 128, kWgJ = 64;
+constexpr int kWgWaves = 8;   // waves per block: 16 o rows x 64 j each
+constexpr int kWgPitchA = kWgO + 4, kWgPitchB = kWgJ + 4;
+
+struct WgDegree {
+  int64_t rows;     // N d
+  int d, k;         // 2l + 1, output columns (counts[l] C)
+  int64_t xoff, yoff;
+  int ranges, otiles, jtiles;
+  int64_t tile0;    // first block of the degree
+  int64_t ws0;      // first workspace float of the degree: [ranges][O][k]
+  float* gw;        // [O, k] or null (not asked for)
+};
+
+struct WgArgs {
+  WgDegree g[ICTC_LINEAR_MAX_DEGREES];
+  int degrees;
+  int64_t tiles;
+  int64_t xwidth, ywidth;
+  int C, O;
+  int range_rows;
+  float alpha;
+  uint32_t xbytes, ybytes;
+};
+
+template <int LAYOUT>
+__global__ void __launch_bounds__(64 * kWgWaves)
+degree_linear_wgrad_kernel(const float* __restrict__ gy, const float* __restrict__ x, float* __restrict__ ws,
+                           const WgArgs a) {
+  const int64_t b = blockIdx.x;
+  int z = 0;
+  while (z + 1 < a.degrees && b >= a.g[z + 1].tile0) ++z;
+  const WgDegree g = a.g[z];
+  if (g.gw == nullptr) return;   // uniform: the degree's gradient is not asked for
+  const int64_t t = b - g.tile0;
+  const int ot = static_cast<int>(t % g.otiles);
+  const int64_t rest = t / g.otiles;
+  const int jt = static_cast<int>(rest % g.jtiles);
+  const int range = static_cast<int>(rest / g.jtiles);
+  const int o0 = ot * kWgO, j0 = jt * kWgJ;
+  const int64_t r0 = static_cast<int64_t>(range) * a.range_rows;
+  const int64_t r1 = r0 + a.range_rows < g.rows ? r0 + a.range_rows : g.rows;
+  const int d = g.d, C = a.C, O = a.O;
+  __shared__ float sA[2][32][kWgPitchA];   // [buffer][row][o]
+  __shared__ float sB[2][32][kWgPitchB];   // [buffer][row][j]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const rsrc_t ry = make_rsrc(gy, a.ybytes), rx = make_rsrc(x, a.xbytes);
+  // A staging: element e = tid + T i (T threads, i < NA): o = e % 128, row e / 128; o past O (or
+  // past the tile) reads o = 0 of its row: those accumulator rows are never stored.
+  constexpr int T = 64 * kWgWaves, NA = 32 * kWgO / T, NB = 32 * kWgJ / T, AR = T / kWgO, BR = T / kWgJ;
+  constexpr int OU = kWgO / 16 / kWgWaves;   // 16-row MFMA tiles per wave
+  const int ao = tid & 127, arr = tid >> 7;
+  const int aoc = o0 + ao < O ? o0 + ao : 0;
+  // B staging: element e = tid + T i (i < NB): j = e % 64, row e / 64; j past k reads column 0
+  const int bj = tid & 63, brr = tid >> 6;
+  const int bjc = j0 + bj < g.k ? j0 + bj : 0;
+  uint32_t bcol;   // byte offset of column bjc inside a row's degree block (m = 0)
+  if constexpr (LAYOUT == kWgIrMul) {
+    const int blk = bjc / C, c = bjc - blk * C;
+    bcol = static_cast<uint32_t>(blk * d * C + c) * 4u;
+  } else {
+    bcol = static_cast<uint32_t>(bjc * d) * 4u;
+  }
+  // Row rho = n d + m of a chunk starting at c0 = n0 d + m0: the row q of the chunk has
+  // n = n0 + (m0 + q) / d, computed as floor((m0 + q + 0.5) / d) in float (exact: m0 + q < 47 and
+  // the rounding error is far below 0.5 / d).  Offsets are 32-bit bytes (tensors below 2 GiB).
+  const float inv_d = 1.f / static_cast<float>(d);
+  const uint32_t yw4 = static_cast<uint32_t>(a.ywidth) * 4u, xw4 = static_cast<uint32_t>(a.xwidth) * 4u;
+  const uint32_t yo4 = static_cast<uint32_t>(g.yoff) * 4u + static_cast<uint32_t>(aoc * d) * 4u;
+  const uint32_t xo4 = static_cast<uint32_t>(g.xoff) * 4u + bcol;
+  const uint32_t mstep = (LAYOUT == kWgIrMul ? static_cast<uint32_t>(C) : 1u) * 4u;
+  float ra[NA], rb[NB];
+  auto fetch = [&](int64_t c0) {
+    const int n0 = static_cast<int>(c0 / d), m0 = static_cast<int>(c0 - static_cast<int64_t>(n0) * d);
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+      const int q = m0 + arr + AR * i;
+      const int dn = static_cast<int>((static_cast<float>(q) + 0.5f) * inv_d), m = q - dn * d;
+      // rows past r1 belong to the next range (or past the end): an out-of-range offset reads 0
+      const uint32_t off = c0 + arr + AR * i < r1 ? static_cast<uint32_t>(n0 + dn) * yw4 + yo4 + static_cast<uint32_t>(m) * 4u
+                                                  : 0xFFFFFFF0u;
+      ra[i] = buf_load<1>(ry, off).v[0];
+    }
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const int q = m0 + brr + BR * i;
+      const int dn = static_cast<int>((static_cast<float>(q) + 0.5f) * inv_d), m = q - dn * d;
+      const uint32_t off = c0 + brr + BR * i < r1 ? static_cast<uint32_t>(n0 + dn) * xw4 + xo4 + static_cast<uint32_t>(m) * mstep
+                                                  : 0xFFFFFFF0u;
+      rb[i] = buf_load<1>(rx, off).v[0];
+    }
+  };
+  auto stage = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < NA; ++i) sA[buf][arr + AR * i][ao] = ra[i];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) sB[buf][brr + BR * i][bj] = rb[i];
+  };
+  f32x4_t acc[OU][4] = {};
+  const int fr = lane & 15, fq = (lane >> 4) * 4;
+  auto mfma_chunk = [&](int buf) {
+#pragma unroll
+    for (int kg = 0; kg < 32; kg += 16) {
+      float av[OU][4], bv[4][4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+#pragma unroll
+        for (int u = 0; u < OU; ++u) av[u][j] = sA[buf][kg + fq + j][wave * 16 * OU + u * 16 + fr];
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) bv[tt][j] = sB[buf][kg + fq + j][tt * 16 + fr];
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int u = 0; u < OU; ++u)
+#pragma unroll
+          for (int tt = 0; tt < 4; ++tt)
+            acc[u][tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[u][j], bv[tt][j], acc[u][tt], 0, 0, 0);
+    }
+  };
+  fetch(r0);
+  stage(0);
+  __syncthreads();
+  int buf = 0;
+  for (int64_t c0 = r0; c0 < r1; c0 += 32) {
+    const bool more = c0 + 32 < r1;
+    if (more) fetch(c0 + 32);
+    mfma_chunk(buf);
+    if (more) stage(buf ^ 1);
+    __syncthreads();
+    buf ^= 1;
+  }
+  float* __restrict__ part = ws + g.ws0 + static_cast<int64_t>(range) * O * g.k;
+#pragma unroll
+  for (int u = 0; u < OU; ++u)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int o = o0 + wave * 16 * OU + u * 16 + 4 * (lane >> 4) + v;
+      if (o >= O) continue;
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        const int j = j0 + tt * 16 + fr;
+        if (j < g.k) part[static_cast<int64_t>(o) * g.k + j] = acc[u][tt][v];
+      }
+    }
+}
+
+// gW_l = alpha * the sum of the degree's range partials, in range order (one thread per entry).
+__global__ void __launch_bounds__(256) degree_linear_wgrad_sum_kernel(const float* __restrict__ ws, const WgArgs a,
+                                                                      int64_t entries) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < entries;
+       i += static_cast<int64_t>(gridDim.x) * 256) {
+    int64_t base = 0;
+    int z = 0;
+    for (; z < a.degrees; ++z) {
+      const int64_t n = static_cast<int64_t>(a.O) * a.g[z].k;
+      if (i < base + n) break;
+      base += n;
+    }
+    const WgDegree& g = a.g[z];
+    if (g.gw == nullptr) continue;
+    const int64_t e = i - base, stride = static_cast<int64_t>(a.O) * g.k;
+    const float* p = ws + g.ws0 + e;
+    float s = 0.f;
+    int r = 0;
+    for (; r + 4 <= g.ranges; r += 4) {   // four loads in flight, added in range order
+      const float v0 = p[r * stride], v1 = p[(r + 1) * stride], v2 = p[(r + 2) * stride], v3 = p[(r + 3) * stride];
+      s = (((s + v0) + v1) + v2) + v3;
+    }
+    for (; r < g.ranges; ++r) s += p[r * stride];
+    g.gw[e] = a.alpha * s;
+  }
+}
+
+// Compute units of the current device (256 on MI355X), read once per device.
+int compute_units() {
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    cached[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+  }
+  return cached[dev];
+}
+
+// Workspace floats of one weight-adjoint call, and the launch geometry (0 for an empty call).
+int wgrad_prepare(const ictc_degree_linear_desc* desc, int layout, float alpha, int64_t nodes, float* const* grad_w,
+                  WgArgs* a, int64_t* ws_floats, int64_t* entries) {
+  if (desc == nullptr || nodes < 0 || (layout != kWgIrMul && layout != kWgMulIr)) return ICTC_ERR_INVALID_ARGUMENT;
+  if (desc->lmax < 0 || desc->lmax >= ICTC_LINEAR_MAX_DEGREES || desc->channels < 1 || desc->out_channels < 1)
+    return ICTC_ERR_INVALID_ARGUMENT;
+  *a = WgArgs{};
+  a->degrees = desc->lmax + 1;
+  a->C = desc->channels;
+  a->O = desc->out_channels;
+  a->alpha = alpha;
+  int64_t xw = 0;
+  for (int l = 0; l <= desc->lmax; ++l) {
+    if (desc->counts[l] < 0) return ICTC_ERR_INVALID_ARGUMENT;
+    if (layout == kWgMulIr && desc->counts[l] != 1) return ICTC_ERR_INVALID_ARGUMENT;
+    xw += static_cast<int64_t>(desc->counts[l]) * (2 * l + 1) * desc->channels;
+  }
+  a->xwidth = xw;
+  a->ywidth = static_cast<int64_t>(desc->out_channels) * (desc->lmax + 1) * (desc->lmax + 1);
+  const int64_t xb = nodes * a->xwidth * 4, yb = nodes * a->ywidth * 4;
+  if (xb >= 0x7FFFFFF0 || yb >= 0x7FFFFFF0) return ICTC_ERR_UNSUPPORTED;   // 32-bit buffer offsets
+  a->xbytes = static_cast<uint32_t>(xb);
+  a->ybytes = static_cast<uint32_t>(yb);
+  int64_t xoff = 0, work = 0, columns = 0;
+  for (int l = 0; l <= desc->lmax; ++l) {
+    WgDegree& g = a->g[l];
+    g.d = 2 * l + 1;
+    g.rows = nodes * g.d;
+    g.k = desc->counts[l] * desc->channels;
+    g.xoff = layout == kWgIrMul ? xoff : static_cast<int64_t>(desc->channels) * l * l;
+    g.yoff = static_cast<int64_t>(desc->out_channels) * l * l;
+    g.gw = g.k > 0 ? grad_w[l] : nullptr;
+    xoff += static_cast<int64_t>(g.k) * g.d;
+    g.otiles = (desc->out_channels + kWgO - 1) / kWgO;
+    g.jtiles = (g.k + kWgJ - 1) / kWgJ;
+    if (g.gw) {
+      work += g.rows * g.otiles * g.jtiles;
+      columns += static_cast<int64_t>(g.otiles) * g.jtiles;
+    }
+  }
+  // ranges: blocks = sum ceil(rows / R) tiles <= work / R + columns <= the resident capacity
+  const int64_t room = static_cast<int64_t>(kWgBlocksPerCu) * compute_units() - columns;
+  int64_t rr = room > 0 ? (work + room - 1) / room : work;
+  rr = (rr + 31) / 32 * 32;
+  a->range_rows = static_cast<int>(rr < kWgMinRows ? kWgMinRows : (rr > (1 << 30) ? (1 << 30) : rr));
+  int64_t tiles = 0, ws = 0, ent = 0;
+  for (int l = 0; l <= desc->lmax; ++l) {
+    WgDegree& g = a->g[l];
+    g.ranges = g.gw ? static_cast<int>((g.rows + a->range_rows - 1) / a->range_rows) : 0;
+    g.tile0 = tiles;
+    g.ws0 = ws;
+    tiles += static_cast<int64_t>(g.ranges) * g.otiles * g.jtiles;
+    ws += static_cast<int64_t>(g.ranges) * desc->out_channels * g.k;
+    ent += static_cast<int64_t>(desc->out_channels) * g.k;
+  }
+  a->tiles = tiles;
+  *ws_floats = ws;
+  *entries = ent;
+  return ICTC_OK;
+}
+
 }  // namespace
 }  // namespace ictc
 
@@ -365,6 +628,45 @@ int ictc_hip_degree_linear_input_grad(const ictc_degree_linear_desc* desc, const
 int ictc_hip_degree_linear_mul_ir(const ictc_degree_linear_desc* desc, const float* x, const float* const* weights,
                                   float alpha, float* y, int64_t nodes, hipStream_t stream) {
   return ictc::launch<ictc::kMulIr>(desc, x, weights, alpha, y, nodes, stream);
+}
+
+int64_t ictc_hip_degree_linear_weight_grad_workspace(const ictc_degree_linear_desc* desc, int x_layout,
+                                                     int64_t nodes) {
+  float* none[ICTC_LINEAR_MAX_DEGREES];
+  float dummy = 0.f;
+  for (int l = 0; l < ICTC_LINEAR_MAX_DEGREES; ++l) none[l] = &dummy;   // every degree asked for
+  ictc::WgArgs a;
+  int64_t ws = 0, entries = 0;
+  const int st = ictc::wgrad_prepare(desc, x_layout, 1.f, nodes, none, &a, &ws, &entries);
+  return st == ICTC_OK ? ws : -static_cast<int64_t>(st);
+}
+
+int ictc_hip_degree_linear_weight_grad(const ictc_degree_linear_desc* desc, int x_layout, const float* grad_y,
+                                       const float* x, float alpha, float* workspace, int64_t workspace_floats,
+                                       float* const* grad_weights, int64_t nodes, hipStream_t stream) {
+  if (grad_weights == nullptr) return ICTC_ERR_INVALID_ARGUMENT;
+  ictc::WgArgs a;
+  int64_t ws = 0, entries = 0;
+  const int st = ictc::wgrad_prepare(desc, x_layout, alpha, nodes, grad_weights, &a, &ws, &entries);
+  if (st != ICTC_OK) return st;
+  if (entries == 0) return ICTC_OK;
+  // no rows: no ranges, and the sum kernel writes zero gradients
+  if (nodes > 0 && (grad_y == nullptr || x == nullptr || workspace == nullptr || workspace_floats < ws))
+    return ICTC_ERR_INVALID_ARGUMENT;
+  if (a.tiles > 0x7fffffff) return ICTC_ERR_UNSUPPORTED;
+  if (a.tiles > 0) {
+    if (x_layout == ictc::kWgIrMul)
+      hipLaunchKernelGGL(ictc::degree_linear_wgrad_kernel<ictc::kWgIrMul>, dim3(static_cast<unsigned>(a.tiles)),
+                         dim3(64 * ictc::kWgWaves), 0, stream, grad_y, x, workspace, a);
+    else
+      hipLaunchKernelGGL(ictc::degree_linear_wgrad_kernel<ictc::kWgMulIr>, dim3(static_cast<unsigned>(a.tiles)),
+                         dim3(64 * ictc::kWgWaves), 0, stream, grad_y, x, workspace, a);
+    if (hipGetLastError() != hipSuccess) return ICTC_ERR_LAUNCH;
+  }
+  const int64_t blocks = (entries + 255) / 256;
+  hipLaunchKernelGGL(ictc::degree_linear_wgrad_sum_kernel, dim3(static_cast<unsigned>(blocks < 4096 ? blocks : 4096)),
+                     dim3(256), 0, stream, workspace, a, entries);
+  return hipGetLastError() == hipSuccess ? ICTC_OK : ICTC_ERR_LAUNCH;
 }
 
 }  // extern "C"

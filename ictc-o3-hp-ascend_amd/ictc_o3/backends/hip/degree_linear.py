@@ -8,9 +8,10 @@ kernels' packed ir_mul output and written in the mul_ir node layout.
 x rows hold, per degree l, ``counts[l]`` path blocks of [2l+1][C]; y rows hold, per degree,
 [O][2l+1]; ``weights[l]`` is [O, counts[l] C].  The map is bilinear in (x, W): its input
 adjoint is the second kernel (``ictc_hip_degree_linear_input_grad``), whose own adjoints are
-the forward kernel again, and every weight adjoint is the dense product
-alpha * gY_l^T X_l on the rearranged blocks (``linear.mm``), so derivatives of any order stay
-on these routes.
+the forward kernel again, and every weight adjoint alpha * gY_l^T X_l is a third kernel
+(``ictc_hip_degree_linear_weight_grad``: split-row MFMA partials summed in order) that reads
+both layouts in place; its own adjoints are the forward and input-adjoint kernels with the
+weight cotangent as weights, so derivatives of any order stay on these kernels.
 """
 from __future__ import annotations
 
@@ -21,7 +22,6 @@ import torch
 
 from ... import _lib
 from ...autograd.adjoint_requirements import required_gradients
-from .linear import mm
 
 
 class DegreeLinearPlan:
@@ -38,6 +38,7 @@ class DegreeLinearPlan:
         self.in_width = sum(c * (2 * l + 1) * self.channels for l, c in enumerate(self.counts))
         self.out_width = self.out_channels * (self.lmax + 1) ** 2
         self._transposed = None
+        self._ws_floats = {}   # (x layout, nodes) -> weight-adjoint workspace floats
 
     def x_rows(self, x: torch.Tensor, l: int) -> torch.Tensor:
         """Packed x -> the degree-l rows [N (2l+1), counts[l] C] (column k C + c)."""
@@ -90,20 +91,78 @@ def _input_grad_raw(plan: DegreeLinearPlan, gy, weights, alpha):
     return gx
 
 
-def _scaled(t: torch.Tensor, alpha: float) -> torch.Tensor:
-    """alpha * t, without a launch when alpha is 1."""
-    return t if alpha == 1.0 else t * alpha
+_IR_MUL, _MUL_IR = 0, 1   # x layouts of the weight adjoint (the forward's, the mul_ir map's)
 
 
-def _weight_grads(plan: DegreeLinearPlan, gy, x, alpha, need):
-    """alpha * gY_l^T X_l per degree (dense products on rearranged rows; differentiable)."""
-    out = []
-    for l, n in enumerate(need):
-        if not n or plan.counts[l] == 0:
-            out.append(None)
-            continue
-        out.append(_scaled(mm(plan.y_rows(gy, l).t(), plan.x_rows(x, l)), alpha))
-    return out
+def _weight_grad_raw(plan: DegreeLinearPlan, layout: int, gy, x, alpha, need):
+    """[alpha * gY_l^T X_l if need[l] and counts[l] else None] in one kernel pair."""
+    nodes = gy.shape[0]
+    grads = [torch.empty(plan.out_channels, k * plan.channels, device=gy.device, dtype=torch.float32)
+             if n and k else None for n, k in zip(need, plan.counts)]
+    if not any(g is not None for g in grads):
+        return grads
+    key = (layout, nodes)
+    floats = plan._ws_floats.get(key)
+    if floats is None:
+        floats = _lib.lib().ictc_hip_degree_linear_weight_grad_workspace(ctypes.byref(plan.desc), layout, nodes)
+        _lib.check(-int(floats) if floats < 0 else 0, "ictc_hip_degree_linear_weight_grad_workspace")
+        plan._ws_floats[key] = floats
+    ws = torch.empty(max(int(floats), 1), device=gy.device, dtype=torch.float32)
+    ptrs = (ctypes.c_void_p * (plan.lmax + 1))()
+    for l, g in enumerate(grads):
+        ptrs[l] = g.data_ptr() if g is not None and g.numel() else None
+    _lib.check(_lib.lib().ictc_hip_degree_linear_weight_grad(
+        ctypes.byref(plan.desc), layout, gy.data_ptr() if gy.numel() else None, x.data_ptr() if x.numel() else None,
+        float(alpha), ws.data_ptr(), int(floats), ptrs, nodes, _lib.stream_of(gy.device)),
+        "ictc_hip_degree_linear_weight_grad")
+    return grads
+
+
+class _WeightGrad(torch.autograd.Function):
+    """The weight adjoint as a differentiable map of (gy, x): <gW, V> = alpha sum gy . (X V^T) rows,
+    so d/dgy is the forward map of x with weights V and d/dx the input adjoint of gy with weights V
+    (for the mul_ir layout: the mul_ir map and its transposed map)."""
+
+    @staticmethod
+    def forward(ctx, plan, alpha, layout, need, gy, x):
+        ctx.plan, ctx.alpha, ctx.layout, ctx.need = plan, alpha, layout, need
+        ctx.save_for_backward(gy, x)
+        grads = _weight_grad_raw(plan, layout, gy, x, alpha, need)
+        ctx.live = [g is not None for g in grads]
+        return tuple(g for g in grads if g is not None)
+
+    @staticmethod
+    def backward(ctx, *gbar):
+        gy, x = ctx.saved_tensors
+        plan, alpha = ctx.plan, ctx.alpha
+        it = iter(gbar)
+        vs = []
+        for l, live in enumerate(ctx.live):
+            v = next(it) if live else None
+            k = plan.counts[l] * plan.channels
+            vs.append(v.contiguous() if v is not None else
+                      torch.zeros(plan.out_channels, k, device=gy.device, dtype=torch.float32))
+        dgy = dx = None
+        if ctx.layout == _IR_MUL:
+            if ctx.needs_input_grad[4]:
+                dgy = _Forward.apply(plan, alpha, x, *vs)
+            if ctx.needs_input_grad[5]:
+                dx = _InputGrad.apply(plan, alpha, gy, *vs)
+        else:
+            if ctx.needs_input_grad[4]:
+                dgy = _MulIr.apply(plan, alpha, x, *vs)
+            if ctx.needs_input_grad[5]:
+                dx = _MulIr.apply(plan.transposed(), alpha, gy, *[v.t().contiguous() for v in vs])
+        return None, None, None, None, dgy, dx
+
+
+def _weight_grads(plan: DegreeLinearPlan, gy, x, alpha, need, layout: int = _IR_MUL):
+    """alpha * gY_l^T X_l per degree (None where not needed), differentiable."""
+    need = tuple(bool(n) and plan.counts[l] > 0 for l, n in enumerate(need))
+    if not any(need):
+        return [None] * len(need)
+    live = iter(_WeightGrad.apply(plan, float(alpha), layout, need, gy.contiguous(), x.contiguous()))
+    return [next(live) if n else None for n in need]
 
 
 class _Forward(torch.autograd.Function):
@@ -183,9 +242,7 @@ class _MulIr(torch.autograd.Function):
         gx = None
         if need[0]:
             gx = _MulIr.apply(plan.transposed(), ctx.alpha, gy, *[w.t().contiguous() for w in weights])
-        gw = [_scaled(mm(plan.y_rows(gy, l).t(), plan.mul_ir_rows(x, l)), ctx.alpha) if n else None
-              for l, n in enumerate(need[1:])]
-        return (None, None, gx, *gw)
+        return (None, None, gx, *_weight_grads(plan, gy, x, ctx.alpha, need[1:], _MUL_IR))
 
 
 def degree_linear_mul_ir(x: torch.Tensor, weights: Sequence[torch.Tensor], plan: "DegreeLinearPlan",

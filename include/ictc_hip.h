@@ -483,9 +483,9 @@ int ictc_hip_silu_second(const float* x, const float* grad, const float* cotange
  *                                    (weights is a host array of lmax + 1 device pointers).
  *   forward:    y[n, o, m]     = alpha sum_{k,c} weights[l][o, k C + c] x[n, k, m, c]
  *   input_grad: grad_x[n,k,m,c] = alpha sum_o grad_y[n, o, m] weights[l][o, k C + c]
- * (the adjoint of the forward in x; the weight gradient is the caller's dense product).  y and
- * grad_x are fully overwritten; a degree with counts[l] = 0 gets zero y rows.  Fixed
- * summation order (bit-identical run to run).
+ * (the adjoint of the forward in x; the weight adjoint is ictc_hip_degree_linear_weight_grad
+ * below).  y and grad_x are fully overwritten; a degree with counts[l] = 0 gets zero y rows.
+ * Fixed summation order (bit-identical run to run).
  */
 #define ICTC_LINEAR_MAX_DEGREES 8
 typedef struct ictc_degree_linear_desc {
@@ -515,6 +515,29 @@ int ictc_hip_degree_linear_input_grad(const ictc_degree_linear_desc* desc, const
 int ictc_hip_degree_linear_mul_ir(const ictc_degree_linear_desc* desc, const float* x,
                                   const float* const* weights, float alpha, float* y,
                                   int64_t nodes, hipStream_t stream);
+
+/*
+ * Weight adjoint of the two maps above, per degree l (rows rho = n d + m, d = 2l + 1):
+ *   grad_weights[l][o, j] = alpha sum_{n, m} grad_y[n, o, m] x[rho, j]
+ * with x in the forward's layout (x_layout 0: x[n, k, m, c], j = k C + c) or in the mul_ir map's
+ * (x_layout 1: x[n, c, m] at offset C l^2, j = c; counts[l] = 1 for every l).  It replaces the
+ * weight gradient autograd forms for reference pure_cartesian_ictd_fix.py:629-661 (the
+ * path-preserving linear) and :1145-1195 (the product's o3.Linear) from rearranged copies of both
+ * operands.  grad_weights is a host array of lmax + 1 device pointers [O, counts[l] C]; a null
+ * entry skips that degree.  The rows of a degree are split into ranges whose 128 x 64 partials go
+ * to `workspace` (at least ictc_hip_degree_linear_weight_grad_workspace(desc, x_layout, nodes)
+ * floats, caller-owned; the query returns minus the status code for an invalid descriptor or
+ * layout) and are then summed in range order (bit-identical run to run); every
+ * asked-for gradient is fully overwritten (zero for nodes = 0).  x and grad_y must each be below
+ * 2 GiB (ICTC_ERR_UNSUPPORTED otherwise).
+ */
+int64_t ictc_hip_degree_linear_weight_grad_workspace(const ictc_degree_linear_desc* desc, int x_layout,
+                                                     int64_t nodes);
+
+int ictc_hip_degree_linear_weight_grad(const ictc_degree_linear_desc* desc, int x_layout,
+                                       const float* grad_y, const float* x, float alpha,
+                                       float* workspace, int64_t workspace_floats,
+                                       float* const* grad_weights, int64_t nodes, hipStream_t stream);
 
 /*
  * Row-major fp32 product C[m,n] = alpha * op(A) op(B) + beta * C on rocBLAS, for the dense

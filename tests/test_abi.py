@@ -178,3 +178,36 @@ def test_message_rejects_node_tensors_beyond_32bit_offsets():
                                                 too_many, 4, 8, None) == 2
     assert lib.ictc_hip_message_edge_grad(ctypes.byref(d3), fake, fake, fake, fake, fake, fake, None,
                                           fake, fake, fake, too_many, 4, 8, 0, None) == 2
+
+
+def test_degree_linear_weight_grad_workspace_and_validation():
+    """Workspace size of the weight adjoint ([ranges][O][k] floats per degree, the ranges sized so
+    that the launch's 128 x 64 tiles fit three blocks per CU of 256 CUs, the device count this
+    GPU-less host falls back to) and its argument checks, all before any launch."""
+    from ictc_o3 import _lib
+    from ictc_o3.backends.hip.degree_linear import DegreeLinearPlan
+    lib = _lib.lib()
+    plan = DegreeLinearPlan((4, 6, 7, 6), 128, 128)
+    n = 2048
+    jt = [-(-k * 128 // 64) for k in plan.counts]
+    work = sum(n * (2 * l + 1) * j for l, j in enumerate(jt))
+    room = 3 * 256 - sum(jt)
+    rows = max(256, -(-(-(-work // room)) // 32) * 32)
+    assert rows == 576
+    ranges = [-(-(n * (2 * l + 1)) // rows) for l in range(4)]
+    assert sum(r * j for r, j in zip(ranges, jt)) <= 3 * 256
+    want = sum(r * 128 * k * 128 for r, k in zip(ranges, plan.counts))
+    assert lib.ictc_hip_degree_linear_weight_grad_workspace(ctypes.byref(plan.desc), 0, n) == want
+    assert lib.ictc_hip_degree_linear_weight_grad_workspace(ctypes.byref(plan.desc), 0, 0) == 0
+    # the mul_ir layout takes one channel block per degree; an unknown layout is rejected
+    assert lib.ictc_hip_degree_linear_weight_grad_workspace(ctypes.byref(plan.desc), 1, n) == -1
+    assert lib.ictc_hip_degree_linear_weight_grad_workspace(ctypes.byref(plan.desc), 2, n) == -1
+    fake = ctypes.c_void_p(16)  # never dereferenced: every call below fails validation
+    ptrs = (ctypes.c_void_p * 4)(fake, fake, fake, fake)
+    wg = lib.ictc_hip_degree_linear_weight_grad
+    assert wg(ctypes.byref(plan.desc), 0, fake, fake, 1.0, fake, want - 1, ptrs, n, None) == 1   # workspace too small
+    assert wg(ctypes.byref(plan.desc), 0, None, fake, 1.0, fake, want, ptrs, n, None) == 1       # no grad_y
+    assert wg(ctypes.byref(plan.desc), 0, fake, fake, 1.0, fake, want, None, n, None) == 1       # no outputs
+    assert wg(ctypes.byref(plan.desc), 0, fake, fake, 1.0, fake, want, ptrs, -1, None) == 1      # negative rows
+    # x beyond 2 GiB of 32-bit buffer offsets
+    assert wg(ctypes.byref(plan.desc), 0, fake, fake, 1.0, fake, 1 << 40, ptrs, 1 << 20, None) == 2

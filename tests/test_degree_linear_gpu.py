@@ -35,10 +35,11 @@ def _reference(x, weights, counts, c, o, alpha):
 # the vector path (C a multiple of 32) at the cfg-4 shape, with column counts that end inside a
 # 128-column tile (32, 96, 64: the clamped weight runs), with a degree without path blocks, and
 # with O not a multiple of 32 (its input adjoint on the element-wise path); the element-wise path
-# with odd C and O
+# with odd C and O; rows of a degree split over several 512-row ranges of the weight adjoint
+# (the last one partial) and O past one 128-row tile
 CASES = [((4, 6, 7, 6), 128, 128, 2048, 1 / 50.0), ((3, 4, 4), 64, 64, 77, 0.3), ((1, 3, 2), 32, 64, 45, 0.7),
          ((3, 0, 2), 64, 96, 70, 1.5), ((1, 1), 96, 40, 29, 1.0), ((2, 0, 3), 40, 24, 33, 1.0),
-         ((1,), 16, 8, 5, 2.0)]
+         ((1,), 16, 8, 5, 2.0), ((2, 3, 1), 64, 160, 600, 0.5)]
 
 
 @pytest.mark.parametrize("counts,c,o,nodes,alpha", CASES)
@@ -132,7 +133,7 @@ def test_channel_linear_up(gpu, lmax, c, nodes):
         assert_rel(a, b, what=f"linear_up second derivative {i}")
 
 
-@pytest.mark.parametrize("lmax,c,o,nodes", [(3, 128, 128, 2048), (2, 64, 32, 91), (1, 48, 40, 37)])
+@pytest.mark.parametrize("lmax,c,o,nodes", [(3, 128, 128, 2048), (2, 64, 32, 91), (1, 48, 40, 37), (1, 64, 136, 700)])
 def test_mul_ir_map(gpu, lmax, c, o, nodes):
     """y[n, l][o][m] = alpha sum_c W_l[o, c] x[n, l][c][m] (the product block's o3.Linear): mul_ir
     in and out, values and first and second derivatives against float64 torch; a plan with more
