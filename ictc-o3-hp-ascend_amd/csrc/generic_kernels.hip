@@ -19,12 +19,13 @@
 //   dg[p]      = sum_k dout_k * sum_i M_p[k][i] x_i
 //   dx[l1, i] += sum_k M_p[k][i] go_k                  (registers, one input degree at a time)
 //   dY[l2, j] += s_p * sum_{i,k} Chat_p[i][j][k] x_i go_k   (per lane, then summed over lanes)
-// The dY term is contracted per lane against the CG rows Chat_p[i][k][0..n2) (stored [i][k][j],
-// read with wave-uniform scalar loads), and the path's n2 lane partials are summed over the wave
-// by one transposing butterfly (a fixed order).  (The ICTC coupling tensors are dense -- 49,684
-// of the 52,570 entries up to degree 6 are nonzero -- so this costs sum_p n1 n2 n3 FMAs per
-// channel; it measured faster than first reducing the per-entry products x_i go_k over the
-// channels, which is bound by the latency of one cross-lane sum per 16 bond entries.)
+// For every degree <= 4 the dY term first reduces the products x_i go_k over the chunk's 64
+// channels on the matrix cores (T = X^T G, one 16 x 16 tile of v_mfma_f32_16x16x4_f32 per path),
+// then each lane contracts its (up to) four T entries with their CG rows Chat_p[i][k][0..n2)
+// (stored [i][k][j]) and the path's n2 lane partials are summed over the wave by one transposing
+// butterfly (a fixed order).  Above degree 4 (tiles past 16 x 16) it contracts per lane against
+// the CG rows read with wave-uniform scalar loads: sum_p n1 n2 n3 FMAs per channel, the ICTC
+// coupling tensors being dense (49,684 of the 52,570 entries up to degree 6 are nonzero).
 #include "generic.hpp"
 
 #include "ictc_common.hpp"
@@ -113,6 +114,9 @@ __device__ void build_bonds(const GenTable& t, const float* sY, float* sM, int l
     });
   }
 }
+
+// LDS -> LDS visibility inside the wave (lanes reading what other lanes wrote).
+__device__ __forceinline__ void wave_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
 // Per-lane byte offset of channel c in a row, or for lanes past C an offset beyond every
 // descriptor's range (their loads return 0 and their values are never stored).
@@ -291,27 +295,73 @@ __device__ void backward_instance(const GenTable& t, const float* sM, const BwdL
         }
       });
       if (want_dy) {
-        with_width<NM>(q.n2, [&](auto N2) {
-          // this lane's sum_{i,k} Chat[i][k][j] x_i go_k against the CG rows (scalar loads), then
-          // summed over the lanes (a fixed butterfly) and added by the owner lanes
-          using WS = WaveSums<N2>;
-          float part[N2];
+        if constexpr (NM == 9) {
+          // T[i][k] = sum over the chunk's 64 channels of x_i go_k on the matrix cores: A = the x
+          // rows (lane l gives row l % 16), B = the go rows (column l % 16), four consecutive
+          // v_mfma_f32_16x16x4_f32 per 16 channels with channel 16 g + 4 (l / 16) + j in both
+          // operands (rows and columns past n1 / n3 repeat the last one and are not used); two
+          // accumulators over alternate channel groups.  Lane l then holds T[4 (l / 16) + v][l % 16].
+          wave_sync();
+          const int fr = lane & 15, fq = (lane >> 4) * 4;
+          const float* ar = L.sX + (fr < q.n1 ? fr : q.n1 - 1) * kLanes + fq;
+          const float* br = L.sG + (fr < q.n3 ? fr : q.n3 - 1) * kLanes + fq;
+          f32x4 t0 = {0.f, 0.f, 0.f, 0.f}, t1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int j = 0; j < N2; ++j) part[j] = 0.f;
-          for (int i = 0; i < q.n1; ++i) {
-            const float xi = L.sX[i * kLanes + lane];
-#pragma unroll 4
-            for (int k = 0; k < q.n3; ++k) {
-              const float tk = xi * L.sG[k * kLanes + lane];
-              const float* row = cg + (i * q.n3 + k) * N2;
+          for (int g4 = 0; g4 < 4; g4 += 2) {
+            const f32x4 a0 = *reinterpret_cast<const f32x4*>(ar + 16 * g4);
+            const f32x4 b0 = *reinterpret_cast<const f32x4*>(br + 16 * g4);
+            const f32x4 a1 = *reinterpret_cast<const f32x4*>(ar + 16 * g4 + 16);
+            const f32x4 b1 = *reinterpret_cast<const f32x4*>(br + 16 * g4 + 16);
 #pragma unroll
-              for (int j = 0; j < N2; ++j) part[j] = fmaf(row[j], tk, part[j]);
+            for (int j = 0; j < 4; ++j) {
+              t0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a0[j], b0[j], t0, 0, 0, 0);
+              t1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a1[j], b1[j], t1, 0, 0, 0);
             }
           }
-          const float tot = WS::reduce(part, lane);
-          const int j = WS::index(lane);
-          if (WS::owner(lane) && j < N2) L.sDY[q.l2 * q.l2 + j] = fmaf(t.scale[p], tot, L.sDY[q.l2 * q.l2 + j]);
-        });
+          // dY_j += s sum_{i,k} Chat[i][k][j] T[i][k]: each lane its (up to) four entries with their
+          // CG rows (per-lane loads), then the lane partials summed by one transposing butterfly
+          // (a fixed order)
+          with_width<NM>(q.n2, [&](auto N2) {
+            using WS = WaveSums<N2>;
+            float part[N2];
+#pragma unroll
+            for (int j = 0; j < N2; ++j) part[j] = 0.f;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+              const int i = fq + v;
+              const bool use = i < q.n1 && fr < q.n3;
+              const float tv = use ? t0[v] + t1[v] : 0.f;
+              const float* row = cg + (use ? i * q.n3 + fr : 0) * N2;
+#pragma unroll
+              for (int j = 0; j < N2; ++j) part[j] = fmaf(row[j], tv, part[j]);
+            }
+            const float tot = WS::reduce(part, lane);
+            const int j = WS::index(lane);
+            if (WS::owner(lane) && j < N2) L.sDY[q.l2 * q.l2 + j] = fmaf(t.scale[p], tot, L.sDY[q.l2 * q.l2 + j]);
+          });
+        } else {
+          with_width<NM>(q.n2, [&](auto N2) {
+            // this lane's sum_{i,k} Chat[i][k][j] x_i go_k against the CG rows (scalar loads), then
+            // summed over the lanes (a fixed butterfly) and added by the owner lanes
+            using WS = WaveSums<N2>;
+            float part[N2];
+#pragma unroll
+            for (int j = 0; j < N2; ++j) part[j] = 0.f;
+            for (int i = 0; i < q.n1; ++i) {
+              const float xi = L.sX[i * kLanes + lane];
+#pragma unroll 4
+              for (int k = 0; k < q.n3; ++k) {
+                const float tk = xi * L.sG[k * kLanes + lane];
+                const float* row = cg + (i * q.n3 + k) * N2;
+#pragma unroll
+                for (int j = 0; j < N2; ++j) part[j] = fmaf(row[j], tk, part[j]);
+              }
+            }
+            const float tot = WS::reduce(part, lane);
+            const int j = WS::index(lane);
+            if (WS::owner(lane) && j < N2) L.sDY[q.l2 * q.l2 + j] = fmaf(t.scale[p], tot, L.sDY[q.l2 * q.l2 + j]);
+          });
+        }
       }
       if (dg && on) dg[static_cast<int64_t>(p) * C + c] = dgv;
       if (more) {
