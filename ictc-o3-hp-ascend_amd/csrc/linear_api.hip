@@ -56,7 +56,9 @@ struct LinearArgs {
 
 // MODE kForward: A = x rows (K = x columns), B^T = W rows, D -> y.  kInputGrad: A = gy rows
 // (K = O), B = W, D -> gx columns.  kMulIr: A = mul_ir x rows (K = C, stride d), B^T = W rows,
-// D -> y (mul_ir).  VEC (channels, and for kInputGrad out_channels, multiples of 32): every
+// D -> y (mul_ir).  kMulIrT: kMulIr with the weights given transposed (B = W [K, O] rows read
+// like kInputGrad's, so no transposed copy of W is made).  VEC (channels, and for kInputGrad and
+// kMulIrT out_channels, multiples of 32): every
 // 32-wide K chunk is full, each K chunk of an x row lies in one path block and weight rows are
 // float4-aligned, so operands are fetched into registers one chunk ahead (their loads in flight
 // while the MFMAs of the current chunk run); with two LDS buffers
@@ -64,14 +66,15 @@ struct LinearArgs {
 // chunk), with one (NBUF 1, half the LDS and so twice the resident blocks) after a second barrier.
 // The forward's long K (counts C) takes two buffers, the input adjoint's short K (O) one.
 // Without VEC, element by element, one chunk at a time.
-enum LinearMode { kForward = 0, kInputGrad = 1, kMulIr = 2 };
+enum LinearMode { kForward = 0, kInputGrad = 1, kMulIr = 2, kMulIrT = 3 };
 
 template <int MODE, bool VEC, int NBUF, int TN>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NBUF == 1 ? (TN > kTile ? 5 : 8) : 4)))
 degree_linear_kernel(const float* __restrict__ in, float* __restrict__ out, const LinearArgs a) {
-  constexpr bool FWD = MODE != kInputGrad;      // D -> mul_ir y rows, B^T = W rows
+  constexpr bool FWD = MODE != kInputGrad;      // D -> mul_ir y rows
+  constexpr bool BT = MODE == kInputGrad || MODE == kMulIrT;   // B = W rows over K (staged transposed)
   constexpr int NT = TN / 16;                   // 16-column MFMA tiles per wave
-  static_assert(FWD ? TN == kTile : (TN == kTile || TN == kTileIg), "column tile");
+  static_assert(BT ? (TN == kTile || TN == kTileIg) : TN == kTile, "column tile");
   constexpr bool STRIDED = MODE != kForward;    // A rows read at stride d over K (mul_ir)
   // the degree's geometry in registers (read once from the kernel arguments)
   const DegreeGeometry g = a.g[blockIdx.z];
@@ -105,7 +108,8 @@ degree_linear_kernel(const float* __restrict__ in, float* __restrict__ out, cons
   // reads stay conflict-free.
   constexpr int CPT = TN / 8;
   const int wk = tid >> 3, wc = (tid & 7) * CPT;
-  auto bsw = [](int col) { return FWD ? 0 : ((col >> (CPT == 16 ? 4 : 3)) & 3) * 8; };
+  auto bsw = [](int col) { return BT ? ((col >> (CPT == 16 ? 4 : 3)) & 3) * 8 : 0; };
+  const int wld = MODE == kInputGrad ? g.k : ncols;   // BT: floats per weight row (over the columns)
   f32x4_t acc[NT] = {};
   const int fr = lane & 15, fq = (lane >> 4) * 4;
   auto mfma_chunk = [&](int buf) {
@@ -141,7 +145,7 @@ degree_linear_kernel(const float* __restrict__ in, float* __restrict__ out, cons
   if constexpr (VEC) {
     // registers of one chunk: A (8 floats of the thread's row), B (8 floats, or CPT of the
     // input adjoint's weight row)
-    constexpr int NRB = FWD ? 2 : CPT / 4;
+    constexpr int NRB = BT ? CPT / 4 : 2;
     f32x4_t ra0, ra1, rb[NRB];
     // Every K chunk is full under VEC (kdim a multiple of 32), and no load is conditional on the
     // lane: a select or a branch on a loaded value would wait for the load at the fetch instead of
@@ -161,16 +165,16 @@ degree_linear_kernel(const float* __restrict__ in, float* __restrict__ out, cons
         ra0 = *reinterpret_cast<const f32x4_t*>(p);
         ra1 = *reinterpret_cast<const f32x4_t*>(p + 4);
       }
-      if constexpr (FWD) {
+      if constexpr (!BT) {
         const int col = c0 + ar < ncols ? c0 + ar : ncols - 1;   // weight row col, 8 consecutive k
         const float* p = g.w + static_cast<int64_t>(col) * g.k + k0 + akq;
         rb[0] = *reinterpret_cast<const f32x4_t*>(p);
         rb[1] = *reinterpret_cast<const f32x4_t*>(p + 4);
       } else {
-        // ncols (counts C) is a multiple of 32 and CPT is 8 or 16: the clamped run of CPT
+        // ncols is a multiple of 32 under VEC and CPT is 8 or 16: the clamped run of CPT
         // columns stays in range
         const int col = c0 + wc < ncols ? c0 + wc : ncols - CPT;
-        const float* p = g.w + static_cast<int64_t>(k0 + wk) * g.k + col;
+        const float* p = g.w + static_cast<int64_t>(k0 + wk) * wld + col;
 #pragma unroll
         for (int q = 0; q < NRB; ++q) rb[q] = *reinterpret_cast<const f32x4_t*>(p + 4 * q);
       }
@@ -178,7 +182,7 @@ degree_linear_kernel(const float* __restrict__ in, float* __restrict__ out, cons
     auto stage = [&](int buf) {
       *reinterpret_cast<f32x4_t*>(&sA[buf][ar][akq]) = ra0;
       *reinterpret_cast<f32x4_t*>(&sA[buf][ar][akq + 4]) = ra1;
-      if constexpr (FWD) {
+      if constexpr (!BT) {
         *reinterpret_cast<f32x4_t*>(&sB[buf][ar][akq]) = rb[0];
         *reinterpret_cast<f32x4_t*>(&sB[buf][ar][akq + 4]) = rb[1];
       } else {
@@ -216,7 +220,7 @@ degree_linear_kernel(const float* __restrict__ in, float* __restrict__ out, cons
     }
   } else {
     for (int k0 = 0; k0 < kdim; k0 += kKc) {
-      if constexpr (FWD) {
+      if constexpr (!BT) {
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
           const int kk = k0 + akq + u;
@@ -244,7 +248,7 @@ degree_linear_kernel(const float* __restrict__ in, float* __restrict__ out, cons
         for (int u = 0; u < 8; ++u) {
           const int col = c0 + wc + u;
           sB[0][wc + u][wk ^ bsw(wc + u)] =
-              (kk < kdim && col < ncols) ? g.w[static_cast<int64_t>(kk) * g.k + col] : 0.f;
+              (kk < kdim && col < ncols) ? g.w[static_cast<int64_t>(kk) * wld + col] : 0.f;
         }
       }
       __syncthreads();
@@ -323,7 +327,7 @@ int launch(const ictc_degree_linear_desc* desc, const float* in, const float* co
   int64_t max_rows = 0;
   const int st = prepare(desc, weights, alpha, nodes, &a, &degrees, &max_rows, &max_cols, MODE != kInputGrad);
   if (st != ICTC_OK) return st;
-  if (MODE == kMulIr) {   // one channel block per degree: x mul_ir [N, C (L+1)^2]
+  if (MODE == kMulIr || MODE == kMulIrT) {   // one channel block per degree: x mul_ir [N, C (L+1)^2]
     for (int l = 0; l <= desc->lmax; ++l)
       if (desc->counts[l] != 1) return ICTC_ERR_INVALID_ARGUMENT;
   }
@@ -334,7 +338,8 @@ int launch(const ictc_degree_linear_desc* desc, const float* in, const float* co
   // two LDS buffers for the long K of the forward (counts C), one for the short K of the others;
   // the input adjoint's vector path takes 128 columns per block (its B tile is read once per
   // 64 x 128 outputs instead of 64 x 64)
-  const bool vec = desc->channels % 32 == 0 && (MODE != kInputGrad || desc->out_channels % 32 == 0);
+  const bool vec = desc->channels % 32 == 0 &&
+                   ((MODE != kInputGrad && MODE != kMulIrT) || desc->out_channels % 32 == 0);
   constexpr int kTn = MODE == kInputGrad ? kTileIg : kTile;
   const int tn = vec ? kTn : kTile;
   const dim3 grid(static_cast<unsigned>(row_tiles), static_cast<unsigned>((max_cols + tn - 1) / tn),
@@ -628,6 +633,12 @@ int ictc_hip_degree_linear_input_grad(const ictc_degree_linear_desc* desc, const
 int ictc_hip_degree_linear_mul_ir(const ictc_degree_linear_desc* desc, const float* x, const float* const* weights,
                                   float alpha, float* y, int64_t nodes, hipStream_t stream) {
   return ictc::launch<ictc::kMulIr>(desc, x, weights, alpha, y, nodes, stream);
+}
+
+int ictc_hip_degree_linear_mul_ir_transposed(const ictc_degree_linear_desc* desc, const float* x,
+                                             const float* const* weights, float alpha, float* y, int64_t nodes,
+                                             hipStream_t stream) {
+  return ictc::launch<ictc::kMulIrT>(desc, x, weights, alpha, y, nodes, stream);
 }
 
 int64_t ictc_hip_degree_linear_weight_grad_workspace(const ictc_degree_linear_desc* desc, int x_layout,

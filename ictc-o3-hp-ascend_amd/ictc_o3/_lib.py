@@ -15,7 +15,7 @@ import torch  # noqa: F401  (must precede CDLL, see module docstring)
 
 MAX_PATHS = 128
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libictc_hip.so")
-ABI_VERSION = 17
+ABI_VERSION = 18
 
 
 class TpDesc(ctypes.Structure):
@@ -97,6 +97,8 @@ _SIGNATURES = {
                                                          _P, _I64, _P]),
     "ictc_hip_degree_linear_mul_ir": (ctypes.c_int, [ctypes.POINTER(DegreeLinearDesc), _P, _P, ctypes.c_float, _P,
                                                      _I64, _P]),
+    "ictc_hip_degree_linear_mul_ir_transposed": (ctypes.c_int, [ctypes.POINTER(DegreeLinearDesc), _P, _P,
+                                                                ctypes.c_float, _P, _I64, _P]),
     "ictc_hip_degree_linear_weight_grad_workspace": (_I64, [ctypes.POINTER(DegreeLinearDesc), ctypes.c_int, _I64]),
     "ictc_hip_degree_linear_weight_grad": (ctypes.c_int, [ctypes.POINTER(DegreeLinearDesc), ctypes.c_int, _P, _P,
                                                           ctypes.c_float, _P, _I64, _P, _I64, _P]),

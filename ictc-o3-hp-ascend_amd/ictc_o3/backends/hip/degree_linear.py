@@ -211,12 +211,38 @@ def _check_weights(weights, plan, device):
             raise ValueError("weights must be float32 on the features' device")
 
 
-def _mul_ir_raw(plan: "DegreeLinearPlan", x, weights, alpha):
+def _mul_ir_raw(plan: "DegreeLinearPlan", x, weights, alpha, transposed: bool = False):
+    """alpha W_l x per degree, or alpha W_l^T x with W_l [plan.channels, plan.out_channels]."""
     y = torch.empty(x.shape[0], plan.out_width, device=x.device, dtype=torch.float32)
-    _lib.check(_lib.lib().ictc_hip_degree_linear_mul_ir(
+    name = "ictc_hip_degree_linear_mul_ir_transposed" if transposed else "ictc_hip_degree_linear_mul_ir"
+    _lib.check(getattr(_lib.lib(), name)(
         ctypes.byref(plan.desc), x.data_ptr() if x.numel() else None, _pointers(weights), float(alpha),
-        y.data_ptr() if y.numel() else None, x.shape[0], _lib.stream_of(x.device)), "ictc_hip_degree_linear_mul_ir")
+        y.data_ptr() if y.numel() else None, x.shape[0], _lib.stream_of(x.device)), name)
     return y
+
+
+class _MulIrT(torch.autograd.Function):
+    """y = alpha W_l^T x per degree for the plan with channels and out_channels swapped, reading
+    W_l [O, C] (the o3.Linear weight) as it is stored: the input adjoint of _MulIr without a
+    transposed weight copy.  Adjoints: in x the _MulIr map of the cotangent, in W the weight
+    adjoint with gY = x and X = the cotangent."""
+
+    @staticmethod
+    def forward(ctx, plan_t, alpha, x, *weights):
+        ctx.plan_t, ctx.alpha = plan_t, alpha
+        ctx.save_for_backward(x, *weights)
+        return _mul_ir_raw(plan_t, x, list(weights), alpha, transposed=True)
+
+    @staticmethod
+    def backward(ctx, z):
+        x, *weights = ctx.saved_tensors
+        need = required_gradients((x, *weights), ctx.needs_input_grad[2:])
+        if z is None or not any(need):
+            return (None, None, None) + (None,) * len(weights)
+        z = z.contiguous()
+        plan = ctx.plan_t.transposed()
+        gx = _MulIr.apply(plan, ctx.alpha, z, *weights) if need[0] else None
+        return (None, None, gx, *_weight_grads(plan, x, z, ctx.alpha, need[1:], _MUL_IR))
 
 
 class _MulIr(torch.autograd.Function):
@@ -241,7 +267,7 @@ class _MulIr(torch.autograd.Function):
         plan = ctx.plan
         gx = None
         if need[0]:
-            gx = _MulIr.apply(plan.transposed(), ctx.alpha, gy, *[w.t().contiguous() for w in weights])
+            gx = _MulIrT.apply(plan.transposed(), ctx.alpha, gy, *weights)
         return (None, None, gx, *_weight_grads(plan, gy, x, ctx.alpha, need[1:], _MUL_IR))
 
 

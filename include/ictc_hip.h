@@ -517,6 +517,17 @@ int ictc_hip_degree_linear_mul_ir(const ictc_degree_linear_desc* desc, const flo
                                   int64_t nodes, hipStream_t stream);
 
 /*
+ * The same map with the weights given transposed: weights[l] [channels, out_channels] and
+ *   y[n, o, m] = alpha sum_c weights[l][c, o] x[n, c, m]
+ * i.e. the input adjoint of ictc_hip_degree_linear_mul_ir for the descriptor with channels and
+ * out_channels swapped, applied to its own weights without a transposed copy of them (the
+ * backward of the product block's o3.Linear, pure_cartesian_ictd_fix.py:1145-1195).
+ */
+int ictc_hip_degree_linear_mul_ir_transposed(const ictc_degree_linear_desc* desc, const float* x,
+                                             const float* const* weights, float alpha, float* y,
+                                             int64_t nodes, hipStream_t stream);
+
+/*
  * Weight adjoint of the two maps above, per degree l (rows rho = n d + m, d = 2l + 1):
  *   grad_weights[l][o, j] = alpha sum_{n, m} grad_y[n, o, m] x[rho, j]
  * with x in the forward's layout (x_layout 0: x[n, k, m, c], j = k C + c) or in the mul_ir map's
