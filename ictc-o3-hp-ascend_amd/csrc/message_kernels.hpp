@@ -799,8 +799,17 @@ struct NodeUOf {
   static constexpr NodeU tab = make_node_u<LIN, LE, LOUT, L1>();
 };
 
+// Resident waves per SIMD the compiler is held to for an edge-gradient launch of an lmax-3 set
+// (register budget 512 / waves), where its LDS allows more waves than its unconstrained register
+// allocation: input degree 2 first order at 4 (128 VGPRs; its 39.7 KB table allows 4 blocks per
+// CU, 130 VGPRs would allow 3), input degree 3 tangent at 3 (168 VGPRs; 173 allowed 2, its 50 KB
+// table 3).
+constexpr int msg_edge_grad_waves(int lin, int l1, bool jvp) {
+  return lin < 3 ? 1 : l1 == 2 && !jvp ? 4 : l1 == 3 && jvp ? 3 : 1;
+}
+
 template <int LIN, int LE, int LOUT, int L1, bool JVP, bool ACC = false>
-__global__ void __launch_bounds__(kMsgBlock)
+__global__ void __launch_bounds__(kMsgBlock) __attribute__((amdgpu_waves_per_eu(msg_edge_grad_waves(LIN, L1, JVP))))
 msg_edge_grad_degree_kernel(const float* __restrict__ x, const float* __restrict__ y, const float* __restrict__ g,
                           const MsgTangent t, const float* __restrict__ go, const int64_t* __restrict__ src,
                           const int64_t* __restrict__ rowptr, const int64_t* __restrict__ perm,
