@@ -396,7 +396,9 @@ template <int LAYOUT>
 __global__ void __launch_bounds__(64 * kWgWaves)
 degree_linear_wgrad_kernel(const float* __restrict__ gy, const float* __restrict__ x, float* __restrict__ ws,
                            const WgArgs a) {
-  const int64_t b = blockIdx.x;
+  // XCD-contiguous block order: the column tiles of one row range (which read the same gY rows)
+  // run on one XCD and share its L2
+  const int64_t b = xcd_block(blockIdx.x, gridDim.x);
   int z = 0;
   while (z + 1 < a.degrees && b >= a.g[z + 1].tile0) ++z;
   const WgDegree g = a.g[z];
