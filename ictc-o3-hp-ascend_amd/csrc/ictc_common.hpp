@@ -206,6 +206,18 @@ __device__ __forceinline__ void buf_store_lane(rsrc_t r, bool live, uint32_t off
   buf_store<1>(r, live ? off : 0xFFFFFFF0u, Vec<1>{{v}});
 }
 
+// Compute units of the current device (256 on MI355X), read once per device.
+inline int compute_units() {
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    cached[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+  }
+  return cached[dev];
+}
+
 // Workgroups are dispatched to the GPU's XCDs (each with its own L2) round-robin by block
 // index.  xcd_block(b, n) renumbers the n blocks of a launch so that each XCD receives one
 // contiguous range of work items (XCD x gets items [start(x), start(x) + count(x))), which

@@ -543,18 +543,6 @@ __global__ void __launch_bounds__(256) degree_linear_wgrad_sum_kernel(const floa
   }
 }
 
-// Compute units of the current device (256 on MI355X), read once per device.
-int compute_units() {
-  static int cached[64] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int n = 0;
-    cached[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
-  }
-  return cached[dev];
-}
-
 // Workspace floats of one weight-adjoint call, and the launch geometry (0 for an empty call).
 int wgrad_prepare(const ictc_degree_linear_desc* desc, int layout, float alpha, int64_t nodes, float* const* grad_w,
                   WgArgs* a, int64_t* ws_floats, int64_t* entries) {

@@ -15,7 +15,7 @@ import torch  # noqa: F401  (must precede CDLL, see module docstring)
 
 MAX_PATHS = 128
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libictc_hip.so")
-ABI_VERSION = 18
+ABI_VERSION = 19
 
 
 class TpDesc(ctypes.Structure):
@@ -105,6 +105,9 @@ _SIGNATURES = {
     "ictc_hip_silu_second": (ctypes.c_int, [_P, _P, _P, _P, _P, _I64, _P]),
     "ictc_hip_edge_embedding": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _P, _P, _P, ctypes.c_int, ctypes.c_int,
                                                ctypes.c_float, _I64, _P]),
+    "ictc_hip_radial_mlp_workspace": (_I64, [_I64]),
+    "ictc_hip_radial_mlp": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _P, ctypes.c_float, _P, _P, _P, _P, _P, _P, _I64,
+                                           _P, _P, _P, ctypes.c_int, _I64, _P]),
     "ictc_hip_sgemm": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, _I64, _I64, _I64, ctypes.c_float, _P, _I64, _P,
                                       _I64, ctypes.c_float, _P, _I64, _P]),
     "ictc_hip_radius_graph_count": (ctypes.c_int, [ctypes.POINTER(CellGrid), _P, _P, _P, _P, _I64, _P, _P]),

@@ -50,6 +50,7 @@ from ictc_o3.backends.hip.radial_message import fold_projection, packed_radial_g
 from ictc_o3.basis.ictd_irreps import EdgeWeightedPathPreservingTensorProduct
 from ictc_o3.ops.symmetric_contraction import ICTDBridgeUSymmetricContractionSO3
 
+from . import radial_mlp
 from .activation import silu
 from .embedding import edge_embedding
 from .geometry import edge_vectors, one_hot_rows
@@ -174,8 +175,12 @@ class Interaction(nn.Module):
     def radial_hidden(self, edge_feats):
         """self.fc up to its last Linear: (the last layer's input [E, 64], its weight [P*C, 64]),
         each normalised SiLU's constant folded into the next layer's weight instead of scaling
-        the [E, 64] activations."""
+        the [E, 64] activations.  On the GPU the three layers and their activations run as one
+        kernel per derivative order (mace_hip.radial_mlp)."""
         layers = [m for m in self.fc if isinstance(m, nn.Linear)]
+        w = [lin.weight for lin in layers]
+        if len(layers) == 4 and radial_mlp.supported(edge_feats, *w[:3]):
+            return radial_mlp.radial_hidden(edge_feats, *w[:3], SILU_SCALE), w[3] * SILU_SCALE
         h = layers[0](edge_feats)
         for lin in layers[1:-1]:
             h = linear(silu(h), lin.weight * SILU_SCALE)

@@ -472,6 +472,38 @@ int ictc_hip_silu_second(const float* x, const float* grad, const float* cotange
                          float* grad_grad, float* grad_x, int64_t n, hipStream_t stream);
 
 /*
+ * Radial MLP of the MACE interaction up to its last Linear, on fp32 MFMA (reference
+ * mace_ictc/models/pure_cartesian_ictd_fix.py:1545-1553 `fc` without its last layer, applied to
+ * the edge features at :1795; _Normalize2MomSiLU :610-619).  Per edge, with f [E, B] row-major
+ * (1 <= B <= 16), weights in nn.Linear layout w1 [64, B], w2 [64, 64], w3 [64, 64] and `scale`
+ * the normalised-SiLU constant applied to the activations that feed w2 and w3:
+ *   h = silu(scale w3 silu(scale w2 silu(w1 f)))                               [E, 64]
+ * Modes:
+ *   ICTC_RADIAL_VALUE:   out_hidden = h.
+ *   ICTC_RADIAL_VJP:     for grad_hidden g [E, 64]: out_grad_feats = J^T g [E, B] and
+ *                        grad_w1/2/3 = the gradients of <g, h> in the weights (each optional).
+ *   ICTC_RADIAL_VJP_VJP: for g and cotangent u [E, B] of the VJP's feature gradient, the
+ *                        derivatives of <u, J^T g>: out_grad_grad_hidden = J u [E, 64] (its
+ *                        gradient in g), out_grad_feats = its gradient in f, grad_w1/2/3 = its
+ *                        gradients in the weights (each optional).
+ * Weight gradients are summed over edges through a workspace of
+ * ictc_hip_radial_mlp_workspace(edges) floats (caller-owned; minus the status code for invalid
+ * sizes) in a fixed order (bit-identical run to run) and fully overwrite grad_w1/2/3 (zero for
+ * edges = 0).  Replaces the Linear/SiLU chain of the reference's radial network and its autograd
+ * derivatives (one GEMM per layer and direction, elementwise passes per activation).
+ */
+enum ictc_radial_mode { ICTC_RADIAL_VALUE = 0, ICTC_RADIAL_VJP = 1, ICTC_RADIAL_VJP_VJP = 2 };
+#define ICTC_RADIAL_WIDTH 64
+#define ICTC_RADIAL_MAX_BASIS 16
+int64_t ictc_hip_radial_mlp_workspace(int64_t edges);
+
+int ictc_hip_radial_mlp(int mode, const float* feats, const float* w1, const float* w2, const float* w3,
+                        float scale, const float* grad_hidden, const float* cotangent, float* out_hidden,
+                        float* out_grad_feats, float* out_grad_grad_hidden, float* workspace,
+                        int64_t workspace_floats, float* grad_w1, float* grad_w2, float* grad_w3,
+                        int num_basis, int64_t edges, hipStream_t stream);
+
+/*
  * Per-degree channel linear on fp32 MFMA (v_mfma_f32_16x16x4_f32), for the path-preserving
  * message linear of the MACE interaction (reference
  * mace_ictc/models/pure_cartesian_ictd_fix.py:629-661; native route ictc_o3/ascendc/linear.py:

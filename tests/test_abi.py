@@ -211,3 +211,33 @@ def test_degree_linear_weight_grad_workspace_and_validation():
     assert wg(ctypes.byref(plan.desc), 0, fake, fake, 1.0, fake, want, ptrs, -1, None) == 1      # negative rows
     # x beyond 2 GiB of 32-bit buffer offsets
     assert wg(ctypes.byref(plan.desc), 0, fake, fake, 1.0, fake, 1 << 40, ptrs, 1 << 20, None) == 2
+
+
+def test_radial_mlp_workspace_and_validation():
+    """Workspace of the radial-MLP weight gradients (one [64 x 16 + 2 x 64 x 64] partial per block,
+    one block of four 16-edge tiles per CU at most: 256 CUs on this GPU-less host) and the
+    argument checks, all before any launch."""
+    from ictc_o3 import _lib
+    lib = _lib.lib()
+    part = 64 * 16 + 2 * 64 * 64
+    assert lib.ictc_hip_radial_mlp_workspace(0) == 0
+    assert lib.ictc_hip_radial_mlp_workspace(1) == part
+    assert lib.ictc_hip_radial_mlp_workspace(64 * 5) == 5 * part
+    assert lib.ictc_hip_radial_mlp_workspace(105_634) == 256 * part
+    assert lib.ictc_hip_radial_mlp_workspace(-1) == -1
+    fake = ctypes.c_void_p(16)  # never dereferenced: every call below fails validation or does nothing
+    rm = lib.ictc_hip_radial_mlp
+
+    def call(mode=0, basis=8, edges=100, out=fake, w=fake, gw=(None, None, None), ws=None, wsf=0, g=fake, u=fake,
+             gf=None, gg=None):
+        return rm(mode, fake, w, fake, fake, 1.0, g, u, out, gf, gg, ws, wsf, *gw, basis, edges, None)
+
+    assert call(mode=3) == 2 and call(mode=-1) == 2                 # unknown mode
+    assert call(basis=0) == 2 and call(basis=17) == 2               # basis beyond the kernel's 16
+    assert call(edges=-1) == 1 and call(w=None) == 1                # negative rows, missing weight
+    assert call(out=None) == 1                                      # VALUE without an output
+    assert call(mode=1, out=None) == 0                              # VJP asked for nothing: no launch
+    assert call(mode=1, g=None, gf=fake) == 1                       # VJP without the adjoint
+    assert call(mode=2, u=None, gg=fake) == 1                       # VJP_VJP without the cotangent
+    assert call(mode=1, gw=(fake, None, None), ws=fake, wsf=part - 1, edges=1) == 1   # workspace too small
+    assert call(mode=1, gw=(None, fake, None), ws=None, wsf=part, edges=1) == 1       # no workspace
