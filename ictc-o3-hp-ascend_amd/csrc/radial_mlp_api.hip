@@ -51,10 +51,15 @@ constexpr int kLdW1 = kRb + 4;           // of W1 (zero-padded to 16 inputs)
 constexpr int kLdS = 4 * 16 + 4;         // of a staged [feature][64 edges] factor
 constexpr int kStage = 2 * kRw * kLdS;   // floats of the block's staging area (two factors)
 constexpr int kPart = kRw * kRb + 2 * kRw * kRw;   // one block's partial: dW1 [64][16], dW2, dW3
-constexpr int kRBlocksPerCu = 1;         // weight-gradient launches: blocks per CU
-constexpr int kSumRows = 64;             // partial entries per block of the sum kernel
+// Weight-gradient launches: blocks per CU (the VJP kernel's registers allow two resident blocks,
+// the double backward's one); the workspace is sized for the larger count.
+constexpr int kRBlocksPerCuVjp = 2;
+constexpr int kRBlocksPerCuVjpVjp = 1;
+constexpr int kSumRows = 16;             // partial entries per block of the sum kernel ...
+constexpr int kSumParts = 16;            // ... each summed by this many threads
 
 static_assert(kRw == 64 && kRb == 16, "tiling assumes 64 hidden features and at most 16 basis functions");
+static_assert(kSumRows * kSumParts == 256 && kPart % kSumRows == 0, "sum kernel geometry");
 
 struct RadialArgs {
   const float* f;    // [E, B]
@@ -252,12 +257,41 @@ __device__ __forceinline__ void pair16(f32x4& acc, float* S, const T64& x, f32x4
   __syncthreads();
 }
 
-template <int MODE>
+// One layer's activation from its pre-activation z: a = silu(z) and d = silu'(z) (z itself is
+// not kept).
+struct Act {
+  T64 a, d;
+};
+
+__device__ __forceinline__ Act activate(const T64& z) {
+  Act o;
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const float zv = z.t[t][v], sv = sigmoid(zv);
+      o.a.t[t][v] = zv * sv;
+      o.d.t[t][v] = dsilu(zv, sv);
+    }
+  return o;
+}
+
+__device__ __forceinline__ T64 mul64(const T64& x, const T64& y) {
+  return map64([&](int t, int v) { return x.t[t][v] * y.t[t][v]; });
+}
+// silu'(z) x from (z, sigmoid(z))
+__device__ __forceinline__ T64 dmul64(const T64& z, const T64& s, const T64& x) {
+  return map64([&](int t, int v) { return dsilu(z.t[t][v], s.t[t][v]) * x.t[t][v]; });
+}
+
+// MODE: ICTC_RADIAL_*; WG: the launch accumulates weight gradients (persistent blocks, block
+// barriers in the weight-gradient phases).
+template <int MODE, bool WG>
 __global__ void __launch_bounds__(kRThreads) radial_mlp_kernel(const RadialArgs a) {
   __shared__ __align__(16) float sW1[kRw * kLdW1];
   __shared__ __align__(16) float sW2[kRw * kLdW];
   __shared__ __align__(16) float sW3[kRw * kLdW];
-  __shared__ __align__(16) float sS[MODE == ICTC_RADIAL_VALUE ? 4 : kStage];
+  __shared__ __align__(16) float sS[WG ? kStage : 4];
 
   for (int i = threadIdx.x; i < kRw * kRb; i += kRThreads) {
     const int o = i / kRb, k = i % kRb;
@@ -274,142 +308,137 @@ __global__ void __launch_bounds__(kRThreads) radial_mlp_kernel(const RadialArgs 
   const int r = lane & 15, q = lane >> 4;
   const int64_t t0 = static_cast<int64_t>(blockIdx.x) * a.tiles / gridDim.x;
   const int64_t t1 = static_cast<int64_t>(blockIdx.x + 1) * a.tiles / gridDim.x;
-  // every wave runs the same number of rounds (the weight-gradient phases hold block barriers);
-  // a tile past the block's range is computed on dead lanes and contributes zero
+  // with weight gradients every wave runs the same number of rounds (their phases hold block
+  // barriers); a tile past the block's range is computed on dead lanes and contributes zero
   const int64_t rounds = (t1 - t0 + kRWaves - 1) / kRWaves;
+  WgradAcc acc;
+  if constexpr (WG) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc.w3[i] = acc.w2[i] = zero4();
+    acc.w1 = zero4();
+  }
 
-  if constexpr (MODE == ICTC_RADIAL_VALUE) {
-    for (int64_t i = 0; i < rounds; ++i) {
-      const int64_t t = t0 + kRWaves * i + wave;
-      if (t >= t1) break;
-      const int64_t e = t * 16 + r;
-      const bool live = e < a.edges;
-      const int64_t row = live ? e : a.edges - 1;
-      const T64 z1 = forward_first(sW1, load_basis(a.f, row, a.basis, q, true), r, q);
+  for (int64_t i = 0; i < rounds; ++i) {
+    const int64_t t = t0 + kRWaves * i + wave;
+    if (!WG && t >= t1) break;
+    const int64_t e = t * 16 + r;
+    const bool live = t < t1 && e < a.edges;
+    const int64_t row = live ? e : a.edges - 1;
+    const f32x4 x0 = load_basis(a.f, row, a.basis, q, true);
+    if constexpr (MODE == ICTC_RADIAL_VALUE) {
+      const T64 z1 = forward_first(sW1, x0, r, q);
       const T64 a1 = silu64(z1, sigmoid64(z1));
       const T64 z2 = forward64(sW2, a1, r, q);
       const T64 a2 = silu64(z2, sigmoid64(z2));
       const T64 z3 = forward64(sW3, a2, r, q);
       store64(a.h, row, live, q, silu64(z3, sigmoid64(z3)));
-    }
-  } else {
-    const bool wg = a.ws != nullptr;   // block-uniform
-    WgradAcc acc;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) acc.w3[i] = acc.w2[i] = zero4();
-    acc.w1 = zero4();
-
-    for (int64_t i = 0; i < rounds; ++i) {
-      const int64_t t = t0 + kRWaves * i + wave;
-      const int64_t e = t * 16 + r;
-      const bool live = t < t1 && e < a.edges;
-      const int64_t row = live ? e : a.edges - 1;
-      const f32x4 x0 = load_basis(a.f, row, a.basis, q, true);
+    } else if constexpr (MODE == ICTC_RADIAL_VJP) {
       const T64 g = load64(a.g, row, live, q);
+      const Act L1 = activate(forward_first(sW1, x0, r, q));
+      const Act L2 = activate(forward64(sW2, L1.a, r, q));
+      const Act L3 = activate(forward64(sW3, L2.a, r, q));
+      const T64 c3 = mul64(g, L3.d);
+      if constexpr (WG) pair64(acc.w3, sS, c3, L2.a, r, q, wave);
+      const T64 c2 = mul64(adjoint64(sW3, c3, r, q), L2.d);
+      if constexpr (WG) pair64(acc.w2, sS, c2, L1.a, r, q, wave);
+      const T64 c1 = mul64(adjoint64(sW2, c2, r, q), L1.d);
+      if constexpr (WG) pair16(acc.w1, sS, c1, x0, r, q, wave);
+      if (a.gf != nullptr) {   // the MFMA operands come from every lane: outside the live test
+        const f32x4 d = adjoint_first(sW1, c1, r, q);
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          if (live && 4 * q + v < a.basis) a.gf[row * a.basis + 4 * q + v] = d[v];
+      }
+    } else {
+      // (z, sigmoid(z)) per layer, from which silu, silu' and silu'' are rebuilt where used:
+      // fewer live registers than keeping the three of them
+      const f32x4 xu = load_basis(a.u, row, a.basis, q, live);
       const T64 z1 = forward_first(sW1, x0, r, q);
       const T64 s1 = sigmoid64(z1);
-      const T64 a1 = silu64(z1, s1);
-      const T64 z2 = forward64(sW2, a1, r, q);
+      const T64 t1v = forward_first(sW1, xu, r, q);
+      const T64 z2 = forward64(sW2, silu64(z1, s1), r, q);
       const T64 s2 = sigmoid64(z2);
-      const T64 a2 = silu64(z2, s2);
-      const T64 z3 = forward64(sW3, a2, r, q);
+      const T64 t2v = forward64(sW2, dmul64(z1, s1, t1v), r, q);
+      const T64 z3 = forward64(sW3, silu64(z2, s2), r, q);
       const T64 s3 = sigmoid64(z3);
-      if constexpr (MODE == ICTC_RADIAL_VJP) {
-        const T64 c3 = map64([&](int i, int v) { return g.t[i][v] * dsilu(z3.t[i][v], s3.t[i][v]); });
-        if (wg) pair64(acc.w3, sS, c3, a2, r, q, wave);
-        const T64 p2 = adjoint64(sW3, c3, r, q);
-        const T64 c2 = map64([&](int i, int v) { return p2.t[i][v] * dsilu(z2.t[i][v], s2.t[i][v]); });
-        if (wg) pair64(acc.w2, sS, c2, a1, r, q, wave);
-        const T64 p1 = adjoint64(sW2, c2, r, q);
-        const T64 c1 = map64([&](int i, int v) { return p1.t[i][v] * dsilu(z1.t[i][v], s1.t[i][v]); });
-        if (wg) pair16(acc.w1, sS, c1, x0, r, q, wave);
-        if (a.gf != nullptr) {   // the MFMA operands come from every lane: outside the live test
-          const f32x4 d = adjoint_first(sW1, c1, r, q);
+      const T64 t3v = forward64(sW3, dmul64(z2, s2, t2v), r, q);
+      const T64 g = load64(a.g, row, live, q);
+      if (a.gg != nullptr) store64(a.gg, row, live, q, dmul64(z3, s3, t3v));
+      const T64 A3 = dmul64(z3, s3, g);
+      const T64 B3 = map64([&](int i, int v) { return g.t[i][v] * t3v.t[i][v] * d2silu(z3.t[i][v], s3.t[i][v]); });
+      if constexpr (WG) {
+        pair64(acc.w3, sS, A3, dmul64(z2, s2, t2v), r, q, wave);
+        pair64(acc.w3, sS, B3, silu64(z2, s2), r, q, wave);
+      }
+      const T64 P2 = adjoint64(sW3, A3, r, q);
+      const T64 Q2 = adjoint64(sW3, B3, r, q);
+      const T64 A2 = dmul64(z2, s2, P2);
+      const T64 B2 = map64([&](int i, int v) {
+        return fmaf(P2.t[i][v] * t2v.t[i][v], d2silu(z2.t[i][v], s2.t[i][v]), Q2.t[i][v] * dsilu(z2.t[i][v], s2.t[i][v]));
+      });
+      if constexpr (WG) {
+        pair64(acc.w2, sS, A2, dmul64(z1, s1, t1v), r, q, wave);
+        pair64(acc.w2, sS, B2, silu64(z1, s1), r, q, wave);
+      }
+      const T64 P1 = adjoint64(sW2, A2, r, q);
+      const T64 Q1 = adjoint64(sW2, B2, r, q);
+      const T64 B1 = map64([&](int i, int v) {
+        return fmaf(P1.t[i][v] * t1v.t[i][v], d2silu(z1.t[i][v], s1.t[i][v]), Q1.t[i][v] * dsilu(z1.t[i][v], s1.t[i][v]));
+      });
+      if constexpr (WG) {
+        pair16(acc.w1, sS, dmul64(z1, s1, P1), xu, r, q, wave);
+        pair16(acc.w1, sS, B1, x0, r, q, wave);
+      }
+      if (a.gf != nullptr) {
+        const f32x4 d = adjoint_first(sW1, B1, r, q);
 #pragma unroll
-          for (int v = 0; v < 4; ++v)
-            if (live && 4 * q + v < a.basis) a.gf[row * a.basis + 4 * q + v] = d[v];
-        }
-      } else {
-        const f32x4 xu = load_basis(a.u, row, a.basis, q, live);
-        const T64 t1v = forward_first(sW1, xu, r, q);
-        const T64 ta1 = map64([&](int i, int v) { return t1v.t[i][v] * dsilu(z1.t[i][v], s1.t[i][v]); });
-        const T64 t2v = forward64(sW2, ta1, r, q);
-        const T64 ta2 = map64([&](int i, int v) { return t2v.t[i][v] * dsilu(z2.t[i][v], s2.t[i][v]); });
-        const T64 t3v = forward64(sW3, ta2, r, q);
-        if (a.gg != nullptr)
-          store64(a.gg, row, live, q,
-                  map64([&](int i, int v) { return t3v.t[i][v] * dsilu(z3.t[i][v], s3.t[i][v]); }));
-        const T64 A3 = map64([&](int i, int v) { return g.t[i][v] * dsilu(z3.t[i][v], s3.t[i][v]); });
-        const T64 B3 = map64([&](int i, int v) { return g.t[i][v] * t3v.t[i][v] * d2silu(z3.t[i][v], s3.t[i][v]); });
-        if (wg) {
-          pair64(acc.w3, sS, A3, ta2, r, q, wave);
-          pair64(acc.w3, sS, B3, a2, r, q, wave);
-        }
-        const T64 P2 = adjoint64(sW3, A3, r, q);
-        const T64 Q2 = adjoint64(sW3, B3, r, q);
-        const T64 A2 = map64([&](int i, int v) { return P2.t[i][v] * dsilu(z2.t[i][v], s2.t[i][v]); });
-        const T64 B2 = map64([&](int i, int v) {
-          return fmaf(P2.t[i][v] * t2v.t[i][v], d2silu(z2.t[i][v], s2.t[i][v]), Q2.t[i][v] * dsilu(z2.t[i][v], s2.t[i][v]));
-        });
-        if (wg) {
-          pair64(acc.w2, sS, A2, ta1, r, q, wave);
-          pair64(acc.w2, sS, B2, a1, r, q, wave);
-        }
-        const T64 P1 = adjoint64(sW2, A2, r, q);
-        const T64 Q1 = adjoint64(sW2, B2, r, q);
-        const T64 A1 = map64([&](int i, int v) { return P1.t[i][v] * dsilu(z1.t[i][v], s1.t[i][v]); });
-        const T64 B1 = map64([&](int i, int v) {
-          return fmaf(P1.t[i][v] * t1v.t[i][v], d2silu(z1.t[i][v], s1.t[i][v]), Q1.t[i][v] * dsilu(z1.t[i][v], s1.t[i][v]));
-        });
-        if (wg) {
-          pair16(acc.w1, sS, A1, xu, r, q, wave);
-          pair16(acc.w1, sS, B1, x0, r, q, wave);
-        }
-        if (a.gf != nullptr) {   // the MFMA operands come from every lane: outside the live test
-          const f32x4 d = adjoint_first(sW1, B1, r, q);
-#pragma unroll
-          for (int v = 0; v < 4; ++v)
-            if (live && 4 * q + v < a.basis) a.gf[row * a.basis + 4 * q + v] = d[v];
-        }
+        for (int v = 0; v < 4; ++v)
+          if (live && 4 * q + v < a.basis) a.gf[row * a.basis + 4 * q + v] = d[v];
       }
     }
+  }
 
-    if (wg) {   // the wave's row band of each gradient into the block's partial
-      float* out = a.ws + static_cast<int64_t>(blockIdx.x) * kPart;
+  if constexpr (WG) {   // the wave's row band of each gradient into the block's partial
+    float* out = a.ws + static_cast<int64_t>(blockIdx.x) * kPart;
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int row = 16 * wave + 4 * q + v;
-        out[row * kRb + r] = acc.w1[v];
+    for (int v = 0; v < 4; ++v) {
+      const int row = 16 * wave + 4 * q + v;
+      out[row * kRb + r] = acc.w1[v];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          out[kRw * kRb + row * kRw + 16 * k + r] = acc.w2[k][v];
-          out[kRw * kRb + kRw * kRw + row * kRw + 16 * k + r] = acc.w3[k][v];
-        }
+      for (int k = 0; k < 4; ++k) {
+        out[kRw * kRb + row * kRw + 16 * k + r] = acc.w2[k][v];
+        out[kRw * kRb + kRw * kRw + row * kRw + 16 * k + r] = acc.w3[k][v];
       }
     }
   }
 }
 
-// dW1 = sum of the dW1 partials, dW2 = s sum, dW3 = s sum, each in block order (zero for no blocks).
+// dW1 = sum of the dW1 partials, dW2 = s sum, dW3 = s sum (zero for no blocks).  Thread (c, p) of
+// a block adds the partials of blocks p, p + kSumParts, ... for entry c with four loads in flight,
+// and thread (c, 0) adds the kSumParts results in order: a fixed order, bit-identical run to run.
 __global__ void __launch_bounds__(256) radial_wsum_kernel(const float* __restrict__ ws, int blocks, int basis,
                                                           float scale, float* __restrict__ gw1,
                                                           float* __restrict__ gw2, float* __restrict__ gw3) {
-  __shared__ float part[4][kSumRows];
+  __shared__ float part[kSumParts][kSumRows + 1];
   const int c = threadIdx.x % kSumRows, p = threadIdx.x / kSumRows;
   const int i = blockIdx.x * kSumRows + c;
-  float s = 0.f;
   const float* src = ws + i;
+  constexpr int kStep = kSumParts;
+  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
   int b = p;
-  for (; b + 12 < blocks; b += 16) {   // four loads in flight, added in block order
-    const float v0 = src[static_cast<int64_t>(b) * kPart], v1 = src[static_cast<int64_t>(b + 4) * kPart];
-    const float v2 = src[static_cast<int64_t>(b + 8) * kPart], v3 = src[static_cast<int64_t>(b + 12) * kPart];
-    s = (((s + v0) + v1) + v2) + v3;
+  for (; b + 3 * kStep < blocks; b += 4 * kStep) {
+    s0 += src[static_cast<int64_t>(b) * kPart];
+    s1 += src[static_cast<int64_t>(b + kStep) * kPart];
+    s2 += src[static_cast<int64_t>(b + 2 * kStep) * kPart];
+    s3 += src[static_cast<int64_t>(b + 3 * kStep) * kPart];
   }
-  for (; b < blocks; b += 4) s += src[static_cast<int64_t>(b) * kPart];
-  part[p][c] = s;
+  for (; b < blocks; b += kStep) s0 += src[static_cast<int64_t>(b) * kPart];
+  part[p][c] = (s0 + s1) + (s2 + s3);
   __syncthreads();
   if (p != 0) return;
-  const float tot = ((part[0][c] + part[1][c]) + part[2][c]) + part[3][c];
+  float tot = 0.f;
+#pragma unroll
+  for (int k = 0; k < kSumParts; ++k) tot += part[k][c];
   if (i < kRw * kRb) {
     const int o = i / kRb, k = i % kRb;
     if (gw1 != nullptr && k < basis) gw1[o * basis + k] = tot;
@@ -423,9 +452,10 @@ __global__ void __launch_bounds__(256) radial_wsum_kernel(const float* __restric
 int64_t radial_tiles(int64_t edges) { return (edges + 15) / 16; }
 
 // Blocks of a weight-gradient launch (0 for no edges).
-int radial_wgrad_blocks(int64_t edges) {
+int radial_wgrad_blocks(int64_t edges, int mode) {
   const int64_t need = (radial_tiles(edges) + kRWaves - 1) / kRWaves;
-  const int64_t cap = static_cast<int64_t>(kRBlocksPerCu) * compute_units();
+  const int per_cu = mode == ICTC_RADIAL_VJP_VJP ? kRBlocksPerCuVjpVjp : kRBlocksPerCuVjp;
+  const int64_t cap = static_cast<int64_t>(per_cu) * compute_units();
   return static_cast<int>(need < cap ? need : cap);
 }
 
@@ -434,7 +464,7 @@ int radial_wgrad_blocks(int64_t edges) {
 
 extern "C" int64_t ictc_hip_radial_mlp_workspace(int64_t edges) {
   if (edges < 0) return -ICTC_ERR_INVALID_ARGUMENT;
-  return static_cast<int64_t>(ictc::radial_wgrad_blocks(edges)) * ictc::kPart;
+  return static_cast<int64_t>(ictc::radial_wgrad_blocks(edges, ICTC_RADIAL_VJP)) * ictc::kPart;
 }
 
 extern "C" int ictc_hip_radial_mlp(int mode, const float* feats, const float* w1, const float* w2, const float* w3,
@@ -460,7 +490,7 @@ extern "C" int ictc_hip_radial_mlp(int mode, const float* feats, const float* w1
   if (tiles > (static_cast<int64_t>(1) << 31) - 1) return ICTC_ERR_UNSUPPORTED;
   int blocks = 0;
   if (wgrad) {
-    blocks = radial_wgrad_blocks(edges);
+    blocks = radial_wgrad_blocks(edges, mode);
     if (workspace == nullptr || workspace_floats < static_cast<int64_t>(blocks) * kPart)
       return ICTC_ERR_INVALID_ARGUMENT;
   }
@@ -468,16 +498,17 @@ extern "C" int ictc_hip_radial_mlp(int mode, const float* feats, const float* w1
                mode == ICTC_RADIAL_VJP_VJP ? out_grad_grad_hidden : nullptr, wgrad ? workspace : nullptr,
                edges, tiles, num_basis, scale};
   if (edges > 0) {
-    const int64_t grid = wgrad ? blocks : (tiles + kRWaves - 1) / kRWaves;
+    const dim3 grid(static_cast<unsigned>(wgrad ? blocks : (tiles + kRWaves - 1) / kRWaves)), block(kRThreads);
     if (mode == ICTC_RADIAL_VALUE)
-      hipLaunchKernelGGL(radial_mlp_kernel<ICTC_RADIAL_VALUE>, dim3(static_cast<unsigned>(grid)), dim3(kRThreads), 0,
-                         stream, a);
+      hipLaunchKernelGGL((radial_mlp_kernel<ICTC_RADIAL_VALUE, false>), grid, block, 0, stream, a);
+    else if (mode == ICTC_RADIAL_VJP && wgrad)
+      hipLaunchKernelGGL((radial_mlp_kernel<ICTC_RADIAL_VJP, true>), grid, block, 0, stream, a);
     else if (mode == ICTC_RADIAL_VJP)
-      hipLaunchKernelGGL(radial_mlp_kernel<ICTC_RADIAL_VJP>, dim3(static_cast<unsigned>(grid)), dim3(kRThreads), 0,
-                         stream, a);
+      hipLaunchKernelGGL((radial_mlp_kernel<ICTC_RADIAL_VJP, false>), grid, block, 0, stream, a);
+    else if (wgrad)
+      hipLaunchKernelGGL((radial_mlp_kernel<ICTC_RADIAL_VJP_VJP, true>), grid, block, 0, stream, a);
     else
-      hipLaunchKernelGGL(radial_mlp_kernel<ICTC_RADIAL_VJP_VJP>, dim3(static_cast<unsigned>(grid)), dim3(kRThreads),
-                         0, stream, a);
+      hipLaunchKernelGGL((radial_mlp_kernel<ICTC_RADIAL_VJP_VJP, false>), grid, block, 0, stream, a);
     if (hipGetLastError() != hipSuccess) return ICTC_ERR_LAUNCH;
   }
   if (wgrad) {

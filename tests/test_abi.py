@@ -215,7 +215,7 @@ def test_degree_linear_weight_grad_workspace_and_validation():
 
 def test_radial_mlp_workspace_and_validation():
     """Workspace of the radial-MLP weight gradients (one [64 x 16 + 2 x 64 x 64] partial per block,
-    one block of four 16-edge tiles per CU at most: 256 CUs on this GPU-less host) and the
+    blocks of four 16-edge tiles, at most two per CU: 256 CUs on this GPU-less host) and the
     argument checks, all before any launch."""
     from ictc_o3 import _lib
     lib = _lib.lib()
@@ -223,7 +223,7 @@ def test_radial_mlp_workspace_and_validation():
     assert lib.ictc_hip_radial_mlp_workspace(0) == 0
     assert lib.ictc_hip_radial_mlp_workspace(1) == part
     assert lib.ictc_hip_radial_mlp_workspace(64 * 5) == 5 * part
-    assert lib.ictc_hip_radial_mlp_workspace(105_634) == 256 * part
+    assert lib.ictc_hip_radial_mlp_workspace(105_634) == 512 * part
     assert lib.ictc_hip_radial_mlp_workspace(-1) == -1
     fake = ctypes.c_void_p(16)  # never dereferenced: every call below fails validation or does nothing
     rm = lib.ictc_hip_radial_mlp
