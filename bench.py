@@ -26,7 +26,7 @@ Also reported on the same JSON line:
       against the published fp32 vector peak and the measured rate of a non-packed FMA probe);
     - cfg 4, MACE-style energy + forces (C=128, lmax 3, 2 interactions, correlation 3,
       2,048 atoms at 0.1 A^-3 with 1.5 A minimum separation, r_c 5 A, 10 species):
-      inference and one force-loss training step (AdamW), atom-steps/s, reference timing
+      inference and one force-loss training step (fused AdamW), atom-steps/s, reference timing
       protocol (>= 2 s and 3 warmup calls, median of 5 synchronised calls), run eager (as
       the reference does) and as HIP-graph replays of the captured steps;
     - the HIP periodic radius graph build for the cfg-2 and cfg-4 structures (outside every
@@ -37,7 +37,7 @@ reference) and three launches of each TP kernel at the benchmark sizes, for
 rocprofv3 --pmc passes.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--kernels-only]
-                      [--only tp|tp0|message|sc|mace|graph|linear|generic]
+                      [--only tp|tp0|message|sc|mace|graph|linear|radial|generic]
 """
 from __future__ import annotations
 
@@ -715,7 +715,7 @@ def _bench_mace(device):
                              cutoff=5.0, device=device, seed=0)
         return model, model.species_index(graph["atomic_numbers"])
     model, species = fresh()
-    opt = torch.optim.AdamW(model.parameters(), lr=1e-3)
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-3, fused=True)     # one kernel per update, same AdamW
     train_ms = _median_call_ms(lambda: training_step(model, opt, graph, species=species), device)
     model.eval().requires_grad_(False)
     infer_ms = _median_call_ms(lambda: energy_and_forces(model, **graph, species=species), device)
@@ -728,7 +728,7 @@ def _bench_mace(device):
     infer_graph_ms = _median_call_ms(lambda: captured(graph["positions"]), device)
     del captured
     model, species = fresh()
-    opt = torch.optim.AdamW(model.parameters(), lr=1e-3, capturable=True)
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-3, capturable=True, fused=True)
     step = CapturedTrainingStep(model, opt, graph, species=species)
     train_graph_ms = _median_call_ms(lambda: step(graph["positions"]), device)
     del step
@@ -806,6 +806,59 @@ def _bench_linear(device):
             "weight_grad": leg(wgrad_ms, dense[2], "degree_linear_wgrad_kernel<0> + degree_linear_wgrad_sum_kernel")}
 
 
+RADIAL_EDGES = 105_634     # edges of the cfg-4 MACE graph (2,048 atoms, r_c 5 A)
+
+
+def _bench_radial(device):
+    """The interaction's radial MLP up to its last Linear (8 Bessel features -> 64 -> 64 -> 64,
+    normalised SiLU) at the cfg-4 edge count, per derivative mode on the MFMA kernel
+    (ictc_hip_radial_mlp), beside the composed route it replaced (one GEMM per layer and
+    direction plus the elementwise activation passes, under autograd)."""
+    from mace_hip.radial_mlp import VALUE, VJP, VJP_VJP, _launch, hidden_formula
+    e, b, s = RADIAL_EDGES, 8, 1.6791767923989418
+    gen = torch.Generator().manual_seed(0)
+    f = torch.randn(e, b, generator=gen).to(device)
+    w1 = (torch.randn(64, b, generator=gen) / math.sqrt(b)).to(device)
+    w2 = (torch.randn(64, 64, generator=gen) / 8).to(device)
+    w3 = (torch.randn(64, 64, generator=gen) / 8).to(device)
+    gh = torch.randn(e, 64, generator=gen).to(device)
+    u = torch.randn(e, b, generator=gen).to(device)
+    fwd, adj, wg = b * 64 + 2 * 64 * 64, 2 * 64 * 64 + 64 * b, b * 64 + 2 * 64 * 64
+    modes = {   # (call, useful FLOPs per edge, kernel)
+        "value": (lambda: _launch(VALUE, f, w1, w2, w3, s, hidden=True), 2 * fwd,
+                  "radial_mlp_kernel<0, false>"),
+        "vjp_features": (lambda: _launch(VJP, f, w1, w2, w3, s, gh, grad_feats=True), 2 * (fwd + adj),
+                         "radial_mlp_kernel<1, false>"),
+        "vjp_weights": (lambda: _launch(VJP, f, w1, w2, w3, s, gh, grad_weights=(True, True, True)),
+                        2 * (fwd + adj - 64 * b + wg), "radial_mlp_kernel<1, true> + radial_wsum_kernel"),
+        "vjp_vjp": (lambda: _launch(VJP_VJP, f, w1, w2, w3, s, gh, u, grad_grad=True,
+                                    grad_weights=(True, True, True)),
+                    2 * (2 * fwd + 2 * (adj - 64 * b) + 2 * wg), "radial_mlp_kernel<2, true> + radial_wsum_kernel"),
+    }
+    fr, w1r, w2r, w3r = (t.clone().requires_grad_() for t in (f, w1, w2, w3))
+
+    def composed(mode):
+        h = hidden_formula(fr, w1r, w2r, w3r, s)
+        if mode == "value":
+            return h
+        if mode == "vjp_features":
+            return torch.autograd.grad(h, fr, gh)
+        if mode == "vjp_weights":
+            return torch.autograd.grad(h, (w1r, w2r, w3r), gh)
+        ghr = gh.clone().requires_grad_()
+        gf, = torch.autograd.grad(h, fr, ghr, create_graph=True)
+        return torch.autograd.grad(gf, (w1r, w2r, w3r, ghr), u)
+    out = {"workload": f"cfg4 MACE radial MLP hidden layers: {e:,} edges, 8 -> 64 -> 64 -> 64, fp32"}
+    for name, (fn, per_edge, kernel) in modes.items():
+        ms = _event_ms(fn, device, reps=50, warmup=10)
+        comp = _event_ms(lambda: composed(name), device, reps=10)
+        tf = per_edge * e / (ms * 1e-3) / 1e12
+        out[name] = {"kernel": kernel, "mean_launch_ms": ms, "composed_route_ms": comp,
+                     "roofline": {"bound": "mfma", "achieved": tf, "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                  "frac": tf / MFMA_F32_PEAK_TFLOPS, "flops_per_launch": per_edge * e}}
+    return out
+
+
 def _mace_floor(edges: int, atoms: int, training: bool):
     """Lower bound on the device time of one cfg-4 step: each modelled piece of work at its own
     roofline (unique bytes at 8 TB/s for the HBM-bound message kernels, useful FLOPs at
@@ -834,7 +887,7 @@ def _mace_floor(edges: int, atoms: int, training: bool):
         sc = sc_flops.flop_counts(3, target, 3)
         sc_f = (sc["forward"] + sc["vjp"]) * n * c
         add("message kernels", nbytes=fwd_b + vjp_b)
-        add("radial MLP GEMMs", flops=2 * radial)
+        add("radial MLP", flops=2 * radial)
         add("message linear", flops=2 * lin_f)
         add("channel linears", flops=2 * chan_f)
         add("symmetric contraction", flops=sc_f)
@@ -842,7 +895,7 @@ def _mace_floor(edges: int, atoms: int, training: bool):
             tfwd_b = e * (8 * npath * c + 128 + 8) + n * 4 * c * (2 * nx + noc)
             tvjp_b = e * (12 * npath * c + 128 + 64 + 8) + n * 4 * c * (3 * nx + noc)
             add("message kernels", nbytes=vjp_b + tfwd_b + tvjp_b)
-            add("radial MLP GEMMs", flops=4 * radial)
+            add("radial MLP", flops=4 * radial)
             add("message linear", flops=4 * lin_f)
             add("channel linears", flops=4 * chan_f)
             add("symmetric contraction", flops=2 * sc_f)
@@ -973,7 +1026,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--kernels-only", action="store_true")
     ap.add_argument("--only", choices=("tp", "tp0", "message", "message3", "sc", "mace", "graph", "linear",
-                                       "generic", "valu"),
+                                       "radial", "generic", "valu"),
                     default=None,
                     help="run one section and print its JSON (for profiling)")
     args = ap.parse_args()
@@ -988,9 +1041,9 @@ def main() -> int:
     if args.kernels_only:
         _kernels_only(op.plan, device)
         return 0
-    if args.only in ("tp0", "message", "message3", "sc", "mace", "graph", "linear", "generic", "valu"):
+    if args.only in ("tp0", "message", "message3", "sc", "mace", "graph", "linear", "radial", "generic", "valu"):
         fn = {"tp0": _bench_tp_cfg0, "message": _bench_message, "message3": _bench_message3, "sc": _bench_sc,
-              "mace": _bench_mace, "graph": _bench_graph, "linear": _bench_linear,
+              "mace": _bench_mace, "graph": _bench_graph, "linear": _bench_linear, "radial": _bench_radial,
               "generic": _bench_generic, "valu": _valu_form_cycles}[args.only]
         print(json.dumps({args.only: fn(device)}), flush=True)
         return 0
@@ -1007,6 +1060,7 @@ def main() -> int:
         others = {"tp_cfg0": _bench_tp_cfg0(device), "message_cfg2": _bench_message(device),
                   "message_cfg4_lmax3": _bench_message3(device), "sc_cfg3": _bench_sc(device),
                   "mace_cfg4": _bench_mace(device), "message_linear_cfg4": _bench_linear(device),
+                  "radial_mlp_cfg4": _bench_radial(device),
                   "radius_graph": _bench_graph(device), "tp_generic_l4": _bench_generic(device)}
         if not args.no_cpu:
             others["tp_cfg0"]["cpu_baseline"] = _cpu_tp_cfg0()

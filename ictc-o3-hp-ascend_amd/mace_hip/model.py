@@ -198,11 +198,13 @@ class Interaction(nn.Module):
         hidden, weight = self.radial_hidden(edge_feats)
         return linear(hidden, weight * self.tp.weight.reshape(-1, 1))
 
-    def forward(self, h, harmonics, edge_feats, src, dst, mask, species):
+    def forward(self, h, harmonics, edge_feats, src, dst, mask, species, scalars=None):
         """mask: the reference multiplies the gates by (r <= r_max) (:1801-1808).  The radial
         features carry the cutoff envelope, exactly 0 from r_max on, and fc has no biases, so
         the gates are already exactly 0 wherever the mask is 0: the product is an identity and
-        is skipped (mask is accepted for the signature)."""
+        is skipped (mask is accepted for the signature).  scalars: h's l = 0 block as its own
+        tensor when the caller has it (the previous product's), so the self connection does not
+        slice h (a slice's backward zero-fills a gradient of h's full width)."""
         n = h.shape[0]
         x1 = self.linear_up.to_ir_mul(h)
         plan = self.tp.hip_plan(self.input_lmax, self.edge_lmax)
@@ -217,7 +219,7 @@ class Interaction(nn.Module):
             m = packed_radial_graph_message(plan, x1, harmonics, hidden, weight, None, src, dst, nodes_dst=n,
                                             edge_chunk_size=self.edge_chunk_size)
         message = self.message_linear(m, 1.0 / max(self.avg_num_neighbors, 1e-8))
-        sc = self.self_connection(h[:, :self.channels], species)
+        sc = self.self_connection(h[:, :self.channels] if scalars is None else scalars, species)
         return message, sc
 
 
@@ -232,10 +234,13 @@ class Product(nn.Module):
         self.linear = IrrepsLinear(channels, target_lmax)
 
     def forward(self, message, sc, species):
+        """(node features, their l = 0 block): the block is returned as the tensor the features
+        are concatenated from, so its users need no slice of them."""
         out = self.linear(self.symmetric_contractions(message, node_type_idx=species))
         # _add_product_self_connection (:94-118): an l = 0 skip lands on the scalar block
         scalar, rest = out.split([self.channels, out.shape[1] - self.channels], dim=-1)
-        return torch.cat([scalar + sc, rest], dim=-1)
+        scalar = scalar + sc
+        return (torch.cat([scalar, rest], dim=-1) if rest.shape[1] else scalar), scalar
 
 
 class MaceICTC(nn.Module):
@@ -311,11 +316,12 @@ class MaceICTC(nn.Module):
         # one-hot attributes): its weight gradient is a GEMM, not an atomic index_add
         h = linear(one_hot_rows(species, self.num_elements), self.node_embedding.weight)
         energy = None
+        scalars = h
         for t, (interaction, product) in enumerate(zip(self.interactions, self.products)):
-            message, sc = interaction(h, harmonics, edge_feats, edge_src, edge_dst, mask, species)
-            h = product(message, sc, species)
+            message, sc = interaction(h, harmonics, edge_feats, edge_src, edge_dst, mask, species, scalars)
+            h, scalars = product(message, sc, species)
             if t < len(self.interactions) - 1:
-                e = self.layer_readouts[t](h[:, :self.channels])
+                e = self.layer_readouts[t](scalars)
             else:
                 e = self.last_readout(h)
             energy = e if energy is None else energy + e

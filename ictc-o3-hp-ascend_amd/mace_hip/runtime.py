@@ -225,7 +225,8 @@ class CapturedEnergyAndForces:
 class CapturedTrainingStep:
     """One force-loss training step (energy + forces with create_graph, loss backward, optimizer
     step) captured once and replayed on new positions.  The optimizer must keep its state on
-    the device (``torch.optim.AdamW(..., capturable=True)``); gradients are released before
+    the device (``torch.optim.AdamW(..., capturable=True)``, which may also be ``fused=True``: one
+    update kernel for all parameters, 0.3 ms less per cfg-4 step); gradients are released before
     capture so that backward writes them into the graph's own buffers on every replay."""
 
     def __init__(self, model, optimizer, graph: dict, *, species=None, warmup: int = 3):

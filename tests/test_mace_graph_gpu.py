@@ -37,14 +37,15 @@ def test_captured_inference_replays_match_eager(gpu):
             assert_rel(got[key], eager[key], rtol=1e-5, what=f"replay {step} {key}")
 
 
-def test_captured_training_step_replays_match_eager(gpu):
+@pytest.mark.parametrize("fused", [False, True])
+def test_captured_training_step_replays_match_eager(gpu, fused):
     from mace_hip import CapturedTrainingStep, training_step
     model_a, graph, _, _ = _setup(gpu, atoms=96)
     model_b, _, _, _ = _setup(gpu, atoms=96)
     for (na, pa), (nb, pb) in zip(model_a.named_parameters(), model_b.named_parameters()):
         assert na == nb and torch.equal(pa, pb)
-    opt_a = torch.optim.AdamW(model_a.parameters(), lr=1e-3, capturable=True)
-    opt_b = torch.optim.AdamW(model_b.parameters(), lr=1e-3, capturable=True)
+    opt_a = torch.optim.AdamW(model_a.parameters(), lr=1e-3, capturable=True, fused=fused)
+    opt_b = torch.optim.AdamW(model_b.parameters(), lr=1e-3, capturable=True, fused=fused)
     # warm-up steps inside the capture helper advance model_b; advance model_a identically
     warm = dict(graph)
     for _ in range(3):
