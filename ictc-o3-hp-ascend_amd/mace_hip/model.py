@@ -313,8 +313,12 @@ class MaceICTC(nn.Module):
         if species is None:
             species = self.species_index(atomic_numbers)
         # the embedding as the product one_hot(species) @ W^T (the reference's node_embedding on
-        # one-hot attributes): its weight gradient is a GEMM, not an atomic index_add
-        h = linear(one_hot_rows(species, self.num_elements), self.node_embedding.weight)
+        # one-hot attributes): its weight gradient is a GEMM, not an atomic index_add; a frozen
+        # embedding (inference) is the same rows picked directly
+        if self.node_embedding.weight.requires_grad and torch.is_grad_enabled():
+            h = linear(one_hot_rows(species, self.num_elements), self.node_embedding.weight)
+        else:
+            h = self.node_embedding.weight.t().index_select(0, species)
         energy = None
         scalars = h
         for t, (interaction, product) in enumerate(zip(self.interactions, self.products)):

@@ -66,10 +66,12 @@ def energy_and_forces(model, positions, atomic_numbers, batch, edge_src, edge_ds
         atomic = model(pos, atomic_numbers, batch, edge_src, edge_dst, edge_shifts, cell, species=species)
         # per-structure sums as one_hot(batch)^T @ atomic: a fixed summation order
         energy = mm(one_hot_rows(batch, cell.shape[0]).t(), atomic.unsqueeze(1)).squeeze(1)
-        # keep the coordinate dependency for zero-edge graphs (a 3-element sum: no multi-block
-        # reduction, so the step stays capturable into a HIP graph)
-        force = -torch.autograd.grad(energy.sum() + pos[:1].sum() * 0.0, pos, create_graph=training,
-                                     retain_graph=training)[0]
+        total = energy.sum()
+        if edge_src.numel() == 0:
+            # keep the coordinate dependency of a graph without edges (a 3-element sum: no
+            # multi-block reduction, so the step stays capturable into a HIP graph)
+            total = total + pos[:1].sum() * 0.0
+        force = -torch.autograd.grad(total, pos, create_graph=training, retain_graph=training)[0]
     result = {"energy": energy, "forces": force, "atomic_energy": atomic}
     return result if training else {k: v.detach() for k, v in result.items()}
 
