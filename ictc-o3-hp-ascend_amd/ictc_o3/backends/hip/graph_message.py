@@ -370,11 +370,31 @@ def vjp(plan, graph, need, x, y, g, go, bonds=None, slot=None, forward_node=None
     return tuple(o if n else None for o, n in zip(outs, need))
 
 
+def message_bonds(plan: TensorProductPlan, harmonics: torch.Tensor) -> Optional[torch.Tensor]:
+    """The bond rows the message forward derives from the harmonics [E, (L_e+1)^2] (the harmonics
+    themselves for degree sets whose kernels build them in-kernel; None without edges), for a
+    caller that issues them ahead, e.g. on another stream, and passes them to
+    ``packed_graph_message``."""
+    edges = harmonics.shape[0]
+    if edges == 0:
+        return None
+    y = harmonics.contiguous()
+    if bond_width(plan) == 0:
+        return y
+    out = torch.empty(edges, bond_width(plan), device=y.device, dtype=torch.float32)
+    _lib.check(_lib.lib().ictc_hip_message_bonds(ctypes.byref(plan.desc), y.data_ptr(), out.data_ptr(), edges,
+                                                 _lib.stream_of(y.device)), "ictc_hip_message_bonds")
+    return out
+
+
 def packed_graph_message(plan: TensorProductPlan, features: torch.Tensor, harmonics: torch.Tensor,
                          gates: torch.Tensor, src: torch.Tensor, dst: torch.Tensor, *,
-                         nodes_dst: Optional[int] = None, mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+                         nodes_dst: Optional[int] = None, mask: Optional[torch.Tensor] = None,
+                         bonds: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Packed ir_mul message: features [N_src, C(L_in+1)^2], harmonics [E,(L_e+1)^2],
-    gates [E, P*C] (path weights folded in), src/dst int64 [E] -> [N_dst, NOC*C]."""
+    gates [E, P*C] (path weights folded in), src/dst int64 [E] -> [N_dst, NOC*C].  bonds: the
+    harmonics' ``message_bonds`` for this plan when the caller has them (derived data: the
+    harmonics stay the differentiated input)."""
     nodes_src = features.shape[0]
     nodes_dst = nodes_src if nodes_dst is None else int(nodes_dst)
     graph = message_graph(src, dst, nodes_src, nodes_dst)
@@ -385,7 +405,7 @@ def packed_graph_message(plan: TensorProductPlan, features: torch.Tensor, harmon
         slots = torch.tensor(plan.slot_of_path, device=gates.device)
         gates = gates.new_zeros(rows, len(plan.full_paths), c).index_copy(
             1, slots, gates.reshape(rows, plan.num_paths, c)).reshape(rows, len(plan.full_paths) * c)
-    out = _Forward.apply(plan, graph, features.contiguous(), harmonics.contiguous(), gates.contiguous())
+    out = _Forward.apply(plan, graph, features.contiguous(), harmonics.contiguous(), gates.contiguous(), bonds)
     if not plan.is_full:
         keep = torch.tensor(plan.output_rows, device=gates.device)
         out = out.reshape(nodes_dst, -1, c).index_select(1, keep).reshape(nodes_dst, len(plan.output_rows) * c)

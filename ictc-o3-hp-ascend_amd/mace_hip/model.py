@@ -44,7 +44,7 @@ import torch.nn.functional as F
 
 from ictc_o3.backends.hip.degree_linear import (DegreeLinearPlan, degree_linear, degree_linear_adjoint,
                                                  degree_linear_mul_ir)
-from ictc_o3.backends.hip.graph_message import packed_graph_message
+from ictc_o3.backends.hip.graph_message import message_bonds, packed_graph_message
 from ictc_o3.backends.hip.harmonics import direction_harmonics_packed
 from ictc_o3.backends.hip.radial_message import fold_projection, packed_radial_graph_message
 from ictc_o3.basis.ictd_irreps import EdgeWeightedPathPreservingTensorProduct
@@ -198,19 +198,26 @@ class Interaction(nn.Module):
         hidden, weight = self.radial_hidden(edge_feats)
         return linear(hidden, weight * self.tp.weight.reshape(-1, 1))
 
-    def forward(self, h, harmonics, edge_feats, src, dst, mask, species, scalars=None):
+    def message_bonds(self, harmonics):
+        """The bond rows the message forward derives from the harmonics (see forward's bonds)."""
+        return message_bonds(self.tp.hip_plan(self.input_lmax, self.edge_lmax), harmonics)
+
+    def forward(self, h, harmonics, edge_feats, src, dst, mask, species, scalars=None, gates=None, bonds=None):
         """mask: the reference multiplies the gates by (r <= r_max) (:1801-1808).  The radial
         features carry the cutoff envelope, exactly 0 from r_max on, and fc has no biases, so
         the gates are already exactly 0 wherever the mask is 0: the product is an identity and
         is skipped (mask is accepted for the signature).  scalars: h's l = 0 block as its own
         tensor when the caller has it (the previous product's), so the self connection does not
-        slice h (a slice's backward zero-fills a gradient of h's full width)."""
+        slice h (a slice's backward zero-fills a gradient of h's full width).  gates: this
+        interaction's message gates, and bonds the bond rows of the harmonics, when the caller has
+        produced them already (on a side stream)."""
         n = h.shape[0]
         x1 = self.linear_up.to_ir_mul(h)
         plan = self.tp.hip_plan(self.input_lmax, self.edge_lmax)
         if self.edge_chunk_size is None:
-            gates = self.message_gates(edge_feats)
-            m = packed_graph_message(plan, x1, harmonics, gates, src, dst, nodes_dst=n)
+            if gates is None:
+                gates = self.message_gates(edge_feats)
+            m = packed_graph_message(plan, x1, harmonics, gates, src, dst, nodes_dst=n, bonds=bonds)
         else:
             # the radial MLP's last layer produced one receiver range at a time inside the message
             # (reference capacity mode, capacity_message.py:109-179): no [E, P*C] gate tensor
@@ -243,6 +250,19 @@ class Product(nn.Module):
         return (torch.cat([scalar, rest], dim=-1) if rest.shape[1] else scalar), scalar
 
 
+_SIDE_STREAMS: Dict[int, torch.cuda.Stream] = {}
+
+
+def _side_stream(device: torch.device) -> "torch.cuda.Stream":
+    """One default-priority side stream per device, created once."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    stream = _SIDE_STREAMS.get(index)
+    if stream is None:
+        stream = torch.cuda.Stream(device=index)
+        _SIDE_STREAMS[index] = stream
+    return stream
+
+
 class MaceICTC(nn.Module):
     def __init__(self, *, channels: int = 128, lmax: int = 3, num_interactions: int = 2, correlation: int = 3,
                  atomic_numbers=tuple(range(1, 11)), cutoff: float = 5.0, avg_num_neighbors: float = 50.0,
@@ -250,6 +270,8 @@ class MaceICTC(nn.Module):
         super().__init__()
         self.channels, self.lmax, self.cutoff = int(channels), int(lmax), float(cutoff)
         self.num_basis, self.cutoff_p = int(num_basis), int(cutoff_p)
+        # radial MLPs and gates on a second stream beside the interactions (GPU, whole gates)
+        self.overlap_radial = True
         self.atomic_numbers = [int(z) for z in atomic_numbers]
         self.num_elements = len(self.atomic_numbers)
         table = torch.full((max(self.atomic_numbers) + 1,), -1, dtype=torch.int64)
@@ -319,14 +341,51 @@ class MaceICTC(nn.Module):
             h = linear(one_hot_rows(species, self.num_elements), self.node_embedding.weight)
         else:
             h = self.node_embedding.weight.t().index_select(0, species)
+        side = self._side_work(edge_feats, harmonics)
         energy = None
         scalars = h
         for t, (interaction, product) in enumerate(zip(self.interactions, self.products)):
-            message, sc = interaction(h, harmonics, edge_feats, edge_src, edge_dst, mask, species, scalars)
+            gates = bonds = None
+            if side is not None:
+                gates, bonds, ready = side[t]
+                torch.cuda.current_stream(pos.device).wait_event(ready)
+            message, sc = interaction(h, harmonics, edge_feats, edge_src, edge_dst, mask, species, scalars,
+                                      gates, bonds)
             h, scalars = product(message, sc, species)
             if t < len(self.interactions) - 1:
                 e = self.layer_readouts[t](scalars)
             else:
                 e = self.last_readout(h)
             energy = e if energy is None else energy + e
+        if side is not None:   # join the side stream (nothing left on it unwaited, also under capture)
+            torch.cuda.current_stream(pos.device).wait_stream(_side_stream(pos.device))
         return energy.reshape(-1)
+
+    def _side_work(self, edge_feats, harmonics):
+        """Each interaction's message gates (radial MLP and its [E, P*C] last layer) and bond rows,
+        issued on a second stream: they depend only on the edge features and harmonics, so
+        interaction t+1's run beside interaction t's message, contraction and linears, and the
+        autograd engine runs their adjoints on that stream too (beside the other interaction's
+        backward).  Returns [(gates, bonds, ready event)] per interaction, or None where this does
+        not apply (CPU, radial streaming)."""
+        if not (self.overlap_radial and edge_feats.is_cuda
+                and all(i.edge_chunk_size is None for i in self.interactions)):
+            return None
+        main = torch.cuda.current_stream(edge_feats.device)
+        side = _side_stream(edge_feats.device)
+        side.wait_stream(main)
+        out = []
+        with torch.cuda.stream(side):
+            for interaction in self.interactions:
+                gates = interaction.message_gates(edge_feats)
+                bonds = interaction.message_bonds(harmonics)
+                ev = torch.cuda.Event()
+                ev.record(side)
+                out.append((gates, bonds, ev))
+        for gates, bonds, _ in out:   # used on the main stream: not reusable by side allocations before
+            gates.record_stream(main)
+            if bonds is not None:
+                bonds.record_stream(main)
+        for t in (edge_feats, harmonics):   # read on the side stream: not reusable on the main one before
+            t.record_stream(side)
+        return out
