@@ -36,7 +36,7 @@ SPLIT_ROWS_LARGE = 8192
 SPLIT_LARGE_OUTPUT = 1 << 17
 SPLIT_SINGLE_GEMM_OUTPUT = 4096
 ROW_MAJOR_RIGHT_BELOW_K = 16
-TALL_ROWS = 32768          # edge-sized left operand ...
+TALL_ROWS = 8192           # edge-sized left operand ...
 TALL_MAX_RIGHT = 1 << 22   # ... against a weight-sized right operand: column-major right operand
 
 
