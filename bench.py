@@ -720,9 +720,14 @@ def _bench_mace(device):
     model.eval().requires_grad_(False)
     infer_ms = _median_call_ms(lambda: energy_and_forces(model, **graph, species=species), device)
     infer_peak = _peak_bytes(lambda: energy_and_forces(model, **graph, species=species), device)
-    model.set_message_streaming(16384)         # radial streaming: no [E, P*C] gate tensor
-    stream_ms = _median_call_ms(lambda: energy_and_forces(model, **graph, species=species), device)
-    stream_peak = _peak_bytes(lambda: energy_and_forces(model, **graph, species=species), device)
+    streaming = {}
+    for size in (16384, 24576):                # radial streaming: no [E, P*C] gate tensor
+        model.set_message_streaming(size)
+        eager_ms = _median_call_ms(lambda: energy_and_forces(model, **graph, species=species), device)
+        peak = _peak_bytes(lambda: energy_and_forces(model, **graph, species=species), device)
+        captured = CapturedEnergyAndForces(model, **graph, species=species)
+        streaming[size] = (eager_ms, _median_call_ms(lambda: captured(graph["positions"]), device), peak)
+        del captured
     model.set_message_streaming(None)
     captured = CapturedEnergyAndForces(model, **graph, species=species)
     infer_graph_ms = _median_call_ms(lambda: captured(graph["positions"]), device)
@@ -751,9 +756,13 @@ def _bench_mace(device):
             "inference_hip_graph": leg(infer_graph_ms, 11.0e3, "HIP graph replay"),
             "training_hip_graph": leg(train_graph_ms, 3.81e3, "HIP graph replay"),
             "inference_radial_streaming": {
-                **leg(stream_ms, 11.0e3, "eager, radial streaming over 16,384-edge receiver ranges"),
-                "peak_bytes": stream_peak, "peak_bytes_whole_gates": infer_peak,
-                "gate_tensor_bytes": graph["edge_src"].numel() * 23 * 128 * 4}}
+                **leg(streaming[16384][0], 11.0e3, "eager, radial streaming over 16,384-edge receiver ranges"),
+                "peak_bytes": streaming[16384][2], "peak_bytes_whole_gates": infer_peak,
+                "gate_tensor_bytes": graph["edge_src"].numel() * 23 * 128 * 4,
+                "ratio_to_whole_gates_eager": streaming[16384][0] / infer_ms,
+                "ranges": {str(size): {"eager_ms": e, "replay_ms": r, "peak_bytes": pk,
+                                       "ratio_eager": e / infer_ms, "ratio_replay": r / infer_graph_ms}
+                           for size, (e, r, pk) in streaming.items()}}}
 
 
 LIN_COUNTS, LIN_C, MFMA_F32_PEAK_TFLOPS = (4, 6, 7, 6), 128, 157.3   # fp32 MFMA, dense (published)
