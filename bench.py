@@ -37,7 +37,7 @@ reference) and three launches of each TP kernel at the benchmark sizes, for
 rocprofv3 --pmc passes.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--kernels-only]
-                      [--only tp|tp0|message|sc|mace|graph|linear|radial|generic]
+                      [--only tp|tp0|message|sc|mace|mace_steps|graph|linear|radial|generic]
 """
 from __future__ import annotations
 
@@ -765,6 +765,37 @@ def _bench_mace(device):
                            for size, (e, r, pk) in streaming.items()}}}
 
 
+def _bench_mace_steps(device, modes=("inference", "training"), replays: int = 20):
+    """The captured inference and/or training step alone, replayed a fixed number of times after
+    its capture (3 eager warm-up calls inside the capture helper, then 3 replays): a kernel trace
+    of a one-mode run divides into per-step figures (calls / (replays + 6))."""
+    from mace_hip import CapturedEnergyAndForces, CapturedTrainingStep, create_model
+    _, graph = _mace_graph(device)
+    out = {"replays_after_warmup": replays, "executions_per_mode": replays + 6}
+    for mode in modes:
+        model = create_model(channels=128, lmax=3, num_interactions=2, correlation=3, atomic_numbers=MACE_ZS,
+                             cutoff=5.0, device=device, seed=0)
+        species = model.species_index(graph["atomic_numbers"])
+        if mode == "inference":
+            model.eval().requires_grad_(False)
+            step = CapturedEnergyAndForces(model, **graph, species=species)
+        else:
+            opt = torch.optim.AdamW(model.parameters(), lr=1e-3, capturable=True, fused=True)
+            step = CapturedTrainingStep(model, opt, graph, species=species)
+        for _ in range(3):
+            step(graph["positions"])
+        torch.cuda.synchronize(device)
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(replays):
+            step(graph["positions"])
+        end.record()
+        torch.cuda.synchronize(device)
+        out[mode] = {"mean_replay_ms": start.elapsed_time(end) / replays}
+        del step
+    return out
+
+
 LIN_COUNTS, LIN_C, MFMA_F32_PEAK_TFLOPS = (4, 6, 7, 6), 128, 157.3   # fp32 MFMA, dense (published)
 
 
@@ -1034,8 +1065,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--kernels-only", action="store_true")
-    ap.add_argument("--only", choices=("tp", "tp0", "message", "message3", "sc", "mace", "graph", "linear",
-                                       "radial", "generic", "valu"),
+    ap.add_argument("--only", choices=("tp", "tp0", "message", "message3", "sc", "mace", "mace_steps",
+                                       "mace_steps_inference", "mace_steps_training", "graph", "linear", "radial",
+                                       "generic", "valu"),
                     default=None,
                     help="run one section and print its JSON (for profiling)")
     args = ap.parse_args()
@@ -1050,9 +1082,13 @@ def main() -> int:
     if args.kernels_only:
         _kernels_only(op.plan, device)
         return 0
-    if args.only in ("tp0", "message", "message3", "sc", "mace", "graph", "linear", "radial", "generic", "valu"):
+    if args.only in ("tp0", "message", "message3", "sc", "mace", "mace_steps", "mace_steps_inference",
+                     "mace_steps_training", "graph", "linear", "radial", "generic", "valu"):
         fn = {"tp0": _bench_tp_cfg0, "message": _bench_message, "message3": _bench_message3, "sc": _bench_sc,
-              "mace": _bench_mace, "graph": _bench_graph, "linear": _bench_linear, "radial": _bench_radial,
+              "mace": _bench_mace, "mace_steps": _bench_mace_steps,
+              "mace_steps_inference": lambda d: _bench_mace_steps(d, ("inference",)),
+              "mace_steps_training": lambda d: _bench_mace_steps(d, ("training",)),
+              "graph": _bench_graph, "linear": _bench_linear, "radial": _bench_radial,
               "generic": _bench_generic, "valu": _valu_form_cycles}[args.only]
         print(json.dumps({args.only: fn(device)}), flush=True)
         return 0
