@@ -55,7 +55,7 @@ sys.path.insert(0, os.path.join(ROOT, "ictc-o3-hp-ascend_amd"))
 import torch  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0                       # MI355X HBM3E, GB/s
-PUBLISHED_FWD_VJP_INST_S = 0.729e6          # reference HP on Ascend 910B3
+PUBLISHED_FWD_VJP_INST_S = 0.729e6          # the reference HP path on an Ascend 910B3 (its published figure)
 C, L, ROWS_VJP, ROWS_FWD = 128, 3, 131072, 262144
 P = 23
 X_W, Y_W, G_W, O_W = C * (L + 1) ** 2, (L + 1) ** 2, P * C, 99 * C
