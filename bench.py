@@ -37,7 +37,7 @@ reference) and three launches of each TP kernel at the benchmark sizes, for
 rocprofv3 --pmc passes.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--kernels-only]
-                      [--only tp|tp0|message|sc|mace|mace_steps|graph|linear|radial|generic]
+                      [--only tp|tp0|message|sc|mace|mace_steps|graph|linear|radial|l4|valu]
 """
 from __future__ import annotations
 
@@ -422,9 +422,8 @@ def _bench_tp_cfg0(device):
 GEN_C, GEN_L, GEN_ROWS = 64, 4, 65536
 
 
-def _bench_generic(device):
-    """Degree-generic kernels (run-time path tables; every degree set with a degree above 3): the
-    TP forward and VJP at C = 64, degrees (4, 4, 4) (42 paths), 65,536 instances.  Reported
+def _tp_degree_leg(device, lin: int, le: int, lout: int):
+    """Forward and VJP of the TP at C = 64 over GEN_ROWS instances of degrees (lin, le, lout),
     against both bounds: algorithmic HBM bytes (x, Y, g read and out written; the VJP also reads
     dout and writes dx, dY, dg) and the FMA work the kernels execute (forward 2·NB·C per instance
     plus 2·Σ_p n1 n2 n3 for the bond rows; the VJP 2·2·NB·C for dg and dx, 2·Σ_p n1 n2 n3·C for
@@ -432,13 +431,12 @@ def _bench_generic(device):
     from ictc_o3 import EdgeTensorProduct
     from ictc_o3.backends.hip.harmonics import direction_harmonics_packed
     from ictc_o3.backends.hip.tensor_product import _backward_raw, _forward_raw
-    op = EdgeTensorProduct.create(channels=GEN_C, input_lmax=GEN_L, edge_lmax=GEN_L, device=device)
+    op = EdgeTensorProduct.create(channels=GEN_C, input_lmax=lin, edge_lmax=le, output_lmax=lout, device=device)
     plan = op.plan
-    assert plan.generic
     gen = torch.Generator(device=device).manual_seed(5)
     x = torch.randn(GEN_ROWS, plan.x_width, device=device, generator=gen)
     n = torch.nn.functional.normalize(torch.randn(GEN_ROWS, 3, device=device, generator=gen), dim=-1)
-    y = direction_harmonics_packed(n, GEN_L).contiguous()
+    y = direction_harmonics_packed(n, le).contiguous()
     g = torch.randn(GEN_ROWS, plan.full_gate_width, device=device, generator=gen)
     go = torch.randn(GEN_ROWS, plan.full_out_width, device=device, generator=gen)
     fwd_ms = _event_ms(lambda: _forward_raw(plan, x, y, g), device, reps=10)
@@ -460,10 +458,21 @@ def _bench_generic(device):
                 "valu": {"fma_flops_per_instance": flops, "achieved": tf, "peak": VALU_PEAK_TFLOPS,
                          "unit": "TFLOP/s", "frac": tf / VALU_PEAK_TFLOPS}}
 
-    return {"workload": f"degree-generic TP C{GEN_C}, degrees ({GEN_L},{GEN_L},{GEN_L}), {len(paths)} paths, "
-                        f"{GEN_ROWS:,} instances, ir_mul",
-            "kernels": "gen_tp_forward_kernel, gen_tp_backward_kernel",
+    return {"workload": f"TP C{GEN_C}, degrees ({lin},{le},{lout}), {len(paths)} paths, {GEN_ROWS:,} instances, "
+                        f"ir_mul",
             "forward": leg(fwd_ms, fwd_bytes, fwd_flops), "vjp": leg(vjp_ms, vjp_bytes, vjp_flops)}
+
+
+def _bench_tp_l4(device):
+    """Degree-4 tensor products: the symmetric (4, 4, 4) set (42 paths) on its compiled kernels,
+    and the (4, 4, 3) set on the degree-generic ones (run-time path tables: every set with a degree
+    above 3 other than the compiled ones)."""
+    out = _tp_degree_leg(device, GEN_L, GEN_L, GEN_L)
+    out["kernels"] = "tp_forward_kernel<4,4,4,1>, tp_backward_wide_kernel<4,4,4>"
+    gen = _tp_degree_leg(device, GEN_L, GEN_L, GEN_L - 1)
+    gen["kernels"] = "gen_tp_forward_kernel, gen_tp_backward_kernel"
+    out["generic_443"] = gen
+    return out
 
 
 def _cpu_tp_cfg0(budget_s: float = 10.0, rows: int = 8192):
@@ -1067,7 +1076,7 @@ def main() -> int:
     ap.add_argument("--kernels-only", action="store_true")
     ap.add_argument("--only", choices=("tp", "tp0", "message", "message3", "sc", "mace", "mace_steps",
                                        "mace_steps_inference", "mace_steps_training", "graph", "linear", "radial",
-                                       "generic", "valu"),
+                                       "l4", "valu"),
                     default=None,
                     help="run one section and print its JSON (for profiling)")
     args = ap.parse_args()
@@ -1083,13 +1092,13 @@ def main() -> int:
         _kernels_only(op.plan, device)
         return 0
     if args.only in ("tp0", "message", "message3", "sc", "mace", "mace_steps", "mace_steps_inference",
-                     "mace_steps_training", "graph", "linear", "radial", "generic", "valu"):
+                     "mace_steps_training", "graph", "linear", "radial", "l4", "valu"):
         fn = {"tp0": _bench_tp_cfg0, "message": _bench_message, "message3": _bench_message3, "sc": _bench_sc,
               "mace": _bench_mace, "mace_steps": _bench_mace_steps,
               "mace_steps_inference": lambda d: _bench_mace_steps(d, ("inference",)),
               "mace_steps_training": lambda d: _bench_mace_steps(d, ("training",)),
               "graph": _bench_graph, "linear": _bench_linear, "radial": _bench_radial,
-              "generic": _bench_generic, "valu": _valu_form_cycles}[args.only]
+              "l4": _bench_tp_l4, "valu": _valu_form_cycles}[args.only]
         print(json.dumps({args.only: fn(device)}), flush=True)
         return 0
     elapsed, vjp_ms, fwd_ms = _time_gpu(args, op.plan, device)
@@ -1106,7 +1115,7 @@ def main() -> int:
                   "message_cfg4_lmax3": _bench_message3(device), "sc_cfg3": _bench_sc(device),
                   "mace_cfg4": _bench_mace(device), "message_linear_cfg4": _bench_linear(device),
                   "radial_mlp_cfg4": _bench_radial(device),
-                  "radius_graph": _bench_graph(device), "tp_generic_l4": _bench_generic(device)}
+                  "radius_graph": _bench_graph(device), "tp_l4": _bench_tp_l4(device)}
         if not args.no_cpu:
             others["tp_cfg0"]["cpu_baseline"] = _cpu_tp_cfg0()
             others["message_cfg2"]["cpu_baseline"] = _cpu_message()

@@ -4,7 +4,10 @@ Steps:
   1. generate ``generated/ictc_cg_table.hpp`` (CG constants from the frozen basis);
   2. write one translation unit per (input_lmax, edge_lmax, output_lmax, kernel
      kind) with the explicit template instantiation, plus ``tp_instances.def``
-     listing the compiled combinations for the dispatch tables;
+     listing the compiled combinations for the dispatch tables (every degree <= 3),
+     and the tensor-product units of the wide sets in ``WIDE_COMBOS`` (listed in
+     ``tp_wide_instances.def``; other sets with a degree of 4 to 6 run the
+     degree-generic kernels);
   3. compile every TU to an object in parallel, largest first;
   4. link the objects and the API TUs into ``ictc_o3/lib/libictc_hip.so``;
   5. build ``libictc_stream_probe.so`` beside bench.py from the repository root's
@@ -53,6 +56,8 @@ API_SOURCES = ["tp_api.hip", "harmonics_api.hip", "message_api.hip", "sc_api.hip
 # dynamic linker then binds to
 LINK_LIBS = ["-L/opt/rocm/lib", "-lrocblas"]
 HARM_LMAX = 6
+# degree sets above 3 with compiled tensor-product kernels (the symmetric lmax-4 set)
+WIDE_COMBOS = [(4, 4, 4)]
 INSTANCE_KINDS = {
     "fwd": ("tp_kernels.hpp", "template int launch_forward<{a}, {b}, {c}>(const ictc_tp_desc&, "
             "const float*, const float*, const float*, float*, int64_t, hipStream_t);"),
@@ -117,7 +122,16 @@ def _generate(combos) -> list:
                     os.path.join(GEN, "ictc_cg_table.hpp")], check=True)
     _write_if_changed(os.path.join(GEN, "tp_instances.def"),
                       "".join(f"ICTC_DECLARE({a}, {b}, {c})\n" for a, b, c in combos))
+    _write_if_changed(os.path.join(GEN, "tp_wide_instances.def"),
+                      "".join(f"ICTC_DECLARE({a}, {b}, {c})\n" for a, b, c in WIDE_COMBOS))
     units = []
+    for a, b, c in WIDE_COMBOS:
+        for kind in ("fwd", "bwd"):
+            header, line = INSTANCE_KINDS[kind]
+            path = os.path.join(GEN, f"tp_inst_{a}{b}{c}_{kind}.hip")
+            _write_if_changed(path, f'#define ICTC_CG_WIDE 1\n#include "{header}"\nnamespace ictc {{\n'
+                                    f'{line.format(a=a, b=b, c=c)}\n}}  // namespace ictc\n')
+            units.append((_cost(a, b, c, kind), path))
     for a, b, c in combos:
         for kind, (header, line) in INSTANCE_KINDS.items():
             path = os.path.join(GEN, f"{'msg' if kind == 'msg' else 'tp'}_inst_{a}{b}{c}_{kind}.hip")

@@ -274,4 +274,20 @@ struct WaveSums {
   }
 };
 
+// Channel sums of N per-lane partials (one per harmonic component) stored to N floats at rsrc
+// r: one transposing butterfly per group of 16 components.
+template <int N>
+__device__ __forceinline__ void store_channel_sums(const float (&v)[N], int lane, rsrc_t r) {
+  static_for<0, (N + 15) / 16>([&](auto H) {
+    constexpr int h0 = 16 * H, nh = N - h0 < 16 ? N - h0 : 16;
+    using WS = WaveSums<nh>;
+    float part[nh];
+#pragma unroll
+    for (int j = 0; j < nh; ++j) part[j] = v[h0 + j];
+    const float tot = WS::reduce(part, lane);
+    const int j = WS::index(lane);
+    if (WS::owner(lane) && j < nh) buf_store<1, 0>(r, static_cast<uint32_t>(h0 + j) * 4u, Vec<1>{{tot}});
+  });
+}
+
 }  // namespace ictc

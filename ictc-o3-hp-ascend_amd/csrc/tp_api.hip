@@ -15,6 +15,37 @@ namespace ictc {
 #include "generated/tp_instances.def"
 #undef ICTC_DECLARE
 
+// Compiled wide degree sets (a degree of 4; tp_wide_instances.def), dispatched ahead of the
+// degree-generic kernels.
+#define ICTC_DECLARE(A, B, C)                                                                  \
+  extern template int launch_forward<A, B, C>(const ictc_tp_desc&, const float*, const float*,   \
+                                              const float*, float*, int64_t, hipStream_t);      \
+  extern template int launch_backward<A, B, C>(const ictc_tp_desc&, const float*, const float*,  \
+                                               const float*, const float*, float*, float*, float*, \
+                                               int64_t, hipStream_t);
+#include "generated/tp_wide_instances.def"
+#undef ICTC_DECLARE
+
+inline bool same_degrees(const ictc_tp_desc* d, int a, int b, int c) {
+  return d->input_lmax == a && d->edge_lmax == b && d->output_lmax == c;
+}
+
+FwdLaunch wide_forward(const ictc_tp_desc* d) {
+#define ICTC_DECLARE(A, B, C) \
+  if (same_degrees(d, A, B, C)) return &launch_forward<A, B, C>;
+#include "generated/tp_wide_instances.def"
+#undef ICTC_DECLARE
+  return nullptr;
+}
+
+BwdLaunch wide_backward(const ictc_tp_desc* d) {
+#define ICTC_DECLARE(A, B, C) \
+  if (same_degrees(d, A, B, C)) return &launch_backward<A, B, C>;
+#include "generated/tp_wide_instances.def"
+#undef ICTC_DECLARE
+  return nullptr;
+}
+
 // Dispatch tables of the per-degree instantiations (every degree <= 3), indexed by
 // input_lmax*16 + edge_lmax*4 + output_lmax; entries of combinations left out of a
 // (development) build are null and report UNSUPPORTED.
@@ -82,6 +113,8 @@ int ictc_hip_tp_forward(const ictc_tp_desc* desc, const float* features, const f
   if (rows < 0) return ICTC_ERR_INVALID_ARGUMENT;
   if (rows == 0) return ICTC_OK;
   if (!features || !harmonics || !gates || !out) return ICTC_ERR_INVALID_ARGUMENT;
+  if (const ictc::FwdLaunch wide = ictc::wide_forward(desc))
+    return wide(*desc, features, harmonics, gates, out, rows, stream);
   if (ictc::generic_degrees(*desc))
     return ictc::generic_tp_forward(*desc, features, harmonics, gates, out, rows, stream);
   const ictc::FwdLaunch fn = ictc::kFwdTable[ictc::table_index(desc)];
@@ -99,6 +132,9 @@ int ictc_hip_tp_backward(const ictc_tp_desc* desc, const float* features, const 
   if (!harmonics || !gates || !grad_out) return ICTC_ERR_INVALID_ARGUMENT;
   if ((grad_harmonics || grad_gates) && !features) return ICTC_ERR_INVALID_ARGUMENT;
   if (!grad_features && !grad_harmonics && !grad_gates) return ICTC_OK;
+  if (const ictc::BwdLaunch wide = ictc::wide_backward(desc))
+    return wide(*desc, features, harmonics, gates, grad_out, grad_features, grad_harmonics, grad_gates, rows,
+                stream);
   if (ictc::generic_degrees(*desc))
     return ictc::generic_tp_backward(*desc, features, harmonics, gates, grad_out, grad_features, grad_harmonics,
                                      grad_gates, rows, stream);

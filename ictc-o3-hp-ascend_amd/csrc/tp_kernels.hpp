@@ -19,9 +19,17 @@
 // The instance loop never round-trips intermediates through HBM: the forward reads
 // x, Y, g once and writes out once; the VJP reads x, Y, g, dout once and writes
 // dx, dY, dg once.
+//
+// Degree sets with an input degree of 4 take the VJP variant tp_backward_wide_kernel, which keeps
+// only one input degree's x and dx rows in registers at a time (units compiled for those sets
+// define ICTC_CG_WIDE and read the CG tables up to degree 4).
 #pragma once
 #include "ictc_common.hpp"
+#ifdef ICTC_CG_WIDE
+#include "generated/ictc_cg_table_wide.hpp"
+#else
 #include "generated/ictc_cg_table.hpp"
+#endif
 
 namespace ictc {
 
@@ -40,7 +48,7 @@ constexpr int kBwdPrefetch = 2;
 constexpr int kBlock = 256;
 constexpr int kWavesPerBlock = kBlock / kWave;
 
-template <int LIN, int LE, int LOUT, int TILE>
+template <int LIN, int LE, int LOUT, int TILE, int NT = kBlock>
 __device__ __forceinline__ void build_bond(const float (*sY)[Paths<LIN, LE, LOUT>::NY],
                                            float (*sM)[Paths<LIN, LE, LOUT>::NB > 0 ? Paths<LIN, LE, LOUT>::NB : 1],
                                            const ictc_tp_desc& d, int tid) {
@@ -52,7 +60,7 @@ __device__ __forceinline__ void build_bond(const float (*sY)[Paths<LIN, LE, LOUT
     constexpr int boff = PS::tab.bond[p];
     constexpr int cgo = CGTab<l1, l2, l3>::offset;
     const float s = d.scale[p];
-    for (int t = tid; t < TILE * ni * no; t += kBlock) {
+    for (int t = tid; t < TILE * ni * no; t += NT) {
       const int e = t / (ni * no);
       const int r = t - e * (ni * no);  // M_p stored [k][i]: r = k*ni + i
       const int k = r / ni;
@@ -67,18 +75,18 @@ __device__ __forceinline__ void build_bond(const float (*sY)[Paths<LIN, LE, LOUT
 }
 
 // Stage the tile's harmonics in LDS and build the bond matrices of all tile instances.
-template <int LIN, int LE, int LOUT, int TILE>
+template <int LIN, int LE, int LOUT, int TILE, int NT = kBlock>
 __device__ __forceinline__ void stage_tile(const float* __restrict__ y, int64_t e0, int64_t rows,
                                            float (*sY)[Paths<LIN, LE, LOUT>::NY],
                                            float (*sM)[Paths<LIN, LE, LOUT>::NB > 0 ? Paths<LIN, LE, LOUT>::NB : 1],
                                            const ictc_tp_desc& d, int tid) {
   constexpr int NY = Paths<LIN, LE, LOUT>::NY;
-  for (int t = tid; t < TILE * NY; t += kBlock) {
+  for (int t = tid; t < TILE * NY; t += NT) {
     const int e = t / NY;
     sY[e][t - e * NY] = (e0 + e < rows) ? y[(e0 + e) * NY + (t - e * NY)] : 0.f;
   }
   __syncthreads();
-  build_bond<LIN, LE, LOUT, TILE>(sY, sM, d, tid);
+  build_bond<LIN, LE, LOUT, TILE, NT>(sY, sM, d, tid);
   __syncthreads();
 }
 
@@ -170,8 +178,10 @@ tp_forward_kernel(const float* __restrict__ x, const float* __restrict__ y,
 // (measured at C128/lmax3: 2.16 -> 2.10 ms; the forward's loads measure slower with it).
 // Outputs whose pointer is null get an empty buffer descriptor: their stores are
 // dropped by the hardware range check, so the instance body has no branches.
+// NV = 2 asks for three waves per SIMD (168 registers; the <3,3,3,2> instance needs 170 without
+// the bound and measured 2.07 ms at two waves per SIMD, 2.04 ms at three).
 template <int LIN, int LE, int LOUT, int NV>
-__global__ void __launch_bounds__(kBlock)
+__global__ void __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(NV == 2 ? 3 : 1)))
 tp_backward_kernel(const float* __restrict__ x, const float* __restrict__ y,
                    const float* __restrict__ g, const float* __restrict__ go,
                    float* __restrict__ dx, float* __restrict__ dy, float* __restrict__ dg,
@@ -248,35 +258,31 @@ tp_backward_kernel(const float* __restrict__ x, const float* __restrict__ y,
         Vec<NV> o[no];
         static_for<0, no>([&](auto K) { o[K] = pre_o[p % D][K]; });
         request(Int<p + D>{});             // issued ahead of this path's dg store
+        // dg and dx in one pass over the bond entries: each M_p[i][k] is read once and used for
+        // both (two passes kept the path's ni*no entries live in registers between them); every
+        // dx row still accumulates in ascending k
         Vec<NV> dgv;
 #pragma unroll
         for (int v = 0; v < NV; ++v) dgv.v[v] = 0.f;
+        Vec<NV> gov[no];
         static_for<0, no>([&](auto K) {
+#pragma unroll
+          for (int v = 0; v < NV; ++v) gov[K].v[v] = gv.v[v] * o[K].v[v];
           Vec<NV> base;
 #pragma unroll
           for (int v = 0; v < NV; ++v) base.v[v] = 0.f;
           static_for<0, ni>([&](auto I) {
             const float m = bond[boff + K * ni + I];
 #pragma unroll
-            for (int v = 0; v < NV; ++v) base.v[v] = fmaf(xr[l1 * l1 + I].v[v], m, base.v[v]);
+            for (int v = 0; v < NV; ++v) {
+              base.v[v] = fmaf(xr[l1 * l1 + I].v[v], m, base.v[v]);
+              dxr[l1 * l1 + I].v[v] = fmaf(m, gov[K].v[v], dxr[l1 * l1 + I].v[v]);
+            }
           });
 #pragma unroll
           for (int v = 0; v < NV; ++v) dgv.v[v] = fmaf(base.v[v], o[K].v[v], dgv.v[v]);
         });
         buf_store<NV>(rdg, vo + p * row, dgv);
-        Vec<NV> gov[no];
-        static_for<0, no>([&](auto K) {
-#pragma unroll
-          for (int v = 0; v < NV; ++v) gov[K].v[v] = gv.v[v] * o[K].v[v];
-        });
-        static_for<0, ni>([&](auto I) {
-          static_for<0, no>([&](auto K) {
-            const float m = bond[boff + K * ni + I];
-#pragma unroll
-            for (int v = 0; v < NV; ++v)
-              dxr[l1 * l1 + I].v[v] = fmaf(m, gov[K].v[v], dxr[l1 * l1 + I].v[v]);
-          });
-        });
         float part[nj];
 #pragma unroll
         for (int j = 0; j < nj; ++j) part[j] = 0.f;
@@ -298,12 +304,130 @@ tp_backward_kernel(const float* __restrict__ x, const float* __restrict__ y,
 #pragma unroll
       for (int m = 0; m < NX; ++m) buf_store<NV>(rdx, vo + m * row, dxr[m]);
     }
-    // channel sums of the NY partials, one transposing butterfly
-    using WS = WaveSums<NY>;
-    const float tot = WS::reduce(dyl, lane);
-    const int j = WS::index(lane);
-    const rsrc_t rdy = make_rsrc(dy ? dy + e * NY : nullptr, NY * 4u);
-    if (WS::owner(lane) && j < NY) buf_store<1, 0>(rdy, static_cast<uint32_t>(j) * 4u, Vec<1>{{tot}});
+    store_channel_sums<NY>(dyl, lane, make_rsrc(dy ? dy + e * NY : nullptr, NY * 4u));
+  }
+}
+
+// First path of input degree a in the enumeration order (paths ascend in l1), or the path count.
+template <int LIN, int LE, int LOUT>
+constexpr int first_path_of_degree(int a) {
+  constexpr PathTable t = Paths<LIN, LE, LOUT>::tab;
+  for (int p = 0; p < t.n; ++p)
+    if (t.l1[p] >= a) return p;
+  return t.n;
+}
+
+// Fused VJP for wide degree sets (input degree 4: 25 x rows).  Same per-path arithmetic and
+// output as tp_backward_kernel, reorganised by input degree: the x rows of degree a are
+// requested while degree a - 1 is computed, and the dx rows of degree a are accumulated and
+// stored with that degree, so x and dx occupy 2 (2a + 1) + (2a + 3) registers per channel
+// instead of 2 NX.  One channel per lane (NV = 1), and one instance per single-wave workgroup:
+// each wave builds its own bond rows, so no wave waits at a barrier for another's build.
+// Measured at C64/(4,4,4), 65,536 instances: 300 registers with all x and dx rows resident (one
+// wave per SIMD, 2.91 ms); 247 per degree (two waves, 1.89 ms); 118 with the single pass over
+// the bond entries (four waves, 1.44 ms); one-wave workgroups 1.415 ms.
+constexpr int kWideBlock = kWave;
+template <int LIN, int LE, int LOUT>
+__global__ void __launch_bounds__(kWideBlock)
+tp_backward_wide_kernel(const float* __restrict__ x, const float* __restrict__ y,
+                        const float* __restrict__ g, const float* __restrict__ go,
+                        float* __restrict__ dx, float* __restrict__ dy, float* __restrict__ dg,
+                        const ictc_tp_desc d, int64_t rows) {
+  using PS = Paths<LIN, LE, LOUT>;
+  constexpr int NX = PS::NX, NY = PS::NY, NP = PS::N, NOC = PS::NOC;
+  constexpr int NBS = PS::NB > 0 ? PS::NB : 1;
+  constexpr int WMAX = 2 * LIN + 1;
+  __shared__ float sY[1][NY];
+  __shared__ float sM[1][NBS];
+  const int lane = threadIdx.x;
+  const int64_t e = blockIdx.x;
+  const int C = d.channels;
+  const uint32_t row = static_cast<uint32_t>(C) * 4u;
+  stage_tile<LIN, LE, LOUT, 1, kWideBlock>(y, e, rows, sY, sM, d, lane);
+  {
+    const int le = 0;
+    const rsrc_t rx = make_rsrc(x ? x + e * NX * C : nullptr, NX * row);
+    const rsrc_t rg = make_rsrc(g + e * NP * C, NP * row);
+    const rsrc_t rgo = make_rsrc(go + e * NOC * C, NOC * row);
+    const rsrc_t rdx = make_rsrc(dx ? dx + e * NX * C : nullptr, NX * row);
+    const rsrc_t rdg = make_rsrc(dg ? dg + e * NP * C : nullptr, NP * row);
+    float dyl[NY];
+#pragma unroll
+    for (int j = 0; j < NY; ++j) dyl[j] = 0.f;
+    for (int c = lane; c < C; c += kWave) {
+      const uint32_t vo = static_cast<uint32_t>(c) * 4u;
+      const float* __restrict__ bond = opaque_lds_row(&sM[le][0]);
+      constexpr int D = kBwdPrefetch;
+      float pre_g[D];                      // rows of the next D paths, in flight
+      float pre_o[D][2 * LOUT + 1];
+      auto request = [&](auto Q) {
+        constexpr int q = Q;
+        if constexpr (q < NP) {
+          constexpr int nq = 2 * PS::tab.l3[q] + 1, oq = PS::tab.out[q];
+          pre_g[q % D] = buf_load<1, kNonTemporal>(rg, vo + q * row).v[0];
+          static_for<0, nq>([&](auto K) { pre_o[q % D][K] = buf_load<1, kNonTemporal>(rgo, vo + (oq + K) * row).v[0]; });
+        }
+      };
+      float xn[WMAX];                      // the next input degree's x rows, in flight
+      xn[0] = buf_load<1, kNonTemporal>(rx, vo).v[0];
+      static_for<0, D>(request);
+      static_for<0, LIN + 1>([&](auto A) {
+        constexpr int a = A, ni = 2 * a + 1;
+        constexpr int p0 = first_path_of_degree<LIN, LE, LOUT>(a), p1 = first_path_of_degree<LIN, LE, LOUT>(a + 1);
+        float xr[ni], dxr[ni];
+#pragma unroll
+        for (int i = 0; i < ni; ++i) {
+          xr[i] = xn[i];
+          dxr[i] = 0.f;
+        }
+        if constexpr (a < LIN) {
+#pragma unroll
+          for (int i = 0; i < ni + 2; ++i) xn[i] = buf_load<1, kNonTemporal>(rx, vo + ((a + 1) * (a + 1) + i) * row).v[0];
+        }
+        static_for<p0, p1>([&](auto P) {
+          constexpr int p = P;
+          constexpr int l2 = PS::tab.l2[p], l3 = PS::tab.l3[p];
+          constexpr int nj = 2 * l2 + 1, no = 2 * l3 + 1;
+          constexpr int boff = PS::tab.bond[p];
+          using CG = CGTab<a, l2, l3>;
+          const float gv = pre_g[p % D];
+          float o[no];
+          static_for<0, no>([&](auto K) { o[K] = pre_o[p % D][K]; });
+          request(Int<p + D>{});           // issued ahead of this path's dg store
+          float dgv = 0.f;
+          float gov[no];
+          static_for<0, no>([&](auto K) {
+            gov[K] = gv * o[K];
+            float base = 0.f;
+            static_for<0, ni>([&](auto I) {
+              const float m = bond[boff + K * ni + I];
+              base = fmaf(xr[I], m, base);
+              dxr[I] = fmaf(m, gov[K], dxr[I]);
+            });
+            dgv = fmaf(base, o[K], dgv);
+          });
+          buf_store<1>(rdg, vo + p * row, Vec<1>{{dgv}});
+          float part[nj];
+#pragma unroll
+          for (int j = 0; j < nj; ++j) part[j] = 0.f;
+          static_for<0, ni>([&](auto I) {
+            static_for<0, no>([&](auto K) {
+              const float t = xr[I] * gov[K];
+              static_for<0, nj>([&](auto J) {
+                constexpr float cg = CG::v[(I * nj + J) * no + K];
+                if constexpr (cg != 0.0f) part[J] = fmaf(cg, t, part[J]);
+              });
+            });
+          });
+          const float s = d.scale[p];
+#pragma unroll
+          for (int j = 0; j < nj; ++j) dyl[l2 * l2 + j] = fmaf(s, part[j], dyl[l2 * l2 + j]);
+        });
+#pragma unroll
+        for (int i = 0; i < ni; ++i) buf_store<1>(rdx, vo + (a * a + i) * row, Vec<1>{{dxr[i]}});
+      });
+    }
+    store_channel_sums<NY>(dyl, lane, make_rsrc(dy ? dy + e * NY : nullptr, NY * 4u));
   }
 }
 
@@ -332,7 +456,11 @@ template <int LIN, int LE, int LOUT>
 int launch_backward(const ictc_tp_desc& d, const float* x, const float* y, const float* g,
                     const float* go, float* dx, float* dy, float* dg, int64_t rows, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>((rows + kBwdTile - 1) / kBwdTile));
-  if (d.channels % (2 * kWave) == 0)
+  if constexpr (LIN >= 4) {
+    if (rows > 0x7fffffff) return ICTC_ERR_INVALID_ARGUMENT;   // one workgroup per instance
+    hipLaunchKernelGGL((tp_backward_wide_kernel<LIN, LE, LOUT>), dim3(static_cast<unsigned>(rows)),
+                       dim3(kWideBlock), 0, stream, x, y, g, go, dx, dy, dg, d, rows);
+  } else if (d.channels % (2 * kWave) == 0)
     hipLaunchKernelGGL((tp_backward_kernel<LIN, LE, LOUT, 2>), grid, dim3(kBlock), 0, stream, x, y, g,
                        go, dx, dy, dg, d, rows);
   else

@@ -62,7 +62,8 @@ typedef enum ictc_status {
  * and keeps its own output rows.
  *
  * Degrees: every degree <= 6.  Degree sets with all degrees <= 3 run kernels compiled per
- * degree set (path loops unrolled, CG constants folded); the others run degree-generic
+ * degree set (path loops unrolled, CG constants folded), and so do ictc_hip_tp_forward and
+ * ictc_hip_tp_backward for the (4, 4, 4) set; the others run degree-generic
  * kernels that read the path table and the CG tensors at run time (one wave per instance),
  * behind every tensor-product and graph-message entry point except the two message tangent
  * entry points, which return ICTC_ERR_UNSUPPORTED for such degree sets.

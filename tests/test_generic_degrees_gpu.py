@@ -1,6 +1,6 @@
-"""GPU parity of the degree-generic kernels (degree sets with a degree of 4 to 6, whose path
-tables and CG tensors the kernels read at run time) against the float64 oracle, through the
-C ABI: tensor product forward / VJP / mixed second derivatives, graph message forward / VJP /
+"""GPU parity of the degree sets with a degree of 4 to 6 against the float64 oracle, through the
+C ABI: the degree-generic kernels (path tables and CG tensors read at run time), and for the TP
+entry points at (4, 4, 4) the compiled per-degree forward and the wide VJP: tensor product forward / VJP / mixed second derivatives, graph message forward / VJP /
 mixed second derivatives (the substitution route: these degrees have no fused tangent
 kernels), the message VJP through the allocation-free entry point, and size-independent
 properties at a larger size (rotation equivariance, the adjoint identity, message over the
@@ -22,9 +22,11 @@ from oracle.tensor_product import TensorProductOracle
 pytestmark = pytest.mark.gpu
 
 # (C, input_lmax, edge_lmax, output_lmax): C = 70 covers a partial second channel chunk; (4, 2, 1)
-# has an input degree without any path (4 > 2 + 1), whose feature-gradient rows are zero.
-TP_CASES = [(32, 4, 4, 4, "ir_mul"), (16, 6, 6, 6, "ir_mul"), (70, 5, 3, 6, "mul_ir"), (24, 4, 2, 1, "ir_mul"),
-            (8, 0, 5, 5, "ir_mul")]
+# has an input degree without any path (4 > 2 + 1), whose feature-gradient rows are zero.  The
+# (4, 4, 4) cases run the compiled kernels: C = 32 a partial first chunk, C = 70 a partial second
+# chunk of the wide VJP, C = 128 the two-channels-per-lane forward.
+TP_CASES = [(32, 4, 4, 4, "ir_mul"), (70, 4, 4, 4, "mul_ir"), (128, 4, 4, 4, "ir_mul"), (16, 6, 6, 6, "ir_mul"),
+            (70, 5, 3, 6, "mul_ir"), (24, 4, 2, 1, "ir_mul"), (8, 0, 5, 5, "ir_mul")]
 MSG_CASES = [(32, 4, 4, 4, False), (70, 5, 2, 4, True), (16, 6, 6, 6, False), (24, 4, 2, 1, True)]
 
 
