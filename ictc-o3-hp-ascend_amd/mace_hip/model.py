@@ -50,7 +50,7 @@ from ictc_o3.backends.hip.radial_message import fold_projection, packed_radial_g
 from ictc_o3.basis.ictd_irreps import EdgeWeightedPathPreservingTensorProduct
 from ictc_o3.ops.symmetric_contraction import ICTDBridgeUSymmetricContractionSO3
 
-from . import radial_mlp
+from . import radial_mlp, species_linear
 from .activation import silu
 from .embedding import edge_embedding
 from .geometry import edge_vectors, one_hot_rows
@@ -132,6 +132,9 @@ class SpeciesLinear(nn.Module):
 
     def forward(self, x: torch.Tensor, species: torch.Tensor) -> torch.Tensor:
         s, c = self.num_elements, self.channels
+        if species_linear.supported(x, self.weight, species):
+            # a frozen weight: one kernel per node block (and its transpose as the adjoint)
+            return species_linear.species_linear(x, self.weight, species)
         # all species at once (one GEMM), then pick each node's own block
         y = linear(x, self.weight.reshape(s * c, c)).reshape(-1, s, c)
         return y.gather(1, species.view(-1, 1, 1).expand(-1, 1, c)).squeeze(1)

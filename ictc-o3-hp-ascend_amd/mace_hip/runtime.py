@@ -48,6 +48,9 @@ def create_model(*, channels=64, lmax=3, edge_lmax=None, num_interactions=2, cor
     return model.to(device=device, dtype=dtype)
 
 
+_ONE_BLOCK_SUM = 65536   # atoms of one structure summed by a plain reduction (see energy_and_forces)
+
+
 def energy_and_forces(model, positions, atomic_numbers, batch, edge_src, edge_dst, edge_shifts, cell, *,
                       training=False, species=None):
     """-> {"energy": [B], "forces": [N,3], "atomic_energy": [N]}; cell [B,3,3], shifts in lattice
@@ -64,9 +67,16 @@ def energy_and_forces(model, positions, atomic_numbers, batch, edge_src, edge_ds
     with torch.enable_grad():
         pos = positions if positions.requires_grad else positions.detach().requires_grad_(True)
         atomic = model(pos, atomic_numbers, batch, edge_src, edge_dst, edge_shifts, cell, species=species)
-        # per-structure sums as one_hot(batch)^T @ atomic: a fixed summation order
-        energy = mm(one_hot_rows(batch, cell.shape[0]).t(), atomic.unsqueeze(1)).squeeze(1)
-        total = energy.sum()
+        if cell.shape[0] == 1 and n <= _ONE_BLOCK_SUM:
+            # one structure: its energy is the sum of every atomic energy, one reduction kernel
+            # whose adjoint is a broadcast (at this size torch reduces in one workgroup, with no
+            # cross-block staging to clear: the step stays capturable into a HIP graph)
+            energy = atomic.sum(0, keepdim=True)
+            total = energy.reshape(())
+        else:
+            # per-structure sums as one_hot(batch)^T @ atomic: a fixed summation order
+            energy = mm(one_hot_rows(batch, cell.shape[0]).t(), atomic.unsqueeze(1)).squeeze(1)
+            total = energy.sum()
         if edge_src.numel() == 0:
             # keep the coordinate dependency of a graph without edges (a 3-element sum: no
             # multi-block reduction, so the step stays capturable into a HIP graph)

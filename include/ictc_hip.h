@@ -460,6 +460,23 @@ int ictc_hip_edge_embedding(int mode, const float* vectors, const float* grad_di
                             hipStream_t stream);
 
 /*
+ * Element-conditioned linear map on a scalar block (the MACE interaction's self connection):
+ *   ICTC_SPECIES_APPLY    : out[n][o] = sum_i weight[species[n]][o][i] x[n][i]
+ *   ICTC_SPECIES_TRANSPOSE: out[n][i] = sum_o weight[species[n]][o][i] x[n][o]   (the input
+ *                           adjoint of APPLY)
+ * weight [num_species, channels, channels] (one torch Linear weight per species, row o), x and out
+ * [nodes, channels], species [nodes] int64 in [0, num_species) (validated by the caller; a value
+ * outside reads species 0).  Replaces ElementConditionedLinearSO3 on the l = 0 block (reference
+ * mace_ictc/models/pure_cartesian_ictd_fix.py:335-390), whose library-op form is one product with
+ * every species' weight followed by a gather of each node's block.  1 <= channels <=
+ * ICTC_SPECIES_MAX_CHANNELS.
+ */
+enum ictc_species_mode { ICTC_SPECIES_APPLY = 0, ICTC_SPECIES_TRANSPOSE = 1 };
+#define ICTC_SPECIES_MAX_CHANNELS 4096
+int ictc_hip_species_linear(int mode, const float* weight, const float* x, const int64_t* species, float* out,
+                            int channels, int num_species, int64_t nodes, hipStream_t stream);
+
+/*
  * SiLU derivative forms of force training's double backward through the radial MLP: for the
  * first-order backward y = grad * silu'(x) and a cotangent of y, one elementwise pass over n
  * floats writes

@@ -241,3 +241,21 @@ def test_radial_mlp_workspace_and_validation():
     assert call(mode=2, u=None, gg=fake) == 1                       # VJP_VJP without the cotangent
     assert call(mode=1, gw=(fake, None, None), ws=fake, wsf=part - 1, edges=1) == 1   # workspace too small
     assert call(mode=1, gw=(None, fake, None), ws=None, wsf=part, edges=1) == 1       # no workspace
+
+
+def test_species_linear_validation():
+    """ictc_hip_species_linear rejects bad modes, channel counts and missing tensors before any
+    launch, and an empty node set does nothing."""
+    from ictc_o3 import _lib
+    lib = _lib.lib()
+    fake = ctypes.c_void_p(16)  # never dereferenced: every call below fails validation or does nothing
+    sl = lib.ictc_hip_species_linear
+
+    def call(mode=0, w=fake, x=fake, s=fake, out=fake, c=128, ns=10, nodes=100):
+        return sl(mode, w, x, s, out, c, ns, nodes, None)
+
+    assert call(mode=2) == 1 and call(mode=-1) == 1                 # unknown mode
+    assert call(c=0) == 1 and call(c=4097) == 1                     # channels outside 1..4096
+    assert call(ns=0) == 1 and call(nodes=-1) == 1                  # no species, negative rows
+    assert call(w=None) == 1 and call(x=None) == 1 and call(s=None) == 1 and call(out=None) == 1
+    assert call(nodes=0, w=None) == 0                               # nothing to do: no launch
