@@ -51,7 +51,8 @@ FLAGS = ["--offload-arch=" + ARCH, "-O3", "-std=c++20", "-fPIC", "-Wno-c99-desig
 
 API_SOURCES = ["tp_api.hip", "harmonics_api.hip", "message_api.hip", "sc_api.hip", "graph_api.hip",
                "elementwise_api.hip", "blas_api.hip", "linear_api.hip", "generic_kernels.hip",
-               "edge_embedding_api.hip", "radial_mlp_api.hip", "species_linear_api.hip"]
+               "edge_embedding_api.hip", "radial_mlp_api.hip", "species_linear_api.hip",
+               "readout_api.hip"]
 # rocBLAS (the channel-linear products): the same SONAME as the copy torch loads, which the
 # dynamic linker then binds to
 LINK_LIBS = ["-L/opt/rocm/lib", "-lrocblas"]

@@ -97,7 +97,7 @@ const char* ictc_hip_status_string(int status) {
   }
 }
 
-int ictc_hip_abi_version(void) { return 20; }
+int ictc_hip_abi_version(void) { return 21; }
 
 int ictc_hip_tp_slot_count(int input_lmax, int edge_lmax, int output_lmax) {
   constexpr int L = ictc::kGenericMaxL;

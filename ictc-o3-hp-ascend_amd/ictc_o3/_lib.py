@@ -15,7 +15,7 @@ import torch  # noqa: F401  (must precede CDLL, see module docstring)
 
 MAX_PATHS = 128
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libictc_hip.so")
-ABI_VERSION = 20
+ABI_VERSION = 21
 
 
 class TpDesc(ctypes.Structure):
@@ -103,6 +103,8 @@ _SIGNATURES = {
     "ictc_hip_degree_linear_weight_grad": (ctypes.c_int, [ctypes.POINTER(DegreeLinearDesc), ctypes.c_int, _P, _P,
                                                           ctypes.c_float, _P, _I64, _P, _I64, _P]),
     "ictc_hip_silu_second": (ctypes.c_int, [_P, _P, _P, _P, _P, _I64, _P]),
+    "ictc_hip_readout": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _P, _P, ctypes.c_float, _P, _P, _P, _P, ctypes.c_int,
+                                        ctypes.c_int, _I64, _P]),
     "ictc_hip_species_linear": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _P, ctypes.c_int, ctypes.c_int, _I64, _P]),
     "ictc_hip_edge_embedding": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _P, _P, _P, ctypes.c_int, ctypes.c_int,
                                                ctypes.c_float, _I64, _P]),

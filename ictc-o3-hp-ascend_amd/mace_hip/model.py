@@ -51,6 +51,7 @@ from ictc_o3.basis.ictd_irreps import EdgeWeightedPathPreservingTensorProduct
 from ictc_o3.ops.symmetric_contraction import ICTDBridgeUSymmetricContractionSO3
 
 from . import radial_mlp, species_linear
+from .readout import readout, supported as readout_supported
 from .activation import silu
 from .embedding import edge_embedding
 from .geometry import edge_vectors, one_hot_rows
@@ -173,6 +174,7 @@ class Interaction(nn.Module):
         # None: the gates are one [E, P*C] tensor; an int: radial streaming over receiver ranges of
         # at most that many edges (the reference's _ascend_edge_chunk_size)
         self.edge_chunk_size: Optional[int] = None
+        self._gate_weight = None   # (weights' identity and version, folded last-layer weight) when frozen
         self.self_connection = SpeciesLinear(num_elements, channels)
 
     def radial_hidden(self, edge_feats):
@@ -180,14 +182,17 @@ class Interaction(nn.Module):
         each normalised SiLU's constant folded into the next layer's weight instead of scaling
         the [E, 64] activations.  On the GPU the three layers and their activations run as one
         kernel per derivative order (mace_hip.radial_mlp)."""
+        return self._hidden(edge_feats), self.fc[-1].weight * SILU_SCALE
+
+    def _hidden(self, edge_feats):
         layers = [m for m in self.fc if isinstance(m, nn.Linear)]
         w = [lin.weight for lin in layers]
         if len(layers) == 4 and radial_mlp.supported(edge_feats, *w[:3]):
-            return radial_mlp.radial_hidden(edge_feats, *w[:3], SILU_SCALE), w[3] * SILU_SCALE
+            return radial_mlp.radial_hidden(edge_feats, *w[:3], SILU_SCALE)
         h = layers[0](edge_feats)
         for lin in layers[1:-1]:
             h = linear(silu(h), lin.weight * SILU_SCALE)
-        return silu(h), layers[-1].weight * SILU_SCALE
+        return silu(h)
 
     def radial_mlp(self, edge_feats):
         """self.fc on the edge features: the gates [E, P*C]."""
@@ -197,9 +202,17 @@ class Interaction(nn.Module):
     def message_gates(self, edge_feats):
         """The gates times the TP's frozen path weight (the reference's gates * weight,
         ``backends/ascend/packed_tensor_product.py:163-164``), folded into the rows of the radial
-        MLP's last weight ([P*C, 64]) rather than applied to the [E, P*C] gates."""
-        hidden, weight = self.radial_hidden(edge_feats)
-        return linear(hidden, weight * self.tp.weight.reshape(-1, 1))
+        MLP's last weight ([P*C, 64]) rather than applied to the [E, P*C] gates.  With no gradient
+        to either weight the folded [P*C, 64] weight is kept until one of them is replaced or
+        modified in place."""
+        hidden = self._hidden(edge_feats)
+        last = self.fc[-1].weight
+        if torch.is_grad_enabled() and (last.requires_grad or self.tp.weight.requires_grad):
+            return linear(hidden, last * SILU_SCALE * self.tp.weight.reshape(-1, 1))
+        key = tuple((id(t), t.data_ptr(), t._version) for t in (last, self.tp.weight))
+        if self._gate_weight is None or self._gate_weight[0] != key:
+            self._gate_weight = (key, last * SILU_SCALE * self.tp.weight.reshape(-1, 1))
+        return linear(hidden, self._gate_weight[1])
 
     def message_bonds(self, harmonics):
         """The bond rows the message forward derives from the harmonics (see forward's bonds)."""
@@ -318,7 +331,8 @@ class MaceICTC(nn.Module):
         """Atomic energies [N] (reference forward :2879-3106, baseline route)."""
         # shift_e @ cell_e as three multiply-adds per edge (not a batched GEMM of 3 x 3 matrices)
         # index_select rather than advanced indexing (cheaper to issue; same gather)
-        edge_cell = cell.index_select(0, batch.index_select(0, edge_src)).to(pos.dtype)
+        # (one structure: its cell broadcast over the edges, no per-edge gather of it)
+        edge_cell = (cell[0] if cell.shape[0] == 1 else cell.index_select(0, batch.index_select(0, edge_src))).to(pos.dtype)
         shift_vecs = (edge_shifts.to(pos.dtype).unsqueeze(-1) * edge_cell).sum(1)
         # pos[dst] - pos[src] with a fixed-order (atomic-free) adjoint: forces are reproducible
         vec = edge_vectors(pos, edge_src, edge_dst) + shift_vecs
@@ -347,6 +361,8 @@ class MaceICTC(nn.Module):
         side = self._side_work(edge_feats, harmonics)
         energy = None
         scalars = h
+        last = len(self.interactions) - 1
+        deferred = None   # the second-to-last layer's scalars, read out with the last layer's
         for t, (interaction, product) in enumerate(zip(self.interactions, self.products)):
             gates = bonds = None
             if side is not None:
@@ -355,14 +371,31 @@ class MaceICTC(nn.Module):
             message, sc = interaction(h, harmonics, edge_feats, edge_src, edge_dst, mask, species, scalars,
                                       gates, bonds)
             h, scalars = product(message, sc, species)
-            if t < len(self.interactions) - 1:
+            if t == last - 1 and self._fused_readout(scalars, h):
+                deferred = scalars
+                continue
+            if t < last:
                 e = self.layer_readouts[t](scalars)
+            elif deferred is not None:
+                lin1, _, lin2 = self.last_readout
+                e = readout(deferred, h, self.layer_readouts[t - 1].weight, lin1.weight, lin2.weight, SILU_SCALE)
             else:
                 e = self.last_readout(h)
             energy = e if energy is None else energy + e
         if side is not None:   # join the side stream (nothing left on it unwaited, also under capture)
             torch.cuda.current_stream(pos.device).wait_stream(_side_stream(pos.device))
         return energy.reshape(-1)
+
+    def _fused_readout(self, scalars, h):
+        """Whether the second-to-last layer's readout and the last layer's run as one kernel
+        (mace_hip.readout: frozen fp32 GPU weights, the last readout Linear -> SiLU -> Linear)."""
+        if len(self.interactions) < 2 or len(self.last_readout) != 3:
+            return False
+        lin1, act, lin2 = self.last_readout
+        if not isinstance(act, NormalizedSiLU) or lin2.weight.shape[0] != 1:
+            return False
+        w_lin = self.layer_readouts[len(self.interactions) - 2].weight
+        return w_lin.shape[0] == 1 and readout_supported(scalars, scalars, w_lin, lin1.weight, lin2.weight)
 
     def _side_work(self, edge_feats, harmonics):
         """Each interaction's message gates (radial MLP and its [E, P*C] last layer) and bond rows,

@@ -477,6 +477,25 @@ int ictc_hip_species_linear(int mode, const float* weight, const float* x, const
                             int channels, int num_species, int64_t nodes, hipStream_t stream);
 
 /*
+ * Atomic-energy readouts of the MACE model, one pass per derivative order.  Per node n, with x the
+ * last layer's scalar features [nodes, channels] and y an earlier layer's (or null):
+ *   ICTC_READOUT_VALUE: out_atomic[n] = w_lin . y[n] + sum_j w2[j] scale silu(w1[j] . x[n])
+ *   ICTC_READOUT_VJP  : for grad_atomic g: grad_y[n] = g[n] w_lin (if non-null) and
+ *                       grad_x[n] = sum_j w1[j] scale w2[j] silu'(w1[j] . x[n]) g[n] (if non-null)
+ * w_lin [channels], w1 [hidden, channels], w2 [hidden].  Replaces the per-layer readout (bias-free
+ * Linear(C, 1), reference EquivariantScalarReadoutSO3, mace_ictc/models/pure_cartesian_ictd_layers.py:
+ * 46-70) of one inner layer and the last layer's MLP readout (Linear(C, H), normalised SiLU,
+ * Linear(H, 1); mace_ictc/models/pure_cartesian_ictd_fix.py:1434-1449), summed, with their
+ * adjoints.  1 <= channels <= ICTC_READOUT_MAX_CHANNELS, 1 <= hidden <= ICTC_READOUT_MAX_HIDDEN.
+ */
+enum ictc_readout_mode { ICTC_READOUT_VALUE = 0, ICTC_READOUT_VJP = 1 };
+#define ICTC_READOUT_MAX_CHANNELS 1024
+#define ICTC_READOUT_MAX_HIDDEN 256
+int ictc_hip_readout(int mode, const float* y, const float* w_lin, const float* x, const float* w1,
+                     const float* w2, float scale, const float* grad_atomic, float* out_atomic, float* grad_y,
+                     float* grad_x, int channels, int hidden, int64_t nodes, hipStream_t stream);
+
+/*
  * SiLU derivative forms of force training's double backward through the radial MLP: for the
  * first-order backward y = grad * silu'(x) and a cotangent of y, one elementwise pass over n
  * floats writes

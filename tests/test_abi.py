@@ -259,3 +259,26 @@ def test_species_linear_validation():
     assert call(ns=0) == 1 and call(nodes=-1) == 1                  # no species, negative rows
     assert call(w=None) == 1 and call(x=None) == 1 and call(s=None) == 1 and call(out=None) == 1
     assert call(nodes=0, w=None) == 0                               # nothing to do: no launch
+
+
+def test_readout_validation():
+    """ictc_hip_readout rejects bad modes, sizes and missing tensors before any launch, and a VJP
+    asked for nothing or an empty node set does nothing."""
+    from ictc_o3 import _lib
+    lib = _lib.lib()
+    fake = ctypes.c_void_p(16)  # never dereferenced: every call below fails validation or does nothing
+    ro = lib.ictc_hip_readout
+
+    def call(mode=0, y=fake, wl=fake, x=fake, w1=fake, w2=fake, g=fake, out=fake, gy=None, gx=None, c=128, h=16,
+             nodes=100):
+        return ro(mode, y, wl, x, w1, w2, 1.0, g, out, gy, gx, c, h, nodes, None)
+
+    assert call(mode=2) == 1 and call(mode=-1) == 1                 # unknown mode
+    assert call(c=0) == 1 and call(c=1025) == 1                     # channels outside 1..1024
+    assert call(h=0) == 1 and call(h=257) == 1 and call(nodes=-1) == 1
+    assert call(x=None) == 1 and call(w1=None) == 1 and call(w2=None) == 1 and call(wl=None) == 1
+    assert call(out=None) == 1                                      # VALUE without an output
+    assert call(mode=1, g=None, gx=fake) == 1                       # VJP without the adjoint
+    assert call(mode=1, y=None, gy=fake) == 1                       # grad_y without y
+    assert call(mode=1) == 0                                        # VJP asked for nothing: no launch
+    assert call(nodes=0, x=None) == 0                               # nothing to do
