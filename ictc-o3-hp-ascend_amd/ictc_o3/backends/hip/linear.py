@@ -71,6 +71,25 @@ def _sgemm(a: torch.Tensor, b: torch.Tensor, *, row_major_b: bool = False) -> to
     return out
 
 
+def sgemm_into(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+    """out = a [M, K] @ b [K, N] on rocBLAS with no autograd record, into a caller-owned row-major
+    out (a row slice of a larger matrix is fine); the operands' storage orders are passed as is."""
+    m, k = a.shape
+    n = b.shape[1]
+    if out.shape != (m, n) or out.stride(1) != 1 or out.dtype != torch.float32:
+        raise ValueError("sgemm_into needs a row-major float32 output of shape [M, N]")
+    if m == 0 or n == 0:
+        return out
+    if k == 0:
+        return out.zero_()
+    a, ta, lda = _storage(a)
+    b, tb, ldb = _storage(b)
+    _lib.check(_lib.lib().ictc_hip_sgemm(ta, tb, m, n, k, 1.0, a.data_ptr(), lda, b.data_ptr(), ldb, 0.0,
+                                         out.data_ptr(), max(out.stride(0), 1), _lib.stream_of(a.device)),
+               "ictc_hip_sgemm")
+    return out
+
+
 def _plain(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     if not a.is_cuda:
         return a @ b

@@ -20,6 +20,13 @@ Schedule (edges in receiver-CSR slot order; for a dst-sorted edge list that is t
 * a backward that is itself differentiated (force-loss training) materialises the full gates
   differentiably and takes the ordinary message adjoint, as the reference keeps its native
   recursive schedule for higher derivatives (``capacity_message.py:36-48``).
+
+Two ranges are in flight: consecutive ranges alternate between the caller's stream and a second
+(default-priority) stream, each stream with its own range buffers and, in the backward, its own
+node-gradient and weight-gradient accumulators (added once at the end), so one range's GEMM and
+kernels run beside the other's.  A single range at a time leaves most of the GPU idle at these sizes:
+a 16,384-edge range launches ~600 receiver blocks per message kernel.  Peak scratch is two ranges'
+buffers.
 """
 from __future__ import annotations
 
@@ -32,7 +39,7 @@ import torch
 from ... import _lib
 from ...autograd.adjoint_requirements import required_gradients
 from .graph_message import MessageGraph, bond_width, message_graph, vjp
-from .linear import mm
+from .linear import mm, sgemm_into
 from .tensor_product import TensorProductPlan
 
 
@@ -62,6 +69,7 @@ class RangePlan:
             torch.cumsum(counts, 0, out=rp[1:])
             perm = torch.sort(src_r, stable=True).indices if s1 > s0 else None
             self.source_csr.append((rp, perm))
+        self.max_rows = max([1] + [s1 - s0 for _, _, s0, s1 in self.ranges])
 
 
 def range_plan(graph: MessageGraph, edge_chunk_size: int) -> RangePlan:
@@ -79,92 +87,147 @@ def _slot_order(t: Optional[torch.Tensor], graph: MessageGraph) -> Optional[torc
     return t.index_select(0, graph.perm_dst)
 
 
-def _range_gates(hidden, weight, bias, mask, s0, s1):
-    g = mm(hidden[s0:s1], weight.t())
+def _range_gates_into(out, hidden, weight, bias, mask, s0, s1):
+    """The range's gates hidden[s0:s1] @ W^T (+ b) (* mask) into a stream's range buffer."""
+    g = sgemm_into(hidden[s0:s1], weight.t(), out[:s1 - s0])
     if bias is not None:
-        g = g + bias
+        g += bias
     if mask is not None:
-        g = g * mask[s0:s1].unsqueeze(1)
-    return g.contiguous()
+        g *= mask[s0:s1].unsqueeze(1)
+    return g
 
 
-def _range_bonds(plan: TensorProductPlan, y, s0, s1):
+def _range_bonds(plan: TensorProductPlan, y, s0, s1, out):
     yr = y[s0:s1]
     if bond_width(plan) == 0:
         return yr
-    out = torch.empty(s1 - s0, bond_width(plan), device=y.device, dtype=torch.float32)
     _lib.check(_lib.lib().ictc_hip_message_bonds(ctypes.byref(plan.desc), yr.data_ptr(), out.data_ptr(), s1 - s0,
                                                  _lib.stream_of(y.device)), "ictc_hip_message_bonds")
     return out
 
 
+_SIDE: dict = {}
+
+
+def _streams(device: torch.device):
+    """(the caller's stream, this module's second stream on the device, created once)."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    side = _SIDE.get(index)
+    if side is None:
+        side = _SIDE[index] = torch.cuda.Stream(device=index)
+    return torch.cuda.current_stream(device), side
+
+
+class _TwoStreams:
+    """Fork onto the second stream (it waits for the caller's work so far), mark the inputs it reads,
+    and join it back at the end: the caller's stream then holds every range's results."""
+
+    def __init__(self, device, reads):
+        self.main, self.side = _streams(device)
+        self.reads = [t for t in reads if t is not None]
+
+    def __enter__(self):
+        self.side.wait_stream(self.main)
+        for t in self.reads:
+            t.record_stream(self.side)
+        return (self.main, self.side)
+
+    def __exit__(self, *exc):
+        self.main.wait_stream(self.side)
+        return False
+
+
 def _forward_raw(plan, graph, ranges: RangePlan, x, y, hidden, weight, bias, mask):
     """x [N_src, NX*C]; y, hidden, mask in slot order."""
-    lib, stream = _lib.lib(), _lib.stream_of(x.device)
+    lib, dev = _lib.lib(), x.device
     width = plan.full_out_width
-    out = torch.empty(graph.nodes_dst, width, device=x.device, dtype=torch.float32)
-    for (n0, n1, s0, s1), rowptr in zip(ranges.ranges, ranges.rowptr):
-        if s1 == s0:
-            out[n0:n1].zero_()
-            continue
-        g = _range_gates(hidden, weight, bias, mask, s0, s1)
-        bonds = _range_bonds(plan, y, s0, s1)
-        _lib.check(lib.ictc_hip_message_forward(
-            ctypes.byref(plan.desc), x.data_ptr(), bonds.data_ptr(), g.data_ptr(), ranges.src_sorted[s0:s1].data_ptr(),
-            rowptr.data_ptr(), None, out[n0:n1].data_ptr(), graph.nodes_src, n1 - n0, s1 - s0, stream),
-            "ictc_hip_message_forward")
+    out = torch.empty(graph.nodes_dst, width, device=dev, dtype=torch.float32)
+    rows = ranges.max_rows
+    # one gate (and bond) buffer per stream, reused by that stream's ranges in its own order
+    gbuf = [torch.empty(rows, plan.full_gate_width, device=dev, dtype=torch.float32) for _ in range(2)]
+    bw = bond_width(plan)
+    bbuf = [torch.empty(rows, bw, device=dev, dtype=torch.float32) if bw else None for _ in range(2)]
+    with _TwoStreams(dev, (x, y, hidden, weight, bias, mask, out, gbuf[1], bbuf[1])) as streams:
+        for i, ((n0, n1, s0, s1), rowptr) in enumerate(zip(ranges.ranges, ranges.rowptr)):
+            k = i % 2
+            with torch.cuda.stream(streams[k]):
+                if s1 == s0:
+                    out[n0:n1].zero_()
+                    continue
+                g = _range_gates_into(gbuf[k], hidden, weight, bias, mask, s0, s1)
+                bonds = _range_bonds(plan, y, s0, s1, bbuf[k])
+                _lib.check(lib.ictc_hip_message_forward(
+                    ctypes.byref(plan.desc), x.data_ptr(), bonds.data_ptr(), g.data_ptr(),
+                    ranges.src_sorted[s0:s1].data_ptr(), rowptr.data_ptr(), None, out[n0:n1].data_ptr(),
+                    graph.nodes_src, n1 - n0, s1 - s0, _lib.stream_of(dev)), "ictc_hip_message_forward")
     return out
 
 
 def _backward_raw(plan, graph, ranges: RangePlan, need, x, y, hidden, weight, bias, mask, go):
     """First-order adjoints (dx, dy, dhidden, dweight, dbias), y/hidden/dy/dhidden in slot order."""
     nx, ny, nh, nw, nb = need
-    lib, stream = _lib.lib(), _lib.stream_of(x.device)
+    lib = _lib.lib()
     dev = x.device
-    dx = torch.zeros_like(x) if nx else None
-    dy = torch.empty(y.shape[0], plan.y_width, device=dev, dtype=torch.float32) if ny else None
-    dh = torch.empty_like(hidden) if nh else None
-    dw = torch.zeros_like(weight) if nw else None
-    db = torch.zeros_like(bias) if (nb and bias is not None) else None
     need_dg = nh or nw or nb
     nch = lib.ictc_hip_message_chunks(plan.channels)
+    dy = torch.empty(y.shape[0], plan.y_width, device=dev, dtype=torch.float32) if ny else None
+    dyp = torch.empty(y.shape[0], nch, plan.y_width, device=dev, dtype=torch.float32) if ny else None
+    dh = torch.empty_like(hidden) if nh else None
     # the range products dg_r @ W read W column-major (copied once here, not per range): 47 vs
     # 130 us for a 16,384-row range of the cfg-4 shape
     weight_cm = weight.t().contiguous().t() if nh else None
-    for (n0, n1, s0, s1), rowptr, (rp_src, perm_src) in zip(ranges.ranges, ranges.rowptr, ranges.source_csr):
-        rows = s1 - s0
-        if rows == 0:
-            continue
-        g = _range_gates(hidden, weight, bias, mask, s0, s1)
-        yr = y[s0:s1]   # the edge kernels read the harmonics rows
-        dyp = torch.empty(rows, nch, plan.y_width, device=dev, dtype=torch.float32) if ny else None
-        dg = torch.empty(rows, plan.full_gate_width, device=dev, dtype=torch.float32) if need_dg else None
-        dxe = torch.empty(rows, plan.x_width, device=dev, dtype=torch.float32) if nx else None
-        go_r = go[n0:n1]
-        _lib.check(lib.ictc_hip_message_edge_grad(
-            ctypes.byref(plan.desc), x.data_ptr() if (ny or need_dg) else None, yr.data_ptr(), g.data_ptr(),
-            go_r.data_ptr(), ranges.src_sorted[s0:s1].data_ptr(), rowptr.data_ptr(), None, _lib.ptr(dyp),
-            _lib.ptr(dg), _lib.ptr(dxe), graph.nodes_src, n1 - n0, rows, 0, stream), "ictc_hip_message_edge_grad")
-        if ny:
-            if nch == 1:
-                dy[s0:s1] = dyp[:, 0]
-            else:
-                torch.sum(dyp, 1, out=dy[s0:s1])
-        if need_dg:
-            if mask is not None:
-                dg = dg * mask[s0:s1].unsqueeze(1)
-            if nh:
-                dh[s0:s1] = mm(dg, weight_cm)
-            if nw:
-                dw += mm(dg.t(), hidden[s0:s1])
-            if db is not None:
-                db += dg.sum(0)
-        if nx:
-            part = torch.empty_like(x)
-            _lib.check(lib.ictc_hip_message_node_grad(
-                ctypes.byref(plan.desc), dxe.data_ptr(), rp_src.data_ptr(), _lib.ptr(perm_src), part.data_ptr(),
-                graph.nodes_src, rows, stream), "ictc_hip_message_node_grad")
-            dx += part
+    rows = ranges.max_rows
+
+    def buffers():
+        """One stream's range buffers and its node-, weight- and bias-gradient accumulators."""
+        return dict(g=torch.empty(rows, plan.full_gate_width, device=dev, dtype=torch.float32),
+                    dg=torch.empty(rows, plan.full_gate_width, device=dev, dtype=torch.float32) if need_dg else None,
+                    dxe=torch.empty(rows, plan.x_width, device=dev, dtype=torch.float32) if nx else None,
+                    part=torch.empty_like(x) if nx else None, dx=torch.zeros_like(x) if nx else None,
+                    dw=torch.zeros_like(weight) if nw else None,
+                    db=torch.zeros_like(bias) if (nb and bias is not None) else None)
+    buf = [buffers(), buffers()]
+    reads = (x, y, hidden, weight, bias, mask, go, weight_cm, dyp, dh, *buf[1].values())
+    with _TwoStreams(dev, reads) as streams:
+        for i, ((n0, n1, s0, s1), rowptr, (rp_src, perm_src)) in enumerate(
+                zip(ranges.ranges, ranges.rowptr, ranges.source_csr)):
+            r = s1 - s0
+            if r == 0:
+                continue
+            bk = buf[i % 2]
+            with torch.cuda.stream(streams[i % 2]):
+                stream = _lib.stream_of(dev)
+                g = _range_gates_into(bk["g"], hidden, weight, bias, mask, s0, s1)
+                dg = bk["dg"][:r] if need_dg else None
+                dxe = bk["dxe"][:r] if nx else None
+                _lib.check(lib.ictc_hip_message_edge_grad(
+                    ctypes.byref(plan.desc), x.data_ptr() if (ny or need_dg) else None, y[s0:s1].data_ptr(),
+                    g.data_ptr(), go[n0:n1].data_ptr(), ranges.src_sorted[s0:s1].data_ptr(), rowptr.data_ptr(), None,
+                    _lib.ptr(dyp[s0:s1] if ny else None), _lib.ptr(dg), _lib.ptr(dxe), graph.nodes_src, n1 - n0, r,
+                    0, stream), "ictc_hip_message_edge_grad")
+                if need_dg:
+                    if mask is not None:
+                        dg *= mask[s0:s1].unsqueeze(1)
+                    if nh:
+                        sgemm_into(dg, weight_cm, dh[s0:s1])
+                    if nw:
+                        bk["dw"] += mm(dg.t(), hidden[s0:s1])
+                    if bk["db"] is not None:
+                        bk["db"] += dg.sum(0)
+                if nx:
+                    _lib.check(lib.ictc_hip_message_node_grad(
+                        ctypes.byref(plan.desc), dxe.data_ptr(), rp_src.data_ptr(), _lib.ptr(perm_src),
+                        bk["part"].data_ptr(), graph.nodes_src, r, stream), "ictc_hip_message_node_grad")
+                    bk["dx"] += bk["part"]
+    if ny:   # channel-chunk partials of every range, summed once
+        if nch == 1:
+            dy.copy_(dyp[:, 0])
+        else:
+            torch.sum(dyp, 1, out=dy)
+    # the two streams' partial sums, in a fixed order (the same on every run)
+    dx = buf[0]["dx"] + buf[1]["dx"] if nx else None
+    dw = buf[0]["dw"] + buf[1]["dw"] if nw else None
+    db = buf[0]["db"] + buf[1]["db"] if buf[0]["db"] is not None else None
     return dx, dy, dh, dw, db
 
 
