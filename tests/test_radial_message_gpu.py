@@ -221,3 +221,23 @@ def test_mace_streaming_peak_memory_at_cfg4_size(gpu):
         del out
     gate_bytes = edges * 23 * 128 * 4
     assert peaks[None] - peaks[16384] >= gate_bytes, (peaks, gate_bytes)
+
+
+def test_mace_streaming_is_deterministic(gpu):
+    """Two receiver ranges run on two streams; every sum still has a fixed order, so streamed
+    energies and forces (frozen model) and training gradients are bit-identical run to run, with
+    several ranges in flight (47-edge ranges)."""
+    from mace_hip import energy_and_forces, force_loss
+    model, graph = _mace(gpu, 64, 80, 5)
+    model.set_message_streaming(47)
+    params = [p for p in model.parameters() if p.requires_grad]
+    first = energy_and_forces(model, **graph, training=True)
+    g1 = torch.autograd.grad(force_loss(first, 80), params)
+    second = energy_and_forces(model, **graph, training=True)
+    g2 = torch.autograd.grad(force_loss(second, 80), params)
+    assert torch.equal(first["forces"], second["forces"]) and torch.equal(first["energy"], second["energy"])
+    assert all(torch.equal(a, b) for a, b in zip(g1, g2))
+    model.eval().requires_grad_(False)
+    a = energy_and_forces(model, **graph)
+    b = energy_and_forces(model, **graph)
+    assert torch.equal(a["forces"], b["forces"]) and torch.equal(a["energy"], b["energy"])
